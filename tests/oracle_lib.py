@@ -1,0 +1,197 @@
+"""ctypes bindings to the CPU oracle (oracle/liboracle.so), the checker every
+parity test compares against. Test infrastructure: nothing in the product
+imports this module."""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(ROOT, "oracle", "liboracle.so")
+
+_lib = None
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+I = ctypes.c_int
+U32 = ctypes.c_uint32
+U64 = ctypes.c_uint64
+F = ctypes.c_float
+L = ctypes.c_long
+
+
+def ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+        _lib = ctypes.CDLL(LIB_PATH)
+        sigs = {
+            "oracle_golden_digest": (U64, [ctypes.c_char_p, ctypes.c_char_p, I, I, I, I]),
+            "oracle_f32_to_bf16": (None, [P, SZ, P]),
+            "oracle_codebook": (I, [U32, SZ, P, P, P]),
+            "oracle_codebook_quantize": (I, [U32, P, SZ, P]),
+            "oracle_rotation_random": (None, [I, U64, P]),
+            "oracle_rotation_apply": (None, [P, I, P, P]),
+            "oracle_rotation_apply_inverse": (None, [P, I, P, P]),
+            "oracle_qjl_random": (None, [I, I, U64, P]),
+            "oracle_packed_words": (SZ, [SZ, U32]),
+            "oracle_pack_codes": (None, [P, SZ, U32, P]),
+            "oracle_unpack_codes": (None, [P, SZ, U32, P]),
+            "oracle_qjl_packed_len": (SZ, [SZ]),
+            "oracle_qjl_project_and_pack": (None, [P, I, I, P, P]),
+            "oracle_qjl_estimate": (F, [P, I, I, P, P, F]),
+            "oracle_compressor_new": (P, [I, U32, I, P, P]),
+            "oracle_compressor_free": (None, [P]),
+            "oracle_compress": (None, [P, P, SZ, P, P, P, P]),
+            "oracle_scores": (None, [P, P, SZ, P, P, P, P, I, P]),
+            "oracle_attend_values": (None, [P, P, SZ, P, P, P, P, P]),
+            "oracle_affine_quantize": (None, [P, SZ, I, I, I, P, P, P, I, I, I]),
+            "oracle_affine_dequantize": (None, [P, P, P, SZ, I, I, I, P]),
+            "oracle_mask_allowed": (I, [SZ, SZ, L]),
+            "oracle_attend_bf16": (None, [P, P, P, I, I, I, I, SZ, I, F, I, SZ, SZ, L, P, P, P]),
+            "oracle_attend_affine": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, I, I, I, F, I,
+                                            SZ, SZ, L, P, P, P]),
+            "oracle_attend_codebook": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, F, I, SZ,
+                                              SZ, L, P, P, P]),
+        }
+        for name, (res, args) in sigs.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+# ------------------------------------------------------------------ helpers
+def bf16_from_f32(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_bf16(ptr(x), x.size, ptr(out))
+    return out
+
+
+def bf16_to_f32(b):
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def golden_digest(kind, plan, prealloc, round_mode=0, wmax0=1, clip_low=0):
+    return lib().oracle_golden_digest(kind.encode(), plan.encode(), int(prealloc), round_mode,
+                                      wmax0, clip_low)
+
+
+def codebook(bits, n_iter=1000):
+    n = 1 << bits
+    b = np.empty(n + 1, np.float64)
+    c = np.empty(n, np.float64)
+    mse = ctypes.c_double()
+    rc = lib().oracle_codebook(bits, n_iter, ptr(b), ptr(c), ctypes.byref(mse))
+    assert rc == 0
+    return b, c, mse.value
+
+
+def rotation(dim, seed):
+    r = np.empty((dim, dim), np.float32)
+    lib().oracle_rotation_random(dim, seed, ptr(r))
+    return r
+
+
+def qjl_matrix(dim, m, seed):
+    p = np.empty((m, dim), np.float32)
+    lib().oracle_qjl_random(dim, m, seed, ptr(p))
+    return p
+
+
+def affine_quantize(w_bf16, gs, bits, round_mode=0, wmax0=1, clip_low=0):
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    d = w.shape[-1]
+    rows = w.size // d
+    packed = np.zeros(w.shape[:-1] + (d * bits // 32,), np.uint32)
+    scales = np.zeros(w.shape[:-1] + (d // gs,), np.uint16)
+    biases = np.zeros_like(scales)
+    lib().oracle_affine_quantize(ptr(w), rows, d, gs, bits, ptr(packed), ptr(scales),
+                                 ptr(biases), round_mode, wmax0, clip_low)
+    return packed, scales, biases
+
+
+def affine_dequantize(packed, scales, biases, gs, bits):
+    d = packed.shape[-1] * 32 // bits
+    rows = packed.size // packed.shape[-1]
+    out = np.empty(packed.shape[:-1] + (d,), np.uint16)
+    lib().oracle_affine_dequantize(ptr(np.ascontiguousarray(packed)), ptr(np.ascontiguousarray(scales)),
+                                   ptr(np.ascontiguousarray(biases)), rows, d, gs, bits, ptr(out))
+    return out
+
+
+class Compressor:
+    """TurboQuantCompressor over given R and Phi."""
+
+    def __init__(self, dim, bits, m, R, phi):
+        self.dim, self.bits, self.m = dim, bits, m
+        self.R = np.ascontiguousarray(R, np.float32)
+        self.phi = np.ascontiguousarray(phi, np.float32)
+        self.h = lib().oracle_compressor_new(dim, bits, m, ptr(self.R), ptr(self.phi))
+        assert self.h
+        self.w1 = lib().oracle_packed_words(dim, bits)
+        self.w2 = lib().oracle_qjl_packed_len(m)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().oracle_compressor_free(self.h)
+
+    def compress(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.dim)
+        n = x.shape[0]
+        s1 = np.zeros((n, self.w1), np.uint64)
+        s2 = np.zeros((n, self.w2), np.uint64)
+        rn = np.zeros(n, np.float32)
+        sc = np.zeros(n, np.float32)
+        lib().oracle_compress(self.h, ptr(x), n, ptr(s1), ptr(s2), ptr(rn), ptr(sc))
+        return s1, s2, rn, sc
+
+    def scores(self, q, comp, two_stage=False):
+        s1, s2, rn, sc = comp
+        q = np.ascontiguousarray(q, np.float32)
+        out = np.empty(s1.shape[0], np.float32)
+        lib().oracle_scores(self.h, ptr(q), s1.shape[0], ptr(s1), ptr(s2), ptr(rn), ptr(sc),
+                            int(two_stage), ptr(out))
+        return out
+
+    def attend_values(self, w, comp):
+        s1, s2, rn, sc = comp
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.empty(self.dim, np.float32)
+        lib().oracle_attend_values(self.h, ptr(w), s1.shape[0], ptr(s1), ptr(s2), ptr(rn),
+                                   ptr(sc), ptr(out))
+        return out
+
+
+def attend_bf16(q, K, V, scale, causal=False, q_start=0, first_held=0, window=-1):
+    """q [B,H,L,D] bf16 bits; K,V [B,Hkv,N,D] bf16 bits."""
+    B, H, Lq, D = q.shape
+    Hkv, N = K.shape[1], K.shape[2]
+    of = np.empty((B, H, Lq, D), np.float32)
+    ob = np.empty((B, H, Lq, D), np.uint16)
+    lse = np.empty((B, H, Lq), np.float32)
+    lib().oracle_attend_bf16(ptr(np.ascontiguousarray(q)), ptr(np.ascontiguousarray(K)),
+                             ptr(np.ascontiguousarray(V)), B, H, Hkv, Lq, N, D, scale,
+                             int(causal), q_start, first_held, window, ptr(of), ptr(ob), ptr(lse))
+    return of, ob, lse
+
+
+def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0, first_held=0,
+                  window=-1):
+    B, H, Lq, D = q.shape
+    Hkv, N = kt[0].shape[1], kt[0].shape[2]
+    of = np.empty((B, H, Lq, D), np.float32)
+    ob = np.empty((B, H, Lq, D), np.uint16)
+    lse = np.empty((B, H, Lq), np.float32)
+    c = [np.ascontiguousarray(a) for a in (*kt, *vt)]
+    lib().oracle_attend_affine(ptr(np.ascontiguousarray(q)), *[ptr(a) for a in c], B, H, Hkv, Lq,
+                               N, D, gs, bits_k, bits_v, scale, int(causal), q_start, first_held,
+                               window, ptr(of), ptr(ob), ptr(lse))
+    return of, ob, lse
