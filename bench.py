@@ -1,0 +1,212 @@
+"""Quantized-KV decode benchmark (the headline).
+
+One step = quantize-on-append of one new K and V token for every sequence
+(MLX affine, 3-bit, group 64) followed by fused decode attention over the
+whole cache: B=32 sequences, 16 query / 8 KV heads, head_dim 256, 32,768
+cached tokens per sequence. Inputs are synthetic (seeded N(0,1) with 1% of
+channels x10, generated on the device) and resident in HBM before timing.
+
+Prints one JSON line: value = decode tokens/s (B / step time); the roofline
+block prices the decode kernel's algorithmic bytes (packed K/V codes, scales
+and biases of the live context, plus Q in and O out) per launch against the
+launch duration measured with HIP events on the stream it runs on. The CPU
+baseline times the oracle's dequantize-then-attend (the reference semantics
+restated in C++) on a bounded sample of the same cache.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "lumen-rs_amd"))
+
+METRIC = "quantized-KV decode attn achieved HBM GB/s + tokens/s @ B=32, 32K ctx"
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU time budget for the baseline sample")
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(the multi-GPU sharding is a design in DESIGN.md)"}))
+        sys.exit(2)
+
+    import tqkv as T
+
+    hip = T.hip()
+    hip._ok(hip.h.hipSetDevice(0), "hipSetDevice")
+    B, H, HKV, D, N, GS, BITS = args.batch, 16, 8, 256, args.context, 64, 3
+    scale = D ** -0.5
+    steps, warmup = args.steps, args.warmup
+    cap = (N + warmup + steps + 255) // 256 * 256
+    words, groups = D * BITS // 32, D // GS
+    slabs = B * HKV
+
+    stream = hip.stream()
+    cache = {}
+    for name in ("k", "v"):
+        cache[name] = (T.DeviceArray((slabs, cap, words), np.uint32),
+                       T.DeviceArray((slabs, cap, groups), np.uint16),
+                       T.DeviceArray((slabs, cap, groups), np.uint16))
+
+    # Fill the first N tokens: synthesize bf16 K/V chunks on the device and
+    # quantize them into place with the append kernel.
+    chunk = 1024
+    tmp = T.DeviceArray((slabs, chunk, D), np.uint16)
+    for name, seed in (("k", 11), ("v", 22)):
+        pk, sc, bi = cache[name]
+        for c0 in range(0, N, chunk):
+            n = min(chunk, N - c0)
+            T.synth_bf16(tmp.ptr, slabs * n, D, seed * 1000003 + c0, 0.01, 10.0, stream)
+            T.affine_quantize(tmp.ptr, slabs, n, D, GS, BITS, pk.ptr, sc.ptr, bi.ptr, cap, c0,
+                              stream)
+    del tmp
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H, D, 33, 0.0, 1.0, stream)
+    newk = T.DeviceArray((slabs, 1, D), np.uint16)
+    newv = T.DeviceArray((slabs, 1, D), np.uint16)
+    T.synth_bf16(newk.ptr, slabs, D, 44, 0.01, 10.0, stream)
+    T.synth_bf16(newv.ptr, slabs, D, 55, 0.01, 10.0, stream)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    ws_bytes = T.decode_workspace_size(B, H, HKV, D, cap)
+    ws = T.DeviceArray((ws_bytes,), np.uint8, np.zeros(ws_bytes, np.uint8))
+    hip.sync()
+
+    kp = tuple(a.ptr for a in cache["k"])
+    vp = tuple(a.ptr for a in cache["v"])
+    ev = [(hip.event(), hip.event()) for _ in range(steps)]
+
+    def step(i, events=None):
+        pos = N + i  # the new token's row
+        T.affine_quantize(newk.ptr, slabs, 1, D, GS, BITS, *kp, cap, pos, stream)
+        T.affine_quantize(newv.ptr, slabs, 1, D, GS, BITS, *vp, cap, pos, stream)
+        seg = T.affine_seg(kp, vp, cap, pos + 1)
+        if events:
+            hip.record(events[0], stream)
+        T.decode_attend_affine(q.ptr, B, H, HKV, D, GS, BITS, BITS, scale, [seg], out.ptr,
+                               ws.ptr, ws_bytes, stream)
+        if events:
+            hip.record(events[1], stream)
+
+    for i in range(warmup):
+        step(i)
+    hip._ok(hip.h.hipStreamSynchronize(stream), "sync")
+    t0, t1 = hip.event(), hip.event()
+    hip.record(t0, stream)
+    wall0 = time.perf_counter()
+    for i in range(steps):
+        step(warmup + i, ev[i])
+    hip.record(t1, stream)
+    total_ms = hip.elapsed_ms(t0, t1)
+    wall = time.perf_counter() - wall0
+    hip.sync()
+    dec_ms = [hip.elapsed_ms(a, b) for a, b in ev]
+    dec_avg_ms = float(np.mean(dec_ms))
+
+    row_bytes = words * 4 + 2 * groups * 2  # packed codes + bf16 scales + bf16 biases
+    ctx_avg = N + warmup + (steps - 1) / 2.0 + 1
+    alg_bytes = 2 * slabs * ctx_avg * row_bytes + 2 * B * H * D * 2  # K+V, then Q in + O out
+    achieved = alg_bytes / (dec_avg_ms * 1e-3) / 1e9
+    ms_per_step = total_ms / steps
+    tokens_per_s = B / (ms_per_step * 1e-3)
+
+    # Sanity of the result itself: finite, not all zero.
+    o = T.bf16_to_f32(out.numpy()) if hasattr(T, "bf16_to_f32") else None
+    if o is None:
+        o = (out.numpy().astype(np.uint32) << 16).view(np.float32)
+    assert np.all(np.isfinite(o)) and np.abs(o).max() > 0, "decode output is not sane"
+
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 2: batched decode over a 3-bit affine cache "
+                        "(append 1 token + fused decode attention per step)",
+            "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N,
+            "bits_k": BITS, "bits_v": BITS, "group_size": GS,
+            "layers": 1,
+        },
+        "hbm_gbps": round(achieved, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_affine_kernel<256,3,3,2,32,4>",
+            "alg_bytes_per_launch": int(alg_bytes),
+            "avg_launch_ms": round(dec_avg_ms, 5),
+        },
+        "host_wall_ms_per_step": round(wall / steps * 1e3, 4),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(T, cache, q, out, B, H, HKV, D, N, GS, BITS,
+                                              scale, cap, args.cpu_seconds)
+    print(json.dumps(result))
+
+
+def cpu_baseline(T, cache, q, out, B, H, HKV, D, N, GS, BITS, scale, cap, budget_s):
+    """The oracle's dequantize-then-attend (the reference's CPU semantics,
+    restated in C++, OpenMP over heads) on a bounded sample: whole sequences
+    of the same cache, as many as fit the time budget."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    qh = q.numpy()
+    triples = {}
+    for name in ("k", "v"):
+        triples[name] = [a.numpy().reshape(B, HKV, cap, -1) for a in cache[name]]
+
+    def one(b):
+        kt = tuple(np.ascontiguousarray(a[b:b + 1, :, :N]) for a in triples["k"])
+        vt = tuple(np.ascontiguousarray(a[b:b + 1, :, :N]) for a in triples["v"])
+        t = time.perf_counter()
+        O.attend_affine(qh[b:b + 1], kt, vt, GS, BITS, BITS, scale)
+        return time.perf_counter() - t
+
+    first = one(0)
+    n_seq = max(1, min(B, int(budget_s / max(first, 1e-3))))
+    times = [first] + [one(b) for b in range(1, n_seq)]
+    per_seq = float(np.median(times))
+    return {
+        "value": round(1.0 / per_seq, 3),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_seq} of {B} sequences of the same cache, {HKV} KV heads x {N} tokens each "
+                  f"(median {per_seq:.3f} s per sequence-step); C++ restatement of "
+                  "dequantize-then-attend, OpenMP over heads",
+    }
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,84 @@
+// Status codes, the per-thread last error, the per-device scratch buffer.
+#include <cstdarg>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+
+namespace tqkv {
+
+static thread_local char g_last_error[512] = "";
+
+int32_t fail(int32_t status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int32_t ok() {
+  g_last_error[0] = '\0';
+  return TQKV_OK;
+}
+
+namespace {
+struct Scratch {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_scratch_mu;
+std::vector<Scratch> g_scratch;
+}  // namespace
+
+int32_t scratch_for_current_device(size_t bytes, void** out) {
+  int dev = 0;
+  TQKV_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch.size() <= size_t(dev)) g_scratch.resize(size_t(dev) + 1);
+  Scratch& s = g_scratch[size_t(dev)];
+  if (s.bytes < bytes) {
+    // Growing frees the old buffer: wait for work that may still use it.
+    if (s.ptr) {
+      TQKV_HIP(hipDeviceSynchronize());
+      TQKV_HIP(hipFree(s.ptr));
+      s.ptr = nullptr;
+      s.bytes = 0;
+    }
+    size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    if (hipMalloc(&s.ptr, want) != hipSuccess) {
+      s.ptr = nullptr;
+      return fail(TQKV_ENOMEM, "scratch hipMalloc of %zu bytes failed", want);
+    }
+    // Zero once: the decode kernel's arrival counters live at its head and
+    // every call leaves them at zero again.
+    TQKV_HIP(hipMemset(s.ptr, 0, want));
+    s.bytes = want;
+  }
+  *out = s.ptr;
+  return TQKV_OK;
+}
+
+}  // namespace tqkv
+
+extern "C" {
+
+const char* tqkv_status_string(int32_t status) {
+  switch (status) {
+    case TQKV_OK: return "TQKV_OK";
+    case TQKV_EINVAL_SHAPE: return "TQKV_EINVAL_SHAPE";
+    case TQKV_EINVAL_TARGET: return "TQKV_EINVAL_TARGET";
+    case TQKV_EUNSUPPORTED: return "TQKV_EUNSUPPORTED";
+    case TQKV_EDEVICE: return "TQKV_EDEVICE";
+    case TQKV_ENOMEM: return "TQKV_ENOMEM";
+    case TQKV_EINVAL_ARG: return "TQKV_EINVAL_ARG";
+  }
+  return "TQKV_UNKNOWN";
+}
+
+const char* tqkv_last_error(void) { return tqkv::g_last_error; }
+
+int32_t tqkv_version(void) { return 100; }
+
+}  // extern "C"

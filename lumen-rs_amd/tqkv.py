@@ -1,0 +1,256 @@
+"""ctypes binding to libtqkv.so (the C ABI in include/tqkv.h) plus a minimal
+HIP runtime helper for device buffers, streams and events.
+
+Device memory comes from the same HIP runtime libtqkv.so links
+(/opt/rocm/lib/libamdhip64.so), so no second runtime (such as the one bundled
+with PyTorch wheels) is loaded into the process. The library fails loudly when
+it is not built: there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtqkv.so")
+HIP_PATH = "/opt/rocm/lib/libamdhip64.so"
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+
+OK = 0
+EINVAL_SHAPE = 1
+EINVAL_TARGET = 2
+EUNSUPPORTED = 3
+EDEVICE = 4
+ENOMEM = 5
+EINVAL_ARG = 6
+
+
+class TqkvError(RuntimeError):
+    def __init__(self, status, detail):
+        super().__init__(f"{status_name(status)}: {detail}")
+        self.status = status
+
+
+class AffineSeg(ctypes.Structure):
+    _fields_ = [("k_packed", P), ("k_scales", P), ("k_biases", P),
+                ("v_packed", P), ("v_scales", P), ("v_biases", P),
+                ("cap", I64), ("n", I64), ("shared", I32), ("reserved", I32)]
+
+
+_lib = None
+_hip = None
+
+_SIGS = {
+    "tqkv_status_string": (ctypes.c_char_p, [I32]),
+    "tqkv_last_error": (ctypes.c_char_p, []),
+    "tqkv_version": (I32, []),
+    "tqkv_affine_quantize": (I32, [P, I64, I64, I32, I32, I32, P, P, P, I64, I64, P]),
+    "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
+    "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
+                                        ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
+    "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
+    "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
+}
+
+
+def lib():
+    """Load libtqkv.so; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `make -C lumen-rs_amd` "
+                               "or __graft_entry__.build()")
+        hip()  # the runtime first, from /opt/rocm
+        _lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(_lib, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def exported_symbols():
+    """Names libtqkv.so exports (dlsym succeeds), for the ABI check."""
+    out = []
+    for name in _SIGS:
+        try:
+            getattr(lib(), name)
+            out.append(name)
+        except AttributeError:
+            pass
+    return out
+
+
+def status_name(status):
+    return lib().tqkv_status_string(status).decode()
+
+
+def check(status):
+    if status != OK:
+        raise TqkvError(status, lib().tqkv_last_error().decode())
+    return status
+
+
+# ---------------------------------------------------------------- HIP runtime
+class Hip:
+    """The few HIP runtime calls the tests and the bench need."""
+
+    H2D, D2H, D2D = 1, 2, 3
+
+    def __init__(self):
+        self.h = ctypes.CDLL(HIP_PATH, mode=ctypes.RTLD_GLOBAL)
+        sig = {
+            "hipMalloc": [ctypes.POINTER(P), SZ],
+            "hipFree": [P],
+            "hipMemcpy": [P, P, SZ, I32],
+            "hipMemcpyAsync": [P, P, SZ, I32, P],
+            "hipMemsetAsync": [P, I32, SZ, P],
+            "hipDeviceSynchronize": [],
+            "hipStreamCreate": [ctypes.POINTER(P)],
+            "hipStreamDestroy": [P],
+            "hipStreamSynchronize": [P],
+            "hipEventCreate": [ctypes.POINTER(P)],
+            "hipEventDestroy": [P],
+            "hipEventRecord": [P, P],
+            "hipEventSynchronize": [P],
+            "hipEventElapsedTime": [ctypes.POINTER(F32), P, P],
+            "hipGetDeviceCount": [ctypes.POINTER(I32)],
+            "hipGetErrorString": [I32],
+            "hipSetDevice": [I32],
+        }
+        for name, args in sig.items():
+            fn = getattr(self.h, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p if name == "hipGetErrorString" else I32
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {self.h.hipGetErrorString(rc).decode()}")
+
+    def device_count(self):
+        n = I32(0)
+        rc = self.h.hipGetDeviceCount(ctypes.byref(n))
+        return n.value if rc == 0 else 0
+
+    def malloc(self, nbytes):
+        p = P()
+        self._ok(self.h.hipMalloc(ctypes.byref(p), max(int(nbytes), 1)), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        if p:
+            self._ok(self.h.hipFree(p), "hipFree")
+
+    def sync(self):
+        self._ok(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        p = self.malloc(arr.nbytes)
+        self._ok(self.h.hipMemcpy(p, arr.ctypes.data, arr.nbytes, self.H2D), "hipMemcpy H2D")
+        return p
+
+    def copy_in(self, dst, arr):
+        arr = np.ascontiguousarray(arr)
+        self._ok(self.h.hipMemcpy(dst, arr.ctypes.data, arr.nbytes, self.H2D), "hipMemcpy H2D")
+
+    def download(self, p, shape, dtype):
+        out = np.empty(shape, dtype)
+        self._ok(self.h.hipMemcpy(out.ctypes.data, p, out.nbytes, self.D2H), "hipMemcpy D2H")
+        return out
+
+    def stream(self):
+        s = P()
+        self._ok(self.h.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s.value
+
+    def event(self):
+        e = P()
+        self._ok(self.h.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, ev, stream=None):
+        self._ok(self.h.hipEventRecord(ev, stream), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self._ok(self.h.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = F32(0)
+        self._ok(self.h.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        _hip = Hip()
+    return _hip
+
+
+class DeviceArray:
+    """A device buffer with a numpy shape and dtype; freed on delete."""
+
+    def __init__(self, shape, dtype, data=None):
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.ptr = hip().malloc(self.nbytes)
+        if data is not None:
+            data = np.ascontiguousarray(data, dtype=self.dtype)
+            assert data.shape == self.shape, (data.shape, self.shape)
+            hip().copy_in(self.ptr, data)
+
+    @classmethod
+    def of(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        return cls(arr.shape, arr.dtype, arr)
+
+    def numpy(self):
+        return hip().download(self.ptr, self.shape, self.dtype)
+
+    def __del__(self):
+        try:
+            if self.ptr and _hip is not None:
+                _hip.free(self.ptr)
+        except Exception:
+            pass
+        self.ptr = None
+
+
+# ---------------------------------------------------------------- wrappers
+def affine_quantize(x, n_slabs, s, dim, gs, bits, packed, scales, biases, dst_cap=None,
+                    dst_start=0, stream=None):
+    """x, packed, scales, biases: device pointers."""
+    check(lib().tqkv_affine_quantize(x, n_slabs, s, dim, gs, bits, packed, scales, biases,
+                                     s if dst_cap is None else dst_cap, dst_start, stream))
+
+
+def affine_dequantize(packed, scales, biases, rows, dim, gs, bits, out, stream=None):
+    check(lib().tqkv_affine_dequantize(packed, scales, biases, rows, dim, gs, bits, out, stream))
+
+
+def affine_seg(k_triple, v_triple, cap, n, shared=False):
+    """k_triple / v_triple: (packed, scales, biases) device pointers."""
+    return AffineSeg(k_triple[0], k_triple[1], k_triple[2], v_triple[0], v_triple[1],
+                     v_triple[2], cap, n, int(shared), 0)
+
+
+def decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, out,
+                         workspace=None, workspace_bytes=0, stream=None):
+    arr = (AffineSeg * len(segs))(*segs)
+    check(lib().tqkv_decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, arr,
+                                          len(segs), out, workspace, workspace_bytes, stream))
+
+
+def decode_workspace_size(B, H, H_kv, D, total):
+    return lib().tqkv_decode_workspace_size(B, H, H_kv, D, total)
+
+
+def synth_bf16(out, rows, dim, seed, outlier_frac=0.0, outlier_mult=1.0, stream=None):
+    check(lib().tqkv_synth_bf16(out, rows, dim, seed, outlier_frac, outlier_mult, stream))

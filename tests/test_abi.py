@@ -1,0 +1,36 @@
+"""libtqkv.so loads and exports every entry point include/tqkv.h declares
+(no GPU needed: nothing here launches a kernel)."""
+import ctypes
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared():
+    text = open(os.path.join(ROOT, "include", "tqkv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tqkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import tqkv
+    lib = tqkv.lib()
+    names = declared()
+    assert len(names) >= 6
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_status_strings_without_a_gpu():
+    import tqkv
+    assert tqkv.status_name(tqkv.EUNSUPPORTED) == "TQKV_EUNSUPPORTED"
+    assert tqkv.status_name(12345) == "TQKV_UNKNOWN"
+    assert tqkv.lib().tqkv_version() >= 100
+
+
+def test_workspace_size_is_host_arithmetic():
+    import tqkv
+    n = tqkv.decode_workspace_size(32, 16, 8, 256, 32768)
+    assert n > 32 * 16 * 256 * 4
+    assert tqkv.decode_workspace_size(0, 16, 8, 256, 10) == 0

@@ -1,0 +1,181 @@
+"""Quantize-on-append and fused decode on the GPU, through the C ABI, against
+the CPU oracle: packed codes, scales and biases bit-exact; attention within
+2e-2 max-abs and 1e-3 mean-abs (bf16) of dequantize-then-attend."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from inputs import grid_bf16, kv_bf16
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 1e-3
+
+
+@pytest.fixture(scope="module")
+def T():
+    import tqkv
+    assert tqkv.hip().device_count() > 0, "no GPU visible"
+    return tqkv
+
+
+def quantize_gpu(T, x, gs, bits, dst_cap=None, dst_start=0):
+    """x: bf16 [slabs, s, dim] -> device triple [slabs, cap, .] as numpy."""
+    slabs, s, dim = x.shape
+    cap = s if dst_cap is None else dst_cap
+    dx = T.DeviceArray.of(x)
+    words, groups = dim * bits // 32, dim // gs
+    pk = T.DeviceArray((slabs, cap, words), np.uint32, np.full((slabs, cap, words), 0xDEADBEEF, np.uint32))
+    sc = T.DeviceArray((slabs, cap, groups), np.uint16, np.full((slabs, cap, groups), 0x7777, np.uint16))
+    bi = T.DeviceArray((slabs, cap, groups), np.uint16, np.full((slabs, cap, groups), 0x7777, np.uint16))
+    print(f"[quantize] slabs={slabs} s={s} dim={dim} gs={gs} bits={bits} cap={cap}", flush=True)
+    T.affine_quantize(dx.ptr, slabs, s, dim, gs, bits, pk.ptr, sc.ptr, bi.ptr, cap, dst_start)
+    T.hip().sync()
+    return pk.numpy(), sc.numpy(), bi.numpy()
+
+
+@pytest.mark.parametrize("dim,gs,bits", [
+    (64, 64, 4), (128, 64, 4), (128, 64, 3), (256, 64, 3), (128, 64, 8), (256, 32, 4),
+    (512, 128, 8), (1024, 64, 4), (32, 32, 4), (128, 64, 2), (128, 64, 6), (128, 32, 5),
+    (256, 128, 3),
+])
+@pytest.mark.parametrize("kind", ["normal_outliers", "golden_grid"])
+def test_quantize_bit_exact(T, dim, gs, bits, kind):
+    shape = (3, 37, dim)
+    x = kv_bf16(shape, 100 + dim + bits, frac=0.02, mult=8.0) if kind == "normal_outliers" \
+        else grid_bf16(shape, 200 + dim + bits)
+    pk, sc, bi = quantize_gpu(T, x, gs, bits)
+    wpk, wsc, wbi = O.affine_quantize(x, gs, bits)
+    assert np.array_equal(sc, wsc)
+    assert np.array_equal(bi, wbi)
+    assert np.array_equal(pk, wpk)
+
+
+def test_quantize_writes_only_its_rows(T):
+    x = kv_bf16((4, 5, 128), 7)
+    pk, sc, bi = quantize_gpu(T, x, 64, 4, dst_cap=16, dst_start=9)
+    wpk, wsc, wbi = O.affine_quantize(x, 64, 4)
+    assert np.array_equal(pk[:, 9:14], wpk) and np.array_equal(sc[:, 9:14], wsc)
+    assert np.all(pk[:, :9] == 0xDEADBEEF) and np.all(pk[:, 14:] == 0xDEADBEEF)
+    assert np.all(sc[:, :9] == 0x7777) and np.all(bi[:, 14:] == 0x7777)
+
+
+def test_quantize_rejects_bad_layouts(T):
+    with pytest.raises(T.TqkvError) as e:
+        T.affine_quantize(0, 1, 1, 96, 64, 4, 0, 0, 0)
+    assert e.value.status in (T.EUNSUPPORTED, T.EINVAL_SHAPE)
+    with pytest.raises(T.TqkvError) as e:
+        T.affine_quantize(0, 1, 1, 128, 64, 7, 0, 0, 0)
+    assert e.value.status == T.EUNSUPPORTED
+    with pytest.raises(T.TqkvError) as e:
+        T.affine_quantize(0, 1, 4, 128, 64, 4, 0, 0, 0, 3, 0)  # 4 rows into 3
+    assert e.value.status == T.EINVAL_SHAPE
+
+
+def test_dequantize_bit_exact(T):
+    x = kv_bf16((2, 40, 256), 9, frac=0.01, mult=10.0)
+    wpk, wsc, wbi = O.affine_quantize(x, 64, 3)
+    out = T.DeviceArray((2, 40, 256), np.uint16)
+    pk, sc, bi = T.DeviceArray.of(wpk), T.DeviceArray.of(wsc), T.DeviceArray.of(wbi)
+    T.affine_dequantize(pk.ptr, sc.ptr, bi.ptr, 80, 256, 64, 3, out.ptr)
+    T.hip().sync()
+    assert np.array_equal(out.numpy(), O.affine_dequantize(wpk, wsc, wbi, 64, 3))
+
+
+# ------------------------------------------------------------------ decode
+def _cache(x, gs, bits, cap=None):
+    """Quantize with the oracle and upload as a [B, Hkv, cap, .] view."""
+    B, Hkv, N, D = x.shape
+    cap = N if cap is None else cap
+    pk, sc, bi = O.affine_quantize(x, gs, bits)
+    def pad(a):
+        out = np.zeros((B, Hkv, cap, a.shape[-1]), a.dtype)
+        out[:, :, :N] = a
+        return out
+    host = (pk, sc, bi)
+    dev = tuple(__import__("tqkv").DeviceArray.of(pad(a)) for a in host)
+    return host, dev
+
+
+def run_decode(T, q, segs_host, B, H, Hkv, D, gs, bk, bv, scale):
+    """segs_host: list of (k_dev, v_dev, cap, n, shared)."""
+    dq = T.DeviceArray.of(q)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    segs = [T.affine_seg(tuple(a.ptr for a in k), tuple(a.ptr for a in v), cap, n, sh)
+            for (k, v, cap, n, sh) in segs_host]
+    T.decode_attend_affine(dq.ptr, B, H, Hkv, D, gs, bk, bv, scale, segs, out.ptr)
+    T.hip().sync()
+    return out.numpy()
+
+
+def check_close(got_bf16, want_f32, want_bf16):
+    got = O.bf16_to_f32(got_bf16)
+    err = np.abs(got - want_f32)
+    print(f"[decode] max_abs={err.max():.3e} mean_abs={err.mean():.3e} "
+          f"vs_bf16_max={np.abs(got - O.bf16_to_f32(want_bf16)).max():.3e}", flush=True)
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
+
+
+DECODE_CASES = [
+    # (B, H, Hkv, D, N, bits_k, bits_v, gs, cap_extra)
+    (1, 32, 8, 128, 8192, 4, 4, 64, 0),     # config 1 shape
+    (2, 16, 8, 256, 4096, 3, 3, 64, 256),    # config 2 shape, shorter context
+    (1, 16, 4, 256, 4100, 4, 4, 64, 0),      # native_quant_attention.rs:377 cases
+    (1, 16, 4, 256, 4100, 8, 8, 64, 0),
+    (1, 24, 4, 256, 777, 4, 4, 64, 0),
+    (1, 24, 8, 128, 513, 3, 3, 64, 0),
+    (1, 16, 2, 256, 20, 4, 4, 64, 5),
+    (1, 16, 2, 512, 9000, 8, 8, 64, 0),
+    (1, 16, 8, 256, 40000, 4, 4, 64, 0),
+    (2, 32, 8, 128, 3000, 8, 4, 64, 0),      # config 4 widths (K8/V4)
+    (3, 8, 8, 64, 1, 4, 4, 32, 3),           # a single key
+    (1, 8, 1, 128, 777, 3, 3, 32, 0),        # gqa 8 over one KV head
+    (1, 4, 4, 128, 100, 3, 8, 128, 0),
+]
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,N,bk,bv,gs,extra", DECODE_CASES)
+def test_decode_matches_dequantize_then_attend(T, B, H, Hkv, D, N, bk, bv, gs, extra):
+    print(f"[decode] B={B} H={H}/{Hkv} D={D} N={N} bits={bk}/{bv} gs={gs}", flush=True)
+    seed = B * 1000003 + H * 1009 + D * 17 + N + bk * 7 + bv
+    q = kv_bf16((B, H, 1, D), seed)
+    k = kv_bf16((B, Hkv, N, D), seed + 1, frac=0.01, mult=10.0)
+    v = kv_bf16((B, Hkv, N, D), seed + 2, frac=0.01, mult=10.0)
+    scale = 1.0 / np.sqrt(D)
+    (kh, kd), (vh, vd) = _cache(k, gs, bk, N + extra), _cache(v, gs, bv, N + extra)
+    got = run_decode(T, q, [(kd, vd, N + extra, N, False)], B, H, Hkv, D, gs, bk, bv, scale)
+    wf, wb, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale)
+    check_close(got, wf, wb)
+
+
+def test_decode_shared_prefix_plus_suffix(T):
+    # sdpa_split semantics (native_attention.rs:174-208): one softmax over a
+    # shared batch-1 prefix and each row's own suffix.
+    B, H, Hkv, D, P, S, gs = 3, 8, 2, 128, 700, 130, 64
+    q = kv_bf16((B, H, 1, D), 5)
+    kp, vp = kv_bf16((1, Hkv, P, D), 6), kv_bf16((1, Hkv, P, D), 7)
+    ks, vs = kv_bf16((B, Hkv, S, D), 8), kv_bf16((B, Hkv, S, D), 9)
+    (kph, kpd), (vph, vpd) = _cache(kp, gs, 8), _cache(vp, gs, 4)
+    (ksh, ksd), (vsh, vsd) = _cache(ks, gs, 8, S + 10), _cache(vs, gs, 4, S + 10)
+    got = run_decode(T, q, [(kpd, vpd, P, P, True), (ksd, vsd, S + 10, S, False)], B, H, Hkv, D,
+                     gs, 8, 4, 0.1)
+    kfull = tuple(np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
+                  for a, b in zip(kph, ksh))
+    vfull = tuple(np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
+                  for a, b in zip(vph, vsh))
+    wf, wb, _ = O.attend_affine(q, kfull, vfull, gs, 8, 4, 0.1)
+    check_close(got, wf, wb)
+
+
+def test_decode_rejects_unreadable_layouts(T):
+    q = T.DeviceArray((1, 12, 1, 128), np.uint16)
+    out = T.DeviceArray((1, 12, 1, 128), np.uint16)
+    seg = T.affine_seg((q.ptr,) * 3, (q.ptr,) * 3, 1, 1)
+    for args in [(1, 10, 2, 128, 64, 4, 4), (1, 12, 2, 128, 64, 3, 3), (1, 12, 12, 96, 32, 4, 4), (1, 12, 12, 128, 64, 5, 5)]:
+        with pytest.raises(T.TqkvError) as e:
+            T.decode_attend_affine(q.ptr, *args, 1.0, [seg], out.ptr)
+        assert e.value.status == T.EUNSUPPORTED, args
+    with pytest.raises(T.TqkvError) as e:
+        T.decode_attend_affine(q.ptr, 1, 12, 5, 128, 64, 4, 4, 1.0, [seg], out.ptr)
+    assert e.value.status == T.EINVAL_SHAPE
