@@ -1,11 +1,13 @@
 // Dequantize-then-attend: the oracle for every attention kernel (test
 // infrastructure only).
 //
-// Restates the reference's fallback chain: quantized K/V are dequantized to
-// bf16 (mlx::dequantize for the affine format, gemma4_moe.rs:2394-2399;
-// centroid[c] * sigma -> bf16 for the codebook format, turboquant.rs:428-439),
-// then scaled-dot-product attention runs over them
-// (native_attention.rs:78-110 sdpa, :545-622 mask). Scores, softmax and the
+// Quantized K/V are dequantized, then scaled-dot-product attention runs over
+// them (native_attention.rs:78-110 sdpa, :545-622 mask). Affine caches
+// dequantize either exactly in f32 (scale * code + bias, what the reference's
+// decode paths compute: native_quant_attention.rs:131-132 and
+// quantized_matmul) or to bf16 the way mlx::dequantize does for its prefill
+// path (gemma4_moe.rs:2394-2399); codebook caches dequantize to
+// bf16(centroid[c] * sigma) (turboquant.rs:428-439). Scores, softmax and the
 // weighted sum are computed in f64 here; the result is returned both exactly
 // (f32) and rounded to bf16, the dtype the reference returns. GQA maps query
 // head h to KV head h / (H / H_kv) (native_attention.rs:124-132).
@@ -19,8 +21,12 @@ using namespace oracle;
 
 namespace {
 
+inline double load(uint16_t b) { return double(bf16_to_f32(b)); }
+inline double load(float f) { return double(f); }
+
 // One (b, h, query row): softmax(scale * q.K^T masked) . V over n keys.
-void attend_row(const uint16_t* q, const uint16_t* K, const uint16_t* V, size_t n, int d,
+template <typename T>
+void attend_row(const uint16_t* q, const T* K, const T* V, size_t n, int d,
                 float scale, bool causal, size_t q_abs, size_t first_held, long window,
                 float* out_f32, uint16_t* out_bf16, float* lse) {
   std::vector<double> s(n);
@@ -32,9 +38,9 @@ void attend_row(const uint16_t* q, const uint16_t* K, const uint16_t* V, size_t 
       s[k] = -INFINITY;
       continue;
     }
-    const uint16_t* kr = K + k * size_t(d);
+    const T* kr = K + k * size_t(d);
     double acc = 0.0;
-    for (int i = 0; i < d; ++i) acc += qf[i] * double(bf16_to_f32(kr[i]));
+    for (int i = 0; i < d; ++i) acc += qf[i] * load(kr[i]);
     s[k] = double(scale) * acc;
     if (s[k] > mx) mx = s[k];
   }
@@ -45,8 +51,8 @@ void attend_row(const uint16_t* q, const uint16_t* K, const uint16_t* V, size_t 
       if (s[k] == -INFINITY) continue;
       double p = std::exp(s[k] - mx);
       l += p;
-      const uint16_t* vr = V + k * size_t(d);
-      for (int i = 0; i < d; ++i) o[i] += p * double(bf16_to_f32(vr[i]));
+      const T* vr = V + k * size_t(d);
+      for (int i = 0; i < d; ++i) o[i] += p * load(vr[i]);
     }
   }
   for (int i = 0; i < d; ++i) {
@@ -55,6 +61,41 @@ void attend_row(const uint16_t* q, const uint16_t* K, const uint16_t* V, size_t 
     out_bf16[i] = f32_to_bf16(float(v));
   }
   if (lse) *lse = l > 0.0 ? float(mx + std::log(l)) : -INFINITY;
+}
+
+template <typename T>
+void attend(const uint16_t* q, const T* K, const T* V, int B, int H, int H_kv, int L, size_t N,
+            int D, float scale, int causal, size_t q_start, size_t first_held, long window,
+            float* out_f32, uint16_t* out_bf16, float* lse) {
+  const int G = H / H_kv;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H; ++h) {
+      const int kvh = h / G;
+      const T* Kb = K + (size_t(b) * H_kv + kvh) * N * D;
+      const T* Vb = V + (size_t(b) * H_kv + kvh) * N * D;
+      for (int l = 0; l < L; ++l) {
+        const size_t row = (size_t(b) * H + h) * L + l;
+        attend_row(q + row * D, Kb, Vb, N, D, scale, causal != 0, q_start + size_t(l),
+                   first_held, window, out_f32 + row * D, out_bf16 + row * D,
+                   lse ? lse + row : nullptr);
+      }
+    }
+}
+
+// Exact affine dequantization, scale * code + bias from the stored bf16 scale
+// and bias, in f32: what the reference's decode paths compute in registers
+// (native_quant_attention.rs:131-132, 157-165; quantized_matmul).
+void dequantize_f32(const uint32_t* packed, const uint16_t* scales, const uint16_t* biases,
+                    size_t rows, int dim, int gs, int bits, float* out) {
+  const int groups = dim / gs;
+  const size_t words = size_t(dim) * bits / 32;
+  for (size_t r = 0; r < rows; ++r)
+    for (int i = 0; i < dim; ++i) {
+      const float s = bf16_to_f32(scales[r * groups + i / gs]);
+      const float b = bf16_to_f32(biases[r * groups + i / gs]);
+      out[r * dim + i] = s * float(read_code(packed + r * words, size_t(i), bits)) + b;
+    }
 }
 
 }  // namespace
@@ -69,36 +110,34 @@ void oracle_attend_bf16(const uint16_t* q, const uint16_t* K, const uint16_t* V,
                         int H_kv, int L, size_t N, int D, float scale, int causal,
                         size_t q_start, size_t first_held, long window, float* out_f32,
                         uint16_t* out_bf16, float* lse) {
-  const int G = H / H_kv;
-#pragma omp parallel for collapse(2) schedule(dynamic)
-  for (int b = 0; b < B; ++b)
-    for (int h = 0; h < H; ++h) {
-      const int kvh = h / G;
-      const uint16_t* Kb = K + (size_t(b) * H_kv + kvh) * N * D;
-      const uint16_t* Vb = V + (size_t(b) * H_kv + kvh) * N * D;
-      for (int l = 0; l < L; ++l) {
-        const size_t row = (size_t(b) * H + h) * L + l;
-        attend_row(q + row * D, Kb, Vb, N, D, scale, causal != 0, q_start + size_t(l),
-                   first_held, window, out_f32 + row * D, out_bf16 + row * D,
-                   lse ? lse + row : nullptr);
-      }
-    }
+  attend(q, K, V, B, H, H_kv, L, N, D, scale, causal, q_start, first_held, window, out_f32,
+         out_bf16, lse);
 }
 
-// Affine-quantized K/V triples [B, H_kv, N, .] dequantized to bf16 (MLX
-// dequantize), then oracle_attend_bf16. K and V may use different bit widths.
+// Affine-quantized K/V triples [B, H_kv, N, .] dequantized, then attended.
+// dequant_f32 = 0: mlx::dequantize to bf16 (the reference's prefill path,
+// gemma4_moe.rs:2394-2399); 1: exact f32 scale * code + bias (its decode
+// paths). K and V may use different bit widths.
 void oracle_attend_affine(const uint16_t* q, const uint32_t* kw, const uint16_t* ks,
                           const uint16_t* kb, const uint32_t* vw, const uint16_t* vs,
                           const uint16_t* vb, int B, int H, int H_kv, int L, size_t N, int D,
                           int gs, int bits_k, int bits_v, float scale, int causal,
                           size_t q_start, size_t first_held, long window, float* out_f32,
-                          uint16_t* out_bf16, float* lse) {
+                          uint16_t* out_bf16, float* lse, int dequant_f32) {
   const size_t rows = size_t(B) * H_kv * N;
+  if (dequant_f32) {
+    std::vector<float> K(rows * D), V(rows * D);
+    dequantize_f32(kw, ks, kb, rows, D, gs, bits_k, K.data());
+    dequantize_f32(vw, vs, vb, rows, D, gs, bits_v, V.data());
+    attend(q, K.data(), V.data(), B, H, H_kv, L, N, D, scale, causal, q_start, first_held,
+           window, out_f32, out_bf16, lse);
+    return;
+  }
   std::vector<uint16_t> K(rows * D), V(rows * D);
   affine_dequantize_rows(kw, ks, kb, rows, D, gs, bits_k, K.data());
   affine_dequantize_rows(vw, vs, vb, rows, D, gs, bits_v, V.data());
-  oracle_attend_bf16(q, K.data(), V.data(), B, H, H_kv, L, N, D, scale, causal, q_start,
-                     first_held, window, out_f32, out_bf16, lse);
+  attend(q, K.data(), V.data(), B, H, H_kv, L, N, D, scale, causal, q_start, first_held, window,
+         out_f32, out_bf16, lse);
 }
 
 // Codebook (TurboQuant stage-1) K/V: u8 codes [B, H_kv, N, D] and sigma
@@ -117,8 +156,8 @@ void oracle_attend_codebook(const uint16_t* q, const uint8_t* kc, const float* k
       K[r * D + i] = f32_to_bf16(centroids_k[kc[r * D + i]] * ksig[r]);
       V[r * D + i] = f32_to_bf16(centroids_v[vc[r * D + i]] * vsig[r]);
     }
-  oracle_attend_bf16(q, K.data(), V.data(), B, H, H_kv, L, N, D, scale, causal, q_start,
-                     first_held, window, out_f32, out_bf16, lse);
+  attend(q, K.data(), V.data(), B, H, H_kv, L, N, D, scale, causal, q_start, first_held, window,
+         out_f32, out_bf16, lse);
 }
 
 }  // extern "C"

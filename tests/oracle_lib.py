@@ -56,7 +56,7 @@ def lib():
             "oracle_mask_allowed": (I, [SZ, SZ, L]),
             "oracle_attend_bf16": (None, [P, P, P, I, I, I, I, SZ, I, F, I, SZ, SZ, L, P, P, P]),
             "oracle_attend_affine": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, I, I, I, F, I,
-                                            SZ, SZ, L, P, P, P]),
+                                            SZ, SZ, L, P, P, P, I]),
             "oracle_attend_codebook": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, F, I, SZ,
                                               SZ, L, P, P, P]),
         }
@@ -184,7 +184,9 @@ def attend_bf16(q, K, V, scale, causal=False, q_start=0, first_held=0, window=-1
 
 
 def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0, first_held=0,
-                  window=-1):
+                  window=-1, dequant="f32"):
+    """dequant="f32": exact scale * code + bias (the reference's decode paths);
+    "bf16": mlx::dequantize to bf16 first (its prefill path)."""
     B, H, Lq, D = q.shape
     Hkv, N = kt[0].shape[1], kt[0].shape[2]
     of = np.empty((B, H, Lq, D), np.float32)
@@ -193,5 +195,5 @@ def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0,
     c = [np.ascontiguousarray(a) for a in (*kt, *vt)]
     lib().oracle_attend_affine(ptr(np.ascontiguousarray(q)), *[ptr(a) for a in c], B, H, Hkv, Lq,
                                N, D, gs, bits_k, bits_v, scale, int(causal), q_start, first_held,
-                               window, ptr(of), ptr(ob), ptr(lse))
+                               window, ptr(of), ptr(ob), ptr(lse), int(dequant == "f32"))
     return of, ob, lse

@@ -1,6 +1,9 @@
 """Quantize-on-append and fused decode on the GPU, through the C ABI, against
 the CPU oracle: packed codes, scales and biases bit-exact; attention within
-2e-2 max-abs and 1e-3 mean-abs (bf16) of dequantize-then-attend."""
+2e-2 max-abs and 1e-3 mean-abs (bf16) of dequantize-then-attend with the exact
+dequantization the reference's decode paths use, and at cosine >= 0.9999 of
+attention over the mlx::dequantize'd (bf16) cache, the reference's own bar for
+its fused kernel (native_quant_attention.rs:353-403)."""
 import numpy as np
 import pytest
 
@@ -109,12 +112,38 @@ def run_decode(T, q, segs_host, B, H, Hkv, D, gs, bk, bv, scale):
     return out.numpy()
 
 
-def check_close(got_bf16, want_f32, want_bf16):
-    got = O.bf16_to_f32(got_bf16)
-    err = np.abs(got - want_f32)
-    print(f"[decode] max_abs={err.max():.3e} mean_abs={err.mean():.3e} "
-          f"vs_bf16_max={np.abs(got - O.bf16_to_f32(want_bf16)).max():.3e}", flush=True)
-    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
+def check_close(got_bf16, want_f32, want_mlx_f32=None):
+    """want_f32: oracle with the exact dequantization of the reference's
+    decode paths; want_mlx_f32: oracle over the mlx::dequantize'd (bf16)
+    cache. The kernel must meet the 2e-2 / 1e-3 bar against the first and be
+    no farther from the second than the first is (+ 2e-2): bf16 rounding of
+    large outlier-channel values moves the second by more than the bar."""
+    got = O.bf16_to_f32(got_bf16).astype(np.float64)
+    raw = np.abs(got - want_f32)
+    # A bf16 output cannot resolve finer than half its own grid step: above
+    # |8| that alone is > 2e-2, so max-abs is measured beyond it.
+    err = np.maximum(raw - 0.5 * bf16_ulp(want_f32), 0.0)
+    msg = f"[decode] max_abs={raw.max():.3e} beyond_half_ulp={err.max():.3e} mean_abs={raw.mean():.3e}"
+    if want_mlx_f32 is not None:
+        gap = np.abs(want_f32.astype(np.float64) - want_mlx_f32)
+        err_mlx = np.abs(got - want_mlx_f32)
+        msg += f" vs_mlx_dequant_max={err_mlx.max():.3e} oracle_gap_max={gap.max():.3e}"
+    print(msg, flush=True)
+    assert err.max() <= MAX_ABS and raw.mean() <= MEAN_ABS
+    if want_mlx_f32 is not None:
+        assert err_mlx.max() <= gap.max() + MAX_ABS
+
+
+def bf16_ulp(x):
+    """Spacing of the bf16 grid at |x| (8 significant bits)."""
+    ax = np.maximum(np.abs(np.asarray(x, np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(ax)) - 7)
+
+
+def cosine(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
 
 
 DECODE_CASES = [
@@ -130,7 +159,7 @@ DECODE_CASES = [
     (1, 16, 8, 256, 40000, 4, 4, 64, 0),
     (2, 32, 8, 128, 3000, 8, 4, 64, 0),      # config 4 widths (K8/V4)
     (3, 8, 8, 64, 1, 4, 4, 32, 3),           # a single key
-    (1, 8, 1, 128, 777, 3, 3, 32, 0),        # gqa 8 over one KV head
+    (1, 4, 1, 128, 777, 3, 3, 32, 0),        # all heads on one KV head
     (1, 4, 4, 128, 100, 3, 8, 128, 0),
 ]
 
@@ -145,8 +174,36 @@ def test_decode_matches_dequantize_then_attend(T, B, H, Hkv, D, N, bk, bv, gs, e
     scale = 1.0 / np.sqrt(D)
     (kh, kd), (vh, vd) = _cache(k, gs, bk, N + extra), _cache(v, gs, bv, N + extra)
     got = run_decode(T, q, [(kd, vd, N + extra, N, False)], B, H, Hkv, D, gs, bk, bv, scale)
-    wf, wb, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale)
-    check_close(got, wf, wb)
+    wf, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale)
+    wm, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale, dequant="bf16")
+    check_close(got, wf, wm)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("H,Hkv,D,N", [
+    (16, 4, 256, 4100), (24, 4, 256, 777), (16, 2, 256, 20), (16, 2, 512, 9000),
+    (16, 8, 256, 40000)])
+def test_decode_reference_fused_kernel_cases(T, H, Hkv, D, N, bits):
+    # native_quant_attention.rs:353-403: q ~ N(0, 1/D) in bf16, K/V ~ N(0, 1)
+    # quantized from a buffer 256 tokens longer and read as the first N
+    # (a strided view, as the cache hands it out), scale 1.0; the fused
+    # kernel must agree with SDPA over the dequantized cache at cos >= 0.9999.
+    print(f"[decode-ref] H={H}/{Hkv} D={D} N={N} bits={bits}", flush=True)
+    seed = 0xF5ED + 100 * N + bits
+    q = kv_bf16((1, H, 1, D), seed, std=D ** -0.5)
+    cap = N + 256
+    kbuf, vbuf = kv_bf16((1, Hkv, cap, D), seed + 1), kv_bf16((1, Hkv, cap, D), seed + 2)
+    kt, vt = O.affine_quantize(kbuf, 64, bits), O.affine_quantize(vbuf, 64, bits)
+    kd = tuple(T.DeviceArray.of(a) for a in kt)
+    vd = tuple(T.DeviceArray.of(a) for a in vt)
+    got = run_decode(T, q, [(kd, vd, cap, N, False)], 1, H, Hkv, D, 64, bits, bits, 1.0)
+    cut = lambda t: tuple(np.ascontiguousarray(a[:, :, :N]) for a in t)
+    wm, _, _ = O.attend_affine(q, cut(kt), cut(vt), 64, bits, bits, 1.0, dequant="bf16")
+    wf, _, _ = O.attend_affine(q, cut(kt), cut(vt), 64, bits, bits, 1.0)
+    c = cosine(O.bf16_to_f32(got), wm)
+    print(f"[decode-ref] cos_vs_mlx_dequant={c:.7f}", flush=True)
+    assert c >= 0.9999
+    check_close(got, wf)
 
 
 def test_decode_shared_prefix_plus_suffix(T):
@@ -164,8 +221,9 @@ def test_decode_shared_prefix_plus_suffix(T):
                   for a, b in zip(kph, ksh))
     vfull = tuple(np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
                   for a, b in zip(vph, vsh))
-    wf, wb, _ = O.attend_affine(q, kfull, vfull, gs, 8, 4, 0.1)
-    check_close(got, wf, wb)
+    wf, _, _ = O.attend_affine(q, kfull, vfull, gs, 8, 4, 0.1)
+    wm, _, _ = O.attend_affine(q, kfull, vfull, gs, 8, 4, 0.1, dequant="bf16")
+    check_close(got, wf, wm)
 
 
 def test_decode_rejects_unreadable_layouts(T):

@@ -156,8 +156,25 @@ def test_attend_affine_is_dequantize_then_attend():
     k = _bf16_normal((1, 2, 33, 128), 11)
     v = _bf16_normal((1, 2, 33, 128), 12)
     kt, vt = O.affine_quantize(k, 64, 4), O.affine_quantize(v, 64, 8)
-    of, ob, _ = O.attend_affine(q, kt, vt, 64, 4, 8, 0.1)
+    # mlx::dequantize to bf16, then attention
+    of, ob, _ = O.attend_affine(q, kt, vt, 64, 4, 8, 0.1, dequant="bf16")
     Kd, Vd = O.affine_dequantize(*kt, 64, 4), O.affine_dequantize(*vt, 64, 8)
     want, _ = _brute(q, Kd, Vd, 0.1)
     assert np.abs(of - want).max() < 1e-6
     assert np.array_equal(ob, O.bf16_from_f32(of))
+    # exact dequantization scale * code + bias (numpy from the unpacked codes)
+    of32, _, _ = O.attend_affine(q, kt, vt, 64, 4, 8, 0.1, dequant="f32")
+    def exact(t, bits):
+        c = _codes(t[0], bits, 128).reshape(1, 2, 33, 2, 64).astype(np.float64)
+        s = O.bf16_to_f32(t[1])[..., None].astype(np.float64)
+        b = O.bf16_to_f32(t[2])[..., None].astype(np.float64)
+        return (s * c + b).reshape(1, 2, 33, 128)
+    Ke, Ve = exact(kt, 4), exact(vt, 8)
+    qf = O.bf16_to_f32(q).astype(np.float64)
+    ref = np.zeros((1, 4, 1, 128))
+    for h in range(4):
+        sc = 0.1 * qf[0, h] @ Ke[0, h // 2].T
+        e = np.exp(sc - sc.max())
+        ref[0, h] = e @ Ve[0, h // 2] / e.sum()
+    assert np.abs(of32 - ref).max() < 1e-5
+    assert np.abs(of32 - of).max() > 0  # the two dequantizations differ
