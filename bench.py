@@ -161,12 +161,15 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": None,
-            "kernel": "decode_affine_kernel<256,3,3,2,32,4>",
+            "kernel": "decode_affine_kernel<256,3,3,2,32,1>",
             "alg_bytes_per_launch": int(alg_bytes),
             "avg_launch_ms": round(dec_avg_ms, 5),
         },
         "host_wall_ms_per_step": round(wall / steps * 1e3, 4),
     }
+    probe = T.measure_read_bandwidth(stream)
+    result["read_probe"] = probe
+    result["roofline"]["frac_of_read_probe"] = round(achieved / probe["median_gbps"], 4)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(T, cache, q, out, B, H, HKV, D, N, GS, BITS,
                                               scale, cap, args.cpu_seconds)

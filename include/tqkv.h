@@ -118,11 +118,10 @@ typedef struct tqkv_affine_seg {
  * h / (H / H_kv). bits_k, bits_v in {3, 4, 8}; group_size in {32, 64, 128};
  * D in {64, 128, 256, 512}; H / H_kv in {1, 2, 3, 4, 6, 8} (at most 4 when
  * either width is 3 bits). n_segs in {1, 2}.
- * workspace: device scratch of tqkv_decode_workspace_size() bytes, zero-filled
- * before its first use (each call leaves its arrival counters at zero again),
- * or NULL to use a buffer the library keeps per device (grown on demand).
- * Calls that share a workspace must not overlap in time.
- * One kernel launch per call.
+ * workspace: device scratch of tqkv_decode_workspace_size() bytes for the
+ * split partials, or NULL to use a buffer the library keeps per device (grown
+ * on demand); calls that share a workspace must not overlap in time. One
+ * kernel launch when B * H_kv fills the GPU, else a split launch plus a merge.
  * Returns TQKV_EUNSUPPORTED for a layout outside these sets.
  */
 int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
@@ -147,6 +146,16 @@ size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
  */
 int32_t tqkv_synth_bf16(uint16_t* out, int64_t rows, int32_t dim, uint64_t seed,
                         float outlier_frac, float outlier_mult, tqkv_stream stream);
+
+/*
+ * The reference's memory-bandwidth probe (bandwidth.rs:73-100) for this GPU:
+ * *out = sum of the `bytes / 4` floats at `data` (16-byte aligned), reading
+ * each byte once. scratch: device floats, at least 4096 of them. Two launches
+ * per call; time a call to get the read bandwidth a streaming kernel can
+ * reach, the practical ceiling beside the data-sheet peak.
+ */
+int32_t tqkv_read_probe(const float* data, size_t bytes, float* scratch, size_t scratch_bytes,
+                        float* out, tqkv_stream stream);
 
 #ifdef __cplusplus
 }

@@ -8,20 +8,50 @@ namespace tqkv {
 namespace decode {
 namespace {
 
-// Splits per (batch row, KV head): enough workgroups to fill the chip
-// (~1024), never a split shorter than 64 keys.
-void plan_splits(int B, int H_kv, int64_t total, int* n_splits, int64_t* split_len) {
+// Merges the splits of one (batch row, query head):
+// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), as bf16.
+__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_o,
+                                                           const float* __restrict__ part_m,
+                                                           const float* __restrict__ part_l,
+                                                           int n_splits, int D,
+                                                           uint16_t* __restrict__ out) {
+  const int64_t bh = blockIdx.x;
+  const float* pm = part_m + bh * n_splits;
+  const float* pl = part_l + bh * n_splits;
+  float mx = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, pm[s]);
+  float ls = 0.0f;
+  for (int s = 0; s < n_splits; ++s)
+    if (pm[s] != -INFINITY) ls += pl[s] * exp2f(pm[s] - mx);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float os = 0.0f;
+    for (int s = 0; s < n_splits; ++s)
+      if (pm[s] != -INFINITY) os += part_o[(bh * n_splits + s) * D + d] * exp2f(pm[s] - mx);
+    out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
+  }
+}
+
+
+// Splits per (batch row, KV head). With at least ~2048 wavefronts of whole
+// (batch row, KV head) units the chip is full and each workgroup owns its
+// keys (one launch); otherwise the keys are split until the grid holds ~2048
+// wavefronts, never below 256 keys per split. TQKV_DECODE_SPLITS=k caps the
+// count (tests reach the one-split and the merging paths with it).
+int wanted_splits(int B, int H_kv, int waves, int64_t total) {
   const int64_t units = int64_t(B) * H_kv;
-  int64_t want = (1024 + units - 1) / units;
-  const int64_t most = (total + 63) / 64;
+  const int64_t target_wgs = 2048 / waves;
+  int64_t want = units >= target_wgs ? 1 : (target_wgs + units - 1) / units;
+  const int64_t most = (total + 255) / 256;
   if (want > most) want = most;
-  // TQKV_DECODE_SPLITS=k caps the split count (tests reach the one-split and
-  // the merging paths with it).
   if (const char* env = getenv("TQKV_DECODE_SPLITS")) {
     const long k = strtol(env, nullptr, 10);
     if (k >= 1 && k < want) want = k;
   }
-  if (want < 1) want = 1;
+  return want < 1 ? 1 : int(want);
+}
+
+void plan_splits(int B, int H_kv, int waves, int64_t total, int* n_splits, int64_t* split_len) {
+  const int want = wanted_splits(B, H_kv, waves, total);
   int64_t len = (total + want - 1) / want;
   len = (len + 63) / 64 * 64;
   if (len < 64) len = 64;
@@ -30,18 +60,18 @@ void plan_splits(int B, int H_kv, int64_t total, int* n_splits, int64_t* split_l
   if (*n_splits < 1) *n_splits = 1;
 }
 
-// Arrival counters at the head of the workspace, padded to 256 bytes.
-size_t counter_bytes(int B, int H_kv) { return (size_t(B) * H_kv * sizeof(int) + 255) / 256 * 256; }
-
-// An upper bound on plan_splits' count that never decreases as `total`
-// grows, so a workspace sized for a capacity serves every shorter context.
+// An upper bound on the split count for any context up to `total` keys and
+// any wavefront count, so a workspace sized for a capacity serves every
+// shorter context.
 int max_splits(int B, int H_kv, int64_t total) {
   const int64_t units = int64_t(B) * H_kv;
-  int64_t want = (1024 + units - 1) / units;
-  const int64_t most = (total + 63) / 64;
+  int64_t want = (512 + units - 1) / units;
+  const int64_t most = (total + 255) / 256;
   if (want > most) want = most;
   return want < 1 ? 1 : int(want);
 }
+
+int waves_for_shape(int G, int D) { return G * D <= 1024 ? 8 : 4; }
 
 KernelFn pick(int D, int bk, int bv, int G) {
   switch (D) {
@@ -64,7 +94,7 @@ extern "C" size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv,
                                              int64_t total_tokens) {
   if (B <= 0 || H <= 0 || H_kv <= 0 || D <= 0 || total_tokens <= 0) return 0;
   const size_t ns = size_t(max_splits(B, H_kv, total_tokens));
-  return counter_bytes(B, H_kv) + size_t(B) * H * ns * (size_t(D) + 2) * sizeof(float);
+  return size_t(B) * H * ns * (size_t(D) + 2) * sizeof(float);
 }
 
 extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H,
@@ -108,24 +138,30 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
   a.total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
   if (a.total <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
 
-  plan_splits(B, H_kv, a.total, &a.n_splits, &a.split_len);
-  const size_t need =
-      counter_bytes(B, H_kv) + size_t(B) * H * a.n_splits * (size_t(D) + 2) * sizeof(float);
-  void* ws = workspace;
-  if (!ws) {
-    if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
-  } else if (workspace_bytes < need) {
-    return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
-  }
-  a.counters = static_cast<int*>(ws);
+  const int waves = waves_for_shape(G, D);
+  plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
   a.out = out;
-  a.part_o = reinterpret_cast<float*>(static_cast<char*>(ws) + counter_bytes(B, H_kv));
-  a.part_m = a.part_o + size_t(B) * H * a.n_splits * D;
-  a.part_l = a.part_m + size_t(B) * H * a.n_splits;
+  if (a.n_splits > 1) {
+    const size_t need = size_t(B) * H * a.n_splits * (size_t(D) + 2) * sizeof(float);
+    void* ws = workspace;
+    if (!ws) {
+      if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+    } else if (workspace_bytes < need) {
+      return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+    }
+    a.part_o = static_cast<float*>(ws);
+    a.part_m = a.part_o + size_t(B) * H * a.n_splits * D;
+    a.part_l = a.part_m + size_t(B) * H * a.n_splits;
+  }
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
-                     dim3(kWave * kWaves), 0, st, a);
+                     dim3(kWave * waves), 0, st, a);
   TQKV_LAUNCHED();
+  if (a.n_splits > 1) {
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256), 0,
+                       st, a.part_o, a.part_m, a.part_l, a.n_splits, D, out);
+    TQKV_LAUNCHED();
+  }
   return ok();
 }

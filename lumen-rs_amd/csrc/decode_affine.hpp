@@ -2,36 +2,47 @@
 //
 // Work split: one workgroup per (token split, KV head, batch row); its four
 // wavefronts take contiguous quarters of the split. Inside a wavefront, LPT =
-// D / EPL lanes share one token (each lane owns EPL consecutive channels, all
-// in one quantization group), so a wavefront walks TPW = 64 / LPT tokens per
-// step with coalesced loads of TPW whole rows. All G = H / H_kv query heads
-// of the KV head are served by the same dequantized codes (GQA broadcast).
+// D / EPL lanes (a lane group) own one token pair at a time, each lane EPL
+// consecutive channels, all in one quantization group; a wavefront walks
+// 2 * 64 / LPT consecutive tokens per step with coalesced row loads. All
+// G = H / H_kv query heads of the KV head share the codes (GQA broadcast).
 //
-// Per key and query head the lane computes scale * sum(q * code) +
-// bias * sum(q) over its channels (the affine terms factor out of the inner
-// loop), a butterfly over the LPT lanes finishes the score, and an online
-// softmax in log2 units folds U keys at a time with one rescale. Values
-// accumulate as (p * scale) * code with the bias term p * bias kept apart.
+// Arithmetic is v_dot2_f32_f16 on codes that are never converted: a code ANDed
+// into the low mantissa bits of an f16 half is the exact subnormal
+// c * 2^(o - 24) (o = its bit offset there), so one AND turns a window of the
+// packed stream into an f16x2 operand (plans in pair_plans.hpp).
+//   Keys: pairs of channels of one token against f16 query pairs pre-scaled by
+//   2^(E - o); the score is scale * sum(q * c) + bias * sum(q) per group (the
+//   affine terms factor out), summed over the lane group by a butterfly.
+//   Values: one channel of the token pair against the two tokens' f32 weights
+//   p * scale split into f16 hi + lo parts (~22 significant bits); the bias
+//   term p * bias accumulates apart in f32.
+// The online softmax keeps its running maximum up to kTau (log2 units) behind
+// the true one, so accumulators are rescaled only when it moves by more.
 // Lane groups, then wavefronts (through LDS), merge their (max, sum, acc)
-// states; each workgroup writes one split's unnormalized partial, and the last
-// workgroup of a (batch row, KV head) to finish merges all its splits
-// (native_quant_attention.rs:190-207 does this in a second pass): the decode
-// is one kernel launch. An arrival counter per (batch row, KV head) lives in
-// the workspace; the merging workgroup puts it back to zero.
+// states. When one workgroup owns all keys of its (batch row, KV head) it
+// writes the normalized bf16 output itself: the decode is one launch. Else
+// each workgroup writes its split's unnormalized partial and a small second
+// kernel merges the splits, as native_quant_attention.rs:190-207 does in its
+// pass 2. (A last-arriving-workgroup merge needs a device-scope fence per
+// workgroup, which writes back and invalidates L2 on this multi-XCD part and
+// cost more than the launch it saves.)
 //
-// Decode is HBM-bound (~9-14 FLOP per byte of packed cache), so the kernel
-// uses VALU reductions, not MFMA.
+// Decode is HBM-bound (~1 dot2 per 2 codes per head), so the kernel uses VALU
+// dot products, not MFMA. f16 denormals must be preserved (the default mode).
 #pragma once
 
 #include <cmath>
+#include <type_traits>
+#include <utility>
 
 #include "common.hpp"
+#include "pair_plans.hpp"
 
 namespace tqkv {
 namespace decode {
 
 constexpr int kWave = 64;
-constexpr int kWaves = 4;  // wavefronts per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct Seg {
@@ -54,31 +65,53 @@ struct Args {
   int64_t n0, total;
   int64_t split_len;
   int n_splits;
-  int* counters;  // [B, H_kv], zero between calls
-  uint16_t* out;  // [B, H, 1, D]
+  uint16_t* out;  // [B, H, 1, D], written directly when n_splits == 1
   float* part_o;  // [B, H, n_splits, D]
   float* part_m;  // [B, H, n_splits]
   float* part_l;  // [B, H, n_splits]
 };
 
-// Code e (compile-time) of a lane's little-endian packed words.
-template <int BITS, int E>
-__device__ __forceinline__ uint32_t code_at(const uint32_t* w) {
-  constexpr int bit = E * BITS;
-  constexpr int k = bit / 32, off = bit % 32;
-  constexpr uint32_t mask = (1u << BITS) - 1u;
-  if constexpr (off + BITS <= 32) {
-    return (w[k] >> off) & mask;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2_t as_h2(uint32_t x) { return __builtin_bit_cast(h2_t, x); }
+__device__ __forceinline__ uint32_t h2_bits(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, fully unrolled, so plan
+// lookups and register-array indices are compile-time constants.
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// The 32 bits starting at byte BYTE of a lane's chunk of NW words (bytes past
+// the chunk read as zero).
+template <int NW, int BYTE>
+__device__ __forceinline__ uint32_t window(const uint32_t* w) {
+  constexpr int k = BYTE / 4, r = BYTE % 4;
+  const uint32_t lo = k < NW ? w[k] : 0u;
+  if constexpr (r == 0) {
+    return lo;
   } else {
-    return __builtin_amdgcn_alignbit(w[k + 1], w[k], off) & mask;
+    const uint32_t hi = k + 1 < NW ? w[k + 1] : 0u;
+    return __builtin_amdgcn_alignbyte(hi, lo, r);
   }
 }
 
-template <int BITS, int EPL, int E = 0>
-__device__ __forceinline__ void unpack_all(const uint32_t* w, float* c) {
-  if constexpr (E < EPL) {
-    c[E] = float(code_at<BITS, E>(w));
-    unpack_all<BITS, EPL, E + 1>(w, c);
+// Bytes BYTE and BYTE+1 of token 0's chunk in the low half, the same bytes
+// of token 1's chunk in the high half.
+template <int NW, int BYTE>
+__device__ __forceinline__ uint32_t merge_pair(const uint32_t* w0, const uint32_t* w1) {
+  constexpr int k = BYTE / 4, r = BYTE % 4;
+  if constexpr (r < 3) {
+    constexpr uint32_t sel = uint32_t(r) | uint32_t(r + 1) << 8 | uint32_t(4 + r) << 16 |
+                             uint32_t(5 + r) << 24;
+    return __builtin_amdgcn_perm(w1[k], w0[k], sel);
+  } else {
+    return __builtin_amdgcn_perm(window<NW, BYTE>(w1), window<NW, BYTE>(w0), 0x05040100u);
   }
 }
 
@@ -88,10 +121,68 @@ __device__ __forceinline__ void load_words(uint32_t* dst, const uint32_t* src) {
   for (int i = 0; i < N; ++i) dst[i] = src[i];
 }
 
-template <int D, int BK, int BV, int G, int EPL, int U>
+// Score partial sum of one token: sum over the K plan of dot2(codes, q pair).
+template <int BK, int EPL, int KW>
+__device__ __forceinline__ float k_dot(const uint32_t* w, const uint32_t* qp) {
+  using KP = Plan<BK, EPL>;
+  float acc = 0.0f;
+  static_for<KP::kN>([&](auto J) {
+    constexpr KOp op = KP::k[J];
+    const uint32_t c = window<KW, op.byte>(w) & op.mask;
+    acc = __builtin_amdgcn_fdot2(as_h2(c), as_h2(qp[J]), acc, false);
+  });
+  return acc;
+}
+
+// Values of a token pair: acc[e] += c_t0,e * w0 + c_t1,e * w1 with the two
+// tokens' weights as one f16 pair, over every window of the V plan.
+template <int BV, int EPL, int VW, int G>
+__device__ __forceinline__ void v_accumulate(const uint32_t* w0, const uint32_t* w1,
+                                             const uint32_t* wp, float (*acc)[EPL]) {
+  using VP = Plan<BV, EPL>;
+  static_for<VP::vN>([&](auto I) {
+    constexpr VWin win = VP::vw[I];
+    const uint32_t m = merge_pair<VW, win.byte>(w0, w1);
+    static_for<win.count>([&](auto C) {
+      constexpr VCode vc = VP::vc[win.first + C];
+      const uint32_t codes = m & vc.mask;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        acc[h][vc.e] = __builtin_amdgcn_fdot2(as_h2(codes), as_h2(wp[h]), acc[h][vc.e], false);
+      }
+    });
+  });
+}
+
+// Sum over the N lanes of an aligned lane group (N a power of two <= 64),
+// every lane getting the total: quad permutes, then half-row and row
+// mirrors, then cross-row shuffles.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(
+        __builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+  };
+  if constexpr (N >= 2) v += dpp(v, std::integral_constant<int, 0xb1>{});   // quad [1,0,3,2]
+  if constexpr (N >= 4) v += dpp(v, std::integral_constant<int, 0x4e>{});   // quad [2,3,0,1]
+  if constexpr (N >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // half-row mirror
+  if constexpr (N >= 16) v += dpp(v, std::integral_constant<int, 0x140>{}); // row mirror
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (N >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+// Running maxima may lag the true maximum by up to kTau (log2 units) before
+// the accumulators are rescaled: weights stay <= 2^kTau, and rescales become
+// rare after the first keys.
+constexpr float kTau = 8.0f;
+
+template <int D, int BK, int BV, int G, int EPL, int kWaves>
 __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
+  using KP = Plan<BK, EPL>;
+  using VP = Plan<BV, EPL>;
   constexpr int LPT = D / EPL;
-  constexpr int TPW = kWave / LPT;
+  constexpr int TPW = kWave / LPT;  // lane groups per wavefront
   constexpr int KW = EPL * BK / 32;
   constexpr int VW = EPL * BV / 32;
   constexpr int KROW = D * BK / 32;
@@ -106,24 +197,42 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
   const int ngroups = D / a.gs;
   const int grp = e0 / a.gs;
 
-  // Query channels of this lane for every head of the group, pre-scaled.
-  float qf[G][EPL];
-  float qsum[G];
+  // Query: f16 pairs matching the K plan, each channel scaled by
+  // 2^(E - o) so every product with a code subnormal carries 2^(E - 24);
+  // E per head keeps the largest |q| 2^E below 2^15.
+  uint32_t qp[G][KP::kN];
+  float kfac[G], qbias[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const uint16_t* qp = a.q + (int64_t(b) * a.H + kvh * G + h) * D + e0;
-    qsum[h] = 0.0f;
+    const uint16_t* qrow = a.q + (int64_t(b) * a.H + kvh * G + h) * D + e0;
+    float qr[EPL];
+    float qsum = 0.0f, qmax = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      qf[h][e] = bf16_to_f32(qp[e]) * a.qscale;
-      qsum[h] += qf[h][e];
+      qr[e] = bf16_to_f32(qrow[e]);
+      qsum += qr[e];
+      qmax = fmaxf(qmax, fabsf(qr[e]));
     }
+#pragma unroll
+    for (int off = 1; off < LPT; off <<= 1) qmax = fmaxf(qmax, __shfl_xor(qmax, off, kWave));
+    int ex = 0;
+    if (qmax > 0.0f) frexpf(qmax, &ex);
+    const int E = 15 - ex;
+    static_for<KP::kN>([&](auto J) {
+      constexpr KOp op = KP::k[J];
+      const float lo = __builtin_ldexpf(qr[op.lo_e], E - op.lo_o);
+      float hi = 0.0f;
+      if constexpr (op.hi_e >= 0) hi = __builtin_ldexpf(qr[op.hi_e], E - op.hi_o);
+      qp[h][J] = h2_bits(h2_t{_Float16(lo), _Float16(hi)});
+    });
+    kfac[h] = a.qscale * __builtin_ldexpf(1.0f, 24 - E);
+    qbias[h] = a.qscale * qsum;
   }
 
   const int64_t t_begin = int64_t(split) * a.split_len;
   const int64_t t_end = t_begin + a.split_len < a.total ? t_begin + a.split_len : a.total;
   int64_t chunk = (t_end - t_begin + kWaves - 1) / kWaves;
-  chunk = (chunk + TPW - 1) / TPW * TPW;
+  chunk = (chunk + 2 * TPW - 1) / (2 * TPW) * (2 * TPW);
   const int64_t w_begin = t_begin + wave * chunk;
   const int64_t w_end = w_begin + chunk < t_end ? w_begin + chunk : t_end;
 
@@ -138,83 +247,106 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
     for (int e = 0; e < EPL; ++e) acc[h][e] = 0.0f;
   }
 
-  for (int64_t tb = w_begin; tb < w_end; tb += int64_t(TPW) * U) {
-    uint32_t kwd[U][KW], vwd[U][VW];
-    float ksc[U], kbi[U], vsc[U], vbi[U];
-    bool valid[U];
+  // One step: every lane group takes the token pair (2j, 2j+1) of the next
+  // 2 * TPW keys. Loads of step n+1 are issued before step n computes.
+  struct Buf {
+    uint32_t k[2][KW], v[2][VW];
+    uint16_t ks[2], kb[2], vs[2], vb[2];
+  };
+  auto load = [&](Buf& f, const Seg& s, int64_t row0, int64_t row1) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t t = tb + u * TPW + lane_tok;
-      valid[u] = t < w_end;
-      const int64_t tt = valid[u] ? t : w_begin;  // in-bounds row for idle lanes
-      const bool second = tt >= a.n0;
-      const Seg& s = second ? a.seg[1] : a.seg[0];
-      const int64_t row = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap + (second ? tt - a.n0 : tt);
-      load_words<KW>(kwd[u], s.kw + row * KROW + lane_sub * KW);
-      load_words<VW>(vwd[u], s.vw + row * VROW + lane_sub * VW);
-      ksc[u] = bf16_to_f32(s.ks[row * ngroups + grp]);
-      kbi[u] = bf16_to_f32(s.kb[row * ngroups + grp]);
-      vsc[u] = bf16_to_f32(s.vs[row * ngroups + grp]);
-      vbi[u] = bf16_to_f32(s.vb[row * ngroups + grp]);
+    for (int i = 0; i < 2; ++i) {
+      const int64_t r = i == 0 ? row0 : row1;
+      load_words<KW>(f.k[i], s.kw + r * KROW + lane_sub * KW);
+      load_words<VW>(f.v[i], s.vw + r * VROW + lane_sub * VW);
+      f.ks[i] = s.ks[r * ngroups + grp];
+      f.kb[i] = s.kb[r * ngroups + grp];
+      f.vs[i] = s.vs[r * ngroups + grp];
+      f.vb[i] = s.vb[r * ngroups + grp];
     }
-
-    float sc[U][G];
+  };
+  auto compute = [&](const Buf& f, const bool* valid) {
+    float sc[2][G];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float c[EPL];
-      unpack_all<BK, EPL>(kwd[u], c);
+    for (int i = 0; i < 2; ++i) {
+      const float ks = bf16_to_f32(f.ks[i]), kb = bf16_to_f32(f.kb[i]);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) dot = fmaf(qf[h][e], c[e], dot);
-        float ps = fmaf(ksc[u], dot, kbi[u] * qsum[h]);
-#pragma unroll
-        for (int off = 1; off < LPT; off <<= 1) ps += __shfl_xor(ps, off, kWave);
-        sc[u][h] = valid[u] ? ps : -INFINITY;
+        const float dot = k_dot<BK, EPL, KW>(f.k[i], qp[h]);
+        const float ps = group_sum<LPT>(fmaf(kfac[h] * ks, dot, qbias[h] * kb));
+        sc[i][h] = valid[i] ? ps : -INFINITY;
       }
     }
-
-    float p[U][G];
+    uint32_t wp[G];
+    const float vs0 = bf16_to_f32(f.vs[0]), vs1 = bf16_to_f32(f.vs[1]);
+    const float vb0 = bf16_to_f32(f.vb[0]), vb1 = bf16_to_f32(f.vb[1]);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float mx = m[h];
+      // Online softmax with a lazily moved maximum.
+      const float mx = fmaxf(sc[0][h], sc[1][h]);
+      const bool need = mx > m[h] + kTau;
+      if (__any(need)) {
+        const float mnew = need ? mx : m[h];
+        const float fct = mnew == -INFINITY ? 1.0f : exp2f(m[h] - mnew);
+        l[h] *= fct;
+        bacc[h] *= fct;
 #pragma unroll
-      for (int u = 0; u < U; ++u) mx = fmaxf(mx, sc[u][h]);
-      const float f = mx == -INFINITY ? 1.0f : exp2f(m[h] - mx);
-      float ls = 0.0f;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        p[u][h] = mx == -INFINITY ? 0.0f : exp2f(sc[u][h] - mx);
-        ls += p[u][h];
+        for (int e = 0; e < EPL; ++e) acc[h][e] *= fct;
+        m[h] = mnew;
       }
-      m[h] = mx;
-      l[h] = fmaf(l[h], f, ls);
-      bacc[h] *= f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[h][e] *= f;
+      const float p0 = sc[0][h] == -INFINITY ? 0.0f : exp2f(sc[0][h] - m[h]);
+      const float p1 = sc[1][h] == -INFINITY ? 0.0f : exp2f(sc[1][h] - m[h]);
+      l[h] += p0 + p1;
+      bacc[h] = fmaf(p0, vb0, fmaf(p1, vb1, bacc[h]));
+      wp[h] = h2_bits(h2_t{_Float16(p0 * vs0), _Float16(p1 * vs1)});
     }
+    v_accumulate<BV, EPL, VW, G>(f.v[0], f.v[1], wp, acc);
+  };
 
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float c[EPL];
-      unpack_all<BV, EPL>(vwd[u], c);
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float pv = p[u][h] * vsc[u];
-        bacc[h] = fmaf(p[u][h], vbi[u], bacc[h]);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(pv, c[e], acc[h][e]);
+  // The wavefront's keys, one segment at a time; full steps first, then a
+  // last step whose idle lanes read an in-bounds row and are masked.
+  for (int sg = 0; sg < 2; ++sg) {
+    const Seg& s = a.seg[sg];
+    const int64_t lo = sg == 0 ? w_begin : (w_begin > a.n0 ? w_begin : a.n0);
+    const int64_t hi = sg == 0 ? (w_end < a.n0 ? w_end : a.n0) : w_end;
+    if (lo >= hi) continue;
+    const int64_t off = sg == 0 ? 0 : a.n0;
+    const int64_t slab = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap - off;
+    const int64_t mine = 2 * lane_tok;
+    constexpr int kStep = 2 * TPW;
+    const int64_t n_full = (hi - lo) / kStep;
+    const bool both[2] = {true, true};
+    if (n_full > 0) {
+      Buf cur, nxt;
+      int64_t row = slab + lo + mine;
+      load(cur, s, row, row + 1);
+      for (int64_t it = 0; it < n_full; ++it) {
+        row += kStep;
+        if (it + 1 < n_full) load(nxt, s, row, row + 1);
+        compute(cur, both);
+        cur = nxt;
       }
+    }
+    const int64_t tail = lo + n_full * kStep;
+    if (tail < hi) {
+      Buf f;  // idle lanes re-read the last key of the range, masked out
+      const int64_t t = tail + mine;
+      const bool valid[2] = {t < hi, t + 1 < hi};
+      const int64_t r0 = valid[0] ? t : hi - 1;
+      const int64_t r1 = valid[1] ? t + 1 : hi - 1;
+      load(f, s, slab + r0, slab + r1);
+      compute(f, valid);
     }
   }
 
-  // Fold the bias term, then merge the TPW lane groups of this wavefront.
+  // Undo the code subnormal scale 2^(o - 24) per channel, add the bias term,
+  // then merge the lane groups of this wavefront.
+  static_for<VP::cN>([&](auto C) {
+    constexpr VCode vc = VP::vc[C];
+    constexpr float unscale = float(1 << (24 - vc.o));
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[h][e] += bacc[h];
-  }
+    for (int h = 0; h < G; ++h) acc[h][vc.e] = fmaf(acc[h][vc.e], unscale, bacc[h]);
+  });
 #pragma unroll
   for (int off = LPT; off < kWave; off <<= 1) {
 #pragma unroll
@@ -261,55 +393,33 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       ls += s_l[w][h] * f;
       os += s_acc[w][h][d] * f;
     }
-    const int64_t row = (int64_t(b) * a.H + kvh * G + h) * a.n_splits + split;
-    a.part_o[row * D + d] = os;
-    if (d == 0) {
-      a.part_m[row] = mx;
-      a.part_l[row] = ls;
-    }
-  }
-
-  // The last workgroup of this (batch row, KV head) to arrive merges the
-  // splits: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
-  __shared__ int s_last;
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int* ctr = a.counters + int64_t(b) * a.H_kv + kvh;
-    const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == a.n_splits - 1;
-    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  for (int i = threadIdx.x; i < G * D; i += kWave * kWaves) {
-    const int h = i / D, d = i % D;
     const int64_t bh = int64_t(b) * a.H + kvh * G + h;
-    const float* pm = a.part_m + bh * a.n_splits;
-    const float* pl = a.part_l + bh * a.n_splits;
-    const float* po = a.part_o + bh * a.n_splits * D + d;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < a.n_splits; ++sp) mx = fmaxf(mx, __builtin_nontemporal_load(pm + sp));
-    float ls = 0.0f, os = 0.0f;
-    for (int sp = 0; sp < a.n_splits; ++sp) {
-      const float msp = __builtin_nontemporal_load(pm + sp);
-      if (msp == -INFINITY) continue;
-      const float f = exp2f(msp - mx);
-      ls += __builtin_nontemporal_load(pl + sp) * f;
-      os += __builtin_nontemporal_load(po + int64_t(sp) * D) * f;
+    if (a.n_splits == 1) {
+      a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
+    } else {
+      const int64_t row = bh * a.n_splits + split;
+      a.part_o[row * D + d] = os;
+      if (d == 0) {
+        a.part_m[row] = mx;
+        a.part_l[row] = ls;
+      }
     }
-    a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
   }
 }
 
 using KernelFn = void (*)(Args);
 
+// Wavefronts per workgroup: 8, unless the cross-wave merge buffer
+// (waves x G x D floats) would pass 32 KB of LDS.
+template <int G, int D>
+constexpr int waves_for() {
+  return G * D <= 1024 ? 8 : 4;
+}
+
 template <int D, int BK, int BV, int G>
 KernelFn pick_kernel() {
   constexpr int EPL = (BK == 3 || BV == 3) ? 32 : (G >= 6 ? 8 : 16);
-  constexpr int U = G <= 2 ? 4 : 2;
-  return decode_affine_kernel<D, BK, BV, G, EPL, U>;
+  return decode_affine_kernel<D, BK, BV, G, EPL, waves_for<G, D>()>;
 }
 
 template <int D, int BK, int BV>

@@ -51,9 +51,6 @@ int32_t scratch_for_current_device(size_t bytes, void** out) {
       s.ptr = nullptr;
       return fail(TQKV_ENOMEM, "scratch hipMalloc of %zu bytes failed", want);
     }
-    // Zero once: the decode kernel's arrival counters live at its head and
-    // every call leaves them at zero again.
-    TQKV_HIP(hipMemset(s.ptr, 0, want));
     s.bytes = want;
   }
   *out = s.ptr;

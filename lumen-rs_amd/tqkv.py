@@ -55,6 +55,7 @@ _SIGS = {
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
     "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
+    "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
 }
 
 
@@ -254,3 +255,31 @@ def decode_workspace_size(B, H, H_kv, D, total):
 
 def synth_bf16(out, rows, dim, seed, outlier_frac=0.0, outlier_mult=1.0, stream=None):
     check(lib().tqkv_synth_bf16(out, rows, dim, seed, outlier_frac, outlier_mult, stream))
+
+
+def read_probe(data, nbytes, scratch, scratch_bytes, out, stream=None):
+    check(lib().tqkv_read_probe(data, nbytes, scratch, scratch_bytes, out, stream))
+
+
+def measure_read_bandwidth(stream=None, nbytes=1 << 30, warmup=3, passes=15):
+    """bandwidth.rs:73-100 on this GPU: median and best GB/s of summing a
+    1 GiB random float array (3 warm-up passes, 15 timed, HIP events)."""
+    h = hip()
+    buf = DeviceArray((nbytes // 2,), np.uint16)
+    synth_bf16(buf.ptr, nbytes // 2 // 256, 256, 12345, 0.0, 1.0, stream)
+    scratch = DeviceArray((4096,), np.float32)
+    out = DeviceArray((1,), np.float32)
+    a, b = h.event(), h.event()
+    rates = []
+    for i in range(warmup + passes):
+        h.record(a, stream)
+        read_probe(buf.ptr, nbytes, scratch.ptr, 4096 * 4, out.ptr, stream)
+        h.record(b, stream)
+        ms = h.elapsed_ms(a, b)
+        if i >= warmup:
+            rates.append(nbytes / (ms * 1e-3) / 1e9)
+    rates.sort()
+    mid = len(rates) // 2
+    median = rates[mid] if len(rates) % 2 else 0.5 * (rates[mid - 1] + rates[mid])
+    return {"median_gbps": round(median, 1), "best_gbps": round(rates[-1], 1),
+            "bytes": nbytes, "passes": passes}
