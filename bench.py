@@ -125,6 +125,13 @@ def main():
     alg_bytes = 2 * slabs * ctx_avg * row_bytes + 2 * B * H * D * 2  # K+V, then Q in + O out
     achieved = alg_bytes / (dec_avg_ms * 1e-3) / 1e9
     ms_per_step = total_ms / steps
+    # HBM bytes per decode launch at the default shape, from the two counter
+    # passes recorded in profiles/decode_affine_config2.md (FETCH_SIZE x 2.000
+    # + WRITE_SIZE x 1.000, factors from a 1 GiB read and a 1 GiB write kernel
+    # of the same library). Counters cannot be read inside this process, so a
+    # non-default shape reports null.
+    default_shape = (B, N) == (32, 32768)
+    traffic = int((917933.6 * 2.0 + 256.0) * 1024) if default_shape else None
     tokens_per_s = B / (ms_per_step * 1e-3)
 
     # Sanity of the result itself: finite, not all zero.
@@ -160,8 +167,8 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_affine_kernel<256,3,3,2,32,1>",
+            "traffic": traffic,
+            "kernel": "decode_affine_kernel<256,3,3,2,32,8>",
             "alg_bytes_per_launch": int(alg_bytes),
             "avg_launch_ms": round(dec_avg_ms, 5),
         },
