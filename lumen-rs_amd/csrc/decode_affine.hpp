@@ -115,10 +115,32 @@ __device__ __forceinline__ uint32_t merge_pair(const uint32_t* w0, const uint32_
   }
 }
 
+// N consecutive words of the packed stream, read once and never again:
+// non-temporal vector loads (the cache is streamed, not reused), widest first.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 template <int N>
 __device__ __forceinline__ void load_words(uint32_t* dst, const uint32_t* src) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) dst[i] = src[i];
+  if constexpr (N >= 4) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src));
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+    if constexpr (N > 4) load_words<N - 4>(dst + 4, src + 4);
+  } else if constexpr (N == 3) {
+    const u32x3_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x3_t*>(src));
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+  } else if constexpr (N == 2) {
+    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(src));
+    dst[0] = v.x;
+    dst[1] = v.y;
+  } else if constexpr (N == 1) {
+    dst[0] = __builtin_nontemporal_load(src);
+  }
 }
 
 // Score partial sum of one token: sum over the K plan of dot2(codes, q pair).
@@ -159,9 +181,11 @@ __device__ __forceinline__ void v_accumulate(const uint32_t* w0, const uint32_t*
 // mirrors, then cross-row shuffles.
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
+  // Every source lane of these patterns exists, so bound_ctrl changes
+  // nothing but lets the compiler fold the move into the add (v_add_f32_dpp).
   auto dpp = [](float x, auto ctrl) {
-    return __int_as_float(
-        __builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x),
+                                                      decltype(ctrl)::value, 0xf, 0xf, true));
   };
   if constexpr (N >= 2) v += dpp(v, std::integral_constant<int, 0xb1>{});   // quad [1,0,3,2]
   if constexpr (N >= 4) v += dpp(v, std::integral_constant<int, 0x4e>{});   // quad [2,3,0,1]
@@ -259,13 +283,19 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       const int64_t r = i == 0 ? row0 : row1;
       load_words<KW>(f.k[i], s.kw + r * KROW + lane_sub * KW);
       load_words<VW>(f.v[i], s.vw + r * VROW + lane_sub * VW);
-      f.ks[i] = s.ks[r * ngroups + grp];
-      f.kb[i] = s.kb[r * ngroups + grp];
-      f.vs[i] = s.vs[r * ngroups + grp];
-      f.vb[i] = s.vb[r * ngroups + grp];
+      f.ks[i] = __builtin_nontemporal_load(s.ks + r * ngroups + grp);
+      f.kb[i] = __builtin_nontemporal_load(s.kb + r * ngroups + grp);
+      f.vs[i] = __builtin_nontemporal_load(s.vs + r * ngroups + grp);
+      f.vb[i] = __builtin_nontemporal_load(s.vb + r * ngroups + grp);
     }
   };
-  auto compute = [&](const Buf& f, const bool* valid) {
+  // kMasked: some keys of the step are past the range (score -inf); only the
+  // last step of a range can have them. Full steps skip those guards and use
+  // the bare v_exp_f32: there every score is finite and, after the first
+  // step, so is every running maximum (the first step always moves it).
+  auto compute = [&](const Buf& f, const bool* valid, auto masked) {
+    constexpr bool kMasked = decltype(masked)::value;
+    auto ex2 = [](float x) { return kMasked ? exp2f(x) : __builtin_amdgcn_exp2f(x); };
     float sc[2][G];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -274,7 +304,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       for (int h = 0; h < G; ++h) {
         const float dot = k_dot<BK, EPL, KW>(f.k[i], qp[h]);
         const float ps = group_sum<LPT>(fmaf(kfac[h] * ks, dot, qbias[h] * kb));
-        sc[i][h] = valid[i] ? ps : -INFINITY;
+        sc[i][h] = (!kMasked || valid[i]) ? ps : -INFINITY;
       }
     }
     uint32_t wp[G];
@@ -287,15 +317,15 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       const bool need = mx > m[h] + kTau;
       if (__any(need)) {
         const float mnew = need ? mx : m[h];
-        const float fct = mnew == -INFINITY ? 1.0f : exp2f(m[h] - mnew);
+        const float fct = (kMasked && mnew == -INFINITY) ? 1.0f : ex2(m[h] - mnew);
         l[h] *= fct;
         bacc[h] *= fct;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[h][e] *= fct;
         m[h] = mnew;
       }
-      const float p0 = sc[0][h] == -INFINITY ? 0.0f : exp2f(sc[0][h] - m[h]);
-      const float p1 = sc[1][h] == -INFINITY ? 0.0f : exp2f(sc[1][h] - m[h]);
+      const float p0 = (kMasked && sc[0][h] == -INFINITY) ? 0.0f : ex2(sc[0][h] - m[h]);
+      const float p1 = (kMasked && sc[1][h] == -INFINITY) ? 0.0f : ex2(sc[1][h] - m[h]);
       l[h] += p0 + p1;
       bacc[h] = fmaf(p0, vb0, fmaf(p1, vb1, bacc[h]));
       wp[h] = h2_bits(h2_t{_Float16(p0 * vs0), _Float16(p1 * vs1)});
@@ -316,16 +346,23 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
     constexpr int kStep = 2 * TPW;
     const int64_t n_full = (hi - lo) / kStep;
     const bool both[2] = {true, true};
+    const std::integral_constant<bool, false> full{};
+    const std::integral_constant<bool, true> masked{};
     if (n_full > 0) {
-      Buf cur, nxt;
+      // Two buffers in turn: the loads of the next step are in flight while
+      // this one computes, with no register copies between steps.
+      Buf b0, b1;
       int64_t row = slab + lo + mine;
-      load(cur, s, row, row + 1);
-      for (int64_t it = 0; it < n_full; ++it) {
-        row += kStep;
-        if (it + 1 < n_full) load(nxt, s, row, row + 1);
-        compute(cur, both);
-        cur = nxt;
+      load(b0, s, row, row + 1);
+      int64_t it = 0;
+      for (; it + 2 <= n_full; it += 2) {
+        load(b1, s, row + kStep, row + kStep + 1);
+        compute(b0, both, full);
+        row += 2 * kStep;
+        if (it + 2 < n_full) load(b0, s, row, row + 1);
+        compute(b1, both, full);
       }
+      if (it < n_full) compute(b0, both, full);
     }
     const int64_t tail = lo + n_full * kStep;
     if (tail < hi) {
@@ -335,7 +372,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       const int64_t r0 = valid[0] ? t : hi - 1;
       const int64_t r1 = valid[1] ? t + 1 : hi - 1;
       load(f, s, slab + r0, slab + r1);
-      compute(f, valid);
+      compute(f, valid, masked);
     }
   }
 
