@@ -130,6 +130,17 @@ int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32
                                   int32_t n_segs, uint16_t* out, void* workspace,
                                   size_t workspace_bytes, tqkv_stream stream);
 
+/*
+ * Which decode kernel tqkv_decode_attend_affine runs for a layout: "mfma"
+ * (scores on the matrix cores; group_size 64, D in {64, 128, 256},
+ * H / H_kv in {1, 2, 4, 8} with H / H_kv * D / 64 <= 16), "dot2" (every other
+ * supported layout, or any layout when the environment variable
+ * TQKV_DECODE_KERNEL=dot2 is set), or "" (unsupported). No counterpart in the
+ * reference; for tests and benchmarks.
+ */
+const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
+                                    int32_t bits_k, int32_t bits_v);
+
 /* Bytes of workspace tqkv_decode_attend_affine needs for this shape. */
 size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
                                   int64_t total_tokens);

@@ -1,8 +1,9 @@
 // Host side of the fused affine decode: split planning, workspace, dispatch.
 // The kernel itself (and its design notes) is in decode_affine.hpp.
 #include <cstdlib>
+#include <cstring>
 
-#include "decode_affine.hpp"
+#include "decode_mfma.hpp"
 
 namespace tqkv {
 namespace decode {
@@ -73,7 +74,20 @@ int max_splits(int B, int H_kv, int64_t total) {
 
 int waves_for_shape(int G, int D) { return G * D <= 1024 ? 8 : 4; }
 
-KernelFn pick(int D, int bk, int bv, int G) {
+// The MFMA-scored kernel where its layout applies, else the dot2 kernel.
+// TQKV_DECODE_KERNEL=dot2 forces the dot2 kernel (tests cover both).
+KernelFn pick(int D, int bk, int bv, int G, int gs) {
+  const char* env = getenv("TQKV_DECODE_KERNEL");
+  const bool dot2_only = env && strcmp(env, "dot2") == 0;
+  if (!dot2_only) {
+    KernelFn f = nullptr;
+    switch (D) {
+      case 64: f = pick_mfma_d64(bk, bv, G, gs); break;
+      case 128: f = pick_mfma_d128(bk, bv, G, gs); break;
+      case 256: f = pick_mfma_d256(bk, bv, G, gs); break;
+    }
+    if (f) return f;
+  }
   switch (D) {
     case 64: return pick_d64(bk, bv, G);
     case 128: return pick_d128(bk, bv, G);
@@ -89,6 +103,22 @@ KernelFn pick(int D, int bk, int bv, int G) {
 
 using namespace tqkv;
 using namespace tqkv::decode;
+
+extern "C" const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t D,
+                                               int32_t group_size, int32_t bits_k,
+                                               int32_t bits_v) {
+  if (H <= 0 || H_kv <= 0 || H % H_kv != 0) return "";
+  const int G = H / H_kv;
+  KernelFn fn = pick(D, bits_k, bits_v, G, group_size);
+  if (!fn) return "";
+  KernelFn mf = nullptr;
+  switch (D) {
+    case 64: mf = pick_mfma_d64(bits_k, bits_v, G, group_size); break;
+    case 128: mf = pick_mfma_d128(bits_k, bits_v, G, group_size); break;
+    case 256: mf = pick_mfma_d256(bits_k, bits_v, G, group_size); break;
+  }
+  return fn == mf ? "mfma" : "dot2";
+}
 
 extern "C" size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
                                              int64_t total_tokens) {
@@ -110,7 +140,7 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
   if (!(group_size == 32 || group_size == 64 || group_size == 128) || D % group_size != 0)
     return fail(TQKV_EUNSUPPORTED, "group_size=%d with D=%d", group_size, D);
   const int G = H / H_kv;
-  KernelFn fn = pick(D, bits_k, bits_v, G);
+  KernelFn fn = pick(D, bits_k, bits_v, G, group_size);
   if (!fn)
     return fail(TQKV_EUNSUPPORTED, "decode layout D=%d bits_k=%d bits_v=%d gqa=%d", D, bits_k,
                 bits_v, G);

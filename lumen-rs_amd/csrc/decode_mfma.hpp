@@ -1,0 +1,453 @@
+// Fused decode attention over affine-packed K/V with scores on the matrix
+// cores (MFMA) and values on VALU dot2.
+//
+// Why MFMA for a bandwidth-bound kernel: at 3 bits the dot2 kernel spends one
+// v_dot2 per two codes per query head on the keys alone, which keeps VALU
+// busy enough to cap the stream well below HBM speed. Here the keys cost one
+// AND per two codes whatever the number of heads, and the matrix cores do the
+// multiply-adds beside the VALU work.
+//
+// Step = 16 consecutive tokens of one (batch row, KV head).
+//   Keys: lane l takes token l % 16 and the channel quarter l / 16 of its row
+//   (D/4 channels), turns the packed codes into f16 subnormals with one AND
+//   per pair (plans in pair_plans.hpp) and feeds them as the B operand
+//   (K = channels, N = 16 tokens) of v_mfma_f32_16x16x32_f16. The A operand
+//   holds the queries, one row per (query head, quantization group): row
+//   (h, g) keeps q_h on the channels of group g and zero elsewhere, so the
+//   16x16 result holds per-group partial dots q_h . c_g for every token and
+//   the per-(token, group) affine scale and bias apply afterwards:
+//     score = sum_g scale_g * dot_g + bias_g * sum(q_h over g).
+//   Queries are pre-scaled per channel by 2^(E_h - o) (o = the code's bit
+//   offset in its f16 half) as in the dot2 kernel, so every product carries
+//   the same 2^(E_h - 24).
+//   Values: lanes take a token pair per 8-lane group (D/8 channels a lane)
+//   and accumulate c_t0 * w_t0 + c_t1 * w_t1 with v_dot2 on codes merged from
+//   the two tokens' rows, w = softmax weight * scale as an f16 pair; the
+//   weights come from the score lanes by ds_bpermute.
+// The softmax maximum is uniform across the wavefront and lags the true one
+// by up to kTau (log2 units); it is recomputed (a 16-lane reduction plus one
+// readlane per head) only on steps where some score passes it by more.
+// Requirements: D in {64, 128, 256}; H/H_kv * D/group <= 16 (the A rows);
+// group a multiple of D/8; plans for (bits_k, D/4) and (bits_v, D/8).
+#pragma once
+
+#include "decode_affine.hpp"
+
+namespace tqkv {
+namespace decode {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+template <int BITS, int EPL>
+constexpr bool has_plan() {
+  return (BITS == 3 && (EPL == 32 || EPL == 64)) ||
+         ((BITS == 4 || BITS == 8) && (EPL == 8 || EPL == 16 || EPL == 32 || EPL == 64));
+}
+
+template <int D, int BK, int BV, int G, int NG>
+constexpr bool mfma_layout_ok() {
+  return (D == 64 || D == 128 || D == 256) && has_plan<BK, D / 4>() && has_plan<BV, D / 8>() &&
+         G * NG <= 16 && (D / NG) % (D / 8) == 0;
+}
+
+// Max over the 16 lanes of a DPP row, every lane getting it.
+__device__ __forceinline__ float row_max16(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x),
+                                                      decltype(ctrl)::value, 0xf, 0xf, true));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xb1>{}));   // quad [1,0,3,2]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4e>{}));   // quad [2,3,0,1]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));  // half-row mirror
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row mirror
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+template <int D, int BK, int BV, int G, int NG, int kWaves>
+__global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
+  constexpr int EK = D / 4, EV = D / 8;
+  constexpr int KW = EK * BK / 32, VW = EV * BV / 32;
+  constexpr int KROW = D * BK / 32, VROW = D * BV / 32;
+  constexpr int GS = D / NG;
+  constexpr int M = G * NG;
+  constexpr int HPL = NG >= 4 ? 1 : 4 / NG;  // query heads per key lane
+  constexpr int RPH = NG >= 4 ? 4 : NG;      // result rows per head in a lane
+  constexpr int NSC = NG >= 4 ? 4 : NG;      // key scales a lane reads per token
+  constexpr int NSW = (NSC + 1) / 2;         // ... as words of bf16 pairs
+  constexpr int kStep = 16;
+  using KP = Plan<BK, EK>;
+  using VP = Plan<BV, EV>;
+  constexpr int NM = (KP::kN + 3) / 4;
+  static_assert(mfma_layout_ok<D, BK, BV, G, NG>(), "layout");
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int kt = lane & 15, kj = lane >> 4;  // key lane: token, channel quarter
+  const int vp = lane >> 3, vc = lane & 7;   // value lane: token pair, channel chunk
+  const int ve0 = vc * EV;
+  const int vgrp = ve0 / GS;
+
+  // ---- queries: f32 in LDS, then per-head exponents and group sums
+  __shared__ float s_q[G][D];
+  for (int i = threadIdx.x; i < G * D; i += kWave * kWaves) {
+    const int h = i / D, d = i % D;
+    s_q[h][d] = bf16_to_f32(a.q[(int64_t(b) * a.H + kvh * G + h) * D + d]);
+  }
+  __syncthreads();
+  int E[G];
+  float qsum[G][NG];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float mx = 0.0f;
+    float part[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) part[g] = 0.0f;
+    for (int d = lane; d < D; d += kWave) {
+      mx = fmaxf(mx, fabsf(s_q[h][d]));
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+        if (d / GS == g) part[g] += s_q[h][d];
+    }
+    mx = wave_max(mx);
+    int ex = 0;
+    if (mx > 0.0f) frexpf(mx, &ex);
+    E[h] = 15 - ex;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) qsum[h][g] = wave_sum(part[g]);
+  }
+
+  // A operand: row kt = (head, group); this lane supplies the k slots of
+  // channel quarter kj.
+  h8_t aq[NM];
+  {
+    const int m = kt;
+    const int h = m / NG, g = m % NG;
+    const bool row_ok = m < M;
+    int Eh = 0;
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+      if (hh == h) Eh = E[hh];
+    static_for<NM>([&](auto I) {
+      h8_t v;
+      static_for<8>([&](auto S) {
+        constexpr int J = 4 * decltype(I)::value + decltype(S)::value / 2;
+        float val = 0.0f;
+        if constexpr (J < KP::kN) {
+          constexpr KOp op = KP::k[J];
+          constexpr bool lo = decltype(S)::value % 2 == 0;
+          constexpr int e = lo ? op.lo_e : op.hi_e;
+          constexpr int o = lo ? op.lo_o : op.hi_o;
+          if constexpr (e >= 0) {
+            const int ch = kj * EK + e;
+            if (row_ok && ch / GS == g) val = __builtin_ldexpf(s_q[h][ch], Eh - o);
+          }
+        }
+        v[decltype(S)::value] = _Float16(val);
+      });
+      aq[decltype(I)::value] = v;
+    });
+  }
+
+  // Score constants of this lane's four result rows 4 * kj + r.
+  float kf[4], qb[4];
+  int hl[HPL];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * kj + r;
+    const int h = m / NG, g = m % NG;
+    kf[r] = 0.0f;
+    qb[r] = 0.0f;
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+#pragma unroll
+      for (int gg = 0; gg < NG; ++gg) {
+        if (m < M && hh == h && gg == g) {
+          kf[r] = a.qscale * __builtin_ldexpf(1.0f, 24 - E[hh]);
+          qb[r] = a.qscale * qsum[hh][gg];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < HPL; ++hh) hl[hh] = (4 * kj + hh * RPH) / NG;
+
+  // ---- this wavefront's keys
+  const int64_t t_begin = int64_t(split) * a.split_len;
+  const int64_t t_end = t_begin + a.split_len < a.total ? t_begin + a.split_len : a.total;
+  int64_t chunk = (t_end - t_begin + kWaves - 1) / kWaves;
+  chunk = (chunk + kStep - 1) / kStep * kStep;
+  const int64_t w_begin = t_begin + wave * chunk;
+  const int64_t w_end = w_begin + chunk < t_end ? w_begin + chunk : t_end;
+
+  float m[G], l[G], bacc[G], mlane[HPL];
+  float acc[G][EV];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+    bacc[h] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EV; ++e) acc[h][e] = 0.0f;
+  }
+#pragma unroll
+  for (int hh = 0; hh < HPL; ++hh) mlane[hh] = hl[hh] < G ? -INFINITY : 0.0f;
+
+  struct Buf {
+    uint32_t kw[KW];
+    uint32_t ks[NSW], kb[NSW];
+    uint32_t vw[2][VW];
+    uint16_t vs[2], vb[2];
+  };
+  // krow: this key lane's row; vrow0/1: this value lane's two rows.
+  auto load = [&](Buf& f, const Seg& s, int64_t krow, int64_t vrow0, int64_t vrow1) {
+    load_words<KW>(f.kw, s.kw + krow * KROW + kj * KW);
+    const int64_t so = krow * NG + (4 * kj) % NG;
+    if constexpr (NSC == 1) {
+      f.ks[0] = __builtin_nontemporal_load(s.ks + so);
+      f.kb[0] = __builtin_nontemporal_load(s.kb + so);
+    } else {
+      load_words<NSW>(f.ks, reinterpret_cast<const uint32_t*>(s.ks + so));
+      load_words<NSW>(f.kb, reinterpret_cast<const uint32_t*>(s.kb + so));
+    }
+    load_words<VW>(f.vw[0], s.vw + vrow0 * VROW + vc * VW);
+    load_words<VW>(f.vw[1], s.vw + vrow1 * VROW + vc * VW);
+    f.vs[0] = __builtin_nontemporal_load(s.vs + vrow0 * NG + vgrp);
+    f.vs[1] = __builtin_nontemporal_load(s.vs + vrow1 * NG + vgrp);
+    f.vb[0] = __builtin_nontemporal_load(s.vb + vrow0 * NG + vgrp);
+    f.vb[1] = __builtin_nontemporal_load(s.vb + vrow1 * NG + vgrp);
+  };
+  auto scale_of = [](const uint32_t* w, int i) {
+    const uint32_t x = w[i / 2];
+    return __uint_as_float((i % 2) == 0 ? (x << 16) : (x & 0xffff0000u));
+  };
+
+  // kMasked: keys past the range are in this step (their scores are -inf and
+  // their loads re-read an in-range row).
+  auto compute = [&](const Buf& f, bool kvalid, auto masked) {
+    constexpr bool kMasked = decltype(masked)::value;
+    // Per-group partial dots of the 16 tokens on the matrix cores.
+    f4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
+    static_for<NM>([&](auto I) {
+      uint32_t bw[4];
+      static_for<4>([&](auto S) {
+        constexpr int J = 4 * decltype(I)::value + decltype(S)::value;
+        if constexpr (J < KP::kN) {
+          constexpr KOp op = KP::k[J];
+          bw[decltype(S)::value] = window<KW, op.byte>(f.kw) & op.mask;
+        } else {
+          bw[decltype(S)::value] = 0u;
+        }
+      });
+      const h8_t bv = __builtin_bit_cast(h8_t, (u32x4_t{bw[0], bw[1], bw[2], bw[3]}));
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[decltype(I)::value], bv, c, 0, 0, 0);
+    });
+    float s[HPL];
+#pragma unroll
+    for (int hh = 0; hh < HPL; ++hh) {
+      float acc_s = 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < RPH; ++rr) {
+        const int r = hh * RPH + rr;
+        const float ks = scale_of(f.ks, r % NSC), kb = scale_of(f.kb, r % NSC);
+        acc_s += fmaf(ks * kf[r], c[r], kb * qb[r]);
+      }
+      if constexpr (NG >= 8) acc_s += __shfl_xor(acc_s, 16, kWave);
+      if constexpr (NG >= 16) acc_s += __shfl_xor(acc_s, 32, kWave);
+      s[hh] = (!kMasked || kvalid) ? acc_s : -INFINITY;
+    }
+
+    // Move the (uniform) maximum when a score passes it by more than kTau.
+    bool need = false;
+#pragma unroll
+    for (int hh = 0; hh < HPL; ++hh) need |= (hl[hh] < G) && (s[hh] > mlane[hh] + kTau);
+    if (__any(need)) {
+      float smax[HPL];
+#pragma unroll
+      for (int hh = 0; hh < HPL; ++hh) smax[hh] = row_max16(s[hh]);
+      static_for<G>([&](auto Hc) {
+        constexpr int h = decltype(Hc)::value;
+        constexpr int src = NG >= 4 ? 16 * (h * NG / 4) : 16 * (h / HPL);
+        constexpr int reg = NG >= 4 ? 0 : h % HPL;
+        const float smf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(smax[reg]), src));
+        if (smf > m[h] + kTau) {
+          const float fct = m[h] == -INFINITY ? 0.0f : exp2f(m[h] - smf);
+          m[h] = smf;
+          l[h] *= fct;
+          bacc[h] *= fct;
+#pragma unroll
+          for (int e = 0; e < EV; ++e) acc[h][e] *= fct;
+        }
+      });
+#pragma unroll
+      for (int hh = 0; hh < HPL; ++hh) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+          if (hl[hh] == h) mlane[hh] = m[h];
+      }
+    }
+    float p[HPL];
+#pragma unroll
+    for (int hh = 0; hh < HPL; ++hh) p[hh] = __builtin_amdgcn_exp2f(s[hh] - mlane[hh]);
+
+    // Values: this lane's token pair takes its weights from the score lanes.
+    const float vs0 = bf16_to_f32(f.vs[0]), vs1 = bf16_to_f32(f.vs[1]);
+    const float vb0 = bf16_to_f32(f.vb[0]), vb1 = bf16_to_f32(f.vb[1]);
+    uint32_t wp[G];
+    static_for<G>([&](auto Hc) {
+      constexpr int h = decltype(Hc)::value;
+      constexpr int grp_lane = NG >= 4 ? 16 * (h * NG / 4) : 16 * (h / HPL);
+      constexpr int reg = NG >= 4 ? 0 : h % HPL;
+      const float p0 = __shfl(p[reg], grp_lane + 2 * vp, kWave);
+      const float p1 = __shfl(p[reg], grp_lane + 2 * vp + 1, kWave);
+      l[h] += p0 + p1;
+      bacc[h] = fmaf(p0, vb0, fmaf(p1, vb1, bacc[h]));
+      wp[h] = h2_bits(h2_t{_Float16(p0 * vs0), _Float16(p1 * vs1)});
+    });
+    v_accumulate<BV, EV, VW, G>(f.vw[0], f.vw[1], wp, acc);
+  };
+
+  for (int sg = 0; sg < 2; ++sg) {
+    const Seg& s = a.seg[sg];
+    const int64_t lo = sg == 0 ? w_begin : (w_begin > a.n0 ? w_begin : a.n0);
+    const int64_t hi = sg == 0 ? (w_end < a.n0 ? w_end : a.n0) : w_end;
+    if (lo >= hi) continue;
+    const int64_t off = sg == 0 ? 0 : a.n0;
+    const int64_t slab = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap - off;
+    const int64_t n_full = (hi - lo) / kStep;
+    const std::integral_constant<bool, false> full{};
+    const std::integral_constant<bool, true> masked{};
+    if (n_full > 0) {
+      Buf b0, b1;
+      int64_t base = slab + lo;  // row of the step's first token
+      load(b0, s, base + kt, base + 2 * vp, base + 2 * vp + 1);
+      int64_t it = 0;
+      for (; it + 2 <= n_full; it += 2) {
+        load(b1, s, base + kStep + kt, base + kStep + 2 * vp, base + kStep + 2 * vp + 1);
+        compute(b0, true, full);
+        base += 2 * kStep;
+        if (it + 2 < n_full) load(b0, s, base + kt, base + 2 * vp, base + 2 * vp + 1);
+        compute(b1, true, full);
+      }
+      if (it < n_full) compute(b0, true, full);
+    }
+    const int64_t tail = lo + n_full * kStep;
+    if (tail < hi) {
+      Buf f;
+      const int64_t tk = tail + kt, t0 = tail + 2 * vp, t1 = t0 + 1;
+      load(f, s, slab + (tk < hi ? tk : hi - 1), slab + (t0 < hi ? t0 : hi - 1),
+           slab + (t1 < hi ? t1 : hi - 1));
+      compute(f, tk < hi, masked);
+    }
+  }
+
+  // ---- merge: undo the code scale, add the bias term, sum the token pairs
+  // of the wavefront (its maximum is uniform), then the wavefronts via LDS.
+  static_for<VP::cN>([&](auto C) {
+    constexpr VCode vcd = VP::vc[decltype(C)::value];
+    constexpr float unscale = float(1 << (24 - vcd.o));
+#pragma unroll
+    for (int h = 0; h < G; ++h) acc[h][vcd.e] = fmaf(acc[h][vcd.e], unscale, bacc[h]);
+  });
+#pragma unroll
+  for (int off = 8; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      l[h] += __shfl_xor(l[h], off, kWave);
+#pragma unroll
+      for (int e = 0; e < EV; ++e) acc[h][e] += __shfl_xor(acc[h][e], off, kWave);
+    }
+  }
+
+  __shared__ float s_m[kWaves][G], s_l[kWaves][G];
+  __shared__ float s_acc[kWaves][G][D];
+  if (vp == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      if (vc == 0) {
+        s_m[wave][h] = m[h];
+        s_l[wave][h] = l[h];
+      }
+#pragma unroll
+      for (int e = 0; e < EV; ++e) s_acc[wave][h][ve0 + e] = acc[h][e];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * D; i += kWave * kWaves) {
+    const int h = i / D, d = i % D;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][h]);
+    float ls = 0.0f, os = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = mx == -INFINITY ? 0.0f : exp2f(s_m[w][h] - mx);
+      ls += s_l[w][h] * f;
+      os += s_acc[w][h][d] * f;
+    }
+    const int64_t bh = int64_t(b) * a.H + kvh * G + h;
+    if (a.n_splits == 1) {
+      a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
+    } else {
+      const int64_t row = bh * a.n_splits + split;
+      a.part_o[row * D + d] = os;
+      if (d == 0) {
+        a.part_m[row] = mx;
+        a.part_l[row] = ls;
+      }
+    }
+  }
+}
+
+// The MFMA kernel for a layout, or nullptr where it does not apply (the dot2
+// kernel serves those). Instantiated for group size 64 only.
+template <int D, int BK, int BV, int G>
+KernelFn pick_mfma_g() {
+  constexpr int NG = D / 64;
+  if constexpr (NG >= 1 && mfma_layout_ok<D, BK, BV, G, NG>())
+    return decode_mfma_kernel<D, BK, BV, G, NG, waves_for<G, D>()>;
+  else
+    return nullptr;
+}
+
+template <int D, int BK, int BV>
+KernelFn pick_mfma_bits_g(int G) {
+  switch (G) {
+    case 1: return pick_mfma_g<D, BK, BV, 1>();
+    case 2: return pick_mfma_g<D, BK, BV, 2>();
+    case 4: return pick_mfma_g<D, BK, BV, 4>();
+    case 8: return pick_mfma_g<D, BK, BV, 8>();
+  }
+  return nullptr;
+}
+
+template <int D>
+KernelFn pick_mfma(int bk, int bv, int G, int gs) {
+  if (gs != 64) return nullptr;
+#define TQKV_PAIR(K, V) \
+  if (bk == K && bv == V) return pick_mfma_bits_g<D, K, V>(G);
+  TQKV_PAIR(3, 3) TQKV_PAIR(4, 4) TQKV_PAIR(8, 8)
+  TQKV_PAIR(3, 4) TQKV_PAIR(4, 3) TQKV_PAIR(3, 8)
+  TQKV_PAIR(8, 3) TQKV_PAIR(4, 8) TQKV_PAIR(8, 4)
+#undef TQKV_PAIR
+  return nullptr;
+}
+
+KernelFn pick_mfma_d64(int bk, int bv, int G, int gs);
+KernelFn pick_mfma_d128(int bk, int bv, int G, int gs);
+KernelFn pick_mfma_d256(int bk, int bv, int G, int gs);
+
+}  // namespace decode
+}  // namespace tqkv

@@ -54,6 +54,7 @@ _SIGS = {
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
+    "tqkv_decode_kernel_name": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32]),
     "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
     "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
 }
@@ -247,6 +248,11 @@ def decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, out,
     arr = (AffineSeg * len(segs))(*segs)
     check(lib().tqkv_decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, arr,
                                           len(segs), out, workspace, workspace_bytes, stream))
+
+
+def decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v):
+    """"mfma", "dot2" or "" (unsupported) for a decode layout."""
+    return lib().tqkv_decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v).decode()
 
 
 def decode_workspace_size(B, H, H_kv, D, total):

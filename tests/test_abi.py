@@ -34,3 +34,15 @@ def test_workspace_size_is_host_arithmetic():
     n = tqkv.decode_workspace_size(32, 16, 8, 256, 32768)
     assert n > 32 * 16 * 256 * 4
     assert tqkv.decode_workspace_size(0, 16, 8, 256, 10) == 0
+
+
+def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):
+    import tqkv
+    monkeypatch.delenv("TQKV_DECODE_KERNEL", raising=False)
+    assert tqkv.decode_kernel_name(16, 8, 256, 64, 3, 3) == "mfma"  # config 2
+    assert tqkv.decode_kernel_name(32, 8, 128, 64, 4, 4) == "mfma"  # configs 1 and 3
+    assert tqkv.decode_kernel_name(32, 8, 128, 64, 8, 4) == "mfma"  # config 4
+    assert tqkv.decode_kernel_name(16, 2, 512, 64, 8, 8) == "dot2"
+    assert tqkv.decode_kernel_name(16, 8, 256, 64, 5, 5) == ""
+    monkeypatch.setenv("TQKV_DECODE_KERNEL", "dot2")
+    assert tqkv.decode_kernel_name(16, 8, 256, 64, 3, 3) == "dot2"

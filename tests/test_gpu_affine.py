@@ -164,9 +164,22 @@ DECODE_CASES = [
 ]
 
 
+@pytest.fixture(params=["auto", "dot2"])
+def kernel(request, monkeypatch):
+    """Runs a decode test on the default kernel choice and again with the
+    dot2 kernel forced, so both kernels meet the same bar."""
+    if request.param == "dot2":
+        monkeypatch.setenv("TQKV_DECODE_KERNEL", "dot2")
+    else:
+        monkeypatch.delenv("TQKV_DECODE_KERNEL", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("B,H,Hkv,D,N,bk,bv,gs,extra", DECODE_CASES)
-def test_decode_matches_dequantize_then_attend(T, B, H, Hkv, D, N, bk, bv, gs, extra):
-    print(f"[decode] B={B} H={H}/{Hkv} D={D} N={N} bits={bk}/{bv} gs={gs}", flush=True)
+def test_decode_matches_dequantize_then_attend(T, kernel, B, H, Hkv, D, N, bk, bv, gs, extra):
+    name = T.decode_kernel_name(H, Hkv, D, gs, bk, bv)
+    print(f"[decode] B={B} H={H}/{Hkv} D={D} N={N} bits={bk}/{bv} gs={gs} kernel={name}",
+          flush=True)
     seed = B * 1000003 + H * 1009 + D * 17 + N + bk * 7 + bv
     q = kv_bf16((B, H, 1, D), seed)
     k = kv_bf16((B, Hkv, N, D), seed + 1, frac=0.01, mult=10.0)
@@ -183,7 +196,7 @@ def test_decode_matches_dequantize_then_attend(T, B, H, Hkv, D, N, bk, bv, gs, e
 @pytest.mark.parametrize("H,Hkv,D,N", [
     (16, 4, 256, 4100), (24, 4, 256, 777), (16, 2, 256, 20), (16, 2, 512, 9000),
     (16, 8, 256, 40000)])
-def test_decode_reference_fused_kernel_cases(T, H, Hkv, D, N, bits):
+def test_decode_reference_fused_kernel_cases(T, kernel, H, Hkv, D, N, bits):
     # native_quant_attention.rs:353-403: q ~ N(0, 1/D) in bf16, K/V ~ N(0, 1)
     # quantized from a buffer 256 tokens longer and read as the first N
     # (a strided view, as the cache hands it out), scale 1.0; the fused
@@ -206,7 +219,7 @@ def test_decode_reference_fused_kernel_cases(T, H, Hkv, D, N, bits):
     check_close(got, wf)
 
 
-def test_decode_shared_prefix_plus_suffix(T):
+def test_decode_shared_prefix_plus_suffix(T, kernel):
     # sdpa_split semantics (native_attention.rs:174-208): one softmax over a
     # shared batch-1 prefix and each row's own suffix.
     B, H, Hkv, D, P, S, gs = 3, 8, 2, 128, 700, 130, 64
@@ -237,3 +250,18 @@ def test_decode_rejects_unreadable_layouts(T):
     with pytest.raises(T.TqkvError) as e:
         T.decode_attend_affine(q.ptr, 1, 12, 5, 128, 64, 4, 4, 1.0, [seg], out.ptr)
     assert e.value.status == T.EINVAL_SHAPE
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,N,bk,bv", [(2, 16, 8, 256, 4100, 3, 3), (1, 32, 8, 128, 3333, 4, 4)])
+def test_decode_single_launch_path(T, kernel, monkeypatch, B, H, Hkv, D, N, bk, bv):
+    # One workgroup per (batch row, KV head), normalizing in-kernel: the path
+    # the full-size benchmark takes (B * H_kv fills the GPU there).
+    monkeypatch.setenv("TQKV_DECODE_SPLITS", "1")
+    print(f"[decode-1split] B={B} H={H}/{Hkv} D={D} N={N} bits={bk}/{bv}", flush=True)
+    q = kv_bf16((B, H, 1, D), 77)
+    k = kv_bf16((B, Hkv, N, D), 78, frac=0.01, mult=10.0)
+    v = kv_bf16((B, Hkv, N, D), 79, frac=0.01, mult=10.0)
+    (kh, kd), (vh, vd) = _cache(k, 64, bk, N + 7), _cache(v, 64, bv, N + 7)
+    got = run_decode(T, q, [(kd, vd, N + 7, N, False)], B, H, Hkv, D, 64, bk, bv, D ** -0.5)
+    wf, _, _ = O.attend_affine(q, kh, vh, 64, bk, bv, D ** -0.5)
+    check_close(got, wf)
