@@ -130,6 +130,9 @@ def main():
     # + WRITE_SIZE x 1.000, factors from a 1 GiB read and a 1 GiB write kernel
     # of the same library). Counters cannot be read inside this process, so a
     # non-default shape reports null.
+    kind = T.decode_kernel_name(H, HKV, D, GS, BITS, BITS)
+    kernel = ("decode_mfma_kernel<256,3,3,2,4,8>" if kind == "mfma"
+              else "decode_affine_kernel<256,3,3,2,32,8>")
     default_shape = (B, N) == (32, 32768)
     traffic = int((917933.6 * 2.0 + 256.0) * 1024) if default_shape else None
     tokens_per_s = B / (ms_per_step * 1e-3)
@@ -168,7 +171,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "kernel": "decode_affine_kernel<256,3,3,2,32,8>",
+            "kernel": kernel,
             "alg_bytes_per_launch": int(alg_bytes),
             "avg_launch_ms": round(dec_avg_ms, 5),
         },

@@ -76,9 +76,11 @@ int waves_for_shape(int G, int D) { return G * D <= 1024 ? 8 : 4; }
 
 // The MFMA-scored kernel where its layout applies, else the dot2 kernel.
 // TQKV_DECODE_KERNEL=dot2 forces the dot2 kernel (tests cover both).
-KernelFn pick(int D, int bk, int bv, int G, int gs) {
+// max_rows: the longest segment; the MFMA kernel addresses a segment's rows
+// of one (batch row, KV head) through 32-bit buffer offsets.
+KernelFn pick(int D, int bk, int bv, int G, int gs, int64_t max_rows = 0) {
   const char* env = getenv("TQKV_DECODE_KERNEL");
-  const bool dot2_only = env && strcmp(env, "dot2") == 0;
+  const bool dot2_only = (env && strcmp(env, "dot2") == 0) || max_rows * D >= (int64_t(1) << 31);
   if (!dot2_only) {
     KernelFn f = nullptr;
     switch (D) {
@@ -140,7 +142,9 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
   if (!(group_size == 32 || group_size == 64 || group_size == 128) || D % group_size != 0)
     return fail(TQKV_EUNSUPPORTED, "group_size=%d with D=%d", group_size, D);
   const int G = H / H_kv;
-  KernelFn fn = pick(D, bits_k, bits_v, G, group_size);
+  int64_t max_rows = 0;
+  for (int i = 0; i < n_segs; ++i) max_rows = segs[i].n > max_rows ? segs[i].n : max_rows;
+  KernelFn fn = pick(D, bits_k, bits_v, G, group_size, max_rows);
   if (!fn)
     return fail(TQKV_EUNSUPPORTED, "decode layout D=%d bits_k=%d bits_v=%d gqa=%d", D, bits_k,
                 bits_v, G);

@@ -20,7 +20,9 @@
 //   Queries are pre-scaled per channel by 2^(E_h - o) (o = the code's bit
 //   offset in its f16 half) as in the dot2 kernel, so every product carries
 //   the same 2^(E_h - 24).
-//   Values: lanes take a token pair per 8-lane group (D/8 channels a lane)
+//   Values: lanes take the token pair (j, j + 8) of the step per 8-lane
+//   group j (D/8 channels a lane; each load instruction then reads 8 whole
+//   consecutive rows)
 //   and accumulate c_t0 * w_t0 + c_t1 * w_t1 with v_dot2 on codes merged from
 //   the two tokens' rows, w = softmax weight * scale as an f16 pair; the
 //   weights come from the score lanes by ds_bpermute.
@@ -49,6 +51,45 @@ template <int D, int BK, int BV, int G, int NG>
 constexpr bool mfma_layout_ok() {
   return (D == 64 || D == 128 || D == 256) && has_plan<BK, D / 4>() && has_plan<BV, D / 8>() &&
          G * NG <= 16 && (D / NG) % (D / 8) == 0;
+}
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf2_t as_bf2(uint32_t x) { return __builtin_bit_cast(bf2_t, x); }
+
+// Cache policy of the streamed cache reads: non-temporal.
+constexpr int kNonTemporal = 2;
+
+// A raw buffer descriptor over `bytes` bytes at `base` (32-bit data, no
+// swizzle; the size must fit 32 bits, which the host checks).
+__device__ __forceinline__ rsrc_t buffer_rsrc(const void* base, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), short(0), int(uint32_t(bytes)),
+                                           0x00020000);
+}
+
+// N consecutive words at byte offset voff + soff of a buffer, widest first.
+template <int N>
+__device__ __forceinline__ void buffer_words(uint32_t* dst, rsrc_t r, uint32_t voff,
+                                             uint32_t soff) {
+  if constexpr (N >= 4) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kNonTemporal);
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+    dst[3] = v.w;
+    if constexpr (N > 4) buffer_words<N - 4>(dst + 4, r, voff + 16, soff);
+  } else if constexpr (N == 3) {
+    const u32x3_t v = __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, kNonTemporal);
+    dst[0] = v.x;
+    dst[1] = v.y;
+    dst[2] = v.z;
+  } else if constexpr (N == 2) {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, kNonTemporal);
+    dst[0] = v.x;
+    dst[1] = v.y;
+  } else if constexpr (N == 1) {
+    dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kNonTemporal);
+  }
 }
 
 // Max over the 16 lanes of a DPP row, every lane getting it.
@@ -94,7 +135,10 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   static_assert(mfma_layout_ok<D, BK, BV, G, NG>(), "layout");
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  // readfirstlane: the compiler then knows the wave index (and every range
+  // and buffer descriptor derived from it) is uniform.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
   const int kt = lane & 15, kj = lane >> 4;  // key lane: token, channel quarter
   const int vp = lane >> 3, vc = lane & 7;   // value lane: token pair, channel chunk
   const int ve0 = vc * EV;
@@ -205,37 +249,79 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 #pragma unroll
   for (int hh = 0; hh < HPL; ++hh) mlane[hh] = hl[hh] < G ? -INFINITY : 0.0f;
 
+  // Loads: one buffer descriptor per array over the rows of the range being
+  // walked (base and size wave-uniform, in SGPRs), the lane's offset in a
+  // VGPR and the step's offset in an SGPR, so stepping costs no VALU work.
+  // Every access is in range by construction; the descriptors' size checks
+  // (reads past them return zeros) are a second line of defence.
   struct Buf {
     uint32_t kw[KW];
     uint32_t ks[NSW], kb[NSW];
     uint32_t vw[2][VW];
-    uint16_t vs[2], vb[2];
+    uint32_t vs[2], vb[2];  // bf16 in the low half
   };
-  // krow: this key lane's row; vrow0/1: this value lane's two rows.
-  auto load = [&](Buf& f, const Seg& s, int64_t krow, int64_t vrow0, int64_t vrow1) {
-    load_words<KW>(f.kw, s.kw + krow * KROW + kj * KW);
-    const int64_t so = krow * NG + (4 * kj) % NG;
+  struct Rsrc {
+    rsrc_t kw, ks, kb, vw, vs, vb;
+  };
+  auto make = [&](const Seg& s, int64_t row0, uint32_t nrows) {
+    Rsrc r;
+    r.kw = buffer_rsrc(s.kw + row0 * KROW, uint64_t(nrows) * KROW * 4);
+    r.ks = buffer_rsrc(s.ks + row0 * NG, uint64_t(nrows) * NG * 2);
+    r.kb = buffer_rsrc(s.kb + row0 * NG, uint64_t(nrows) * NG * 2);
+    r.vw = buffer_rsrc(s.vw + row0 * VROW, uint64_t(nrows) * VROW * 4);
+    r.vs = buffer_rsrc(s.vs + row0 * NG, uint64_t(nrows) * NG * 2);
+    r.vb = buffer_rsrc(s.vb + row0 * NG, uint64_t(nrows) * NG * 2);
+    return r;
+  };
+  // Rows are relative to the step's first token; `step` selects the step.
+  auto load = [&](Buf& f, const Rsrc& r, uint32_t step, uint32_t krow, uint32_t vrow0,
+                  uint32_t vrow1) {
+    const uint32_t k_so = step * uint32_t(kStep * KROW * 4);
+    const uint32_t s_so = step * uint32_t(kStep * NG * 2);
+    const uint32_t v_so = step * uint32_t(kStep * VROW * 4);
+    buffer_words<KW>(f.kw, r.kw, (krow * KROW + kj * KW) * 4, k_so);
+    const uint32_t ks_off = (krow * NG + (4 * kj) % NG) * 2;
     if constexpr (NSC == 1) {
-      f.ks[0] = __builtin_nontemporal_load(s.ks + so);
-      f.kb[0] = __builtin_nontemporal_load(s.kb + so);
+      f.ks[0] = __builtin_amdgcn_raw_buffer_load_b16(r.ks, ks_off, s_so, kNonTemporal);
+      f.kb[0] = __builtin_amdgcn_raw_buffer_load_b16(r.kb, ks_off, s_so, kNonTemporal);
     } else {
-      load_words<NSW>(f.ks, reinterpret_cast<const uint32_t*>(s.ks + so));
-      load_words<NSW>(f.kb, reinterpret_cast<const uint32_t*>(s.kb + so));
+      buffer_words<NSW>(f.ks, r.ks, ks_off, s_so);
+      buffer_words<NSW>(f.kb, r.kb, ks_off, s_so);
     }
-    load_words<VW>(f.vw[0], s.vw + vrow0 * VROW + vc * VW);
-    load_words<VW>(f.vw[1], s.vw + vrow1 * VROW + vc * VW);
-    f.vs[0] = __builtin_nontemporal_load(s.vs + vrow0 * NG + vgrp);
-    f.vs[1] = __builtin_nontemporal_load(s.vs + vrow1 * NG + vgrp);
-    f.vb[0] = __builtin_nontemporal_load(s.vb + vrow0 * NG + vgrp);
-    f.vb[1] = __builtin_nontemporal_load(s.vb + vrow1 * NG + vgrp);
+    buffer_words<VW>(f.vw[0], r.vw, (vrow0 * VROW + vc * VW) * 4, v_so);
+    buffer_words<VW>(f.vw[1], r.vw, (vrow1 * VROW + vc * VW) * 4, v_so);
+    f.vs[0] = __builtin_amdgcn_raw_buffer_load_b16(r.vs, (vrow0 * NG + vgrp) * 2, s_so, kNonTemporal);
+    f.vs[1] = __builtin_amdgcn_raw_buffer_load_b16(r.vs, (vrow1 * NG + vgrp) * 2, s_so, kNonTemporal);
+    f.vb[0] = __builtin_amdgcn_raw_buffer_load_b16(r.vb, (vrow0 * NG + vgrp) * 2, s_so, kNonTemporal);
+    f.vb[1] = __builtin_amdgcn_raw_buffer_load_b16(r.vb, (vrow1 * NG + vgrp) * 2, s_so, kNonTemporal);
   };
   auto scale_of = [](const uint32_t* w, int i) {
     const uint32_t x = w[i / 2];
     return __uint_as_float((i % 2) == 0 ? (x << 16) : (x & 0xffff0000u));
   };
+  // The bias term sum_g bias_g * qsum_g runs as bf16 dot2 against the query
+  // sums split in a bf16 high and low part (~16 significant bits).
+  constexpr int QP = RPH >= 2 ? RPH / 2 : 1;
+  uint32_t qbh[HPL][QP], qbl[HPL][QP];
+#pragma unroll
+  for (int hh = 0; hh < HPL; ++hh) {
+#pragma unroll
+    for (int w = 0; w < QP; ++w) {
+      float x0 = qb[hh * RPH + 2 * w], x1 = RPH >= 2 ? qb[hh * RPH + 2 * w + 1] : 0.0f;
+      const uint16_t h0 = f32_to_bf16(x0), h1 = f32_to_bf16(x1);
+      const uint16_t l0 = f32_to_bf16(x0 - bf16_to_f32(h0)), l1 = f32_to_bf16(x1 - bf16_to_f32(h1));
+      qbh[hh][w] = uint32_t(h0) | uint32_t(h1) << 16;
+      qbl[hh][w] = uint32_t(l0) | uint32_t(l1) << 16;
+    }
+  }
+  // mtau: the lane's running maximum plus kTau (+inf on padding rows, which
+  // never move it).
+  float mtau[HPL];
+#pragma unroll
+  for (int hh = 0; hh < HPL; ++hh) mtau[hh] = hl[hh] < G ? -INFINITY : INFINITY;
 
   // kMasked: keys past the range are in this step (their scores are -inf and
-  // their loads re-read an in-range row).
+  // their loads re-read the range's last row).
   auto compute = [&](const Buf& f, bool kvalid, auto masked) {
     constexpr bool kMasked = decltype(masked)::value;
     // Per-group partial dots of the 16 tokens on the matrix cores.
@@ -257,13 +343,24 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     float s[HPL];
 #pragma unroll
     for (int hh = 0; hh < HPL; ++hh) {
-      float acc_s = 0.0f;
+      float sd = 0.0f;
 #pragma unroll
       for (int rr = 0; rr < RPH; ++rr) {
         const int r = hh * RPH + rr;
-        const float ks = scale_of(f.ks, r % NSC), kb = scale_of(f.kb, r % NSC);
-        acc_s += fmaf(ks * kf[r], c[r], kb * qb[r]);
+        sd = fmaf(scale_of(f.ks, r % NSC), c[r], sd);
       }
+      float sb = 0.0f;
+      if constexpr (RPH == 1) {
+        sb = scale_of(f.kb, 0) * qb[hh];
+      } else {
+#pragma unroll
+        for (int w = 0; w < QP; ++w) {
+          const uint32_t kbw = f.kb[((hh * RPH) % NSC) / 2 + w];
+          sb = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(kbw), as_bf2(qbh[hh][w]), sb, false);
+          sb = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(kbw), as_bf2(qbl[hh][w]), sb, false);
+        }
+      }
+      float acc_s = fmaf(kf[hh * RPH], sd, sb);
       if constexpr (NG >= 8) acc_s += __shfl_xor(acc_s, 16, kWave);
       if constexpr (NG >= 16) acc_s += __shfl_xor(acc_s, 32, kWave);
       s[hh] = (!kMasked || kvalid) ? acc_s : -INFINITY;
@@ -272,7 +369,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     // Move the (uniform) maximum when a score passes it by more than kTau.
     bool need = false;
 #pragma unroll
-    for (int hh = 0; hh < HPL; ++hh) need |= (hl[hh] < G) && (s[hh] > mlane[hh] + kTau);
+    for (int hh = 0; hh < HPL; ++hh) need |= s[hh] > mtau[hh];
     if (__any(need)) {
       float smax[HPL];
 #pragma unroll
@@ -295,7 +392,10 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       for (int hh = 0; hh < HPL; ++hh) {
 #pragma unroll
         for (int h = 0; h < G; ++h)
-          if (hl[hh] == h) mlane[hh] = m[h];
+          if (hl[hh] == h) {
+            mlane[hh] = m[h];
+            mtau[hh] = m[h] + kTau;
+          }
       }
     }
     float p[HPL];
@@ -310,8 +410,8 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       constexpr int h = decltype(Hc)::value;
       constexpr int grp_lane = NG >= 4 ? 16 * (h * NG / 4) : 16 * (h / HPL);
       constexpr int reg = NG >= 4 ? 0 : h % HPL;
-      const float p0 = __shfl(p[reg], grp_lane + 2 * vp, kWave);
-      const float p1 = __shfl(p[reg], grp_lane + 2 * vp + 1, kWave);
+      const float p0 = __shfl(p[reg], grp_lane + vp, kWave);
+      const float p1 = __shfl(p[reg], grp_lane + vp + 8, kWave);
       l[h] += p0 + p1;
       bacc[h] = fmaf(p0, vb0, fmaf(p1, vb1, bacc[h]));
       wp[h] = h2_bits(h2_t{_Float16(p0 * vs0), _Float16(p1 * vs1)});
@@ -325,31 +425,34 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     const int64_t hi = sg == 0 ? (w_end < a.n0 ? w_end : a.n0) : w_end;
     if (lo >= hi) continue;
     const int64_t off = sg == 0 ? 0 : a.n0;
-    const int64_t slab = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap - off;
-    const int64_t n_full = (hi - lo) / kStep;
+    const int64_t row0 = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap + (lo - off);
+    const uint32_t nrows = uint32_t(hi - lo);
+    const uint32_t n_full = nrows / kStep;
     const std::integral_constant<bool, false> full{};
     const std::integral_constant<bool, true> masked{};
     if (n_full > 0) {
+      // Two buffers in turn; the prefetch past the last step re-reads the
+      // last step (unconditional loads keep the buffers in place).
+      const Rsrc r = make(s, row0, n_full * kStep);
       Buf b0, b1;
-      int64_t base = slab + lo;  // row of the step's first token
-      load(b0, s, base + kt, base + 2 * vp, base + 2 * vp + 1);
-      int64_t it = 0;
+      load(b0, r, 0, kt, vp, vp + 8);
+      uint32_t it = 0;
       for (; it + 2 <= n_full; it += 2) {
-        load(b1, s, base + kStep + kt, base + kStep + 2 * vp, base + kStep + 2 * vp + 1);
+        load(b1, r, it + 1, kt, vp, vp + 8);
         compute(b0, true, full);
-        base += 2 * kStep;
-        if (it + 2 < n_full) load(b0, s, base + kt, base + 2 * vp, base + 2 * vp + 1);
+        load(b0, r, it + 2 < n_full ? it + 2 : n_full - 1, kt, vp, vp + 8);
         compute(b1, true, full);
       }
       if (it < n_full) compute(b0, true, full);
     }
-    const int64_t tail = lo + n_full * kStep;
-    if (tail < hi) {
+    const uint32_t left = nrows - n_full * kStep;
+    if (left > 0) {
+      // Lanes past the range re-read its last row and are masked.
+      const Rsrc r = make(s, row0 + n_full * kStep, left);
+      const uint32_t last = left - 1;
       Buf f;
-      const int64_t tk = tail + kt, t0 = tail + 2 * vp, t1 = t0 + 1;
-      load(f, s, slab + (tk < hi ? tk : hi - 1), slab + (t0 < hi ? t0 : hi - 1),
-           slab + (t1 < hi ? t1 : hi - 1));
-      compute(f, tk < hi, masked);
+      load(f, r, 0, kt < left ? kt : last, vp < left ? vp : last, vp + 8 < left ? vp + 8 : last);
+      compute(f, kt < left, masked);
     }
   }
 

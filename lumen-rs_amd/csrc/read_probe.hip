@@ -1,8 +1,8 @@
 // The memory-bandwidth probe of the reference (bandwidth.rs:73-100), for this
 // GPU: sum an array of floats, reading every byte exactly once, as a ceiling
 // for what a streaming kernel can read from HBM. One pass is two launches: a
-// grid-stride partial sum per workgroup (16-byte loads, eight in flight per
-// lane), then one workgroup adding the partials.
+// grid-stride partial sum per workgroup (16-byte non-temporal loads, eight in
+// flight per lane), then one workgroup adding the partials.
 #include "common.hpp"
 
 namespace tqkv {
@@ -60,7 +60,14 @@ extern "C" int32_t tqkv_read_probe(const float* data, size_t bytes, float* scrat
   if (!data || !scratch || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (bytes % 16 != 0 || (reinterpret_cast<uintptr_t>(data) & 15u) != 0)
     return fail(TQKV_EINVAL_ARG, "probe buffer must be 16-byte aligned and sized");
-  const int blocks = 4096;
+  // One workgroup per compute unit, eight 16-byte loads in flight per lane:
+  // the fastest streaming shape a sweep of grid sizes, block sizes and loads
+  // in flight found on MI355X (about 7 TB/s; a grid of thousands of
+  // workgroups reads about 20% slower).
+  int dev = 0, cus = 0;
+  TQKV_HIP(hipGetDevice(&dev));
+  TQKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int blocks = cus > 0 && cus <= 4096 ? cus : 256;
   if (scratch_bytes < size_t(blocks) * sizeof(float))
     return fail(TQKV_EINVAL_ARG, "scratch of %zu bytes, need %zu", scratch_bytes,
                 size_t(blocks) * sizeof(float));
