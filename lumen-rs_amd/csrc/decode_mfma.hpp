@@ -254,11 +254,20 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   // VGPR and the step's offset in an SGPR, so stepping costs no VALU work.
   // Every access is in range by construction; the descriptors' size checks
   // (reads past them return zeros) are a second line of defence.
-  struct Buf {
+  // Keys and values of a step load into separate buffers: the pipeline below
+  // scores step i + 1 while it accumulates the values of step i.
+  struct KBuf {
     uint32_t kw[KW];
     uint32_t ks[NSW], kb[NSW];
+  };
+  struct VBuf {
     uint32_t vw[2][VW];
     uint32_t vs[2], vb[2];  // bf16 in the low half
+  };
+  // A scored step's weights, as this value lane needs them: tokens j and
+  // j + 8 of the step for every head.
+  struct Pend {
+    float p0[G], p1[G];
   };
   struct Rsrc {
     rsrc_t kw, ks, kb, vw, vs, vb;
@@ -273,12 +282,10 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     r.vb = buffer_rsrc(s.vb + row0 * NG, uint64_t(nrows) * NG * 2);
     return r;
   };
-  // Rows are relative to the step's first token; `step` selects the step.
-  auto load = [&](Buf& f, const Rsrc& r, uint32_t step, uint32_t krow, uint32_t vrow0,
-                  uint32_t vrow1) {
+  // Loads of step `step`; rows are relative to the step's first token.
+  auto load_k = [&](KBuf& f, const Rsrc& r, uint32_t step, uint32_t krow) {
     const uint32_t k_so = step * uint32_t(kStep * KROW * 4);
     const uint32_t s_so = step * uint32_t(kStep * NG * 2);
-    const uint32_t v_so = step * uint32_t(kStep * VROW * 4);
     buffer_words<KW>(f.kw, r.kw, (krow * KROW + kj * KW) * 4, k_so);
     const uint32_t ks_off = (krow * NG + (4 * kj) % NG) * 2;
     if constexpr (NSC == 1) {
@@ -288,6 +295,10 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       buffer_words<NSW>(f.ks, r.ks, ks_off, s_so);
       buffer_words<NSW>(f.kb, r.kb, ks_off, s_so);
     }
+  };
+  auto load_v = [&](VBuf& f, const Rsrc& r, uint32_t step, uint32_t vrow0, uint32_t vrow1) {
+    const uint32_t s_so = step * uint32_t(kStep * NG * 2);
+    const uint32_t v_so = step * uint32_t(kStep * VROW * 4);
     buffer_words<VW>(f.vw[0], r.vw, (vrow0 * VROW + vc * VW) * 4, v_so);
     buffer_words<VW>(f.vw[1], r.vw, (vrow1 * VROW + vc * VW) * 4, v_so);
     f.vs[0] = __builtin_amdgcn_raw_buffer_load_b16(r.vs, (vrow0 * NG + vgrp) * 2, s_so, kNonTemporal);
@@ -320,9 +331,11 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 #pragma unroll
   for (int hh = 0; hh < HPL; ++hh) mtau[hh] = hl[hh] < G ? -INFINITY : INFINITY;
 
-  // kMasked: keys past the range are in this step (their scores are -inf and
-  // their loads re-read the range's last row).
-  auto compute = [&](const Buf& f, bool kvalid, auto masked) {
+  // Scores of a step and their softmax weights, handed to the value lanes.
+  // When the (uniform) maximum moves, everything accumulated so far and the
+  // weights `prev` of the step still waiting for its values are rescaled.
+  // kMasked: keys past the range are in this step (scores -inf).
+  auto score = [&](const KBuf& f, bool kvalid, auto masked, Pend& prev, Pend& out) {
     constexpr bool kMasked = decltype(masked)::value;
     // Per-group partial dots of the 16 tokens on the matrix cores.
     f4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -366,7 +379,6 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       s[hh] = (!kMasked || kvalid) ? acc_s : -INFINITY;
     }
 
-    // Move the (uniform) maximum when a score passes it by more than kTau.
     bool need = false;
 #pragma unroll
     for (int hh = 0; hh < HPL; ++hh) need |= s[hh] > mtau[hh];
@@ -384,6 +396,8 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
           m[h] = smf;
           l[h] *= fct;
           bacc[h] *= fct;
+          prev.p0[h] *= fct;
+          prev.p1[h] *= fct;
 #pragma unroll
           for (int e = 0; e < EV; ++e) acc[h][e] *= fct;
         }
@@ -401,21 +415,26 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     float p[HPL];
 #pragma unroll
     for (int hh = 0; hh < HPL; ++hh) p[hh] = __builtin_amdgcn_exp2f(s[hh] - mlane[hh]);
-
-    // Values: this lane's token pair takes its weights from the score lanes.
-    const float vs0 = bf16_to_f32(f.vs[0]), vs1 = bf16_to_f32(f.vs[1]);
-    const float vb0 = bf16_to_f32(f.vb[0]), vb1 = bf16_to_f32(f.vb[1]);
-    uint32_t wp[G];
     static_for<G>([&](auto Hc) {
       constexpr int h = decltype(Hc)::value;
       constexpr int grp_lane = NG >= 4 ? 16 * (h * NG / 4) : 16 * (h / HPL);
       constexpr int reg = NG >= 4 ? 0 : h % HPL;
-      const float p0 = __shfl(p[reg], grp_lane + vp, kWave);
-      const float p1 = __shfl(p[reg], grp_lane + vp + 8, kWave);
+      out.p0[h] = __shfl(p[reg], grp_lane + vp, kWave);
+      out.p1[h] = __shfl(p[reg], grp_lane + vp + 8, kWave);
+    });
+  };
+  // Values of a scored step.
+  auto values = [&](const VBuf& f, const Pend& w) {
+    const float vs0 = bf16_to_f32(f.vs[0]), vs1 = bf16_to_f32(f.vs[1]);
+    const float vb0 = bf16_to_f32(f.vb[0]), vb1 = bf16_to_f32(f.vb[1]);
+    uint32_t wp[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float p0 = w.p0[h], p1 = w.p1[h];
       l[h] += p0 + p1;
       bacc[h] = fmaf(p0, vb0, fmaf(p1, vb1, bacc[h]));
       wp[h] = h2_bits(h2_t{_Float16(p0 * vs0), _Float16(p1 * vs1)});
-    });
+    }
     v_accumulate<BV, EV, VW, G>(f.vw[0], f.vw[1], wp, acc);
   };
 
@@ -427,32 +446,59 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     const int64_t off = sg == 0 ? 0 : a.n0;
     const int64_t row0 = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap + (lo - off);
     const uint32_t nrows = uint32_t(hi - lo);
-    const uint32_t n_full = nrows / kStep;
+    const uint32_t n = nrows / kStep;  // full steps
     const std::integral_constant<bool, false> full{};
     const std::integral_constant<bool, true> masked{};
-    if (n_full > 0) {
-      // Two buffers in turn; the prefetch past the last step re-reads the
-      // last step (unconditional loads keep the buffers in place).
-      const Rsrc r = make(s, row0, n_full * kStep);
-      Buf b0, b1;
-      load(b0, r, 0, kt, vp, vp + 8);
-      uint32_t it = 0;
-      for (; it + 2 <= n_full; it += 2) {
-        load(b1, r, it + 1, kt, vp, vp + 8);
-        compute(b0, true, full);
-        load(b0, r, it + 2 < n_full ? it + 2 : n_full - 1, kt, vp, vp + 8);
-        compute(b1, true, full);
+    if (n > 0) {
+      // Iteration i: load keys of step i + 2 and values of step i + 1, score
+      // step i + 1, accumulate the values of step i. Loads past the last
+      // step re-read it (unconditional loads keep the buffers in place).
+      const Rsrc r = make(s, row0, n * kStep);
+      const uint32_t last = n - 1;
+      auto cl = [&](uint32_t x) { return x < last ? x : last; };
+      KBuf k0, k1;
+      VBuf v0, v1;
+      Pend p0, p1;
+#pragma unroll
+      for (int h = 0; h < G; ++h) p1.p0[h] = p1.p1[h] = 0.0f;
+      load_k(k0, r, 0, kt);
+      load_k(k1, r, cl(1), kt);
+      load_v(v0, r, 0, vp, vp + 8);
+      score(k0, true, full, p1, p0);
+      uint32_t i = 0;
+      for (; i + 2 < n; i += 2) {
+        load_k(k0, r, cl(i + 2), kt);
+        load_v(v1, r, i + 1, vp, vp + 8);
+        score(k1, true, full, p0, p1);
+        values(v0, p0);
+        load_k(k1, r, cl(i + 3), kt);
+        load_v(v0, r, i + 2, vp, vp + 8);
+        score(k0, true, full, p1, p0);
+        values(v1, p1);
       }
-      if (it < n_full) compute(b0, true, full);
+      if (i + 1 < n) {
+        load_v(v1, r, i + 1, vp, vp + 8);
+        score(k1, true, full, p0, p1);
+        values(v0, p0);
+        values(v1, p1);
+      } else {
+        values(v0, p0);
+      }
     }
-    const uint32_t left = nrows - n_full * kStep;
+    const uint32_t left = nrows - n * kStep;
     if (left > 0) {
       // Lanes past the range re-read its last row and are masked.
-      const Rsrc r = make(s, row0 + n_full * kStep, left);
-      const uint32_t last = left - 1;
-      Buf f;
-      load(f, r, 0, kt < left ? kt : last, vp < left ? vp : last, vp + 8 < left ? vp + 8 : last);
-      compute(f, kt < left, masked);
+      const Rsrc r = make(s, row0 + n * kStep, left);
+      const uint32_t lst = left - 1;
+      KBuf kf_;
+      VBuf vf_;
+      Pend pz, pt;
+#pragma unroll
+      for (int h = 0; h < G; ++h) pz.p0[h] = pz.p1[h] = 0.0f;
+      load_k(kf_, r, 0, kt < left ? kt : lst);
+      load_v(vf_, r, 0, vp < left ? vp : lst, vp + 8 < left ? vp + 8 : lst);
+      score(kf_, kt < left, masked, pz, pt);
+      values(vf_, pt);
     }
   }
 
