@@ -134,7 +134,7 @@ def main():
     kernel = ("decode_mfma_kernel<256,3,3,2,4,8>" if kind == "mfma"
               else "decode_affine_kernel<256,3,3,2,32,8>")
     default_shape = (B, N) == (32, 32768)
-    traffic = int((917933.6 * 2.0 + 256.0) * 1024) if default_shape else None
+    traffic = int((918749.6 * 2.0 + 256.0) * 1024) if default_shape and kind == "mfma" else None
     tokens_per_s = B / (ms_per_step * 1e-3)
 
     # Sanity of the result itself: finite, not all zero.
