@@ -146,6 +146,140 @@ size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
                                   int64_t total_tokens);
 
 /* ======================================================================
+ * The cache object: growing, rotating and shared-prefix KV caches
+ * ====================================================================== */
+
+/*
+ * Device-resident KV cache with the reference's update/fetch/truncate
+ * semantics, bit for bit (the recorded digests of native_cache/
+ * golden_tests.rs:413-497 replay through it). Kinds and their slots (the
+ * parallel buffers an update extends together, each [B, H_kv, cap, row]):
+ *   TQKV_CACHE_BF16      keys bf16 [k_dim], values bf16 [v_dim]
+ *                        (NativeKvCache :369-812, NativeRotatingKvCache
+ *                        :1145-1280)
+ *   TQKV_CACHE_AFFINE    MLX triples: k packed, k scales, k biases, v packed,
+ *                        v scales, v biases (NativeKvCacheQuantized
+ *                        :835-1126, NativeRotatingKvCacheQuantized :1297-1467)
+ *   TQKV_CACHE_CODEBOOK  k codes u8 [k_dim], k sigma f32, [k QJL signs u32
+ *                        [qjl_words], k residual norm f32,] v codes u8
+ *                        [v_dim], v sigma f32 (NativeRotatingKvCacheTurboQuant
+ *                        :1517-1856; rotating only)
+ * max_size > 0 makes the cache a rotating window of max_size tokens whose
+ * first `keep` are never evicted; max_size == 0 grows in 256-token steps.
+ * prealloc mirrors LUMEN_NATIVE_KV_STEP_PREALLOC (native_cache.rs:39-59):
+ * 1 = step-256 in-place growth and in-place ring writes for one-token
+ * updates, 0 = the legacy concatenating path.
+ */
+#define TQKV_CACHE_BF16 0
+#define TQKV_CACHE_AFFINE 1
+#define TQKV_CACHE_CODEBOOK 2
+
+typedef struct tqkv_cache tqkv_cache;
+
+typedef struct tqkv_cache_config {
+  int32_t kind;
+  int32_t batch;
+  int32_t kv_heads;
+  int32_t k_dim;
+  int32_t v_dim;
+  int32_t group_size; /* affine */
+  int32_t bits_k;     /* affine */
+  int32_t bits_v;     /* affine */
+  int32_t qjl_words;  /* codebook: u32 sign words per key row, 0 = no QJL */
+  int32_t prealloc;
+  int64_t max_size;
+  int64_t keep;
+} tqkv_cache_config;
+
+/*
+ * A view of a cache's slots: rows [0, n) of every (batch row, KV head) slab,
+ * slabs `cap` rows apart; slot[i] is the device address of row 0 of slab 0.
+ * Valid until the next call that updates, truncates, splits or destroys the
+ * cache.
+ */
+typedef struct tqkv_cache_view {
+  int64_t n;
+  int64_t cap;
+  int32_t n_slots;
+  int32_t reserved;
+  void* slot[6];
+  int64_t row_bytes[6];
+} tqkv_cache_view;
+
+typedef struct tqkv_cache_state {
+  int64_t offset;      /* base_offset + tokens held (the reference's offset()) */
+  int64_t idx;         /* ring write position (idx()) */
+  int64_t cached_len;  /* buffer length in tokens (cached_len()), 0 if empty */
+  int64_t base_offset; /* absolute position of the buffer's first token */
+  int64_t view;        /* rows of the last fetched view */
+  int32_t empty;       /* 1 before the first update (empty()) */
+  int32_t n_slots;
+} tqkv_cache_state;
+
+/* Constructors NativeKvCache::new / NativeKvCacheQuantized::new /
+ * NativeRotatingKvCache*::new (native_cache.rs:392, 845, 1159, 1313, 1541);
+ * destroy frees the device buffers. */
+int32_t tqkv_cache_create(const tqkv_cache_config* cfg, tqkv_cache** out);
+int32_t tqkv_cache_destroy(tqkv_cache* cache);
+
+/*
+ * update_and_fetch with the slots' new rows given as they are stored
+ * (native_cache.rs:591, 953, 1235, 1418, 1756, 1804): rows[i] is a device
+ * array [B, H_kv, s, row_i] for slot i. `fetched` (may be NULL) receives the
+ * view the reference returns.
+ */
+int32_t tqkv_cache_update(tqkv_cache* cache, const void* const* rows, int64_t s,
+                          tqkv_cache_view* fetched, tqkv_stream stream);
+
+/*
+ * update_and_fetch from bf16 keys and values [B, H_kv, s, dim]: stored as is
+ * (bf16 kind) or quantized on append straight into the cache rows (affine
+ * kind, mlx::quantize as native_cache.rs:968-971, 1445-1448 call it).
+ * TQKV_EUNSUPPORTED for the codebook kind.
+ */
+int32_t tqkv_cache_append(tqkv_cache* cache, const uint16_t* k, const uint16_t* v, int64_t s,
+                          tqkv_cache_view* fetched, tqkv_stream stream);
+
+/*
+ * truncate_to (native_cache.rs:778-811, 913-940, ring_truncate :304-335):
+ * TQKV_EINVAL_TARGET where the reference returns Err (a target past the
+ * tokens held; a rotating cache that has wrapped; an affine growing cache on
+ * the legacy path). As in the reference, `target` counts the tokens this
+ * buffer holds. Host-side bookkeeping only.
+ */
+int32_t tqkv_cache_truncate(tqkv_cache* cache, int64_t target);
+/* clear() (native_cache.rs:739, 895, 1484): back to empty. */
+int32_t tqkv_cache_clear(tqkv_cache* cache);
+/* offset() / idx() / cached_len() / base_offset() / empty(). */
+int32_t tqkv_cache_get_state(const tqkv_cache* cache, tqkv_cache_state* out);
+/* The whole buffers (keys() / values(): n = cached_len, zero padding included). */
+int32_t tqkv_cache_buffers(const tqkv_cache* cache, tqkv_cache_view* out);
+
+/*
+ * keep_suffix_from (native_cache.rs:464-494): drop the first prefix_len
+ * tokens (now held once by a shared prefix cache) and record base_offset =
+ * prefix_len. Growing caches only.
+ */
+int32_t tqkv_cache_keep_suffix_from(tqkv_cache* cache, int64_t prefix_len, tqkv_stream stream);
+/*
+ * Attach a batch-1 cache holding the shared prefix (SharedPrefixKv,
+ * native_cache.rs:2044-2051); NULL detaches. Decode attention then reads the
+ * prefix's first base_offset tokens once for every batch row and the cache's
+ * own suffix, in one softmax (sdpa_split, native_attention.rs:174-208). The
+ * prefix must outlive the attachment.
+ */
+int32_t tqkv_cache_attach_prefix(tqkv_cache* cache, const tqkv_cache* prefix);
+
+/*
+ * Fused decode attention over the last fetched view (affine kind, k_dim ==
+ * v_dim), plus the attached prefix: tqkv_decode_attend_affine on the cache's
+ * own buffers. q: bf16 [B, H, 1, D]; out: bf16 [B, H, 1, D].
+ */
+int32_t tqkv_cache_decode_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
+                                 float scale, uint16_t* out, void* workspace,
+                                 size_t workspace_bytes, tqkv_stream stream);
+
+/* ======================================================================
  * Benchmark utilities (no counterpart in the reference)
  * ====================================================================== */
 

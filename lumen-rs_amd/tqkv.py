@@ -42,6 +42,24 @@ class AffineSeg(ctypes.Structure):
                 ("cap", I64), ("n", I64), ("shared", I32), ("reserved", I32)]
 
 
+class CacheConfig(ctypes.Structure):
+    _fields_ = [("kind", I32), ("batch", I32), ("kv_heads", I32), ("k_dim", I32),
+                ("v_dim", I32), ("group_size", I32), ("bits_k", I32), ("bits_v", I32),
+                ("qjl_words", I32), ("prealloc", I32), ("max_size", I64), ("keep", I64)]
+
+
+class CacheView(ctypes.Structure):
+    _fields_ = [("n", I64), ("cap", I64), ("n_slots", I32), ("reserved", I32),
+                ("slot", P * 6), ("row_bytes", I64 * 6)]
+
+
+class CacheState(ctypes.Structure):
+    _fields_ = [("offset", I64), ("idx", I64), ("cached_len", I64), ("base_offset", I64),
+                ("view", I64), ("empty", I32), ("n_slots", I32)]
+
+
+CACHE_BF16, CACHE_AFFINE, CACHE_CODEBOOK = 0, 1, 2
+
 _lib = None
 _hip = None
 
@@ -56,6 +74,17 @@ _SIGS = {
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
     "tqkv_decode_kernel_name": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32]),
     "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
+    "tqkv_cache_create": (I32, [ctypes.POINTER(CacheConfig), ctypes.POINTER(P)]),
+    "tqkv_cache_destroy": (I32, [P]),
+    "tqkv_cache_update": (I32, [P, ctypes.POINTER(P), I64, ctypes.POINTER(CacheView), P]),
+    "tqkv_cache_append": (I32, [P, P, P, I64, ctypes.POINTER(CacheView), P]),
+    "tqkv_cache_truncate": (I32, [P, I64]),
+    "tqkv_cache_clear": (I32, [P]),
+    "tqkv_cache_get_state": (I32, [P, ctypes.POINTER(CacheState)]),
+    "tqkv_cache_buffers": (I32, [P, ctypes.POINTER(CacheView)]),
+    "tqkv_cache_keep_suffix_from": (I32, [P, I64, P]),
+    "tqkv_cache_attach_prefix": (I32, [P, P]),
+    "tqkv_cache_decode_attend": (I32, [P, P, I32, F32, P, P, SZ, P]),
     "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
 }
 
@@ -289,3 +318,80 @@ def measure_read_bandwidth(stream=None, nbytes=1 << 30, warmup=3, passes=15):
     median = rates[mid] if len(rates) % 2 else 0.5 * (rates[mid - 1] + rates[mid])
     return {"median_gbps": round(median, 1), "best_gbps": round(rates[-1], 1),
             "bytes": nbytes, "passes": passes}
+
+
+# ---------------------------------------------------------------- the cache object
+class Cache:
+    """The device KV cache (tqkv_cache_*): growing, rotating or shared-prefix,
+    bf16 / affine / codebook slots."""
+
+    def __init__(self, kind, batch, kv_heads, k_dim, v_dim, group_size=64, bits_k=4, bits_v=4,
+                 qjl_words=0, prealloc=True, max_size=0, keep=0):
+        self.cfg = CacheConfig(kind, batch, kv_heads, k_dim, v_dim, group_size, bits_k, bits_v,
+                               qjl_words, int(prealloc), max_size, keep)
+        h = P()
+        check(lib().tqkv_cache_create(ctypes.byref(self.cfg), ctypes.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().tqkv_cache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def update(self, rows, s, stream=None):
+        """rows: device pointers, one per slot ([B, H_kv, s, row])."""
+        arr = (P * len(rows))(*rows)
+        v = CacheView()
+        check(lib().tqkv_cache_update(self.h, arr, s, ctypes.byref(v), stream))
+        return v
+
+    def append(self, k, v, s, stream=None):
+        view = CacheView()
+        check(lib().tqkv_cache_append(self.h, k, v, s, ctypes.byref(view), stream))
+        return view
+
+    def truncate(self, target):
+        """True if accepted, False where the reference returns Err."""
+        rc = lib().tqkv_cache_truncate(self.h, target)
+        if rc == EINVAL_TARGET:
+            return False
+        check(rc)
+        return True
+
+    def clear(self):
+        check(lib().tqkv_cache_clear(self.h))
+
+    def state(self):
+        st = CacheState()
+        check(lib().tqkv_cache_get_state(self.h, ctypes.byref(st)))
+        return st
+
+    def buffers(self):
+        v = CacheView()
+        check(lib().tqkv_cache_buffers(self.h, ctypes.byref(v)))
+        return v
+
+    def keep_suffix_from(self, prefix_len, stream=None):
+        check(lib().tqkv_cache_keep_suffix_from(self.h, prefix_len, stream))
+
+    def attach_prefix(self, prefix):
+        check(lib().tqkv_cache_attach_prefix(self.h, prefix.h if prefix is not None else None))
+
+    def decode_attend(self, q, H, scale, out, workspace=None, workspace_bytes=0, stream=None):
+        check(lib().tqkv_cache_decode_attend(self.h, q, H, scale, out, workspace,
+                                             workspace_bytes, stream))
+
+
+def view_slot(view, i, n_slabs, dtype, last):
+    """Download rows [0, view.n) of slot i of a view as [n_slabs, n, last]."""
+    dtype = np.dtype(dtype)
+    if view.n == 0:
+        return np.zeros((n_slabs, 0, last), dtype)
+    full = hip().download(view.slot[i], (n_slabs, view.cap, last), dtype)
+    return np.ascontiguousarray(full[:, :view.n])

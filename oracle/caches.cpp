@@ -440,6 +440,63 @@ uint64_t golden_digest(const std::string& kind, const std::string& plan, bool pr
   return run(*c, *steps);
 }
 
+// The inputs a golden plan feeds its cache, in order, without running the
+// cache: events (op, n) and, for each update, its arrays as generated
+// (golden_tests.rs:37-65 generators, :236-256 driver). Lets another
+// implementation of the caches replay exactly the reference's recordings.
+GoldenTape golden_tape(const std::string& kind, const std::string& plan) {
+  GoldenTape t;
+  const std::vector<Step>* steps;
+  if (plan == "full") {
+    steps = &kFull;
+    t.max_size = 4096;
+    t.keep = 0;
+  } else if (plan == "small") {
+    steps = &kSmallRing;
+    t.max_size = 12;
+    t.keep = 2;
+  } else if (plan == "large") {
+    steps = &kLargeRing;
+    t.max_size = 300;
+    t.keep = 4;
+  } else {
+    throw std::runtime_error("unknown plan " + plan);
+  }
+  Inputs in(0x0022dedcull);
+  auto put = [&](const Arr& a) { t.data.insert(t.data.end(), a.data.begin(), a.data.end()); };
+  for (const Step& st : *steps) {
+    const size_t times = st.op == 'D' ? st.n : 1;
+    for (size_t r = 0; r < times; ++r) {
+      const int s = st.op == 'D' ? 1 : int(st.n);
+      t.events.push_back({st.op == 'R' ? 'R' : 'U', st.op == 'R' ? int64_t(st.n) : int64_t(s),
+                          int64_t(t.data.size())});
+      if (st.op == 'R') continue;
+      if (kind == "full" || kind == "rot") {
+        put(in.bf16(H, s, 16));
+        put(in.bf16(H, s, 24));
+      } else if (kind == "quant_full" || kind == "rot_quant") {
+        put(in.bf16(H, s, 64));
+        put(in.bf16(H, s, 128));
+      } else if (kind == "tq") {
+        put(in.codes(H, s, 16));
+        put(in.positive(H, s, 1));
+        put(in.codes(H, s, 24));
+        put(in.positive(H, s, 1));
+      } else if (kind == "tq_qjl") {
+        put(in.codes(H, s, 16));
+        put(in.positive(H, s, 1));
+        put(in.words(H, s, 2));
+        put(in.positive(H, s, 1));
+        put(in.codes(H, s, 24));
+        put(in.positive(H, s, 1));
+      } else {
+        throw std::runtime_error("unknown kind " + kind);
+      }
+    }
+  }
+  return t;
+}
+
 bool mask_allowed(size_t q_abs, size_t k_abs, long window) {
   if (!(q_abs >= k_abs)) return false;
   if (window >= 0 && !(q_abs < k_abs + size_t(window))) return false;

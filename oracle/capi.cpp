@@ -19,6 +19,42 @@ uint64_t oracle_golden_digest(const char* kind, const char* plan, int prealloc, 
   return golden_digest(kind, plan, prealloc != 0, ao);
 }
 
+// Golden-plan input tape: returns the number of events (or -1 if the
+// buffers are too small); events as (op, n, at) triples of int64.
+int64_t oracle_golden_tape(const char* kind, const char* plan, int64_t* events,
+                           int64_t max_events, uint8_t* data, int64_t data_cap,
+                           int64_t* data_len, int64_t* max_size, int64_t* keep) {
+  GoldenTape t = golden_tape(kind, plan);
+  *data_len = int64_t(t.data.size());
+  *max_size = t.max_size;
+  *keep = t.keep;
+  if (int64_t(t.events.size()) > max_events || int64_t(t.data.size()) > data_cap) return -1;
+  for (size_t i = 0; i < t.events.size(); ++i) {
+    events[3 * i] = t.events[i].op;
+    events[3 * i + 1] = t.events[i].n;
+    events[3 * i + 2] = t.events[i].at;
+  }
+  std::memcpy(data, t.data.data(), t.data.size());
+  return int64_t(t.events.size());
+}
+
+// FNV-1a digest steps of golden_tests.rs:73-155: a number, raw bytes, and a
+// [1, h, s, last] array of dtype 1 = u8, 2 = u32, 3 = f32, 4 = bf16.
+uint64_t oracle_fnv_num(uint64_t h, uint64_t n) {
+  Digest d;
+  d.h = h;
+  d.num(n);
+  return d.h;
+}
+uint64_t oracle_fnv_array(uint64_t h, int dtype, int hh, int s, int last, const void* data) {
+  Digest d;
+  d.h = h;
+  Arr a(DType(dtype), hh, s, last);
+  if (!a.data.empty()) std::memcpy(a.data.data(), data, a.data.size());
+  digest_array(d, a);
+  return d.h;
+}
+
 // ---- numerics
 void oracle_f32_to_bf16(const float* x, size_t n, uint16_t* out) {
   for (size_t i = 0; i < n; ++i) out[i] = f32_to_bf16(x[i]);

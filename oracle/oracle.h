@@ -151,6 +151,21 @@ uint32_t read_code(const uint32_t* words, size_t i, int bits);
 uint64_t golden_digest(const std::string& kind, const std::string& plan, bool prealloc,
                        const AffineOpts& ao = AffineOpts());
 
+// A golden plan's inputs without the cache (see caches.cpp): events are
+// ('U', rows S, byte offset of the update's arrays in data) or
+// ('R', rewind target, -).
+struct GoldenEvent {
+  char op;
+  int64_t n;
+  int64_t at;
+};
+struct GoldenTape {
+  int64_t max_size = 0, keep = 0;
+  std::vector<GoldenEvent> events;
+  std::vector<uint8_t> data;
+};
+GoldenTape golden_tape(const std::string& kind, const std::string& plan);
+
 // ---------------------------------------------------------------- attention
 // native_attention.rs:545-622: may query row i (absolute q_start+i) attend to
 // key k (absolute first_held+k)?

@@ -59,6 +59,10 @@ def lib():
                                             SZ, SZ, L, P, P, P, I]),
             "oracle_attend_codebook": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, F, I, SZ,
                                               SZ, L, P, P, P]),
+            "oracle_golden_tape": (ctypes.c_int64, [ctypes.c_char_p, ctypes.c_char_p, P,
+                                                    ctypes.c_int64, P, ctypes.c_int64, P, P, P]),
+            "oracle_fnv_num": (U64, [U64, U64]),
+            "oracle_fnv_array": (U64, [U64, I, I, I, I, P]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(_lib, name)
@@ -82,6 +86,33 @@ def bf16_to_f32(b):
 def golden_digest(kind, plan, prealloc, round_mode=0, wmax0=1, clip_low=0):
     return lib().oracle_golden_digest(kind.encode(), plan.encode(), int(prealloc), round_mode,
                                       wmax0, clip_low)
+
+
+FNV_OFFSET = 0xCBF29CE484222325
+
+
+def golden_tape(kind, plan):
+    """A golden plan's inputs: ([(op, n, at)], data bytes, max_size, keep);
+    op 'U' = update of n rows with arrays at data[at:], 'R' = rewind to n."""
+    ev = np.zeros(3 * 8192, np.int64)
+    data = np.zeros(1 << 24, np.uint8)
+    dl, mx, kp = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+    n = lib().oracle_golden_tape(kind.encode(), plan.encode(), ptr(ev), 8192, ptr(data),
+                                 data.size, ctypes.byref(dl), ctypes.byref(mx), ctypes.byref(kp))
+    assert n >= 0
+    events = [(chr(ev[3 * i]), int(ev[3 * i + 1]), int(ev[3 * i + 2])) for i in range(n)]
+    return events, data[:dl.value].copy(), mx.value, kp.value
+
+
+def fnv_num(h, n):
+    return lib().oracle_fnv_num(h, n)
+
+
+def fnv_array(h, dtype_code, arr):
+    """arr: [1 or h, s, last] numpy array; dtype_code 1 u8, 2 u32, 3 f32, 4 bf16."""
+    a = np.ascontiguousarray(arr)
+    hh, s, last = a.shape[-3], a.shape[-2], a.shape[-1]
+    return lib().oracle_fnv_array(h, dtype_code, hh, s, last, ptr(a))
 
 
 def codebook(bits, n_iter=1000):

@@ -1,0 +1,268 @@
+"""The device cache object (tqkv_cache_*) through the C ABI.
+
+1. The reference's golden plans (native_cache/golden_tests.rs:182-497) replay
+   through the device cache, quantize-on-append included for the affine
+   kinds, and every fetched view, buffer and counter folds into the FNV-1a
+   digest the reference recorded: bit-exact growth, ring, trim, rewind.
+2. Rewind refusals the plans do not reach (ring_truncate, native_cache.rs:
+   304-335; the quantized legacy path :923-929).
+3. Decode attention over a cache's fetched view: growing, rotating (the held
+   tokens in ring order), and split into a shared prefix plus suffixes
+   (keep_suffix_from + SharedPrefixKv, native_cache.rs:464-494, 2044-2051),
+   against the oracle's dequantize-then-attend over the same tokens.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from inputs import kv_bf16
+from test_oracle_golden import RECORDED
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 1e-3
+
+
+@pytest.fixture(scope="module")
+def T():
+    import tqkv
+    assert tqkv.hip().device_count() > 0, "no GPU visible"
+    return tqkv
+
+
+# (digest dtype code, numpy dtype, last) per slot
+U8, U32, F32, BF = (1, np.uint8), (2, np.uint32), (3, np.float32), (4, np.uint16)
+SLOTS = {
+    "full": [BF + (16,), BF + (24,)],
+    "rot": [BF + (16,), BF + (24,)],
+    "quant_full": [U32 + (8,), BF + (1,), BF + (1,), U32 + (16,), BF + (2,), BF + (2,)],
+    "rot_quant": [U32 + (8,), BF + (1,), BF + (1,), U32 + (16,), BF + (2,), BF + (2,)],
+    "tq": [U8 + (16,), F32 + (1,), U8 + (24,), F32 + (1,)],
+    "tq_qjl": [U8 + (16,), F32 + (1,), U32 + (2,), F32 + (1,), U8 + (24,), F32 + (1,)],
+}
+H = 2  # golden_tests.rs:273
+
+
+def replay(T, kind, plan, prealloc):
+    events, data, max_size, keep = O.golden_tape(kind, plan)
+    ring = kind not in ("full", "quant_full")
+    quant = kind in ("quant_full", "rot_quant")
+    slots = SLOTS[kind]
+    if quant:
+        cache = T.Cache(T.CACHE_AFFINE, 1, H, 64, 128, 64, 4, 4, prealloc=prealloc,
+                        max_size=max_size if ring else 0, keep=keep if ring else 0)
+    elif kind in ("full", "rot"):
+        cache = T.Cache(T.CACHE_BF16, 1, H, 16, 24, prealloc=prealloc,
+                        max_size=max_size if ring else 0, keep=keep if ring else 0)
+    else:
+        cache = T.Cache(T.CACHE_CODEBOOK, 1, H, 16, 24, qjl_words=2 if kind == "tq_qjl" else 0,
+                        prealloc=prealloc, max_size=max_size, keep=keep)
+
+    def arr(view, i):
+        code, dt, last = slots[i]
+        return T.view_slot(view, i, H, dt, last)
+
+    def state(d):
+        st = cache.state()
+        has = not st.empty
+        bufs = cache.buffers()
+
+        def opt(d, i):
+            if not has:
+                return O.fnv_num(d, 0)
+            return O.fnv_array(O.fnv_num(d, 1), slots[i][0], arr(bufs, i))
+
+        if kind == "full":
+            d = opt(opt(d, 0), 1)
+            return O.fnv_num(O.fnv_num(d, st.offset), 0)
+        if quant:
+            for t in range(2):
+                if not has:
+                    d = O.fnv_num(d, 0)
+                    continue
+                d = O.fnv_num(d, 1)
+                for i in range(3):
+                    d = O.fnv_array(d, slots[3 * t + i][0], arr(bufs, 3 * t + i))
+            d = O.fnv_num(d, st.offset)
+            if ring:
+                d = O.fnv_num(O.fnv_num(d, st.idx), st.cached_len)
+            return d
+        if kind == "rot":
+            d = opt(opt(d, 0), 1)
+        elif kind == "tq":
+            for i in range(4):
+                d = opt(d, i)
+            d = O.fnv_num(O.fnv_num(d, 0), 0)
+        else:
+            for i in (0, 1, 4, 5, 2, 3):
+                d = opt(d, i)
+        return O.fnv_num(O.fnv_num(O.fnv_num(d, st.offset), st.idx), st.cached_len)
+
+    d = O.FNV_OFFSET
+    keepalive = []
+    for op, n, at in events:
+        if op == "R":
+            d = state(O.fnv_num(d, 1 if cache.truncate(n) else 0))
+            continue
+        s = n
+        if quant:
+            k = data[at:at + H * s * 64 * 2].view(np.uint16).reshape(1, H, s, 64)
+            v = data[at + H * s * 64 * 2:at + H * s * 192 * 2].view(np.uint16).reshape(1, H, s, 128)
+            dk, dv = T.DeviceArray.of(k), T.DeviceArray.of(v)
+            view = cache.append(dk.ptr, dv.ptr, s)
+            keepalive = [dk, dv]
+            for t in range(2):
+                d = O.fnv_num(d, 1)
+                for i in range(3):
+                    d = O.fnv_array(d, slots[3 * t + i][0], arr(view, 3 * t + i))
+        else:
+            devs, p = [], at
+            for code, dt, last in slots:
+                nb = H * s * last * np.dtype(dt).itemsize
+                devs.append(T.DeviceArray.of(data[p:p + nb].view(dt).reshape(1, H, s, last)))
+                p += nb
+            view = cache.update([a.ptr for a in devs], s)
+            keepalive = devs
+            for i in range(len(slots)):
+                d = O.fnv_array(d, slots[i][0], arr(view, i))
+        d = state(d)
+    del keepalive
+    cache.close()
+    return d
+
+
+@pytest.mark.parametrize("kind,plan,prealloc,want", RECORDED)
+def test_device_cache_reproduces_reference_recording(T, kind, plan, prealloc, want):
+    print(f"[cache-golden] {kind}/{plan} prealloc={prealloc}", flush=True)
+    got = replay(T, kind, plan, prealloc)
+    assert got == want, f"{got:#x} != {want:#x}"
+
+
+def test_rewind_refusals(T):
+    # A ring that has wrapped refuses any rewind (ring_truncate's
+    # `offset > max_size` arm), but one exactly full does not.
+    c = T.Cache(T.CACHE_BF16, 1, 2, 16, 16, max_size=8, keep=0)
+    x = T.DeviceArray.of(kv_bf16((1, 2, 1, 16), 1))
+    for _ in range(8):
+        c.update([x.ptr, x.ptr], 1)
+    assert c.truncate(6) and c.state().offset == 6 and c.state().idx == 6
+    for _ in range(3):
+        c.update([x.ptr, x.ptr], 1)  # offset 9 > 8: wrapped
+    st = c.state()
+    assert (st.offset, st.cached_len) == (9, 8)
+    assert not c.truncate(8) and c.truncate(9) and not c.truncate(10)
+    # An affine growing cache on the legacy path refuses real rewinds.
+    q = T.Cache(T.CACHE_AFFINE, 1, 2, 64, 64, 64, 4, 4, prealloc=False)
+    y = T.DeviceArray.of(kv_bf16((1, 2, 3, 64), 2))
+    q.append(y.ptr, y.ptr, 3)
+    assert not q.truncate(2) and q.truncate(3) and not q.truncate(4)
+    p = T.Cache(T.CACHE_AFFINE, 1, 2, 64, 64, 64, 4, 4, prealloc=True)
+    p.append(y.ptr, y.ptr, 3)
+    assert p.truncate(2) and p.state().offset == 2
+
+
+def check_close(got_bf16, want_f32):
+    got = O.bf16_to_f32(got_bf16).astype(np.float64)
+    raw = np.abs(got - want_f32)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want_f32), 2.0 ** -126))) - 7)
+    err = np.maximum(raw - 0.5 * ulp, 0.0)
+    print(f"[cache-decode] max_abs={raw.max():.3e} mean_abs={raw.mean():.3e}", flush=True)
+    assert err.max() <= MAX_ABS and raw.mean() <= MEAN_ABS
+
+
+def decode(T, cache, q, H_, scale):
+    dq = T.DeviceArray.of(q)
+    out = T.DeviceArray(q.shape, np.uint16)
+    cache.decode_attend(dq.ptr, H_, scale, out.ptr)
+    T.hip().sync()
+    return out.numpy()
+
+
+@pytest.mark.parametrize("bk,bv", [(4, 4), (8, 4), (3, 3)])
+def test_decode_over_growing_cache(T, bk, bv):
+    # Appends in uneven chunks then single tokens (crossing the 256-token
+    # steps), decodes over the fetched view.
+    B, Hq, Hkv, D = 2, 8, 2, 128 if bk != 3 or bv != 3 else 256
+    c = T.Cache(T.CACHE_AFFINE, B, Hkv, D, D, 64, bk, bv, prealloc=True)
+    ks, vs = [], []
+    for i, s in enumerate([300, 1, 1, 211, 1]):
+        k = kv_bf16((B, Hkv, s, D), 10 + i, frac=0.02, mult=8.0)
+        v = kv_bf16((B, Hkv, s, D), 20 + i, frac=0.02, mult=8.0)
+        dk, dv = T.DeviceArray.of(k), T.DeviceArray.of(v)
+        c.append(dk.ptr, dv.ptr, s)
+        ks.append(k)
+        vs.append(v)
+    K, V = np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
+    assert c.state().offset == K.shape[2] and c.state().view == K.shape[2]
+    q = kv_bf16((B, Hq, 1, D), 99)
+    got = decode(T, c, q, Hq, D ** -0.5)
+    want, _, _ = O.attend_affine(q, O.affine_quantize(K, 64, bk), O.affine_quantize(V, 64, bv),
+                                 64, bk, bv, D ** -0.5)
+    check_close(got, want)
+
+
+def test_decode_over_rotating_cache(T):
+    # A 4-bit window of 96 tokens with 4 sinks: after the ring wraps, decode
+    # sees exactly the sinks plus the newest 92 tokens (in ring order).
+    B, Hq, Hkv, D, W, KEEP = 1, 8, 2, 128, 96, 4
+    c = T.Cache(T.CACHE_AFFINE, B, Hkv, D, D, 64, 4, 4, prealloc=True, max_size=W, keep=KEEP)
+    k_all = kv_bf16((B, Hkv, 200, D), 31, frac=0.02, mult=8.0)
+    v_all = kv_bf16((B, Hkv, 200, D), 32, frac=0.02, mult=8.0)
+    q = kv_bf16((B, Hq, 1, D), 33)
+    pos = 0
+    for s in [40] + [1] * 160:
+        dk = T.DeviceArray.of(np.ascontiguousarray(k_all[:, :, pos:pos + s]))
+        dv = T.DeviceArray.of(np.ascontiguousarray(v_all[:, :, pos:pos + s]))
+        c.append(dk.ptr, dv.ptr, s)
+        pos += s
+        if pos in (40, 95, 96, 97, 150, 200):
+            held = list(range(pos)) if pos <= W else list(range(KEEP)) + list(range(pos - (W - KEEP), pos))
+            K = np.ascontiguousarray(k_all[:, :, held])
+            V = np.ascontiguousarray(v_all[:, :, held])
+            got = decode(T, c, q, Hq, D ** -0.5)
+            want, _, _ = O.attend_affine(q, O.affine_quantize(K, 64, 4), O.affine_quantize(V, 64, 4),
+                                         64, 4, 4, D ** -0.5)
+            print(f"[ring] pos={pos} held={len(held)} view={c.state().view}", flush=True)
+            assert c.state().view == len(held)
+            check_close(got, want)
+
+
+def test_decode_over_shared_prefix(T):
+    # Config-4 layout (K 8-bit / V 4-bit): every sequence prefilled with the
+    # same prefix then its own suffix; keep_suffix_from drops the prefix and a
+    # batch-1 prefix cache serves every row.
+    B, Hq, Hkv, D, P, S = 3, 16, 4, 128, 700, 90
+    pre_k = kv_bf16((1, Hkv, P, D), 41)
+    pre_v = kv_bf16((1, Hkv, P, D), 42)
+    suf_k = kv_bf16((B, Hkv, S, D), 43)
+    suf_v = kv_bf16((B, Hkv, S, D), 44)
+    prefix = T.Cache(T.CACHE_AFFINE, 1, Hkv, D, D, 64, 8, 4)
+    a, b = T.DeviceArray.of(pre_k), T.DeviceArray.of(pre_v)
+    prefix.append(a.ptr, b.ptr, P)
+    seqs = T.Cache(T.CACHE_AFFINE, B, Hkv, D, D, 64, 8, 4)
+    full_k = np.concatenate([np.broadcast_to(pre_k, (B, Hkv, P, D)), suf_k], axis=2)
+    full_v = np.concatenate([np.broadcast_to(pre_v, (B, Hkv, P, D)), suf_v], axis=2)
+    fk, fv = T.DeviceArray.of(np.ascontiguousarray(full_k)), T.DeviceArray.of(np.ascontiguousarray(full_v))
+    seqs.append(fk.ptr, fv.ptr, P + S)
+    seqs.keep_suffix_from(P)
+    st = seqs.state()
+    assert (st.offset, st.base_offset, st.cached_len) == (P + S, P, S)
+    seqs.attach_prefix(prefix)
+    q = kv_bf16((B, Hq, 1, D), 45)
+    got = decode(T, seqs, q, Hq, 0.1)
+    want, _, _ = O.attend_affine(q, O.affine_quantize(full_k, 64, 8), O.affine_quantize(full_v, 64, 4),
+                                 64, 8, 4, 0.1)
+    check_close(got, want)
+    # One more token per sequence lands in the suffix.
+    nk, nv = kv_bf16((B, Hkv, 1, D), 46), kv_bf16((B, Hkv, 1, D), 47)
+    dk, dv = T.DeviceArray.of(nk), T.DeviceArray.of(nv)
+    seqs.append(dk.ptr, dv.ptr, 1)
+    got = decode(T, seqs, q, Hq, 0.1)
+    full_k = np.concatenate([full_k, nk], axis=2)
+    full_v = np.concatenate([full_v, nv], axis=2)
+    want, _, _ = O.attend_affine(q, O.affine_quantize(full_k, 64, 8), O.affine_quantize(full_v, 64, 4),
+                                 64, 8, 4, 0.1)
+    check_close(got, want)
+    seqs.attach_prefix(None)
+    prefix.close()
