@@ -280,6 +280,125 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* cache, const uint16_t* q, int
                                  size_t workspace_bytes, tqkv_stream stream);
 
 /* ======================================================================
+ * TurboQuant codebook format
+ * ====================================================================== */
+
+/*
+ * LloydMaxCodebook::compute (lumen-core/src/lloyd_max.rs:74-122): the 2^bits
+ * level Lloyd-Max quantizer of N(0,1) after n_iter EM iterations, bit-
+ * identical to the reference. Host memory: boundaries [2^bits + 1] (first
+ * -inf, last +inf), centroids [2^bits]. Host-only (no GPU needed).
+ */
+int32_t tqkv_lloyd_max(uint32_t bits, size_t n_iter, double* boundaries, double* centroids);
+/*
+ * RotationMatrix::random (rotation.rs:35-89): a Haar orthogonal [dim, dim]
+ * f32 matrix, row-major, by modified Gram-Schmidt with Mezzadri's sign fix,
+ * from this library's seeded N(0,1) stream (SplitMix64 + Box-Muller; the
+ * reference's rand/ChaCha12 stream is not reproduced: pass the reference's R
+ * where its exact values matter). Host-only.
+ */
+int32_t tqkv_rotation_matrix(int32_t dim, uint64_t seed, float* out);
+/* QJLProjector::new (qjl.rs:40-55): [m, dim] entries N(0,1)/sqrt(m), same
+ * stream. Host-only. */
+int32_t tqkv_qjl_matrix(int32_t dim, int32_t m, uint64_t seed, float* out);
+
+/*
+ * TurboQuantCompressor::compress (compressor.rs:61-116) on the device,
+ * bit-exact given the same R, codebook and Phi: y = R x (sequential f32),
+ * sigma = sqrt(sum y^2 / dim), codes = codebook level of y * (1/sigma)
+ * (f64 decisions; all zero when sigma < 1e-10), and with qjl_m > 0 the
+ * residual against R^T(centroid * sigma), its norm and the QJL sign bits
+ * (bit r of a vector = (Phi_r . residual >= 0), LSB-first in u32 words).
+ * x: [n_slabs, s, dim] f32 (x_is_bf16 = 0) or bf16; row j of slab i writes
+ * row (i * dst_cap + dst_start + j) of codes u8 [., dim], sigma f32 [.],
+ * signs u32 [., ceil(qjl_m / 32)], rnorm f32 [.] (device). rotation f32
+ * [dim, dim] row-major, boundaries f64 [2^bits + 1], centroids_f32 [2^bits]
+ * (the f64 centroids rounded), qjl f32 [qjl_m, dim] (device).
+ * dim in {64, 128, 256, 512}.
+ */
+int32_t tqkv_tq_encode(const void* x, int32_t x_is_bf16, int64_t n_slabs, int64_t s,
+                       int32_t dim, const float* rotation, const double* boundaries,
+                       const float* centroids_f32, int32_t bits, const float* qjl, int32_t qjl_m,
+                       uint8_t* codes, float* sigma, uint32_t* signs, float* rnorm,
+                       int64_t dst_cap, int64_t dst_start, tqkv_stream stream);
+/* rq = R q (RotationMatrix::apply, rotation.rs:91-99), f32 [dim], device. */
+int32_t tqkv_tq_rotate_query(const float* rotation, const float* q, int32_t dim, float* rq,
+                             tqkv_stream stream);
+/* estimate_inner_products_stage1 (compressor.rs:165-184) for n stored keys:
+ * scores[t] = (sum_i rq_i * centroid[c_ti]) * sigma_t, bit-exact. Device. */
+int32_t tqkv_tq_scores(const float* rq, const uint8_t* codes, const float* sigma,
+                       const float* centroids_f32, int32_t dim, int64_t n, float* scores,
+                       tqkv_stream stream);
+/* SimpleCache::attend_values (simple.rs:40-62, 105-118): out = sum_t w_t *
+ * R^T(centroid[c_t] * sigma_t), tokens with |w_t| < 1e-10 skipped, in the
+ * reference's accumulation order. Device. */
+int32_t tqkv_tq_values(const float* rotation, const uint8_t* codes, const float* sigma,
+                       const float* centroids_f32, const float* weights, int32_t dim, int64_t n,
+                       float* out, tqkv_stream stream);
+/* rotate_last_axis (turboquant.rs:258-267): y = x R (transpose = 0) or
+ * y = x R^T (transpose = 1), bf16 rows [rows, dim] in and out, f32
+ * accumulation. The affine+rotation cache mode (gemma4_moe.rs:4154-4173)
+ * rotates keys and queries with it. Device. */
+int32_t tqkv_rotate_bf16(const uint16_t* x, int64_t rows, int32_t dim, const float* rotation,
+                         int32_t transpose, uint16_t* y, tqkv_stream stream);
+
+/* ======================================================================
+ * turboquant_cache::KVCache (traits.rs:9-36) as SimpleCache implements it
+ * ====================================================================== */
+
+/* TurboQuantConfig (lumen-core/src/config.rs:5-28); lloyd_max_iter 0 = 1000. */
+typedef struct tqkv_tq_config {
+  int32_t head_dim;
+  int32_t bits;
+  int32_t qjl_m;
+  int32_t lloyd_max_iter;
+  uint64_t seed;
+} tqkv_tq_config;
+
+typedef struct tqkv_kvcache tqkv_kvcache;
+
+/*
+ * SimpleCache::new(Arc<TurboQuantCompressor>, n_layers, n_kv_heads,
+ * head_dim) (simple.rs:23-37) with TurboQuantCompressor::new(config)
+ * (compressor.rs:20-32), or ::from_files (:35-58) when `rotation` (host
+ * [head_dim, head_dim] row-major) and `qjl` (host [qjl_m, head_dim]) are
+ * given; NULL draws them from the seed (R at seed, Phi at seed + 1).
+ * head_dim in {64, 128, 256, 512}. Compressed vectors live on the device.
+ */
+int32_t tqkv_kvcache_create(const tqkv_tq_config* cfg, const float* rotation, const float* qjl,
+                            int32_t n_layers, int32_t n_kv_heads, tqkv_kvcache** out);
+int32_t tqkv_kvcache_destroy(tqkv_kvcache* cache);
+/* KVCache::store: keys and values host f32 [n_tokens, head_dim], both
+ * compressed (two-stage) and appended. Synchronous. Out-of-range layer or
+ * head (a panic in the reference) is TQKV_EINVAL_ARG. */
+int32_t tqkv_kvcache_store(tqkv_kvcache* cache, int32_t layer, int32_t head, const float* keys,
+                           const float* values, int64_t n_tokens);
+/* KVCache::attend_keys: stage-1 scores (host f32 [seq_len]) for a host f32
+ * query [head_dim], bit-exact with the reference. */
+int32_t tqkv_kvcache_attend_keys(tqkv_kvcache* cache, int32_t layer, int32_t head,
+                                 const float* query, float* scores);
+/* KVCache::attend_values: host weights [seq_len] -> host out [head_dim],
+ * bit-exact with the reference. */
+int32_t tqkv_kvcache_attend_values(tqkv_kvcache* cache, int32_t layer, int32_t head,
+                                   const float* weights, float* out);
+/* KVCache::seq_len (-1 for an out-of-range layer or head). */
+int64_t tqkv_kvcache_seq_len(const tqkv_kvcache* cache, int32_t layer, int32_t head);
+/* KVCache::clear. */
+int32_t tqkv_kvcache_clear(tqkv_kvcache* cache);
+/* KVCache::truncate: keep the first n_keep tokens of every head of a layer
+ * (no-op where fewer are held). */
+int32_t tqkv_kvcache_truncate(tqkv_kvcache* cache, int32_t layer, int64_t n_keep);
+/* SimpleCache::memory_bytes (CompressedVector::size_bytes, config.rs:50-55). */
+int64_t tqkv_kvcache_memory_bytes(const tqkv_kvcache* cache);
+/* The stored CompressedVector fields of vectors [first, first + n) of a
+ * (layer, head) (which_values = 0 keys, 1 values), to host: codes u8 [n,
+ * head_dim], scale [n], QJL sign words u32 [n, ceil(qjl_m / 32)] and
+ * residual norms [n] (any pointer may be NULL). */
+int32_t tqkv_kvcache_read(tqkv_kvcache* cache, int32_t layer, int32_t head,
+                          int32_t which_values, int64_t first, int64_t n, uint8_t* codes,
+                          float* scale, uint32_t* signs, float* residual_norm);
+
+/* ======================================================================
  * Benchmark utilities (no counterpart in the reference)
  * ====================================================================== */
 

@@ -1,0 +1,289 @@
+// TurboQuant codebook format on the device: encode (rotate, normalize,
+// Lloyd-Max codes, QJL residual signs), the SimpleCache estimators, rotation,
+// and fused decode attention over codebook caches.
+//
+// The encode and the estimators are bit-exact restatements of lumen-core's
+// CPU path, so codes, scales, signs and scores equal the reference's given
+// the same R and Phi: every sum runs sequentially from the index the Rust
+// iterates first, products and sums round separately (__fmul_rn / __fadd_rn;
+// the file is also built with -ffp-contract=off), division and square root
+// are correctly rounded, and codebook decisions compare in f64:
+//   compress_one            compressor.rs:61-107  (tq_encode_kernel)
+//   RotationMatrix::apply   rotation.rs:91-99
+//   apply_inverse           rotation.rs:102-113
+//   quantize (linear scan)  lloyd_max.rs:132-144
+//   project_and_pack        qjl.rs:57-74
+//   estimate_..._stage1     compressor.rs:165-184 (tq_scores_kernel)
+//   accumulate_weighted_value / attend_values  simple.rs:40-62, 105-118
+// Rust's f32 `Sum` folds from -0.0, explicit accumulators from +0.0; the
+// kernels start each sum the way the corresponding Rust line does.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace tqkv {
+namespace tq {
+namespace {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float mul(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add(float a, float b) { return __fadd_rn(a, b); }
+// Correctly rounded quotient and square root. (HIP's __fsqrt_rn is the
+// hardware approximation unless OCML_BASIC_ROUNDED_OPERATIONS is set; the
+// plain operator and __builtin_sqrtf are correctly rounded under HIP's
+// default -fhip-fp32-correctly-rounded-divide-sqrt.)
+__device__ __forceinline__ float div_rn(float a, float b) { return a / b; }
+__device__ __forceinline__ float sqrt_rn(float a) { return __builtin_sqrtf(a); }
+
+// Index of the codebook level of x: the first i in 1..n-1 with x < b[i],
+// minus one, or n - 1 if none (lloyd_max.rs:132-144). Binary search over the
+// increasing boundaries gives the linear scan's answer, NaN included.
+__device__ __forceinline__ uint32_t level_of(double x, const double* __restrict__ b, int n) {
+  int lo = 1, hi = n;  // answer index in [lo, hi]; hi = n means "none"
+  while (lo < hi) {
+    const int mid = (lo + hi) / 2;
+    if (x < b[mid]) hi = mid;
+    else lo = mid + 1;
+  }
+  return uint32_t(lo - 1);
+}
+
+// One wavefront per row. x: f32 or bf16 rows [n_slabs, s, D]; row j of slab
+// i goes to row (i * dst_cap + dst_start + j) of the outputs.
+template <int D>
+__global__ __launch_bounds__(kWave) void tq_encode_kernel(
+    const void* __restrict__ xv, int x_bf16, int64_t s, const float* __restrict__ R,
+    const double* __restrict__ bnd, const float* __restrict__ cent_f32, int n_levels,
+    const float* __restrict__ phi, int m, uint8_t* __restrict__ codes, float* __restrict__ sigma,
+    uint32_t* __restrict__ signs, float* __restrict__ rnorm, int64_t dst_cap, int64_t dst_start) {
+  constexpr int PER = D / kWave;
+  __shared__ float xs[D], ys[D], rs[D];
+  __shared__ float s_scale, s_rn;
+  __shared__ uint8_t cs[D];
+  const int lane = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const int64_t dst = (r / s) * dst_cap + dst_start + (r % s);
+  for (int i = lane; i < D; i += kWave)
+    xs[i] = x_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(xv)[r * D + i])
+                   : static_cast<const float*>(xv)[r * D + i];
+  __syncthreads();
+  // y = R x, each y[i] a sequential sum over j from -0.0.
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = lane + k * kWave;
+    const float* row = R + int64_t(i) * D;
+    float acc = -0.0f;
+    for (int j = 0; j < D; ++j) acc = add(acc, mul(row[j], xs[j]));
+    ys[i] = acc;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float ss = -0.0f;
+    for (int i = 0; i < D; ++i) ss = add(ss, mul(ys[i], ys[i]));
+    s_scale = sqrt_rn(div_rn(ss, float(D)));
+  }
+  __syncthreads();
+  const float scale = s_scale;
+  const bool degenerate = scale < 1e-10f;
+  const float inv = degenerate ? 0.0f : div_rn(1.0f, scale);
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = lane + k * kWave;
+    const uint8_t c = degenerate ? uint8_t(0) : uint8_t(level_of(double(mul(ys[i], inv)), bnd, n_levels));
+    cs[i] = c;
+    codes[dst * D + i] = c;
+  }
+  if (lane == 0) sigma[dst] = scale;
+  if (m <= 0) return;
+  __syncthreads();
+  // Residual against the stage-1 reconstruction R^T (centroid * scale),
+  // accumulated row by row from +0.0 as apply_inverse does.
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = lane + k * kWave;
+    float acc = 0.0f;
+    for (int j = 0; j < D; ++j) acc = add(acc, mul(R[int64_t(j) * D + i], mul(cent_f32[cs[j]], scale)));
+    rs[i] = __fsub_rn(xs[i], acc);
+  }
+  __syncthreads();
+  if (lane == 0) {
+    float rn = 0.0f;
+    for (int i = 0; i < D; ++i) rn = add(rn, mul(rs[i], rs[i]));
+    s_rn = sqrt_rn(rn);
+  }
+  __syncthreads();
+  if (lane == 0) rnorm[dst] = s_rn;
+  // QJL signs: bit `row` = (Phi[row] . r >= 0), LSB-first in u32 words.
+  const int words = (m + 31) / 32;
+  for (int base = 0; base < m; base += kWave) {
+    const int row = base + lane;
+    bool bit = false;
+    if (row < m) {
+      const float* p = phi + int64_t(row) * D;
+      float acc = -0.0f;
+      for (int j = 0; j < D; ++j) acc = add(acc, mul(p[j], rs[j]));
+      bit = acc >= 0.0f;
+    }
+    const uint64_t ball = __ballot(bit);
+    if (lane == 0) {
+      const int w0 = base / 32;
+      signs[dst * words + w0] = uint32_t(ball);
+      if (w0 + 1 < words) signs[dst * words + w0 + 1] = uint32_t(ball >> 32);
+    }
+  }
+}
+
+// rq = R q (the rotated query of compressor.rs:170), one wavefront.
+__global__ __launch_bounds__(kWave) void tq_rotate_query_kernel(const float* __restrict__ R,
+                                                                const float* __restrict__ q,
+                                                                int D, float* __restrict__ rq) {
+  for (int i = threadIdx.x; i < D; i += kWave) {
+    float acc = -0.0f;
+    for (int j = 0; j < D; ++j) acc = add(acc, mul(R[int64_t(i) * D + j], q[j]));
+    rq[i] = acc;
+  }
+}
+
+// Stage-1 scores: one thread per token, sum over channels from -0.0, times
+// the token's scale (compressor.rs:165-184).
+__global__ void tq_scores_kernel(const float* __restrict__ rq, const uint8_t* __restrict__ codes,
+                                 const float* __restrict__ sigma,
+                                 const float* __restrict__ cent_f32, int D, int64_t n,
+                                 float* __restrict__ scores) {
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const uint8_t* c = codes + t * D;
+  float acc = -0.0f;
+  for (int i = 0; i < D; ++i) acc = add(acc, mul(rq[i], cent_f32[c[i]]));
+  scores[t] = mul(acc, sigma[t]);
+}
+
+// attend_values: output channel i sums, token by token in order and channel
+// j by channel j, R[j][i] * (centroid * (scale * w)); tokens with |w| < 1e-10
+// are skipped (simple.rs:40-62, 105-118).
+__global__ void tq_values_kernel(const float* __restrict__ R, const uint8_t* __restrict__ codes,
+                                 const float* __restrict__ sigma,
+                                 const float* __restrict__ cent_f32, const float* __restrict__ w,
+                                 int D, int64_t n, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= D) return;
+  float acc = 0.0f;
+  for (int64_t t = 0; t < n; ++t) {
+    const float wt = w[t];
+    if (fabsf(wt) < 1e-10f) continue;
+    const float sc = mul(sigma[t], wt);
+    const uint8_t* c = codes + t * D;
+    for (int j = 0; j < D; ++j) acc = add(acc, mul(R[int64_t(j) * D + i], mul(cent_f32[c[j]], sc)));
+  }
+  out[i] = acc;
+}
+
+// y = x R (x bf16 [rows, D] -> bf16): the GPU path's rotate_last_axis
+// (turboquant.rs:258-267), f32 accumulation. transpose = 1 applies R^T.
+__global__ void tq_rotate_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int D,
+                                      const float* __restrict__ R, int transpose,
+                                      uint16_t* __restrict__ y) {
+  const int64_t r = blockIdx.x;
+  extern __shared__ float xr[];
+  for (int j = threadIdx.x; j < D; j += blockDim.x) xr[j] = bf16_to_f32(x[r * D + j]);
+  __syncthreads();
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < D; ++j)
+      acc = fmaf(xr[j], transpose ? R[int64_t(i) * D + j] : R[int64_t(j) * D + i], acc);
+    y[r * D + i] = f32_to_bf16(acc);
+  }
+}
+
+}  // namespace
+}  // namespace tq
+}  // namespace tqkv
+
+using namespace tqkv;
+using namespace tqkv::tq;
+
+extern "C" int32_t tqkv_tq_encode(const void* x, int32_t x_is_bf16, int64_t n_slabs, int64_t s,
+                                  int32_t dim, const float* rotation, const double* boundaries,
+                                  const float* centroids_f32, int32_t bits, const float* qjl,
+                                  int32_t qjl_m, uint8_t* codes, float* sigma, uint32_t* signs,
+                                  float* rnorm, int64_t dst_cap, int64_t dst_start,
+                                  tqkv_stream stream) {
+  if (bits < 1 || bits > 8) return fail(TQKV_EUNSUPPORTED, "codebook bits=%d", bits);
+  if (!(dim == 64 || dim == 128 || dim == 256 || dim == 512))
+    return fail(TQKV_EUNSUPPORTED, "encode dim=%d not in {64,128,256,512}", dim);
+  if (n_slabs < 0 || s < 0 || dst_start < 0 || dst_start + s > dst_cap)
+    return fail(TQKV_EINVAL_SHAPE, "rows [%lld, %lld) do not fit a buffer of %lld",
+                (long long)dst_start, (long long)(dst_start + s), (long long)dst_cap);
+  if (n_slabs == 0 || s == 0) return ok();
+  if (!x || !rotation || !boundaries || !centroids_f32 || !codes || !sigma)
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (qjl_m < 0 || (qjl_m > 0 && (!qjl || !signs || !rnorm)))
+    return fail(TQKV_EINVAL_ARG, "qjl_m=%d needs the QJL matrix, signs and rnorm", qjl_m);
+  const int64_t rows = n_slabs * s;
+  if (rows > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "too many rows");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int n = 1 << bits;
+#define TQKV_ENC(DIM)                                                                        \
+  case DIM:                                                                                 \
+    hipLaunchKernelGGL(tq_encode_kernel<DIM>, dim3(unsigned(rows)), dim3(kWave), 0, st, x,   \
+                       x_is_bf16, s, rotation, boundaries, centroids_f32, n, qjl, qjl_m,     \
+                       codes, sigma, signs, rnorm, dst_cap, dst_start);                      \
+    break;
+  switch (dim) {
+    TQKV_ENC(64) TQKV_ENC(128) TQKV_ENC(256) TQKV_ENC(512)
+  }
+#undef TQKV_ENC
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_rotate_query(const float* rotation, const float* q, int32_t dim,
+                                        float* rq, tqkv_stream stream) {
+  if (!rotation || !q || !rq) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (dim <= 0) return fail(TQKV_EINVAL_SHAPE, "dim=%d", dim);
+  hipLaunchKernelGGL(tq_rotate_query_kernel, dim3(1), dim3(kWave), 0,
+                     reinterpret_cast<hipStream_t>(stream), rotation, q, dim, rq);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_scores(const float* rq, const uint8_t* codes, const float* sigma,
+                                  const float* centroids_f32, int32_t dim, int64_t n,
+                                  float* scores, tqkv_stream stream) {
+  if (n == 0) return ok();
+  if (!rq || !codes || !sigma || !centroids_f32 || !scores) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (dim <= 0 || n < 0) return fail(TQKV_EINVAL_SHAPE, "dim=%d n=%lld", dim, (long long)n);
+  hipLaunchKernelGGL(tq_scores_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), rq, codes, sigma, centroids_f32, dim,
+                     n, scores);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_values(const float* rotation, const uint8_t* codes, const float* sigma,
+                                  const float* centroids_f32, const float* weights, int32_t dim,
+                                  int64_t n, float* out, tqkv_stream stream) {
+  if (!rotation || !centroids_f32 || !out || (n > 0 && (!codes || !sigma || !weights)))
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (dim <= 0 || n < 0) return fail(TQKV_EINVAL_SHAPE, "dim=%d n=%lld", dim, (long long)n);
+  hipLaunchKernelGGL(tq_values_kernel, dim3(unsigned((dim + 63) / 64)), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), rotation, codes, sigma, centroids_f32,
+                     weights, dim, n, out);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_rotate_bf16(const uint16_t* x, int64_t rows, int32_t dim,
+                                    const float* rotation, int32_t transpose, uint16_t* y,
+                                    tqkv_stream stream) {
+  if (rows == 0) return ok();
+  if (!x || !rotation || !y) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (dim <= 0 || dim > 4096 || rows < 0 || rows > 0x7fffffffLL)
+    return fail(TQKV_EINVAL_SHAPE, "rows=%lld dim=%d", (long long)rows, dim);
+  hipLaunchKernelGGL(tq_rotate_rows_kernel, dim3(unsigned(rows)), dim3(dim < 256 ? dim : 256),
+                     size_t(dim) * sizeof(float), reinterpret_cast<hipStream_t>(stream), x, rows,
+                     dim, rotation, transpose, y);
+  TQKV_LAUNCHED();
+  return ok();
+}

@@ -60,6 +60,11 @@ class CacheState(ctypes.Structure):
 
 CACHE_BF16, CACHE_AFFINE, CACHE_CODEBOOK = 0, 1, 2
 
+
+class TqConfig(ctypes.Structure):
+    _fields_ = [("head_dim", I32), ("bits", I32), ("qjl_m", I32), ("lloyd_max_iter", I32),
+                ("seed", ctypes.c_uint64)]
+
 _lib = None
 _hip = None
 
@@ -74,6 +79,25 @@ _SIGS = {
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
     "tqkv_decode_kernel_name": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32]),
     "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
+    "tqkv_lloyd_max": (I32, [ctypes.c_uint32, SZ, P, P]),
+    "tqkv_rotation_matrix": (I32, [I32, ctypes.c_uint64, P]),
+    "tqkv_qjl_matrix": (I32, [I32, I32, ctypes.c_uint64, P]),
+    "tqkv_tq_encode": (I32, [P, I32, I64, I64, I32, P, P, P, I32, P, I32, P, P, P, P, I64, I64,
+                             P]),
+    "tqkv_tq_rotate_query": (I32, [P, P, I32, P, P]),
+    "tqkv_tq_scores": (I32, [P, P, P, P, I32, I64, P, P]),
+    "tqkv_tq_values": (I32, [P, P, P, P, P, I32, I64, P, P]),
+    "tqkv_rotate_bf16": (I32, [P, I64, I32, P, I32, P, P]),
+    "tqkv_kvcache_create": (I32, [ctypes.POINTER(TqConfig), P, P, I32, I32, ctypes.POINTER(P)]),
+    "tqkv_kvcache_destroy": (I32, [P]),
+    "tqkv_kvcache_store": (I32, [P, I32, I32, P, P, I64]),
+    "tqkv_kvcache_attend_keys": (I32, [P, I32, I32, P, P]),
+    "tqkv_kvcache_attend_values": (I32, [P, I32, I32, P, P]),
+    "tqkv_kvcache_seq_len": (I64, [P, I32, I32]),
+    "tqkv_kvcache_clear": (I32, [P]),
+    "tqkv_kvcache_truncate": (I32, [P, I32, I64]),
+    "tqkv_kvcache_memory_bytes": (I64, [P]),
+    "tqkv_kvcache_read": (I32, [P, I32, I32, I32, I64, I64, P, P, P, P]),
     "tqkv_cache_create": (I32, [ctypes.POINTER(CacheConfig), ctypes.POINTER(P)]),
     "tqkv_cache_destroy": (I32, [P]),
     "tqkv_cache_update": (I32, [P, ctypes.POINTER(P), I64, ctypes.POINTER(CacheView), P]),
@@ -395,3 +419,111 @@ def view_slot(view, i, n_slabs, dtype, last):
         return np.zeros((n_slabs, 0, last), dtype)
     full = hip().download(view.slot[i], (n_slabs, view.cap, last), dtype)
     return np.ascontiguousarray(full[:, :view.n])
+
+
+# ---------------------------------------------------------------- TurboQuant codebook
+def _np_ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def lloyd_max(bits, n_iter=1000):
+    """Host-only: (boundaries f64 [2^bits + 1], centroids f64 [2^bits])."""
+    n = 1 << bits
+    b = np.empty(n + 1, np.float64)
+    c = np.empty(n, np.float64)
+    check(lib().tqkv_lloyd_max(bits, n_iter, _np_ptr(b), _np_ptr(c)))
+    return b, c
+
+
+def rotation_matrix(dim, seed):
+    out = np.empty((dim, dim), np.float32)
+    check(lib().tqkv_rotation_matrix(dim, seed, _np_ptr(out)))
+    return out
+
+
+def qjl_matrix(dim, m, seed):
+    out = np.empty((m, dim), np.float32)
+    check(lib().tqkv_qjl_matrix(dim, m, seed, _np_ptr(out)))
+    return out
+
+
+def tq_encode(x, x_is_bf16, n_slabs, s, dim, R, bnd, cent, bits, phi, m, codes, sigma, signs,
+              rnorm, dst_cap=None, dst_start=0, stream=None):
+    """All pointers device."""
+    check(lib().tqkv_tq_encode(x, int(x_is_bf16), n_slabs, s, dim, R, bnd, cent, bits, phi, m,
+                               codes, sigma, signs, rnorm, s if dst_cap is None else dst_cap,
+                               dst_start, stream))
+
+
+def rotate_bf16(x, rows, dim, R, transpose, y, stream=None):
+    check(lib().tqkv_rotate_bf16(x, rows, dim, R, int(transpose), y, stream))
+
+
+class KVCache:
+    """turboquant_cache::KVCache (SimpleCache semantics) on the device."""
+
+    def __init__(self, head_dim, bits=3, qjl_m=64, seed=42, n_layers=1, n_kv_heads=1,
+                 rotation=None, qjl=None, lloyd_max_iter=1000):
+        self.cfg = TqConfig(head_dim, bits, qjl_m, lloyd_max_iter, seed)
+        self.D = head_dim
+        self.m = qjl_m
+        self._r = None if rotation is None else np.ascontiguousarray(rotation, np.float32)
+        self._q = None if qjl is None else np.ascontiguousarray(qjl, np.float32)
+        h = P()
+        check(lib().tqkv_kvcache_create(ctypes.byref(self.cfg),
+                                        None if self._r is None else _np_ptr(self._r),
+                                        None if self._q is None else _np_ptr(self._q),
+                                        n_layers, n_kv_heads, ctypes.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().tqkv_kvcache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def store(self, layer, head, keys, values):
+        k = np.ascontiguousarray(keys, np.float32).reshape(-1, self.D)
+        v = np.ascontiguousarray(values, np.float32).reshape(-1, self.D)
+        check(lib().tqkv_kvcache_store(self.h, layer, head, _np_ptr(k), _np_ptr(v), k.shape[0]))
+
+    def seq_len(self, layer, head):
+        return lib().tqkv_kvcache_seq_len(self.h, layer, head)
+
+    def attend_keys(self, layer, head, query):
+        q = np.ascontiguousarray(query, np.float32)
+        out = np.empty(self.seq_len(layer, head), np.float32)
+        check(lib().tqkv_kvcache_attend_keys(self.h, layer, head, _np_ptr(q), _np_ptr(out)))
+        return out
+
+    def attend_values(self, layer, head, weights):
+        w = np.ascontiguousarray(weights, np.float32)
+        out = np.empty(self.D, np.float32)
+        check(lib().tqkv_kvcache_attend_values(self.h, layer, head, _np_ptr(w), _np_ptr(out)))
+        return out
+
+    def clear(self):
+        check(lib().tqkv_kvcache_clear(self.h))
+
+    def truncate(self, layer, n_keep):
+        check(lib().tqkv_kvcache_truncate(self.h, layer, n_keep))
+
+    def memory_bytes(self):
+        return lib().tqkv_kvcache_memory_bytes(self.h)
+
+    def read(self, layer, head, values=False, first=0, n=None):
+        if n is None:
+            n = self.seq_len(layer, head) - first
+        W = (self.m + 31) // 32
+        codes = np.empty((n, self.D), np.uint8)
+        scale = np.empty(n, np.float32)
+        signs = np.empty((n, max(W, 1)), np.uint32)
+        rn = np.empty(n, np.float32)
+        check(lib().tqkv_kvcache_read(self.h, layer, head, int(values), first, n, _np_ptr(codes),
+                                      _np_ptr(scale), _np_ptr(signs), _np_ptr(rn)))
+        return codes, scale, signs[:, :W], rn

@@ -115,6 +115,14 @@ def fnv_array(h, dtype_code, arr):
     return lib().oracle_fnv_array(h, dtype_code, hh, s, last, ptr(a))
 
 
+def pack_codes(codes, bits):
+    """bitpack::pack_codes (bitpack.rs:17-33): u8 codes -> u64 words."""
+    c = np.ascontiguousarray(codes, np.uint8)
+    out = np.zeros(lib().oracle_packed_words(c.size, bits), np.uint64)
+    lib().oracle_pack_codes(ptr(c), c.size, bits, ptr(out))
+    return out
+
+
 def codebook(bits, n_iter=1000):
     n = 1 << bits
     b = np.empty(n + 1, np.float64)

@@ -1,0 +1,162 @@
+"""TurboQuant codebook format on the GPU, through the C ABI, against the
+oracle's restatement of lumen-core (compressor.rs, simple.rs):
+
+- tqkv_tq_encode is bit-exact with compress_one given the same R and Phi:
+  codes, scale, residual norm and QJL sign words, f32 and bf16 inputs,
+  outlier channels, an all-zero vector (the sigma < 1e-10 branch);
+- the KVCache API (tqkv_kvcache_*) stores, scores and accumulates values
+  bit-exactly as SimpleCache does, keeps seq_len / truncate / clear /
+  memory_bytes semantics, and meets the reference's own SimpleCache bars
+  (value cosine > 0.95, compression > 2x; simple.rs:151-310).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from inputs import kv_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def T():
+    import tqkv
+    assert tqkv.hip().device_count() > 0, "no GPU visible"
+    return tqkv
+
+
+def tables(T, dim, bits, m, seed=42):
+    R = T.rotation_matrix(dim, seed)
+    phi = T.qjl_matrix(dim, max(m, 1), seed + 1)
+    b, c = T.lloyd_max(bits)
+    return R, phi, b, c
+
+
+def inputs_f32(n, dim, seed):
+    x = np.random.default_rng(seed).standard_normal((n, dim)).astype(np.float32)
+    x[:, np.random.default_rng(seed + 1).permutation(dim)[:max(1, dim // 50)]] *= 8.0
+    x[n // 2] = 0.0  # degenerate vector: all codes 0, scale 0
+    return x
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("m", [0, 64, 100])
+@pytest.mark.parametrize("bf16_in", [False, True])
+def test_encode_bit_exact(T, dim, bits, m, bf16_in):
+    print(f"[tq-encode] dim={dim} bits={bits} m={m} bf16={bf16_in}", flush=True)
+    n = 37
+    R, phi, b, c = tables(T, dim, bits, m)
+    x = inputs_f32(n, dim, dim + bits + m)
+    if bf16_in:
+        xb = O.bf16_from_f32(x)
+        x = O.bf16_to_f32(xb)
+        dx = T.DeviceArray.of(xb)
+    else:
+        dx = T.DeviceArray.of(x)
+    W = (m + 31) // 32
+    dR, dphi = T.DeviceArray.of(R), T.DeviceArray.of(phi)
+    db, dc = T.DeviceArray.of(b), T.DeviceArray.of(c.astype(np.float32))
+    codes = T.DeviceArray((n, dim), np.uint8)
+    sigma = T.DeviceArray((n,), np.float32)
+    signs = T.DeviceArray((n, max(W, 1)), np.uint32, np.zeros((n, max(W, 1)), np.uint32))
+    rnorm = T.DeviceArray((n,), np.float32, np.zeros(n, np.float32))
+    T.tq_encode(dx.ptr, bf16_in, 1, n, dim, dR.ptr, db.ptr, dc.ptr, bits, dphi.ptr, m,
+                codes.ptr, sigma.ptr, signs.ptr, rnorm.ptr)
+    T.hip().sync()
+    comp = O.Compressor(dim, bits, max(m, 1), R, phi[:max(m, 1)])
+    s1, s2, rn, sc = comp.compress(x)
+    got_codes = codes.numpy()
+    packed = np.stack([O.pack_codes(got_codes[i], bits) for i in range(n)])
+    assert np.array_equal(packed, s1), "codes"
+    assert np.array_equal(sigma.numpy().view(np.uint32), sc.view(np.uint32)), "scale"
+    assert np.all(got_codes[n // 2] == 0) and sigma.numpy()[n // 2] == 0.0
+    if m > 0:
+        assert np.array_equal(rnorm.numpy().view(np.uint32), rn.view(np.uint32)), "residual norm"
+        words = signs.numpy()[:, :W]
+        want = s2.view(np.uint32).reshape(n, -1)[:, :W]
+        assert np.array_equal(words, want), "QJL signs"
+
+
+def test_encode_writes_into_cache_rows(T):
+    dim, bits, m = 128, 4, 64
+    R, phi, b, c = tables(T, dim, bits, m)
+    x = inputs_f32(2 * 5, dim, 7).reshape(2, 5, dim)
+    dx = T.DeviceArray.of(x)
+    dR, dphi, db, dc = (T.DeviceArray.of(a) for a in (R, phi, b, c.astype(np.float32)))
+    cap = 12
+    codes = T.DeviceArray((2, cap, dim), np.uint8, np.full((2, cap, dim), 0xAB, np.uint8))
+    sigma = T.DeviceArray((2, cap), np.float32, np.full((2, cap), -1.0, np.float32))
+    signs = T.DeviceArray((2, cap, 2), np.uint32)
+    rnorm = T.DeviceArray((2, cap), np.float32)
+    T.tq_encode(dx.ptr, False, 2, 5, dim, dR.ptr, db.ptr, dc.ptr, bits, dphi.ptr, m, codes.ptr,
+                sigma.ptr, signs.ptr, rnorm.ptr, cap, 6)
+    T.hip().sync()
+    comp = O.Compressor(dim, bits, m, R, phi)
+    s1, _, _, sc = comp.compress(x.reshape(-1, dim))
+    got = codes.numpy()
+    for i in range(2):
+        for j in range(5):
+            assert np.array_equal(O.pack_codes(got[i, 6 + j], bits), s1[i * 5 + j])
+    assert np.all(got[:, :6] == 0xAB) and np.all(got[:, 11:] == 0xAB)
+    assert np.all(sigma.numpy()[:, :6] == -1.0)
+
+
+def test_kvcache_matches_simple_cache(T):
+    dim, bits, m, layers, heads = 128, 3, 64, 2, 2
+    kv = T.KVCache(dim, bits, m, 42, layers, heads)
+    R, phi, _, _ = tables(T, dim, bits, m)
+    comp = O.Compressor(dim, bits, m, R, phi)
+    rng = np.random.default_rng(5)
+    K = rng.standard_normal((40, dim)).astype(np.float32)
+    V = rng.standard_normal((40, dim)).astype(np.float32)
+    kv.store(1, 0, K[:25], V[:25])
+    kv.store(1, 0, K[25:], V[25:])  # appends, like two store() calls
+    assert kv.seq_len(1, 0) == 40 and kv.seq_len(0, 0) == 0 and kv.seq_len(1, 1) == 0
+    ck, cv = comp.compress(K), comp.compress(V)
+    codes, scale, signs, rn = kv.read(1, 0)
+    assert np.array_equal(np.stack([O.pack_codes(r, bits) for r in codes]), ck[0])
+    assert np.array_equal(scale.view(np.uint32), ck[3].view(np.uint32))
+    q = rng.standard_normal(dim).astype(np.float32)
+    s = kv.attend_keys(1, 0, q)
+    assert np.array_equal(s.view(np.uint32), comp.scores(q, ck).view(np.uint32))
+    w = np.exp(s - s.max())
+    w /= w.sum()
+    w[3] = 1e-12  # below the skip threshold
+    out = kv.attend_values(1, 0, w)
+    assert np.array_equal(out.view(np.uint32), comp.attend_values(w, cv).view(np.uint32))
+    # SimpleCache bars: value reconstruction cosine > 0.95 (simple.rs:220),
+    # compression over f32 > 2x (:250).
+    one = np.zeros(40, np.float32)
+    one[7] = 1.0
+    rec = kv.attend_values(1, 0, one)
+    cos = rec @ V[7] / (np.linalg.norm(rec) * np.linalg.norm(V[7]))
+    assert cos > 0.95
+    assert 2 * 40 * dim * 4 / kv.memory_bytes() > 2.0
+    # truncate keeps the first n_keep of every head of the layer; clear empties.
+    kv.store(1, 1, K[:10], V[:10])
+    kv.truncate(1, 12)
+    assert (kv.seq_len(1, 0), kv.seq_len(1, 1)) == (12, 10)
+    assert np.array_equal(kv.attend_keys(1, 0, q).view(np.uint32), s[:12].view(np.uint32))
+    kv.clear()
+    assert kv.seq_len(1, 0) == 0 and kv.memory_bytes() == 0
+    with pytest.raises(T.TqkvError) as e:
+        kv.store(2, 0, K[:1], V[:1])
+    assert e.value.status == T.EINVAL_ARG
+
+
+def test_kvcache_from_given_tables(T):
+    # from_files: an external R (here the oracle's own seed-7 matrix) is
+    # used as given.
+    dim, bits, m = 64, 4, 32
+    R = O.rotation(dim, 7)
+    phi = O.qjl_matrix(dim, m, 8)
+    kv = T.KVCache(dim, bits, m, 0, 1, 1, rotation=R, qjl=phi)
+    x = np.random.default_rng(9).standard_normal((11, dim)).astype(np.float32)
+    kv.store(0, 0, x, x)
+    comp = O.Compressor(dim, bits, m, R, phi)
+    s1, s2, rn, sc = comp.compress(x)
+    codes, scale, signs, rnorm = kv.read(0, 0)
+    assert np.array_equal(np.stack([O.pack_codes(r, bits) for r in codes]), s1)
+    assert np.array_equal(signs, s2.view(np.uint32).reshape(11, -1)[:, :1])
+    assert np.array_equal(rnorm.view(np.uint32), rn.view(np.uint32))
