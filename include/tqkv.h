@@ -141,6 +141,26 @@ int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32
 const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
                                     int32_t bits_k, int32_t bits_v);
 
+/*
+ * Fused decode attention over a codebook cache (the GPU TurboQuant caches'
+ * attention, turboquant.rs:763-923, for one query position): keys and
+ * values stored rotated (y = R x) as u8 codes + f32 sigma [B, H_kv, cap, .];
+ * the query is rotated, attention runs over centroid[c] * sigma in the
+ * rotated basis, and the output returns through R^T. rotation f32 [D, D],
+ * centroids f32 [2^bits] (device). D in {64, 128, 256}; H / H_kv in
+ * {1, 2, 4, 8}. workspace: tqkv_decode_codebook_workspace_size() bytes, or
+ * NULL for the library's per-device buffer.
+ */
+int32_t tqkv_decode_attend_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
+                                    int32_t D, float scale, const float* rotation,
+                                    const float* centroids_k, int32_t bits_k,
+                                    const float* centroids_v, int32_t bits_v,
+                                    const uint8_t* k_codes, const float* k_sigma,
+                                    const uint8_t* v_codes, const float* v_sigma, int64_t cap,
+                                    int64_t n, uint16_t* out, void* workspace,
+                                    size_t workspace_bytes, tqkv_stream stream);
+size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int32_t D, int64_t total_tokens);
+
 /* Bytes of workspace tqkv_decode_attend_affine needs for this shape. */
 size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
                                   int64_t total_tokens);
@@ -189,6 +209,7 @@ typedef struct tqkv_cache_config {
   int32_t prealloc;
   int64_t max_size;
   int64_t keep;
+  uint64_t seed;      /* codebook: rotation seed (QJL at seed + 1); the reference uses 42 */
 } tqkv_cache_config;
 
 /*
@@ -233,9 +254,10 @@ int32_t tqkv_cache_update(tqkv_cache* cache, const void* const* rows, int64_t s,
 
 /*
  * update_and_fetch from bf16 keys and values [B, H_kv, s, dim]: stored as is
- * (bf16 kind) or quantized on append straight into the cache rows (affine
- * kind, mlx::quantize as native_cache.rs:968-971, 1445-1448 call it).
- * TQKV_EUNSUPPORTED for the codebook kind.
+ * (bf16 kind), quantized on append straight into the cache rows (affine
+ * kind, mlx::quantize as native_cache.rs:968-971, 1445-1448 call it), or
+ * compressed by tqkv_tq_encode into codes + sigma (+ QJL signs and residual
+ * norm for keys) (codebook kind; k_dim == v_dim in {64, 128, 256, 512}).
  */
 int32_t tqkv_cache_append(tqkv_cache* cache, const uint16_t* k, const uint16_t* v, int64_t s,
                           tqkv_cache_view* fetched, tqkv_stream stream);
@@ -262,6 +284,15 @@ int32_t tqkv_cache_buffers(const tqkv_cache* cache, tqkv_cache_view* out);
  */
 int32_t tqkv_cache_keep_suffix_from(tqkv_cache* cache, int64_t prefix_len, tqkv_stream stream);
 /*
+ * Codebook kind: use the given rotation (host f32 [k_dim, k_dim] row-major,
+ * the reference's TQRM matrix) and QJL matrix (host f32 [32 * qjl_words,
+ * k_dim], or NULL) instead of drawing them from the seed
+ * (TurboQuantCompressor::from_files, compressor.rs:35-58). Call before the
+ * first append.
+ */
+int32_t tqkv_cache_set_tables(tqkv_cache* cache, const float* rotation, const float* qjl);
+
+/*
  * Attach a batch-1 cache holding the shared prefix (SharedPrefixKv,
  * native_cache.rs:2044-2051); NULL detaches. Decode attention then reads the
  * prefix's first base_offset tokens once for every batch row and the cache's
@@ -271,9 +302,10 @@ int32_t tqkv_cache_keep_suffix_from(tqkv_cache* cache, int64_t prefix_len, tqkv_
 int32_t tqkv_cache_attach_prefix(tqkv_cache* cache, const tqkv_cache* prefix);
 
 /*
- * Fused decode attention over the last fetched view (affine kind, k_dim ==
- * v_dim), plus the attached prefix: tqkv_decode_attend_affine on the cache's
- * own buffers. q: bf16 [B, H, 1, D]; out: bf16 [B, H, 1, D].
+ * Fused decode attention over the last fetched view, plus the attached
+ * prefix: tqkv_decode_attend_affine on the cache's own buffers (affine kind,
+ * k_dim == v_dim), or tqkv_decode_attend_codebook (codebook kind). q: bf16
+ * [B, H, 1, D]; out: bf16 [B, H, 1, D].
  */
 int32_t tqkv_cache_decode_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
                                  float scale, uint16_t* out, void* workspace,

@@ -14,6 +14,7 @@
 // update-free calls in a graph).
 #include <cstring>
 #include <new>
+#include <vector>
 
 #include "cache_plan.hpp"
 #include "common.hpp"
@@ -83,6 +84,13 @@ struct tqkv_cache {
   int64_t view_n = 0;          // rows of the last fetched view
   int64_t base_offset = 0;     // absolute position of row 0 (shared-prefix suffix)
   const tqkv_cache* prefix = nullptr;
+  // codebook kind: device tables, built on first use (or given)
+  float* R = nullptr;          // [D, D] row-major
+  float* phi = nullptr;        // [m, D]
+  double* bnd_k = nullptr;     // [2^bits_k + 1]
+  double* bnd_v = nullptr;
+  float* cent_k = nullptr;     // [2^bits_k], the f64 centroids rounded
+  float* cent_v = nullptr;
 };
 
 namespace {
@@ -157,6 +165,43 @@ int32_t execute(tqkv_cache* c, const cacheplan::Plan& p, int64_t old_len, hipStr
       }
       std::swap(cur, alt);
     }
+  }
+  return TQKV_OK;
+}
+
+int32_t upload(void** dst, const void* src, size_t bytes) {
+  if (*dst == nullptr && hipMalloc(dst, bytes ? bytes : 1) != hipSuccess)
+    return fail(TQKV_ENOMEM, "table hipMalloc of %zu bytes failed", bytes);
+  TQKV_HIP(hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice));
+  return TQKV_OK;
+}
+
+// The codebook kind's tables: Lloyd-Max levels for the key and value widths,
+// the rotation (seed) and the QJL matrix (seed + 1), unless given.
+int32_t codebook_tables(tqkv_cache* c, const float* R_host, const float* phi_host) {
+  const tqkv_cache_config& g = c->cfg;
+  const int D = g.k_dim, m = 32 * g.qjl_words;
+  if (g.k_dim != g.v_dim) return fail(TQKV_EUNSUPPORTED, "codebook caches need k_dim == v_dim");
+  if (!(D == 64 || D == 128 || D == 256 || D == 512))
+    return fail(TQKV_EUNSUPPORTED, "codebook dim=%d not in {64,128,256,512}", D);
+  for (int kv = 0; kv < 2; ++kv) {
+    const int bits = kv ? g.bits_v : g.bits_k;
+    const int n = 1 << bits;
+    std::vector<double> b(size_t(n) + 1), ce(static_cast<size_t>(n));
+    if (int32_t rc = tqkv_lloyd_max(uint32_t(bits), 1000, b.data(), ce.data())) return rc;
+    std::vector<float> cf(ce.begin(), ce.end());
+    if (int32_t rc = upload(reinterpret_cast<void**>(kv ? &c->bnd_v : &c->bnd_k), b.data(), b.size() * 8)) return rc;
+    if (int32_t rc = upload(reinterpret_cast<void**>(kv ? &c->cent_v : &c->cent_k), cf.data(), cf.size() * 4)) return rc;
+  }
+  std::vector<float> R(size_t(D) * D);
+  if (R_host) std::memcpy(R.data(), R_host, R.size() * 4);
+  else if (int32_t rc = tqkv_rotation_matrix(D, g.seed, R.data())) return rc;
+  if (int32_t rc = upload(reinterpret_cast<void**>(&c->R), R.data(), R.size() * 4)) return rc;
+  if (m > 0) {
+    std::vector<float> P(size_t(m) * D);
+    if (phi_host) std::memcpy(P.data(), phi_host, P.size() * 4);
+    else if (int32_t rc = tqkv_qjl_matrix(D, m, g.seed + 1, P.data())) return rc;
+    if (int32_t rc = upload(reinterpret_cast<void**>(&c->phi), P.data(), P.size() * 4)) return rc;
   }
   return TQKV_OK;
 }
@@ -259,6 +304,9 @@ int32_t tqkv_cache_destroy(tqkv_cache* c) {
     release(c->cur[s]);
     release(c->alt[s]);
   }
+  for (void* p : {static_cast<void*>(c->R), static_cast<void*>(c->phi), static_cast<void*>(c->bnd_k),
+                  static_cast<void*>(c->bnd_v), static_cast<void*>(c->cent_k), static_cast<void*>(c->cent_v)})
+    if (p) (void)hipFree(p);
   delete c;
   return ok();
 }
@@ -291,9 +339,38 @@ int32_t tqkv_cache_append(tqkv_cache* c, const uint16_t* k, const uint16_t* v, i
     const void* rows[2] = {k, v};
     return tqkv_cache_update(c, rows, s, fetched, stream);
   }
-  if (c->cfg.kind != TQKV_CACHE_AFFINE)
-    return fail(TQKV_EUNSUPPORTED, "bf16 append into a codebook cache");
   if (s <= 0) return fail(TQKV_EINVAL_SHAPE, "append of %lld rows", (long long)s);
+  if (c->cfg.kind == TQKV_CACHE_CODEBOOK) {
+    // TurboQuantCompressor::compress of keys (with the QJL stage when the
+    // cache keeps signs) and values, straight into the rotating cache rows.
+    if (!c->R)
+      if (int32_t rc = codebook_tables(c, nullptr, nullptr)) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const int64_t old_len = c->st.has ? c->st.len : 0;
+    cacheplan::State next = c->st;
+    const cacheplan::Plan p = cacheplan::update(next, c->pc, s);
+    if (int32_t rc = execute(c, p, old_len, st)) return rc;
+    const tqkv_cache_config& g = c->cfg;
+    const bool qjl = g.qjl_words > 0;
+    const int vi = qjl ? 4 : 2;
+    if (int32_t rc = tqkv_tq_encode(
+            k, 1, c->n_slabs, s, g.k_dim, c->R, c->bnd_k, c->cent_k, g.bits_k, c->phi,
+            32 * g.qjl_words, c->cur[0].ptr, reinterpret_cast<float*>(c->cur[1].ptr),
+            qjl ? reinterpret_cast<uint32_t*>(c->cur[2].ptr) : nullptr,
+            qjl ? reinterpret_cast<float*>(c->cur[3].ptr) : nullptr, c->cur[0].cap, p.write_at,
+            stream))
+      return rc;
+    if (int32_t rc = tqkv_tq_encode(v, 1, c->n_slabs, s, g.v_dim, c->R, c->bnd_v, c->cent_v,
+                                    g.bits_v, nullptr, 0, c->cur[vi].ptr,
+                                    reinterpret_cast<float*>(c->cur[vi + 1].ptr), nullptr, nullptr,
+                                    c->cur[vi].cap, p.write_at, stream))
+      return rc;
+    c->st = next;
+    c->view_n = p.view;
+    if (fetched) fill_view(c, p.view, fetched);
+    return ok();
+  }
+  if (c->cfg.kind != TQKV_CACHE_AFFINE) return fail(TQKV_EINVAL_ARG, "kind=%d", c->cfg.kind);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int64_t old_len = c->st.has ? c->st.len : 0;
   cacheplan::State next = c->st;
@@ -381,6 +458,14 @@ int32_t tqkv_cache_keep_suffix_from(tqkv_cache* c, int64_t prefix_len, tqkv_stre
   return ok();
 }
 
+int32_t tqkv_cache_set_tables(tqkv_cache* c, const float* rotation, const float* qjl) {
+  if (!c) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (c->cfg.kind != TQKV_CACHE_CODEBOOK)
+    return fail(TQKV_EUNSUPPORTED, "tables belong to codebook caches");
+  if (int32_t rc = codebook_tables(c, rotation, qjl)) return rc;
+  return ok();
+}
+
 int32_t tqkv_cache_attach_prefix(tqkv_cache* c, const tqkv_cache* prefix) {
   if (!c) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (!prefix) {
@@ -403,6 +488,17 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* c, const uint16_t* q, int32_t
                                  uint16_t* out, void* workspace, size_t workspace_bytes,
                                  tqkv_stream stream) {
   if (!c || !q || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (c->cfg.kind == TQKV_CACHE_CODEBOOK) {
+    if (!c->R) return fail(TQKV_EINVAL_ARG, "codebook cache has no tables yet (append first)");
+    if (c->view_n <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
+    const tqkv_cache_config& g = c->cfg;
+    const int vi = g.qjl_words > 0 ? 4 : 2;
+    return tqkv_decode_attend_codebook(
+        q, g.batch, H, g.kv_heads, g.k_dim, scale, c->R, c->cent_k, g.bits_k, c->cent_v, g.bits_v,
+        c->cur[0].ptr, reinterpret_cast<const float*>(c->cur[1].ptr), c->cur[vi].ptr,
+        reinterpret_cast<const float*>(c->cur[vi + 1].ptr), c->cur[0].cap, c->view_n, out,
+        workspace, workspace_bytes, stream);
+  }
   if (c->cfg.kind != TQKV_CACHE_AFFINE)
     return fail(TQKV_EUNSUPPORTED, "decode over this cache kind");
   if (c->cfg.k_dim != c->cfg.v_dim)

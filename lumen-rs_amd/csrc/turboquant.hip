@@ -287,3 +287,236 @@ extern "C" int32_t tqkv_rotate_bf16(const uint16_t* x, int64_t rows, int32_t dim
   TQKV_LAUNCHED();
   return ok();
 }
+
+// ---------------------------------------------------------------------------
+// Decode attention over a codebook cache (the GPU TurboQuant caches'
+// fused attention, turboquant.rs:763-923, for one query position): keys and
+// values are stored rotated (y = R x) as codes + sigma, so the query is
+// rotated the same way, attention runs in the rotated basis over
+// centroid[c] * sigma, and the output goes back through R^T.
+namespace tqkv {
+namespace tq {
+namespace {
+
+constexpr int kCbTile = 64;  // tokens per step of a wavefront
+
+// q_rot[b, h, :] = R q[b, h, :] in f32.
+__global__ void cb_rotate_q_kernel(const uint16_t* __restrict__ q, const float* __restrict__ R,
+                                   int D, float* __restrict__ qr) {
+  const int64_t bh = blockIdx.x;
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < D; ++j) acc = fmaf(R[int64_t(i) * D + j], bf16_to_f32(q[bh * D + j]), acc);
+    qr[bh * D + i] = acc;
+  }
+}
+
+// One workgroup of one wavefront per (split, KV head, batch row): partial
+// softmax state over its tokens for the G query heads. Scores: lane = token;
+// values: lane = channels (D / 64 each).
+template <int D, int G>
+__global__ __launch_bounds__(kWave) void cb_decode_kernel(
+    const float* __restrict__ qr, int H, const uint8_t* __restrict__ kc,
+    const float* __restrict__ ks, const uint8_t* __restrict__ vc, const float* __restrict__ vs,
+    int64_t cap, int64_t n, int H_kv, const float* __restrict__ cent_k,
+    const float* __restrict__ cent_v, int n_k, int n_v, float qscale, int64_t split_len,
+    int n_splits, float* __restrict__ part_o, float* __restrict__ part_m,
+    float* __restrict__ part_l) {
+  constexpr int PER = D / kWave;
+  __shared__ float s_q[G][D];
+  __shared__ float s_ck[256], s_cv[256];
+  __shared__ float s_p[G][kCbTile];
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x;
+  for (int i = lane; i < G * D; i += kWave) {
+    const int h = i / D, d = i % D;
+    s_q[h][d] = qr[(int64_t(b) * H + kvh * G + h) * D + d] * qscale;
+  }
+  for (int i = lane; i < 256; i += kWave) {
+    s_ck[i] = i < n_k ? cent_k[i] : 0.0f;
+    s_cv[i] = i < n_v ? cent_v[i] : 0.0f;
+  }
+  __syncthreads();
+  const int64_t slab = (int64_t(b) * H_kv + kvh) * cap;
+  const int64_t t0 = int64_t(split) * split_len;
+  const int64_t t1 = t0 + split_len < n ? t0 + split_len : n;
+  float m[G], l[G], acc[G][PER];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) acc[h][k] = 0.0f;
+  }
+  for (int64_t base = t0; base < t1; base += kCbTile) {
+    const int64_t t = base + lane;
+    const bool valid = t < t1;
+    float sc[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) sc[h] = 0.0f;
+    if (valid) {
+      const uint8_t* row = kc + (slab + t) * D;
+      for (int d = 0; d < D; d += 16) {
+        const uint4 w = *reinterpret_cast<const uint4*>(row + d);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const float c = s_ck[(ws[k / 4] >> (8 * (k % 4))) & 0xffu];
+#pragma unroll
+          for (int h = 0; h < G; ++h) sc[h] = fmaf(s_q[h][d + k], c, sc[h]);
+        }
+      }
+      const float sg = ks[slab + t];
+#pragma unroll
+      for (int h = 0; h < G; ++h) sc[h] *= sg;
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mx = valid ? sc[h] : -INFINITY;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+      const float mn = fmaxf(m[h], mx);
+      const float f = m[h] == -INFINITY ? 0.0f : exp2f(m[h] - mn);
+      l[h] *= f;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) acc[h][k] *= f;
+      m[h] = mn;
+      const float p = valid ? exp2f(sc[h] - mn) : 0.0f;
+      float ps = p;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) ps += __shfl_xor(ps, off, kWave);
+      l[h] += ps;
+      s_p[h][lane] = valid ? p * vs[slab + t] : 0.0f;
+    }
+    __syncthreads();
+    const int cnt = int(t1 - base < kCbTile ? t1 - base : kCbTile);
+    for (int j = 0; j < cnt; ++j) {
+      const uint8_t* row = vc + (slab + base + j) * D;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) {
+        const float c = s_cv[row[lane + k * kWave]];
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[h][k] = fmaf(s_p[h][j], c, acc[h][k]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const int64_t row = (int64_t(b) * H + kvh * G + h) * n_splits + split;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) part_o[row * D + lane + k * kWave] = acc[h][k];
+    if (lane == 0) {
+      part_m[row] = m[h];
+      part_l[row] = l[h];
+    }
+  }
+}
+
+// Merge the splits of one (batch row, head) in the rotated basis, then
+// o = R^T o_rot, as bf16.
+__global__ void cb_merge_kernel(const float* __restrict__ part_o, const float* __restrict__ part_m,
+                                const float* __restrict__ part_l, int n_splits, int D,
+                                const float* __restrict__ R, uint16_t* __restrict__ out) {
+  extern __shared__ float s_o[];
+  const int64_t bh = blockIdx.x;
+  const float* pm = part_m + bh * n_splits;
+  const float* pl = part_l + bh * n_splits;
+  float mx = -INFINITY;
+  for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, pm[s]);
+  float ls = 0.0f;
+  for (int s = 0; s < n_splits; ++s)
+    if (pm[s] != -INFINITY) ls += pl[s] * exp2f(pm[s] - mx);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float os = 0.0f;
+    for (int s = 0; s < n_splits; ++s)
+      if (pm[s] != -INFINITY) os += part_o[(bh * n_splits + s) * D + d] * exp2f(pm[s] - mx);
+    s_o[d] = ls > 0.0f ? os / ls : 0.0f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < D; ++j) acc = fmaf(R[int64_t(j) * D + i], s_o[j], acc);
+    out[bh * D + i] = f32_to_bf16(acc);
+  }
+}
+
+template <int D>
+int32_t launch_cb(int G, dim3 grid, hipStream_t st, const float* qr, int H, const uint8_t* kc,
+                  const float* ks, const uint8_t* vc, const float* vs, int64_t cap, int64_t n,
+                  int H_kv, const float* ck, const float* cv, int nk, int nv, float qscale,
+                  int64_t split_len, int n_splits, float* po, float* pm, float* pl) {
+#define TQKV_CB(GG)                                                                          \
+  case GG:                                                                                  \
+    hipLaunchKernelGGL((cb_decode_kernel<D, GG>), grid, dim3(kWave), 0, st, qr, H, kc, ks, vc, \
+                       vs, cap, n, H_kv, ck, cv, nk, nv, qscale, split_len, n_splits, po, pm, \
+                       pl);                                                                   \
+    break;
+  switch (G) {
+    TQKV_CB(1) TQKV_CB(2) TQKV_CB(4) TQKV_CB(8)
+    default: return fail(TQKV_EUNSUPPORTED, "codebook decode with %d query heads per KV head", G);
+  }
+#undef TQKV_CB
+  TQKV_LAUNCHED();
+  return TQKV_OK;
+}
+
+}  // namespace
+}  // namespace tq
+}  // namespace tqkv
+
+extern "C" size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int32_t D,
+                                                       int64_t total_tokens) {
+  if (B <= 0 || H <= 0 || D <= 0 || total_tokens <= 0) return 0;
+  const int64_t splits = (total_tokens + 511) / 512 < 64 ? (total_tokens + 511) / 512 : 64;
+  return size_t(B) * H * (size_t(D) + size_t(splits) * (size_t(D) + 2)) * sizeof(float);
+}
+
+extern "C" int32_t tqkv_decode_attend_codebook(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,
+    const float* rotation, const float* centroids_k, int32_t bits_k, const float* centroids_v,
+    int32_t bits_v, const uint8_t* k_codes, const float* k_sigma, const uint8_t* v_codes,
+    const float* v_sigma, int64_t cap, int64_t n, uint16_t* out, void* workspace,
+    size_t workspace_bytes, tqkv_stream stream) {
+  if (!q || !rotation || !centroids_k || !centroids_v || !k_codes || !k_sigma || !v_codes ||
+      !v_sigma || !out)
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n <= 0 || n > cap)
+    return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d n=%lld cap=%lld", B, H, H_kv, (long long)n,
+                (long long)cap);
+  if (bits_k < 1 || bits_k > 8 || bits_v < 1 || bits_v > 8)
+    return fail(TQKV_EUNSUPPORTED, "bits %d/%d", bits_k, bits_v);
+  const int G = H / H_kv;
+  const int64_t n_splits64 = (n + 511) / 512 < 64 ? (n + 511) / 512 : 64;
+  const int n_splits = int(n_splits64);
+  const int64_t split_len = (n + n_splits - 1) / n_splits;
+  const size_t need = tqkv_decode_codebook_workspace_size(B, H, D, n);
+  void* ws = workspace;
+  if (!ws) {
+    if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+  } else if (workspace_bytes < need) {
+    return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+  }
+  float* qr = static_cast<float*>(ws);
+  float* po = qr + size_t(B) * H * D;
+  float* pm = po + size_t(B) * H * n_splits * D;
+  float* pl = pm + size_t(B) * H * n_splits;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tq::cb_rotate_q_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256), 0,
+                     st, q, rotation, D, qr);
+  TQKV_LAUNCHED();
+  const dim3 grid{unsigned(n_splits), unsigned(H_kv), unsigned(B)};
+  const float qscale = scale * 1.4426950408889634f;
+  int32_t rc = TQKV_OK;
+  switch (D) {
+    case 64: rc = tq::launch_cb<64>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl); break;
+    case 128: rc = tq::launch_cb<128>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl); break;
+    case 256: rc = tq::launch_cb<256>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl); break;
+    default: return fail(TQKV_EUNSUPPORTED, "codebook decode D=%d not in {64,128,256}", D);
+  }
+  if (rc) return rc;
+  hipLaunchKernelGGL(tq::cb_merge_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256),
+                     size_t(D) * sizeof(float), st, po, pm, pl, n_splits, D, rotation, out);
+  TQKV_LAUNCHED();
+  return ok();
+}

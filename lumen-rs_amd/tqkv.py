@@ -45,7 +45,8 @@ class AffineSeg(ctypes.Structure):
 class CacheConfig(ctypes.Structure):
     _fields_ = [("kind", I32), ("batch", I32), ("kv_heads", I32), ("k_dim", I32),
                 ("v_dim", I32), ("group_size", I32), ("bits_k", I32), ("bits_v", I32),
-                ("qjl_words", I32), ("prealloc", I32), ("max_size", I64), ("keep", I64)]
+                ("qjl_words", I32), ("prealloc", I32), ("max_size", I64), ("keep", I64),
+                ("seed", ctypes.c_uint64)]
 
 
 class CacheView(ctypes.Structure):
@@ -108,6 +109,7 @@ _SIGS = {
     "tqkv_cache_buffers": (I32, [P, ctypes.POINTER(CacheView)]),
     "tqkv_cache_keep_suffix_from": (I32, [P, I64, P]),
     "tqkv_cache_attach_prefix": (I32, [P, P]),
+    "tqkv_cache_set_tables": (I32, [P, P, P]),
     "tqkv_cache_decode_attend": (I32, [P, P, I32, F32, P, P, SZ, P]),
     "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
 }
@@ -350,9 +352,9 @@ class Cache:
     bf16 / affine / codebook slots."""
 
     def __init__(self, kind, batch, kv_heads, k_dim, v_dim, group_size=64, bits_k=4, bits_v=4,
-                 qjl_words=0, prealloc=True, max_size=0, keep=0):
+                 qjl_words=0, prealloc=True, max_size=0, keep=0, seed=42):
         self.cfg = CacheConfig(kind, batch, kv_heads, k_dim, v_dim, group_size, bits_k, bits_v,
-                               qjl_words, int(prealloc), max_size, keep)
+                               qjl_words, int(prealloc), max_size, keep, seed)
         h = P()
         check(lib().tqkv_cache_create(ctypes.byref(self.cfg), ctypes.byref(h)))
         self.h = h.value
@@ -403,6 +405,13 @@ class Cache:
 
     def keep_suffix_from(self, prefix_len, stream=None):
         check(lib().tqkv_cache_keep_suffix_from(self.h, prefix_len, stream))
+
+    def set_tables(self, rotation, qjl=None):
+        self._tables = (np.ascontiguousarray(rotation, np.float32),
+                        None if qjl is None else np.ascontiguousarray(qjl, np.float32))
+        r, q = self._tables
+        check(lib().tqkv_cache_set_tables(self.h, r.ctypes.data_as(P),
+                                          None if q is None else q.ctypes.data_as(P)))
 
     def attach_prefix(self, prefix):
         check(lib().tqkv_cache_attach_prefix(self.h, prefix.h if prefix is not None else None))

@@ -266,3 +266,70 @@ def test_decode_over_shared_prefix(T):
     check_close(got, want)
     seqs.attach_prefix(None)
     prefix.close()
+
+
+def attention_f64(q, K, V, scale, G):
+    """Textbook softmax attention in f64: q [B,H,D], K/V [B,Hkv,N,D]."""
+    B, H, D = q.shape
+    out = np.zeros((B, H, D))
+    for b in range(B):
+        for h in range(H):
+            s = (K[b, h // G] @ q[b, h]) * scale
+            p = np.exp(s - s.max())
+            out[b, h] = (p @ V[b, h // G]) / p.sum()
+    return out
+
+
+@pytest.mark.parametrize("bits,qjl_words", [(4, 2), (3, 0), (8, 0)])
+def test_codebook_cache_append_and_decode(T, bits, qjl_words):
+    # A rotating TurboQuant cache: bf16 K/V compressed on append (bit-exact
+    # with compress_one), then decode attention over the codes in the rotated
+    # basis, un-rotated, against attention over the dequantized cache.
+    B, Hq, Hkv, D, W = 2, 8, 2, 128, 1024
+    c = T.Cache(T.CACHE_CODEBOOK, B, Hkv, D, D, bits_k=bits, bits_v=bits, qjl_words=qjl_words,
+                max_size=W, keep=0, seed=42)
+    k = kv_bf16((B, Hkv, 300, D), 61, frac=0.02, mult=8.0)
+    v = kv_bf16((B, Hkv, 300, D), 62, frac=0.02, mult=8.0)
+    for a, s in [(0, 200), (200, 1), (201, 99)]:
+        dk = T.DeviceArray.of(np.ascontiguousarray(k[:, :, a:a + s]))
+        dv = T.DeviceArray.of(np.ascontiguousarray(v[:, :, a:a + s]))
+        c.append(dk.ptr, dv.ptr, s)
+    st = c.state()
+    assert st.view == 300 and st.offset == 300
+    R = T.rotation_matrix(D, 42)
+    m = 32 * qjl_words
+    phi = T.qjl_matrix(D, max(m, 1), 43)
+    comp = O.Compressor(D, bits, max(m, 1), R, phi[:max(m, 1)])
+    bufs = c.buffers()
+    kc = T.view_slot(bufs, 0, B * Hkv, np.uint8, D)[:, :300]
+    ks = T.view_slot(bufs, 1, B * Hkv, np.float32, 1)[:, :300, 0]
+    vi = 4 if qjl_words else 2
+    vc = T.view_slot(bufs, vi, B * Hkv, np.uint8, D)[:, :300]
+    vsg = T.view_slot(bufs, vi + 1, B * Hkv, np.float32, 1)[:, :300, 0]
+    kf = O.bf16_to_f32(k).reshape(-1, D)
+    s1, s2, rn, sc = comp.compress(kf)
+    assert np.array_equal(np.stack([O.pack_codes(r, bits) for r in kc.reshape(-1, D)]), s1)
+    assert np.array_equal(ks.reshape(-1).view(np.uint32), sc.view(np.uint32))
+    if qjl_words:
+        sg = T.view_slot(bufs, 2, B * Hkv, np.uint32, qjl_words)[:, :300].reshape(-1, qjl_words)
+        assert np.array_equal(sg, s2.view(np.uint32).reshape(len(kf), -1)[:, :qjl_words])
+    _, cent = T.lloyd_max(bits)
+    cent = cent.astype(np.float32).astype(np.float64)
+    Kr = (cent[kc] * ks[..., None]).reshape(B, Hkv, 300, D)
+    Vr = (cent[vc] * vsg[..., None]).reshape(B, Hkv, 300, D)
+    q = kv_bf16((B, Hq, 1, D), 63)
+    qf = O.bf16_to_f32(q).reshape(B, Hq, D).astype(np.float64)
+    qr = qf @ R.astype(np.float64).T  # R q per head
+    want = attention_f64(qr, Kr, Vr, D ** -0.5, Hq // Hkv) @ R.astype(np.float64)  # R^T o
+    got = O.bf16_to_f32(decode(T, c, q, Hq, D ** -0.5)).reshape(B, Hq, D)
+    err = np.abs(got - want)
+    print(f"[codebook-decode] bits={bits} max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
+    assert err.max() <= 2e-2 and err.mean() <= 1e-3
+    # A coarse sanity bar against attention over the unquantized K/V (the
+    # output averages many values, so codebook noise weighs more in it than
+    # in any one score).
+    orig = attention_f64(qf, O.bf16_to_f32(k).astype(np.float64),
+                         O.bf16_to_f32(v).astype(np.float64), D ** -0.5, Hq // Hkv)
+    cos = (got.ravel() @ orig.ravel()) / (np.linalg.norm(got) * np.linalg.norm(orig))
+    print(f"[codebook-decode] cos_vs_unquantized={cos:.4f}", flush=True)
+    assert cos > {8: 0.995, 4: 0.9, 3: 0.85}[bits]
