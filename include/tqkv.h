@@ -161,6 +161,33 @@ int32_t tqkv_decode_attend_codebook(const uint16_t* q, int32_t B, int32_t H, int
                                     size_t workspace_bytes, tqkv_stream stream);
 size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int32_t D, int64_t total_tokens);
 
+/*
+ * Prefill-chunk attention over affine-packed K/V on the matrix cores:
+ * softmax(scale * Q K^T + mask) V for a chunk of L query rows per head.
+ * Replaces dequantized_prefill_attention (gemma4_moe.rs:2382-2411): K and V
+ * dequantize as mlx::dequantize does for bf16 (bf16(bf16(scale * code) +
+ * bias)) in LDS, never in HBM, then attention runs with bf16 operands and f32
+ * accumulation. The mask is build_causal_mask_abs (native_attention.rs:
+ * 545-622) in absolute positions: query row l sits at q_start + l and key k
+ * (counted across both segments) at k_start + k; with causal != 0, key k is
+ * visible iff k_abs <= q_abs and, when window > 0, q_abs < k_abs + window
+ * (window < 0: no window; window == 0 is rejected). causal == 0: every key is
+ * visible. That one rule covers the reference's causal SDPA,
+ * lumen_sdpa_windowed and sdpa_with_mask branches. A row that sees no key
+ * returns zeros.
+ *
+ * q: bf16 [B, H, L, D]; out: bf16 [B, H, L, D]; segs as for
+ * tqkv_decode_attend_affine (1 or 2: a shared prefix, then a suffix).
+ * D in {64, 128, 256}; bits_k, bits_v in {2, 3, 4, 5, 6, 8}; group_size in
+ * {32, 64, 128}. Needs no workspace.
+ */
+int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
+                                   int32_t L, int32_t D, int32_t group_size, int32_t bits_k,
+                                   int32_t bits_v, float scale, const tqkv_affine_seg* segs,
+                                   int32_t n_segs, int64_t q_start, int64_t k_start,
+                                   int32_t causal, int64_t window, uint16_t* out,
+                                   tqkv_stream stream);
+
 /* Bytes of workspace tqkv_decode_attend_affine needs for this shape. */
 size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
                                   int64_t total_tokens);
@@ -310,6 +337,19 @@ int32_t tqkv_cache_attach_prefix(tqkv_cache* cache, const tqkv_cache* prefix);
 int32_t tqkv_cache_decode_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
                                  float scale, uint16_t* out, void* workspace,
                                  size_t workspace_bytes, tqkv_stream stream);
+
+/*
+ * Prefill-chunk attention over the last fetched view (plus the attached
+ * prefix) for the L tokens just appended: tqkv_prefill_attend_affine with
+ * queries at absolute positions [offset - L, offset) and the view's keys
+ * ending at offset, causal, with the given sliding window (< 0: none). The
+ * reference derives the same positions (cache_first_held_pos = kv_offset +
+ * L - kv_actual, gemma4_moe.rs:2228). Affine kind with k_dim == v_dim.
+ * q: bf16 [B, H, L, D]; out: bf16 [B, H, L, D].
+ */
+int32_t tqkv_cache_prefill_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
+                                  int32_t L, float scale, int64_t window, uint16_t* out,
+                                  tqkv_stream stream);
 
 /* ======================================================================
  * TurboQuant codebook format

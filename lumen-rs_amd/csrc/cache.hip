@@ -217,6 +217,28 @@ void fill_view(const tqkv_cache* c, int64_t n, tqkv_cache_view* v) {
   }
 }
 
+// The affine key segments of a cache: the attached prefix's first
+// base_offset rows (shared by every batch row), then the last fetched view.
+int affine_segments(const tqkv_cache* c, tqkv_affine_seg* segs) {
+  auto seg_of = [](const tqkv_cache* x, int64_t n, int shared) {
+    tqkv_affine_seg s{};
+    s.k_packed = reinterpret_cast<const uint32_t*>(x->cur[0].ptr);
+    s.k_scales = reinterpret_cast<const uint16_t*>(x->cur[1].ptr);
+    s.k_biases = reinterpret_cast<const uint16_t*>(x->cur[2].ptr);
+    s.v_packed = reinterpret_cast<const uint32_t*>(x->cur[3].ptr);
+    s.v_scales = reinterpret_cast<const uint16_t*>(x->cur[4].ptr);
+    s.v_biases = reinterpret_cast<const uint16_t*>(x->cur[5].ptr);
+    s.cap = x->cur[0].cap;
+    s.n = n;
+    s.shared = shared;
+    return s;
+  };
+  int n = 0;
+  if (c->prefix && c->base_offset > 0) segs[n++] = seg_of(c->prefix, c->base_offset, 1);
+  if (c->view_n > 0) segs[n++] = seg_of(c, c->view_n, 0);
+  return n;
+}
+
 }  // namespace
 
 extern "C" {
@@ -503,28 +525,34 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* c, const uint16_t* q, int32_t
     return fail(TQKV_EUNSUPPORTED, "decode over this cache kind");
   if (c->cfg.k_dim != c->cfg.v_dim)
     return fail(TQKV_EUNSUPPORTED, "decode needs k_dim == v_dim");
-  auto seg_of = [](const tqkv_cache* x, int64_t n, int shared) {
-    tqkv_affine_seg s{};
-    s.k_packed = reinterpret_cast<const uint32_t*>(x->cur[0].ptr);
-    s.k_scales = reinterpret_cast<const uint16_t*>(x->cur[1].ptr);
-    s.k_biases = reinterpret_cast<const uint16_t*>(x->cur[2].ptr);
-    s.v_packed = reinterpret_cast<const uint32_t*>(x->cur[3].ptr);
-    s.v_scales = reinterpret_cast<const uint16_t*>(x->cur[4].ptr);
-    s.v_biases = reinterpret_cast<const uint16_t*>(x->cur[5].ptr);
-    s.cap = x->cur[0].cap;
-    s.n = n;
-    s.shared = shared;
-    return s;
-  };
   tqkv_affine_seg segs[2];
-  int n = 0;
-  if (c->prefix && c->base_offset > 0) segs[n++] = seg_of(c->prefix, c->base_offset, 1);
-  if (c->view_n > 0) segs[n++] = seg_of(c, c->view_n, 0);
+  const int n = affine_segments(c, segs);
   if (n == 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
   const tqkv_cache_config& g = c->cfg;
   return tqkv_decode_attend_affine(q, g.batch, H, g.kv_heads, g.k_dim, g.group_size, g.bits_k,
                                    g.bits_v, scale, segs, n, out, workspace, workspace_bytes,
                                    stream);
+}
+
+int32_t tqkv_cache_prefill_attend(const tqkv_cache* c, const uint16_t* q, int32_t H, int32_t L,
+                                  float scale, int64_t window, uint16_t* out,
+                                  tqkv_stream stream) {
+  if (!c || !q || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (c->cfg.kind != TQKV_CACHE_AFFINE)
+    return fail(TQKV_EUNSUPPORTED, "prefill attention over this cache kind");
+  if (c->cfg.k_dim != c->cfg.v_dim)
+    return fail(TQKV_EUNSUPPORTED, "prefill attention needs k_dim == v_dim");
+  const int64_t offset = c->base_offset + c->st.offset;
+  if (L <= 0 || L > offset)
+    return fail(TQKV_EINVAL_SHAPE, "L=%d queries but %lld tokens appended", L, (long long)offset);
+  tqkv_affine_seg segs[2];
+  const int n = affine_segments(c, segs);
+  if (n == 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
+  const int64_t keys = segs[0].n + (n == 2 ? segs[1].n : 0);
+  const tqkv_cache_config& g = c->cfg;
+  return tqkv_prefill_attend_affine(q, g.batch, H, g.kv_heads, L, g.k_dim, g.group_size,
+                                    g.bits_k, g.bits_v, scale, segs, n, offset - L,
+                                    offset - keys, 1, window, out, stream);
 }
 
 }  // extern "C"

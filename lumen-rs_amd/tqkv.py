@@ -77,6 +77,9 @@ _SIGS = {
     "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
+    "tqkv_prefill_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, I32, F32,
+                                         ctypes.POINTER(AffineSeg), I32, I64, I64, I32, I64, P,
+                                         P]),
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
     "tqkv_decode_kernel_name": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32]),
     "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
@@ -111,6 +114,7 @@ _SIGS = {
     "tqkv_cache_attach_prefix": (I32, [P, P]),
     "tqkv_cache_set_tables": (I32, [P, P, P]),
     "tqkv_cache_decode_attend": (I32, [P, P, I32, F32, P, P, SZ, P]),
+    "tqkv_cache_prefill_attend": (I32, [P, P, I32, I32, F32, I64, P, P]),
     "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
 }
 
@@ -305,6 +309,15 @@ def decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, out,
                                           len(segs), out, workspace, workspace_bytes, stream))
 
 
+def prefill_attend_affine(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, segs, out,
+                          q_start=0, k_start=0, causal=True, window=-1, stream=None):
+    """Chunk attention: query row l at q_start + l, key k at k_start + k."""
+    arr = (AffineSeg * len(segs))(*segs)
+    check(lib().tqkv_prefill_attend_affine(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, arr,
+                                           len(segs), q_start, k_start, int(causal), window, out,
+                                           stream))
+
+
 def decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v):
     """"mfma", "dot2" or "" (unsupported) for a decode layout."""
     return lib().tqkv_decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v).decode()
@@ -419,6 +432,9 @@ class Cache:
     def decode_attend(self, q, H, scale, out, workspace=None, workspace_bytes=0, stream=None):
         check(lib().tqkv_cache_decode_attend(self.h, q, H, scale, out, workspace,
                                              workspace_bytes, stream))
+
+    def prefill_attend(self, q, H, L, scale, out, window=-1, stream=None):
+        check(lib().tqkv_cache_prefill_attend(self.h, q, H, L, scale, window, out, stream))
 
 
 def view_slot(view, i, n_slabs, dtype, last):
