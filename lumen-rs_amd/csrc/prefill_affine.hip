@@ -1,6 +1,8 @@
 // Host side of the affine prefill-chunk attention: argument checks, the
 // kernel choice and the launch. The kernel and its design notes are in
 // prefill_affine.hpp.
+#include <cmath>
+
 #include "prefill_affine.hpp"
 
 using namespace tqkv;
@@ -42,6 +44,8 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   KernelFn fn = pick(D, bits_k, bits_v);
   if (!fn) return fail(TQKV_EUNSUPPORTED, "prefill head dim D=%d (64, 128 or 256)", D);
   if (causal && window == 0) return fail(TQKV_EINVAL_ARG, "window=0 hides every key");
+  if (!(scale > 0.0f) || !std::isfinite(scale))
+    return fail(TQKV_EINVAL_ARG, "softmax scale %g must be positive and finite", double(scale));
   if (int64_t(B) * H * L * D >= (int64_t(1) << 40))
     return fail(TQKV_EINVAL_SHAPE, "query tensor too large");
 
@@ -63,6 +67,9 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
     if (s.n > 0 && (!s.k_packed || !s.k_scales || !s.k_biases || !s.v_packed || !s.v_scales ||
                     !s.v_biases))
       return fail(TQKV_EINVAL_ARG, "segment %d has a null buffer", i);
+    // Rows of a slab are addressed with 32-bit word offsets.
+    if (s.cap > 0 && s.cap * int64_t(D) * (bits_k > bits_v ? bits_k : bits_v) / 32 >= (int64_t(1) << 32))
+      return fail(TQKV_EINVAL_SHAPE, "segment %d: cap=%lld rows too large", i, (long long)s.cap);
     a.seg[i] = Seg{s.k_packed, s.k_scales, s.k_biases, s.v_packed, s.v_scales, s.v_biases,
                    s.cap, s.shared ? 0 : int64_t(H_kv) * s.cap};
   }
@@ -70,23 +77,25 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   a.n0 = segs[0].n;
   a.total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
   if (a.total <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
+  if (a.total > (int64_t(1) << 31) - 2 * kTile)
+    return fail(TQKV_EINVAL_SHAPE, "%lld keys exceed the kernel's 32-bit key index",
+                (long long)a.total);
   a.q_start = q_start;
   a.k_start = k_start;
   a.window = window < 0 ? -1 : window;
 
   int rows_per_block = 0, threads = 0;
   switch (D) {
-    case 64: rows_per_block = Shape<64>::kRows, threads = Shape<64>::kWaves * kWave; break;
-    case 128: rows_per_block = Shape<128>::kRows, threads = Shape<128>::kWaves * kWave; break;
-    default: rows_per_block = Shape<256>::kRows, threads = Shape<256>::kWaves * kWave; break;
+    case 64: rows_per_block = Shape<64>::kRows, threads = Shape<64>::kThreads; break;
+    case 128: rows_per_block = Shape<128>::kRows, threads = Shape<128>::kThreads; break;
+    default: rows_per_block = Shape<256>::kRows, threads = Shape<256>::kThreads; break;
   }
   const int64_t blocks = (int64_t(L) * a.G + rows_per_block - 1) / rows_per_block;
-  if (blocks > 0x7fffffff || H_kv > 65535 || B > 65535)
-    return fail(TQKV_EINVAL_SHAPE, "grid too large");
+  const int64_t grid = blocks * H_kv * B;
+  if (grid > 0x7fffffff) return fail(TQKV_EINVAL_SHAPE, "grid too large");
   a.n_blocks = int(blocks);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(fn, dim3(unsigned(blocks), unsigned(H_kv), unsigned(B)), dim3(threads), 0,
-                     st, a);
+  hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(threads), 0, st, a);
   TQKV_LAUNCHED();
   return ok();
 }

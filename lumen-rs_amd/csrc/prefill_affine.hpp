@@ -48,6 +48,14 @@ namespace prefill {
 
 constexpr int kWave = 64;
 constexpr int kTile = 64;  // keys per tile
+constexpr int kXcds = 8;   // accelerator dies (each with its own L2) on MI355X
+// LDS row strides (bf16 elements). K rows: D + 8 keeps ds_read_b128 rows
+// 16-byte aligned and 8 consecutive rows on distinct banks. V^T rows:
+// kTile + 4 = 34 dwords, so the 16 rows one ds_read_b64 touches start on
+// distinct even banks.
+template <int D>
+constexpr int kKStride = D + 8;
+constexpr int kVStride = kTile + 4;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kTau = 8.0f;
 
@@ -83,13 +91,18 @@ struct Args {
 };
 
 // Launch shape per head dim: wavefronts per workgroup and query rows per
-// wavefront (128 rows a workgroup; at D = 256 the O accumulators take
-// 16 rows x 256 channels a wavefront).
+// wavefront. More rows a workgroup spread the dequantization of a tile over
+// more matrix-core work; the O accumulators (RW rows x D channels a
+// wavefront) and two wavefronts per SIMD bound RW; D = 256 stays at 128 rows.
+// Loader tasks: 64 keys x D/32 runs x {K, V}, kPer a thread.
 template <int D>
 struct Shape {
-  static constexpr int kWaves = D == 256 ? 8 : 4;
+  static constexpr int kWaves = D == 64 ? 4 : 8;
   static constexpr int kRW = D == 256 ? 16 : 32;
   static constexpr int kRows = kWaves * kRW;
+  static constexpr int kThreads = kWaves * 64;
+  static constexpr int kPer = 4 * D / kThreads;
+  static_assert(kPer * kThreads == 4 * D, "whole loader tasks per thread");
 };
 
 template <typename F, int... Is>
@@ -144,76 +157,141 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf2_t));
 }
 
-// One thread's share of a key tile: a run of 32 codes of one key, for K and
-// for V, with the run's scale and bias (bf16 bits, scale low).
-template <int BK, int BV>
+// One loader task's share of a key tile: a run of 32 codes of one key of K
+// or V (NW >= bits words), with the run's scale and bias (bf16 bits, scale
+// low).
+template <int NW>
 struct Stage {
-  uint32_t kw[BK];
-  uint32_t vw[BV];
-  uint32_t kp, vp;
+  uint32_t w[NW];
+  uint32_t s, b;  // bf16 bits; combined only when used, so the loads stay in flight
   bool ok;
 };
 
-template <int D, int BK, int BV>
-__device__ __forceinline__ void load_stage(Stage<BK, BV>& st, const Args& a, int b, int kvh,
-                                           int64_t kk, int run) {
+// Where the workgroup's loads start: the (batch row, KV head) slab of each
+// segment (uniform, so it stays in scalar registers); rows and the thread's
+// run are 32-bit offsets from there (the host checks that a slab fits).
+struct SlabPtrs {  // one of K or V; segments 0 and 1 as separate fields (no
+                  // indexed array, which would live in scratch memory)
+  const uint32_t* w0;
+  const uint32_t* w1;
+  const uint16_t* s0;
+  const uint16_t* s1;
+  const uint16_t* b0;
+  const uint16_t* b1;
+};
+
+template <int D, int BITS>
+__device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, const uint32_t* w0,
+                                              const uint32_t* w1, const uint16_t* sc0,
+                                              const uint16_t* sc1, const uint16_t* bi0,
+                                              const uint16_t* bi1, int gs, int b, int kvh) {
+  const int64_t r0 = int64_t(b) * s0.b_stride + int64_t(kvh) * s0.cap;
+  const int64_t r1 = int64_t(b) * s1.b_stride + int64_t(kvh) * s1.cap;
+  const int groups = D / gs;
+  return SlabPtrs{w0 + r0 * (D * BITS / 32), w1 + r1 * (D * BITS / 32), sc0 + r0 * groups,
+                  sc1 + r1 * groups,         bi0 + r0 * groups,         bi1 + r1 * groups};
+}
+
+// Loads run `run` of key kk (counted across both segments) of K or V.
+template <int D, int BITS, int NW>
+__device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, const Args& a, int kk,
+                                           int run) {
   st.ok = kk < a.total;
   if (!st.ok) return;
   const bool first = kk < a.n0;
-  const int64_t row = first ? kk : kk - a.n0;
-  const int64_t base = int64_t(b) * (first ? a.seg[0].b_stride : a.seg[1].b_stride) +
-                       int64_t(kvh) * (first ? a.seg[0].cap : a.seg[1].cap) + row;
-  const int groups = D / a.gs;
-  const int64_t g = base * groups + (run * 32) / a.gs;
-  const uint32_t* kw = first ? a.seg[0].kw : a.seg[1].kw;
-  const uint32_t* vw = first ? a.seg[0].vw : a.seg[1].vw;
-  load_words<BK>(st.kw, kw + base * (D * BK / 32) + run * BK);
-  load_words<BV>(st.vw, vw + base * (D * BV / 32) + run * BV);
-  const uint16_t* ks = first ? a.seg[0].ks : a.seg[1].ks;
-  const uint16_t* kb = first ? a.seg[0].kb : a.seg[1].kb;
-  const uint16_t* vs = first ? a.seg[0].vs : a.seg[1].vs;
-  const uint16_t* vb = first ? a.seg[0].vb : a.seg[1].vb;
-  st.kp = uint32_t(ks[g]) | (uint32_t(kb[g]) << 16);
-  st.vp = uint32_t(vs[g]) | (uint32_t(vb[g]) << 16);
+  const uint32_t row = uint32_t(first ? kk : kk - int(a.n0));
+  const uint32_t g = row * uint32_t(D / a.gs) + uint32_t(run * 32) / uint32_t(a.gs);
+  const uint32_t* w = first ? p.w0 : p.w1;
+  const uint16_t* sc = first ? p.s0 : p.s1;
+  const uint16_t* bi = first ? p.b0 : p.b1;
+  load_words<BITS>(st.w, w + (row * (D * BITS / 32) + run * BITS));
+  st.s = sc[g];
+  st.b = bi[g];
+}
+
+// The 32 codes of a run as floats. 2-, 4- and 8-bit codes are split into
+// bytes first so each converts with one v_cvt_f32_ubyteN.
+__device__ __forceinline__ float ubyte(uint32_t x, int j) { return float((x >> (8 * j)) & 0xffu); }
+
+template <int BITS>
+__device__ __forceinline__ void run_codes(const uint32_t* w, float* f) {
+  if constexpr (BITS == 8) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) f[i] = ubyte(w[i / 4], i % 4);
+  } else if constexpr (BITS == 4) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t e = w[k] & 0x0F0F0F0Fu, o = (w[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[8 * k + 2 * j] = ubyte(e, j);
+        f[8 * k + 2 * j + 1] = ubyte(o, j);
+      }
+    }
+  } else if constexpr (BITS == 2) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t x = (w[k] >> (2 * s)) & 0x03030303u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[16 * k + 4 * j + s] = ubyte(x, j);
+      }
+  } else {
+    static_for<32>([&](auto i) { f[i.value] = float(code_at<BITS, i.value>(w)); });
+  }
 }
 
 // mlx::dequantize for bf16: bf16(bf16(scale * code) + bias), two codes at a
-// time; out[i] holds codes 2i (low half) and 2i + 1.
+// time; out[i] holds codes 2i (low half) and 2i + 1. scale * code is exact in
+// f32 (8-bit by at most 8-bit significands), so each rounding is a single
+// RNE conversion, as in MLX's bf16 arithmetic.
 template <int BITS>
 __device__ __forceinline__ void dequant_run(const uint32_t* w, uint32_t sb, uint32_t* out) {
+  float f[32];
+  run_codes<BITS>(w, f);
   const float s = __uint_as_float(sb << 16), bias = __uint_as_float(sb & 0xffff0000u);
-  static_for<16>([&](auto i) {
-    const float c0 = float(code_at<BITS, 2 * i.value>(w));
-    const float c1 = float(code_at<BITS, 2 * i.value + 1>(w));
-    const uint32_t m = pack_bf16(s * c0, s * c1);
-    out[i.value] = pack_bf16(__uint_as_float(m << 16) + bias,
-                             __uint_as_float(m & 0xffff0000u) + bias);
-  });
-}
-
-// Writes the stage into LDS: K row `key` at channels [32 run, 32 run + 32),
-// and the same channels of V into column `key` of V^T. Keys past the end are
-// zero (their scores are masked; zero values keep 0 * v finite).
-template <int D, int BK, int BV>
-__device__ __forceinline__ void store_stage(const Stage<BK, BV>& st, uint16_t* Ks, uint16_t* Vt,
-                                            int key, int run) {
-  constexpr int KSTR = D + 8, VSTR = kTile + 8;
-  uint32_t kv[16], vv[16];
-  if (st.ok) {
-    dequant_run<BK>(st.kw, st.kp, kv);
-    dequant_run<BV>(st.vw, st.vp, vv);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) kv[i] = vv[i] = 0u;
-  }
-  u32x4_t* kd = reinterpret_cast<u32x4_t*>(Ks + key * KSTR + run * 32);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) kd[i] = u32x4_t{kv[4 * i], kv[4 * i + 1], kv[4 * i + 2], kv[4 * i + 3]};
-  uint16_t* vd = Vt + (run * 32) * VSTR + key;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    vd[(2 * i) * VSTR] = uint16_t(vv[i]);
-    vd[(2 * i + 1) * VSTR] = uint16_t(vv[i] >> 16);
+    const uint32_t m = pack_bf16(s * f[2 * i], s * f[2 * i + 1]);
+    out[i] = pack_bf16(__uint_as_float(m << 16) + bias, __uint_as_float(m & 0xffff0000u) + bias);
+  }
+}
+
+// Writes a K task into LDS: row `key` of K at channels [32 run, 32 run + 32).
+// Keys past the end are zero (their scores are masked).
+template <int D, int BITS, int NW>
+__device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int key, int run) {
+  constexpr int KSTR = kKStride<D>;
+  uint32_t v[16];
+  if (st.ok) {
+    dequant_run<BITS>(st.w, st.s | (st.b << 16), v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = 0u;
+  }
+  u32x4_t* d = reinterpret_cast<u32x4_t*>(Ks + key * KSTR + run * 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) d[i] = u32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+}
+
+// Writes a V task into column `key` of V^T, channels [32 run, 32 run + 32).
+// Keys past the end are zero (0 * v stays finite).
+template <int D, int BITS, int NW>
+__device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vt, int key, int run) {
+  constexpr int VSTR = kVStride;
+  uint32_t v[16];
+  if (st.ok) {
+    dequant_run<BITS>(st.w, st.s | (st.b << 16), v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = 0u;
+  }
+  uint16_t* d = Vt + (run * 32) * VSTR + key;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    d[(2 * i) * VSTR] = uint16_t(v[i]);
+    d[(2 * i + 1) * VSTR] = uint16_t(v[i] >> 16);
   }
 }
 
@@ -224,16 +302,25 @@ __global__ __launch_bounds__(Shape<D>::kWaves* kWave) __attribute__((amdgpu_wave
 void prefill_affine_kernel(const Args a) {
   constexpr int kWaves = Shape<D>::kWaves, RW = Shape<D>::kRW, kRows = Shape<D>::kRows;
   constexpr int NR = RW / 16, ND = D / 32, NT = D / 16;
-  constexpr int KSTR = D + 8, VSTR = kTile + 8;
-  static_assert(2 * D <= kWaves * kWave, "one loader task per thread");
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kTile * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VSTR];
+  constexpr int KSTR = kKStride<D>, VSTR = kVStride;
+  constexpr int kPer = Shape<D>::kPer, kThreads = Shape<D>::kThreads;
+  constexpr int NW = BK > BV ? BK : BV;
+  // Two tile buffers: tile t is read from one while tile t + 1 is written
+  // into the other, so a tile costs one barrier.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks2[2][kTile * KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt2[2][D * VSTR];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave, lr = lane % 16, lg = lane / 16;
-  const int blk = a.n_blocks - 1 - int(blockIdx.x);  // longest key ranges first
-  const int kvh = blockIdx.y, b = blockIdx.z;
+  // Workgroup i runs on XCD i % 8 (round-robin dispatch). Consecutive
+  // logical blocks, which share a (batch row, KV head) and so its keys, are
+  // placed on one XCD's L2; within a unit the longest key ranges go first.
+  const int n_wg = int(gridDim.x);
+  int lin = int(blockIdx.x);
+  if (n_wg % kXcds == 0) lin = (lin % kXcds) * (n_wg / kXcds) + lin / kXcds;
+  const int blk = a.n_blocks - 1 - lin % a.n_blocks;
+  const int kvh = (lin / a.n_blocks) % a.H_kv, b = lin / (a.n_blocks * a.H_kv);
   const int64_t rows = int64_t(a.L) * a.G;
   const int64_t row0 = int64_t(blk) * kRows;
   const int64_t row_end = row0 + kRows < rows ? row0 + kRows : rows;
@@ -275,16 +362,73 @@ void prefill_affine_kernel(const Args a) {
 
   if (kk_lo <= kk_hi) {
     const int64_t t_lo = kk_lo / kTile, t_hi = kk_hi / kTile;
-    const bool loader = tid < 2 * D;
-    const int key = tid % kTile, run = tid / kTile;
-    Stage<BK, BV> st;
-    st.ok = false;
-    if (loader) load_stage<D>(st, a, b, kvh, t_lo * kTile + key, run);
-    for (int64_t t = t_lo; t <= t_hi; ++t) {
-      __syncthreads();  // the previous tile's LDS reads are done
-      if (loader) store_stage<D>(st, Ks, Vt, key, run);
-      __syncthreads();
-      if (loader && t < t_hi) load_stage<D>(st, a, b, kvh, (t + 1) * kTile + key, run);
+    const SlabPtrs kp = slabs_for<D, BK>(a.seg[0], a.seg[1], a.seg[0].kw, a.seg[1].kw,
+                                         a.seg[0].ks, a.seg[1].ks, a.seg[0].kb, a.seg[1].kb,
+                                         a.gs, b, kvh);
+    const SlabPtrs vp = slabs_for<D, BV>(a.seg[0], a.seg[1], a.seg[0].vw, a.seg[1].vw,
+                                         a.seg[0].vs, a.seg[1].vs, a.seg[0].vb, a.seg[1].vb,
+                                         a.gs, b, kvh);
+    // Task i of this thread: tid + i * kThreads; the first 2D tasks are K
+    // runs, the rest V runs (a whole wavefront takes one kind, so the kind
+    // and its pointers are uniform).
+    Stage<NW> st[kPer];
+    SlabPtrs tp[kPer];
+    bool tv[kPer];
+    int tkey[kPer], trun[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int task = tid + i * kThreads, r = task % (2 * D);
+      tv[i] = wave * kWave + i * kThreads >= 2 * D;
+      tkey[i] = r % kTile;
+      trun[i] = r / kTile;
+      tp[i].w0 = tv[i] ? vp.w0 : kp.w0;
+      tp[i].w1 = tv[i] ? vp.w1 : kp.w1;
+      tp[i].s0 = tv[i] ? vp.s0 : kp.s0;
+      tp[i].s1 = tv[i] ? vp.s1 : kp.s1;
+      tp[i].b0 = tv[i] ? vp.b0 : kp.b0;
+      tp[i].b1 = tv[i] ? vp.b1 : kp.b1;
+    }
+#define TQKV_LOAD_TILE(T)                                                        \
+  _Pragma("unroll") for (int i = 0; i < kPer; ++i) {                             \
+    if (tv[i])                                                                   \
+      load_stage<D, BV>(st[i], tp[i], a, (T) * kTile + tkey[i], trun[i]);        \
+    else                                                                         \
+      load_stage<D, BK>(st[i], tp[i], a, (T) * kTile + tkey[i], trun[i]);        \
+  }
+#define TQKV_STORE_TILE(BUF)                                                     \
+  _Pragma("unroll") for (int i = 0; i < kPer; ++i) {                             \
+    if (tv[i])                                                                   \
+      store_v<D, BV>(st[i], Vt2[BUF], tkey[i], trun[i]);                         \
+    else                                                                         \
+      store_k<D, BK>(st[i], Ks2[BUF], tkey[i], trun[i]);                         \
+  }
+    TQKV_LOAD_TILE(int(t_lo))
+    // Everything loaded so far (the Q fragments, the first tile) has landed:
+    // without this the compiler's loop-carried wait analysis keeps the Q
+    // loads pending and makes every tile's MFMAs wait for the next tile's
+    // prefetch. (vmcnt(0); expcnt and lgkmcnt unchanged.)
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    TQKV_STORE_TILE(0)
+    if (t_lo < t_hi) {
+      TQKV_LOAD_TILE(int(t_lo) + 1)
+    }
+    __syncthreads();
+    // The two wavefronts on a SIMD (w and w + kWaves / 2) take the tile's
+    // work in opposite orders, so one's dequantization (VALU) runs while the
+    // other's products (MFMA) do.
+    const bool dequant_first = wave >= kWaves / 2;
+    int cur = 0;
+    for (int t = int(t_lo); t <= int(t_hi); ++t, cur ^= 1) {
+      // Tile t + 1 into the other buffer (last read in iteration t - 1,
+      // before the barrier that ended it), then fetch tile t + 2.
+      if (dequant_first && t < t_hi) {
+        TQKV_STORE_TILE(cur ^ 1)
+        if (t + 1 < t_hi) {
+          TQKV_LOAD_TILE(t + 2)
+        }
+      }
+      const uint16_t* Ks = Ks2[cur];
+      const uint16_t* Vt = Vt2[cur];
 
       f4_t sc[4][NR];
 #pragma unroll
@@ -301,31 +445,44 @@ void prefill_affine_kernel(const Args a) {
             sc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[j][s], sc[i][j], 0, 0, 0);
         }
 
-      const int64_t ka_lo = a.k_start + t * kTile;
-      const bool full = (t + 1) * kTile <= a.total &&
-                        (!a.causal || (ka_lo + kTile - 1 <= qa_lo &&
-                                       (a.window < 0 || qa_hi < ka_lo + a.window)));
+      // Mask: only on tiles some row of the block sees in part. Key offset
+      // o in the tile is visible to a row iff lo <= o <= hi.
+      const int64_t kbase = a.k_start + int64_t(t) * kTile;
+      const int rem = a.total - int64_t(t) * kTile < kTile ? int(a.total - int64_t(t) * kTile) : kTile;
+      const bool full = rem == kTile &&
+                        (!a.causal || (kbase + kTile - 1 <= qa_lo &&
+                                       (a.window < 0 || qa_hi < kbase + a.window)));
+      if (!full) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+          int hi = rem - 1, lo = 0;
+          if (a.causal) {
+            const int64_t dq = qabs[j] - kbase;  // the row's own offset
+            if (dq < hi) hi = dq < -1 ? -1 : int(dq);
+            if (a.window >= 0) {
+              const int64_t first = dq - a.window + 1;
+              lo = first < 0 ? 0 : (first > kTile ? kTile : int(first));
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int o = 16 * i + 4 * lg + r;
+              if (o < lo || o > hi) sc[i][j][r] = -INFINITY;
+            }
+        }
+      }
 #pragma unroll
       for (int j = 0; j < NR; ++j) {
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float v = sc[i][j][r] * a.qscale;
-            if (!full) {
-              const int64_t kk = t * kTile + 16 * i + 4 * lg + r;
-              const int64_t kabs = a.k_start + kk;
-              const bool vis = kk < a.total &&
-                               (!a.causal || (kabs <= qabs[j] &&
-                                              (a.window < 0 || qabs[j] < kabs + a.window)));
-              v = vis ? v : -INFINITY;
-            }
-            sc[i][j][r] = v;
-            mx = fmaxf(mx, v);
-          }
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[i][j][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        mx *= a.qscale;  // qscale > 0: the max of the scaled scores
         const bool up = mx > m[j] + kTau;
         if (__any(up)) {
           const float mn = up ? mx : m[j];
@@ -335,11 +492,12 @@ void prefill_affine_kernel(const Args a) {
           for (int t2 = 0; t2 < NT; ++t2) o[t2][j] *= alpha;
           m[j] = mn;
         }
-        const float mref = m[j] == -INFINITY ? 0.0f : m[j];
+        const float nm = m[j] == -INFINITY ? 0.0f : -m[j];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[i][j][r] = __builtin_amdgcn_exp2f(sc[i][j][r] - mref);
+          for (int r = 0; r < 4; ++r)
+            sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm));
       }
 
       const bf2_t kOnes = {__bf16(1.0f), __bf16(1.0f)};
@@ -369,9 +527,19 @@ void prefill_affine_kernel(const Args a) {
             o[t2][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[j], o[t2][j], 0, 0, 0);
         }
       }
+
+      if (!dequant_first && t < t_hi) {
+        TQKV_STORE_TILE(cur ^ 1)
+        if (t + 1 < t_hi) {
+          TQKV_LOAD_TILE(t + 2)
+        }
+      }
+      __syncthreads();
     }
   }
+#undef TQKV_STORE_TILE
 
+#undef TQKV_LOAD_TILE
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     float tot = lsum[j];
