@@ -38,6 +38,9 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget for the baseline sample")
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+                    help="decode: config 2 (the headline); prefill: config 3's "
+                         "2048-token chunk attention")
     return ap.parse_args()
 
 
@@ -52,6 +55,9 @@ def main():
 
     hip = T.hip()
     hip._ok(hip.h.hipSetDevice(0), "hipSetDevice")
+    if args.workload == "prefill":
+        prefill_main(T, hip, args)
+        return
     B, H, HKV, D, N, GS, BITS = args.batch, 16, 8, 256, args.context, 64, 3
     scale = D ** -0.5
     steps, warmup = args.steps, args.warmup
@@ -218,6 +224,137 @@ def cpu_baseline(T, cache, q, out, B, H, HKV, D, N, GS, BITS, scale, cap, budget
         "sample": f"{n_seq} of {B} sequences of the same cache, {HKV} KV heads x {N} tokens each "
                   f"(median {per_seq:.3f} s per sequence-step); C++ restatement of "
                   "dequantize-then-attend, OpenMP over heads",
+    }
+
+
+PEAK_BF16_TFLOPS = 2500.0
+PREFILL_METRIC = "quantized-KV prefill chunk attention tokens/s (MFMA bf16)"
+
+
+def visible_pairs(L, N, q_start, k_start, window):
+    """(query row, key) pairs the absolute-position mask lets through."""
+    qa = q_start + np.arange(L, dtype=np.int64)
+    lo = np.full(L, k_start, np.int64) if window < 0 else np.maximum(k_start, qa - window + 1)
+    hi = np.minimum(qa, k_start + N - 1)
+    return int(np.maximum(hi - lo + 1, 0).sum())
+
+
+def prefill_main(T, hip, args):
+    """BASELINE config 3's prefill: 2048-token chunks over a 4-bit gs64
+    cache, B=4, 32 query / 8 KV heads, D=128, scale 1.0 (Gemma). The timed
+    step is one chunk attention of a global layer at its last chunk (16,384
+    keys, causal); the sliding layer's chunk (3,071 held keys, window 1024)
+    is reported beside it. Algorithmic FLOPs = 4 * D * visible (row, key)
+    pairs per head (QK^T and PV)."""
+    B, H, HKV, D, L, GS, BITS = 4, 32, 8, 128, 2048, 64, 4
+    N_G, N_L, W = 16384, 1023 + 2048, 1024
+    stream = hip.stream()
+    slabs, words, groups = B * HKV, D * BITS // 32, D // GS
+
+    def cache(N, seed):
+        trip = {}
+        tmp = T.DeviceArray((slabs, 1024, D), np.uint16)
+        for name, sd in (("k", seed), ("v", seed + 1)):
+            t3 = (T.DeviceArray((slabs, N, words), np.uint32),
+                  T.DeviceArray((slabs, N, groups), np.uint16),
+                  T.DeviceArray((slabs, N, groups), np.uint16))
+            for c0 in range(0, N, 1024):
+                n = min(1024, N - c0)
+                T.synth_bf16(tmp.ptr, slabs * n, D, sd * 1000003 + c0, 0.01, 10.0, stream)
+                T.affine_quantize(tmp.ptr, slabs, n, D, GS, BITS, *(a.ptr for a in t3), N, c0,
+                                  stream)
+            trip[name] = t3
+        return trip
+
+    cg, cl = cache(N_G, 11), cache(N_L, 21)
+    q = T.DeviceArray((B, H, L, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H * L, D, 33, 0.0, 1.0, stream)
+    out = T.DeviceArray((B, H, L, D), np.uint16)
+    seg_g = T.affine_seg(tuple(a.ptr for a in cg["k"]), tuple(a.ptr for a in cg["v"]), N_G, N_G)
+    seg_l = T.affine_seg(tuple(a.ptr for a in cl["k"]), tuple(a.ptr for a in cl["v"]), N_L, N_L)
+    qs_g, ks_g = N_G - L, 0                 # last chunk of a 16,384-token prompt
+    qs_l, ks_l = N_G - L, N_G - N_L         # the ring's view: newest 1023 + the chunk
+
+    def run(seg, qs, ks, win):
+        T.prefill_attend_affine(q.ptr, B, H, HKV, L, D, GS, BITS, BITS, 1.0, [seg], out.ptr,
+                                qs, ks, True, win, stream)
+
+    def timed(seg, qs, ks, win, n):
+        evs = [(hip.event(), hip.event()) for _ in range(n)]
+        for a, b in evs:
+            hip.record(a, stream)
+            run(seg, qs, ks, win)
+            hip.record(b, stream)
+        hip.sync()
+        return [hip.elapsed_ms(a, b) for a, b in evs]
+
+    for _ in range(args.warmup):
+        run(seg_g, qs_g, ks_g, -1)
+    hip.sync()
+    t0, t1 = hip.event(), hip.event()
+    hip.record(t0, stream)
+    for _ in range(args.steps):
+        run(seg_g, qs_g, ks_g, -1)
+    hip.record(t1, stream)
+    total_ms = hip.elapsed_ms(t0, t1)
+    ms_g = float(np.mean(timed(seg_g, qs_g, ks_g, -1, max(3, args.steps // 4))))
+    ms_l = float(np.mean(timed(seg_l, qs_l, ks_l, W, max(3, args.steps // 4))))
+    fl_g = 4.0 * D * visible_pairs(L, N_G, qs_g, ks_g, -1) * B * H
+    fl_l = 4.0 * D * visible_pairs(L, N_L, qs_l, ks_l, W) * B * H
+    tf_g = fl_g / (ms_g * 1e-3) / 1e12
+    ms_per_step = total_ms / args.steps
+    o = (out.numpy().astype(np.uint32) << 16).view(np.float32)
+    assert np.all(np.isfinite(o)) and np.abs(o).max() > 0, "prefill output is not sane"
+    result = {
+        "metric": PREFILL_METRIC,
+        "value": round(B * L / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 3: one 2048-token prefill chunk attention of a "
+                        "global layer at 16,384 keys (causal), over a 4-bit gs64 cache",
+            "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "chunk": L,
+            "keys": N_G, "bits_k": BITS, "bits_v": BITS, "group_size": GS,
+        },
+        "roofline": {
+            "bound": "mfma", "achieved": round(tf_g, 1), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tf_g / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "kernel": "prefill_affine_kernel<128,4,4>",
+            "alg_flops_per_launch": fl_g, "avg_launch_ms": round(ms_g, 5),
+        },
+        "sliding_layer_chunk": {
+            "keys": N_L, "window": W, "avg_launch_ms": round(ms_l, 5),
+            "tflops": round(fl_l / (ms_l * 1e-3) / 1e12, 1),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = prefill_cpu_baseline(T, cg, q, B, H, HKV, D, L, N_G, GS, BITS,
+                                                      qs_g)
+    print(json.dumps(result))
+
+
+def prefill_cpu_baseline(T, cg, q, B, H, HKV, D, L, N, GS, BITS, q_start):
+    """The oracle's dequantize(bf16)-then-attend on the last 32 query rows of
+    batch row 0 (all heads, all 16,384 keys): tokens/s = rows / time."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    rows = 32
+    qh = q.numpy()[0:1, :, L - rows:]
+    kt = tuple(np.ascontiguousarray(a.numpy().reshape(B, HKV, N, -1)[0:1]) for a in cg["k"])
+    vt = tuple(np.ascontiguousarray(a.numpy().reshape(B, HKV, N, -1)[0:1]) for a in cg["v"])
+    t = time.perf_counter()
+    O.attend_affine(np.ascontiguousarray(qh), kt, vt, GS, BITS, BITS, 1.0, causal=True,
+                    q_start=q_start + L - rows, first_held=0, dequant="bf16")
+    dt = time.perf_counter() - t
+    return {
+        "value": round(rows / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": f"last {rows} query rows of batch row 0, {H} heads x {N} keys "
+                  f"({dt:.2f} s); C++ restatement of dequantize(bf16)-then-attend",
     }
 
 
