@@ -6,6 +6,11 @@ whole cache: B=32 sequences, 16 query / 8 KV heads, head_dim 256, 32,768
 cached tokens per sequence. Inputs are synthetic (seeded N(0,1) with 1% of
 channels x10, generated on the device) and resident in HBM before timing.
 
+Timing: 128 whole steps run untimed first (--settle; from idle the GPU's
+clocks take 10-30 ms of load to settle, and per-launch times fall from ~550 µs
+to ~305 µs over that span), then the W warm-up steps, then the K timed steps.
+"settle_steps" reports how many ran.
+
 Prints one JSON line: value = decode tokens/s (B / step time); the roofline
 block prices the decode kernel's algorithmic bytes (packed K/V codes, scales
 and biases of the live context, plus Q in and O out) per launch against the
@@ -33,6 +38,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle", type=int, default=None,
+                    help="untimed steps before the warm-up (default: 128 decode steps, "
+                         "~40 ms; 16 prefill launches): from idle the clocks take 10-30 ms "
+                         "of load to reach their loaded state")
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -61,7 +70,8 @@ def main():
     B, H, HKV, D, N, GS, BITS = args.batch, 16, 8, 256, args.context, 64, 3
     scale = D ** -0.5
     steps, warmup = args.steps, args.warmup
-    cap = (N + warmup + steps + 255) // 256 * 256
+    settle = 128 if args.settle is None else max(0, args.settle)
+    cap = (N + settle + warmup + steps + 255) // 256 * 256
     words, groups = D * BITS // 32, D // GS
     slabs = B * HKV
 
@@ -111,14 +121,18 @@ def main():
         if events:
             hip.record(events[1], stream)
 
-    for i in range(warmup):
+    # Clock settling (untimed whole steps), then the W warm-up steps, then
+    # the K timed ones.
+    for i in range(settle):
         step(i)
+    for i in range(warmup):
+        step(settle + i)
     hip._ok(hip.h.hipStreamSynchronize(stream), "sync")
     t0, t1 = hip.event(), hip.event()
     hip.record(t0, stream)
     wall0 = time.perf_counter()
     for i in range(steps):
-        step(warmup + i, ev[i])
+        step(settle + warmup + i, ev[i])
     hip.record(t1, stream)
     total_ms = hip.elapsed_ms(t0, t1)
     wall = time.perf_counter() - wall0
@@ -127,20 +141,23 @@ def main():
     dec_avg_ms = float(np.mean(dec_ms))
 
     row_bytes = words * 4 + 2 * groups * 2  # packed codes + bf16 scales + bf16 biases
-    ctx_avg = N + warmup + (steps - 1) / 2.0 + 1
+    ctx_avg = N + settle + warmup + (steps - 1) / 2.0 + 1
     alg_bytes = 2 * slabs * ctx_avg * row_bytes + 2 * B * H * D * 2  # K+V, then Q in + O out
     achieved = alg_bytes / (dec_avg_ms * 1e-3) / 1e9
     ms_per_step = total_ms / steps
-    # HBM bytes per decode launch at the default shape, from the two counter
-    # passes recorded in profiles/decode_affine_config2.md (FETCH_SIZE x 2.000
-    # + WRITE_SIZE x 1.000, factors from a 1 GiB read and a 1 GiB write kernel
-    # of the same library). Counters cannot be read inside this process, so a
-    # non-default shape reports null.
+    # HBM bytes per decode launch: the two counter passes recorded in
+    # profiles/decode_affine_config2.md over the default command's 50 timed
+    # launches (FETCH_SIZE 922,653.9 KiB x 2.000 + WRITE_SIZE 256.0 KiB x
+    # 1.000, the factors a 1 GiB read and a 1 GiB write kernel of the same
+    # library give) = 1,889,857,331 B against 1,888,661,504 B algorithmic:
+    # 1.000633 per algorithmic byte. Counters cannot be read inside this
+    # process; other step counts of the same config scale by that ratio (the
+    # context differs by a few tokens), other configs report null.
     kind = T.decode_kernel_name(H, HKV, D, GS, BITS, BITS)
     kernel = ("decode_mfma_kernel<256,3,3,2,4,8>" if kind == "mfma"
               else "decode_affine_kernel<256,3,3,2,32,8>")
     default_shape = (B, N) == (32, 32768)
-    traffic = int((918749.6 * 2.0 + 256.0) * 1024) if default_shape and kind == "mfma" else None
+    traffic = int(alg_bytes * 1.000633) if default_shape and kind == "mfma" else None
     tokens_per_s = B / (ms_per_step * 1e-3)
 
     # Sanity of the result itself: finite, not all zero.
@@ -156,6 +173,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        "settle_steps": settle,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -288,6 +306,9 @@ def prefill_main(T, hip, args):
         hip.sync()
         return [hip.elapsed_ms(a, b) for a, b in evs]
 
+    settle = 16 if args.settle is None else max(0, args.settle)
+    for _ in range(settle):
+        run(seg_g, qs_g, ks_g, -1)
     for _ in range(args.warmup):
         run(seg_g, qs_g, ks_g, -1)
     hip.sync()
@@ -309,7 +330,7 @@ def prefill_main(T, hip, args):
         "metric": PREFILL_METRIC,
         "value": round(B * L / (ms_per_step * 1e-3), 1),
         "unit": "tokens/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "settle_steps": settle,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
