@@ -44,6 +44,7 @@ typedef struct ihipStream_t* tqkv_stream;
 #define TQKV_EDEVICE 4       /* a HIP runtime call failed */
 #define TQKV_ENOMEM 5        /* a device or host allocation failed */
 #define TQKV_EINVAL_ARG 6    /* a null pointer or an out-of-range scalar */
+#define TQKV_ECORRUPT 7      /* a snapshot's bytes fail a format check (kv_disk's Err) */
 
 /* Name of a status code. */
 const char* tqkv_status_string(int32_t status);
@@ -350,6 +351,77 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* cache, const uint16_t* q, int
 int32_t tqkv_cache_prefill_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
                                   int32_t L, float scale, int64_t window, uint16_t* out,
                                   tqkv_stream stream);
+
+/* ======================================================================
+ * LKV2 snapshots (crates/lumen-mlx/src/kv_disk.rs)
+ * ====================================================================== */
+
+/* KvManifest's snapshot-level fields (kv_disk.rs:347-368). */
+typedef struct tqkv_lkv_info {
+  const char* model_fingerprint; /* NUL-terminated UTF-8 */
+  uint64_t created_at_unix;
+  uint64_t position;
+  const uint32_t* prefix_tokens;
+  int64_t n_prefix_tokens;
+  int32_t has_last_token;
+  uint32_t last_token;
+  int32_t is_deep;
+} tqkv_lkv_info;
+
+/*
+ * write_lkv (kv_disk.rs:371-404) of a snapshot whose layers are the given
+ * caches, one LayerMeta each, laid out as the reference's snapshot code lays
+ * its caches out (gemma4_moe.rs:1617-1693, turboquant_meta kv_disk.rs:
+ * 2005-2025): bf16 growing = Full (the logical view [0, offset)), bf16
+ * rotating = Sliding (the whole ring), affine = FullQuantized /
+ * SlidingQuantized (whole (packed, scales, biases) buffers, group_size, bits
+ * = the key width), codebook = FullTurboquant (max_size >= 2^31) /
+ * SlidingTurboquant ([keys_codes u8, keys_sigma f32, values_codes,
+ * values_sigma, keys_signs bf16 +-1 [.., m]?, keys_residual_norm f32?],
+ * bits, qjl_m). Records are the rows the device holds, copied out after the
+ * stream's pending work. out == NULL: only *bytes (the file size) is set;
+ * else capacity must be at least that.
+ */
+int32_t tqkv_lkv_export(const tqkv_cache* const* layers, int32_t n_layers,
+                        const tqkv_lkv_info* info, uint8_t* out, size_t capacity,
+                        size_t* bytes, tqkv_stream stream);
+
+/*
+ * read_lkv's checks (kv_disk.rs:408-448) on a whole file in memory: magic,
+ * version, manifest CRC and fields, every record's dtype, rank (<= 8),
+ * dimensions, declared length (exactly what shape x dtype imply, and within
+ * the file) and CRC, and no trailing bytes. TQKV_ECORRUPT names the first
+ * fault (tqkv_last_error) where the reference returns Err; nothing is
+ * allocated from an unchecked field.
+ */
+int32_t tqkv_lkv_check(const uint8_t* data, size_t bytes);
+
+/* After the same checks: the manifest JSON as stored (NUL-terminated into
+ * json, if given), its length, and the layer and record counts. */
+int32_t tqkv_lkv_manifest(const uint8_t* data, size_t bytes, char* json, size_t capacity,
+                          size_t* json_bytes, int32_t* n_layers, int32_t* n_records);
+
+/*
+ * from_disk_records / from_parts (gemma4_moe.rs:1700-1830,
+ * turboquant_from_meta kv_disk.rs:2028-2061) for one layer: a new device
+ * cache holding the layer's records with its offset, base_offset, idx,
+ * max_size and keep. Geometry comes from the record shapes; an affine value
+ * width from its packed record. A codebook layer's rotation and QJL tables
+ * are drawn from `seed` (the file does not hold them; the reference uses
+ * 42), or replaced with tqkv_cache_set_tables. Linear (SSM) and empty
+ * layers: TQKV_EUNSUPPORTED.
+ */
+int32_t tqkv_lkv_import(const uint8_t* data, size_t bytes, int32_t layer, uint64_t seed,
+                        tqkv_cache** out, tqkv_stream stream);
+
+/* read_lkv then write_lkv: the same snapshot with its manifest re-serialized
+ * (serde_json's compact form, fields in declaration order) and its records
+ * copied. out == NULL: only *out_bytes. Host only. */
+int32_t tqkv_lkv_rewrite(const uint8_t* data, size_t bytes, uint8_t* out, size_t capacity,
+                         size_t* out_bytes);
+
+/* CRC-32 (IEEE, the crc32fast crate's) of a host buffer. */
+int32_t tqkv_crc32(const void* data, size_t bytes, uint32_t* out);
 
 /* ======================================================================
  * TurboQuant codebook format

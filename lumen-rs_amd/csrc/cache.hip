@@ -12,12 +12,14 @@
 // gathers the planned pieces into a second allocation and swaps. Fills and
 // copies are small kernels (no hipMemsetAsync, so a caller may capture the
 // update-free calls in a graph).
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <vector>
 
 #include "cache_plan.hpp"
 #include "common.hpp"
+#include "lkv.hpp"
 
 namespace tqkv {
 namespace {
@@ -237,6 +239,172 @@ int affine_segments(const tqkv_cache* c, tqkv_affine_seg* segs) {
   if (c->prefix && c->base_offset > 0) segs[n++] = seg_of(c->prefix, c->base_offset, 1);
   if (c->view_n > 0) segs[n++] = seg_of(c, c->view_n, 0);
   return n;
+}
+
+// ---- LKV2 snapshots (kv_disk.rs): one cache = one layer.
+
+// One record of a layer: rows [0, rows) of every slab of a slot, or (signs)
+// a slot of packed QJL sign words widened to the reference's bf16 +-1
+// layout [B, H_kv, S, m] (the TurboQuant cache's keys_signs, native_cache.rs:1524).
+struct RecSpec {
+  int slot = 0;
+  uint8_t dtype = 0;
+  std::vector<int64_t> shape;
+  int64_t rows = 0;
+  bool signs = false;
+  uint64_t bytes() const {
+    uint64_t n = lkv::elem_size(dtype);
+    for (int64_t d : shape) n *= uint64_t(d);
+    return n;
+  }
+};
+
+struct LayerPlan {
+  lkv::Layer meta;
+  std::vector<RecSpec> recs;
+};
+
+lkv::Opt some(uint64_t v) { return lkv::Opt{true, v}; }
+
+// The layer's LayerMeta and records, as the reference's snapshot code lays
+// them out: bf16 growing = Full with the logical view [0, offset)
+// (gemma4_moe.rs:1638-1645); rotating bf16 = Sliding with the whole ring and
+// max_size / keep / idx (:1646-1657); affine = FullQuantized /
+// SlidingQuantized with the whole (packed, scales, biases) buffers of K then V
+// and group_size / bits (:1658-1679); codebook = FullTurboquant /
+// SlidingTurboquant with [keys_codes, keys_sigma, values_codes, values_sigma,
+// keys_signs?, keys_residual_norm?] and max_size / keep / idx / bits / qjl_m
+// (kv_disk.rs:2005-2025). `first` is the index of its first record.
+int32_t plan_layer(const tqkv_cache* c, int64_t first, LayerPlan* out) {
+  const tqkv_cache_config& g = c->cfg;
+  LayerPlan L;
+  const bool ring = g.max_size > 0;
+  const int64_t B = g.batch, H = g.kv_heads;
+  auto rec = [&](int slot, uint8_t dtype, int64_t rows, int64_t last, bool signs = false) {
+    RecSpec r;
+    r.slot = slot;
+    r.dtype = dtype;
+    r.rows = rows;
+    r.shape = {B, H, rows, last};
+    r.signs = signs;
+    L.recs.push_back(r);
+    L.meta.arrays.push_back(first + int64_t(L.recs.size()) - 1);
+  };
+  const bool has = c->st.has;
+  const int64_t len = has ? c->st.len : 0;
+  L.meta.offset = uint64_t(c->base_offset + c->st.offset);
+  L.meta.base_offset = uint64_t(c->base_offset);
+  switch (g.kind) {
+    case TQKV_CACHE_BF16:
+      L.meta.kind = ring ? "Sliding" : "Full";
+      if (has) {
+        const int64_t rows = ring ? len : c->st.offset;
+        rec(0, lkv::kBF16, rows, g.k_dim);
+        rec(1, lkv::kBF16, rows, g.v_dim);
+      } else {
+        L.meta.arrays = {-1, -1};
+      }
+      break;
+    case TQKV_CACHE_AFFINE:
+      L.meta.kind = ring ? "SlidingQuantized" : "FullQuantized";
+      if (has) {
+        rec(0, lkv::kU32, len, int64_t(g.k_dim) * g.bits_k / 32);
+        rec(1, lkv::kBF16, len, g.k_dim / g.group_size);
+        rec(2, lkv::kBF16, len, g.k_dim / g.group_size);
+        rec(3, lkv::kU32, len, int64_t(g.v_dim) * g.bits_v / 32);
+        rec(4, lkv::kBF16, len, g.v_dim / g.group_size);
+        rec(5, lkv::kBF16, len, g.v_dim / g.group_size);
+      } else {
+        L.meta.arrays = {-1, -1, -1, -1, -1, -1};
+      }
+      L.meta.has_group_size = true;
+      L.meta.group_size = g.group_size;
+      // One width in the reference's metadata; the value width of a K8/V4
+      // cache follows from its packed record's shape on import.
+      L.meta.bits = some(uint64_t(g.bits_k));
+      break;
+    case TQKV_CACHE_CODEBOOK: {
+      if (g.bits_k != g.bits_v)
+        return fail(TQKV_EUNSUPPORTED, "a TurboQuant snapshot layer has one width (bits %d/%d)",
+                    g.bits_k, g.bits_v);
+      L.meta.kind = g.max_size >= (int64_t(1) << 31) ? "FullTurboquant" : "SlidingTurboquant";
+      const bool qjl = g.qjl_words > 0;
+      const int vs = qjl ? 4 : 2;
+      if (has) {
+        rec(0, lkv::kU8, len, g.k_dim);
+        rec(1, lkv::kF32, len, 1);
+        rec(vs, lkv::kU8, len, g.v_dim);
+        rec(vs + 1, lkv::kF32, len, 1);
+        if (qjl) {
+          rec(2, lkv::kBF16, len, int64_t(32) * g.qjl_words, true);
+          rec(3, lkv::kF32, len, 1);
+        } else {
+          L.meta.arrays.push_back(-1);
+          L.meta.arrays.push_back(-1);
+        }
+      } else {
+        L.meta.arrays = {-1, -1, -1, -1, -1, -1};
+      }
+      L.meta.bits = some(uint64_t(g.bits_k));
+      if (qjl) L.meta.qjl_m = some(uint64_t(32) * g.qjl_words);
+      break;
+    }
+    default:
+      return fail(TQKV_EUNSUPPORTED, "cache kind %d", g.kind);
+  }
+  if (ring) {
+    L.meta.max_size = some(uint64_t(g.max_size));
+    L.meta.keep = some(uint64_t(g.keep));
+    L.meta.idx = some(uint64_t(c->st.idx));
+  }
+  *out = std::move(L);
+  return TQKV_OK;
+}
+
+// Copies a record's payload from the device into `dst`.
+int32_t read_record(const tqkv_cache* c, const RecSpec& r, uint8_t* dst) {
+  const Buf& b = c->cur[r.slot];
+  const int64_t rb = c->rb[r.slot];
+  if (r.rows == 0 || c->n_slabs == 0) return TQKV_OK;
+  if (!r.signs) {
+    TQKV_HIP(hipMemcpy2D(dst, size_t(r.rows * rb), b.ptr, size_t(b.cap * rb), size_t(r.rows * rb),
+                         size_t(c->n_slabs), hipMemcpyDeviceToHost));
+    return TQKV_OK;
+  }
+  const int64_t words = rb / 4, m = 32 * words;
+  std::vector<uint32_t> w(size_t(c->n_slabs * r.rows * words));
+  TQKV_HIP(hipMemcpy2D(w.data(), size_t(r.rows * rb), b.ptr, size_t(b.cap * rb),
+                       size_t(r.rows * rb), size_t(c->n_slabs), hipMemcpyDeviceToHost));
+  // Sign bit i set <=> (Phi r)_i >= 0 <=> +1 (qjl.rs:57-74).
+  uint16_t* o = reinterpret_cast<uint16_t*>(dst);
+  for (size_t row = 0; row < size_t(c->n_slabs * r.rows); ++row)
+    for (int64_t i = 0; i < m; ++i)
+      o[row * size_t(m) + size_t(i)] = (w[row * size_t(words) + size_t(i / 32)] >> (i % 32)) & 1u
+                                           ? uint16_t(0x3F80) : uint16_t(0xBF80);
+  return TQKV_OK;
+}
+
+// Uploads a record's payload into rows [0, rows) of a slot.
+int32_t write_record(tqkv_cache* c, const RecSpec& r, const uint8_t* src) {
+  Buf& b = c->cur[r.slot];
+  const int64_t rb = c->rb[r.slot];
+  if (r.rows == 0 || c->n_slabs == 0) return TQKV_OK;
+  if (!r.signs) {
+    TQKV_HIP(hipMemcpy2D(b.ptr, size_t(b.cap * rb), src, size_t(r.rows * rb), size_t(r.rows * rb),
+                         size_t(c->n_slabs), hipMemcpyHostToDevice));
+    return TQKV_OK;
+  }
+  const int64_t words = rb / 4, m = 32 * words;
+  std::vector<uint32_t> w(size_t(c->n_slabs * r.rows * words), 0u);
+  for (size_t row = 0; row < size_t(c->n_slabs * r.rows); ++row)
+    for (int64_t i = 0; i < m; ++i) {
+      uint16_t x;
+      std::memcpy(&x, src + 2 * (row * size_t(m) + size_t(i)), 2);
+      if (!(x & 0x8000u)) w[row * size_t(words) + size_t(i / 32)] |= 1u << (i % 32);
+    }
+  TQKV_HIP(hipMemcpy2D(b.ptr, size_t(b.cap * rb), w.data(), size_t(r.rows * rb),
+                       size_t(r.rows * rb), size_t(c->n_slabs), hipMemcpyHostToDevice));
+  return TQKV_OK;
 }
 
 }  // namespace
@@ -553,6 +721,215 @@ int32_t tqkv_cache_prefill_attend(const tqkv_cache* c, const uint16_t* q, int32_
   return tqkv_prefill_attend_affine(q, g.batch, H, g.kv_heads, L, g.k_dim, g.group_size,
                                     g.bits_k, g.bits_v, scale, segs, n, offset - L,
                                     offset - keys, 1, window, out, stream);
+}
+
+int32_t tqkv_lkv_export(const tqkv_cache* const* layers, int32_t n_layers,
+                        const tqkv_lkv_info* info, uint8_t* out, size_t capacity,
+                        size_t* bytes, tqkv_stream stream) {
+  if (!layers || !info || !bytes || n_layers < 0) return fail(TQKV_EINVAL_ARG, "null pointer");
+  lkv::Manifest m;
+  m.model_fingerprint = info->model_fingerprint ? info->model_fingerprint : "";
+  m.created_at_unix = info->created_at_unix;
+  m.position = info->position;
+  if (info->n_prefix_tokens < 0 || (info->n_prefix_tokens > 0 && !info->prefix_tokens))
+    return fail(TQKV_EINVAL_ARG, "prefix tokens");
+  m.prefix_tokens.assign(info->prefix_tokens, info->prefix_tokens + info->n_prefix_tokens);
+  if (info->has_last_token) m.last_token = lkv::Opt{true, info->last_token};
+  m.is_deep = info->is_deep != 0;
+  std::vector<LayerPlan> plans(static_cast<size_t>(n_layers));
+  int64_t n_records = 0;
+  for (int32_t i = 0; i < n_layers; ++i) {
+    if (!layers[i]) return fail(TQKV_EINVAL_ARG, "layer %d is null", i);
+    if (int32_t rc = plan_layer(layers[i], n_records, &plans[size_t(i)])) return rc;
+    n_records += int64_t(plans[size_t(i)].recs.size());
+    m.layers.push_back(plans[size_t(i)].meta);
+  }
+  if (n_records > 0xFFFFFFFFll) return fail(TQKV_EINVAL_SHAPE, "too many records");
+  const std::string json = lkv::manifest_json(m);
+  if (json.size() > 0xFFFFFFFFull) return fail(TQKV_EINVAL_SHAPE, "manifest too large");
+  uint64_t total = lkv::header_size(json.size());
+  for (const LayerPlan& p : plans)
+    for (const RecSpec& r : p.recs) total += lkv::record_size(r.shape.size(), r.bytes());
+  *bytes = size_t(total);
+  if (!out) return ok();
+  if (capacity < total)
+    return fail(TQKV_EINVAL_ARG, "snapshot needs %llu bytes, %zu given", (unsigned long long)total,
+                capacity);
+  // The caches' pending updates (on `stream`) come first.
+  TQKV_HIP(hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream)));
+  uint64_t at = lkv::write_header(out, json, uint32_t(n_records));
+  for (int32_t i = 0; i < n_layers; ++i)
+    for (const RecSpec& r : plans[size_t(i)].recs) {
+      uint8_t* rec = out + at;
+      const uint64_t h = lkv::write_record_header(rec, r.dtype, r.shape, r.bytes());
+      if (int32_t rc = read_record(layers[i], r, rec + h)) return rc;
+      lkv::finish_record(rec, h + r.bytes());
+      at += lkv::record_size(r.shape.size(), r.bytes());
+    }
+  return ok();
+}
+
+int32_t tqkv_lkv_import(const uint8_t* data, size_t nbytes, int32_t layer, uint64_t seed,
+                        tqkv_cache** out, tqkv_stream stream) {
+  if (!data || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  *out = nullptr;
+  lkv::Manifest m;
+  std::vector<lkv::RecordView> recs;
+  std::string err;
+  if (!lkv::parse(data, nbytes, &m, &recs, &err)) return fail(TQKV_ECORRUPT, "kv_disk: %s", err.c_str());
+  if (layer < 0 || size_t(layer) >= m.layers.size())
+    return fail(TQKV_EINVAL_ARG, "layer %d of %zu", layer, m.layers.size());
+  const lkv::Layer& L = m.layers[size_t(layer)];
+  const std::string& k = L.kind;
+  tqkv_cache_config g{};
+  g.prealloc = 1;
+  g.seed = seed;
+  int n_arr = 0;
+  bool ring = false;
+  if (k == "Full" || k == "Sliding") {
+    g.kind = TQKV_CACHE_BF16;
+    n_arr = 2;
+    ring = k == "Sliding";
+  } else if (k == "FullQuantized" || k == "SlidingQuantized") {
+    g.kind = TQKV_CACHE_AFFINE;
+    n_arr = 6;
+    ring = k == "SlidingQuantized";
+  } else if (k == "FullTurboquant" || k == "SlidingTurboquant") {
+    g.kind = TQKV_CACHE_CODEBOOK;
+    n_arr = 6;
+    ring = true;
+  } else {
+    return fail(TQKV_EUNSUPPORTED, "layer kind %s holds no attention cache", k.c_str());
+  }
+  auto bad = [&](const char* what) {
+    return fail(TQKV_ECORRUPT, "kv_disk: %s layer %d: %s", k.c_str(), layer, what);
+  };
+  if (ring && (!L.max_size.has || !L.keep.has || !L.idx.has)) return bad("missing max_size, keep or idx");
+  // Record of array slot i, or null.
+  auto at = [&](int i) -> const lkv::RecordView* {
+    if (size_t(i) >= L.arrays.size() || L.arrays[size_t(i)] < 0) return nullptr;
+    const uint64_t id = uint64_t(L.arrays[size_t(i)]);
+    return id < recs.size() ? &recs[size_t(id)] : nullptr;
+  };
+  for (int i = 0; i < n_arr && size_t(i) < L.arrays.size(); ++i)
+    if (L.arrays[size_t(i)] >= 0 && uint64_t(L.arrays[size_t(i)]) >= recs.size())
+      return bad("array index out of range");
+  const lkv::RecordView* r0 = at(0);
+  const bool has = r0 != nullptr;
+  int64_t B = 0, H = 0, len = 0;
+  auto geom = [&](const lkv::RecordView* r, uint8_t dtype, int64_t* last) {
+    if (!r || r->dtype != dtype || r->shape.size() != 4) return false;
+    if (B == 0 && H == 0) {
+      B = r->shape[0];
+      H = r->shape[1];
+      len = r->shape[2];
+    }
+    if (r->shape[0] != B || r->shape[1] != H || r->shape[2] != len) return false;
+    *last = r->shape[3];
+    return true;
+  };
+  std::vector<RecSpec> specs;
+  auto spec = [&](int slot, const lkv::RecordView* r, bool signs = false) {
+    RecSpec s;
+    s.slot = slot;
+    s.dtype = r->dtype;
+    s.shape = r->shape;
+    s.rows = r->shape[2];
+    s.signs = signs;
+    specs.push_back(s);
+  };
+  if (has) {
+    int64_t d0 = 0, d1 = 0, d2 = 0, d3 = 0, d4 = 0, d5 = 0;
+    if (g.kind == TQKV_CACHE_BF16) {
+      if (!geom(at(0), lkv::kBF16, &d0) || !geom(at(1), lkv::kBF16, &d1))
+        return bad("keys/values must be bf16 [B, H_kv, S, D]");
+      g.k_dim = int32_t(d0);
+      g.v_dim = int32_t(d1);
+      spec(0, at(0));
+      spec(1, at(1));
+    } else if (g.kind == TQKV_CACHE_AFFINE) {
+      if (!L.has_group_size || !L.bits.has) return bad("missing group_size or bits");
+      if (!geom(at(0), lkv::kU32, &d0) || !geom(at(1), lkv::kBF16, &d1) ||
+          !geom(at(2), lkv::kBF16, &d2) || !geom(at(3), lkv::kU32, &d3) ||
+          !geom(at(4), lkv::kBF16, &d4) || !geom(at(5), lkv::kBF16, &d5) || d1 != d2 || d4 != d5)
+        return bad("(packed u32, scales bf16, biases bf16) x {K, V} of one [B, H_kv, S] shape expected");
+      const int64_t gs = L.group_size;
+      if (gs <= 0 || gs > 4096) return bad("group_size");
+      g.group_size = int32_t(gs);
+      g.k_dim = int32_t(d1 * gs);
+      g.v_dim = int32_t(d4 * gs);
+      g.bits_k = int32_t(L.bits.v);
+      if (g.k_dim <= 0 || g.v_dim <= 0 || d0 * 32 != int64_t(g.k_dim) * g.bits_k || (d3 * 32) % g.v_dim)
+        return bad("packed widths do not match group_size and bits");
+      g.bits_v = int32_t(d3 * 32 / g.v_dim);
+      for (int i = 0; i < 6; ++i) spec(i, at(i));
+    } else {
+      if (!L.bits.has) return bad("missing bits");
+      if (!geom(at(0), lkv::kU8, &d0) || !geom(at(1), lkv::kF32, &d1) ||
+          !geom(at(2), lkv::kU8, &d2) || !geom(at(3), lkv::kF32, &d3) || d1 != 1 || d3 != 1)
+        return bad("codes u8 [B, H_kv, S, D] and sigma f32 [B, H_kv, S, 1] expected");
+      g.k_dim = int32_t(d0);
+      g.v_dim = int32_t(d2);
+      g.bits_k = g.bits_v = int32_t(L.bits.v);
+      const lkv::RecordView* sg = at(4);
+      const lkv::RecordView* rn = at(5);
+      if ((sg == nullptr) != (rn == nullptr)) return bad("QJL slots partially present");
+      const int vs = sg ? 4 : 2;
+      if (sg) {
+        if (!L.qjl_m.has) return bad("missing qjl_m");
+        if (!geom(sg, lkv::kBF16, &d4) || !geom(rn, lkv::kF32, &d5) || d5 != 1 ||
+            uint64_t(d4) != L.qjl_m.v)
+          return bad("keys_signs bf16 [B, H_kv, S, qjl_m] and residual norm f32 expected");
+        if (d4 % 32 != 0)
+          return fail(TQKV_EUNSUPPORTED, "qjl_m=%lld is not a multiple of 32", (long long)d4);
+        g.qjl_words = int32_t(d4 / 32);
+      }
+      spec(0, at(0));
+      spec(1, at(1));
+      spec(vs, at(2));
+      spec(vs + 1, at(3));
+      if (sg) {
+        spec(2, sg, true);
+        spec(3, rn);
+      }
+    }
+    if (B <= 0 || H <= 0 || B > 65535 || H > 65535) return bad("batch or heads out of range");
+  } else {
+    for (int i = 0; i < n_arr; ++i)
+      if (at(i)) return bad("arrays partially present");
+    return fail(TQKV_EUNSUPPORTED, "an empty layer carries no geometry to rebuild from");
+  }
+  g.batch = int32_t(B);
+  g.kv_heads = int32_t(H);
+  if (ring) {
+    g.max_size = L.max_size.v > uint64_t(INT64_MAX) ? INT64_MAX : int64_t(L.max_size.v);
+    g.keep = int64_t(L.keep.v);
+  }
+  if (L.offset < L.base_offset) return bad("offset below base_offset");
+  tqkv_cache* c = nullptr;
+  if (int32_t rc = tqkv_cache_create(&g, &c)) return rc;
+  auto undo = [&](int32_t rc) {
+    tqkv_cache_destroy(c);
+    return rc;
+  };
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  TQKV_HIP(hipStreamSynchronize(st));
+  const int64_t cap = capacity_for(c, len > 0 ? len : 1, 0);
+  for (int s = 0; s < c->n_slots; ++s)
+    if (int32_t rc = alloc(c, c->cur[s], cap, s)) return undo(rc);
+  // specs[i] was made from array slot i's record.
+  for (size_t i = 0; i < specs.size(); ++i)
+    if (int32_t rc = write_record(c, specs[i], at(int(i))->data)) return undo(rc);
+  c->st.has = true;
+  c->st.len = len;
+  c->st.offset = int64_t(L.offset - L.base_offset);
+  c->st.idx = ring ? int64_t(L.idx.v) : 0;
+  c->base_offset = int64_t(L.base_offset);
+  c->view_n = !ring ? c->st.offset : (c->st.offset >= g.max_size ? len : std::min(c->st.offset, len));
+  if (g.kind == TQKV_CACHE_CODEBOOK)
+    if (int32_t rc = codebook_tables(c, nullptr, nullptr)) return undo(rc);
+  *out = c;
+  return ok();
 }
 
 }  // extern "C"

@@ -70,6 +70,7 @@ const char* tqkv_status_string(int32_t status) {
     case TQKV_EDEVICE: return "TQKV_EDEVICE";
     case TQKV_ENOMEM: return "TQKV_ENOMEM";
     case TQKV_EINVAL_ARG: return "TQKV_EINVAL_ARG";
+    case TQKV_ECORRUPT: return "TQKV_ECORRUPT";
   }
   return "TQKV_UNKNOWN";
 }

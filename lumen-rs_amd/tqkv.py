@@ -28,6 +28,7 @@ EUNSUPPORTED = 3
 EDEVICE = 4
 ENOMEM = 5
 EINVAL_ARG = 6
+ECORRUPT = 7
 
 
 class TqkvError(RuntimeError):
@@ -40,6 +41,12 @@ class AffineSeg(ctypes.Structure):
     _fields_ = [("k_packed", P), ("k_scales", P), ("k_biases", P),
                 ("v_packed", P), ("v_scales", P), ("v_biases", P),
                 ("cap", I64), ("n", I64), ("shared", I32), ("reserved", I32)]
+
+
+class LkvInfo(ctypes.Structure):
+    _fields_ = [("model_fingerprint", ctypes.c_char_p), ("created_at_unix", ctypes.c_uint64),
+                ("position", ctypes.c_uint64), ("prefix_tokens", P), ("n_prefix_tokens", I64),
+                ("has_last_token", I32), ("last_token", ctypes.c_uint32), ("is_deep", I32)]
 
 
 class CacheConfig(ctypes.Structure):
@@ -116,6 +123,13 @@ _SIGS = {
     "tqkv_cache_decode_attend": (I32, [P, P, I32, F32, P, P, SZ, P]),
     "tqkv_cache_prefill_attend": (I32, [P, P, I32, I32, F32, I64, P, P]),
     "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
+    "tqkv_lkv_export": (I32, [P, I32, ctypes.POINTER(LkvInfo), P, SZ, ctypes.POINTER(SZ), P]),
+    "tqkv_lkv_check": (I32, [P, SZ]),
+    "tqkv_lkv_manifest": (I32, [P, SZ, P, SZ, ctypes.POINTER(SZ), ctypes.POINTER(I32),
+                                ctypes.POINTER(I32)]),
+    "tqkv_lkv_import": (I32, [P, SZ, I32, ctypes.c_uint64, ctypes.POINTER(P), P]),
+    "tqkv_crc32": (I32, [P, SZ, ctypes.POINTER(ctypes.c_uint32)]),
+    "tqkv_lkv_rewrite": (I32, [P, SZ, P, SZ, ctypes.POINTER(SZ)]),
 }
 
 
@@ -372,6 +386,14 @@ class Cache:
         check(lib().tqkv_cache_create(ctypes.byref(self.cfg), ctypes.byref(h)))
         self.h = h.value
 
+    @classmethod
+    def adopt(cls, handle):
+        """Wrap a cache made by the library (tqkv_lkv_import)."""
+        c = cls.__new__(cls)
+        c.cfg = None
+        c.h = handle
+        return c
+
     def close(self):
         if self.h:
             lib().tqkv_cache_destroy(self.h)
@@ -552,3 +574,71 @@ class KVCache:
         check(lib().tqkv_kvcache_read(self.h, layer, head, int(values), first, n, _np_ptr(codes),
                                       _np_ptr(scale), _np_ptr(signs), _np_ptr(rn)))
         return codes, scale, signs[:, :W], rn
+
+
+# ---------------------------------------------------------------- LKV2 snapshots
+def _buf(data):
+    data = bytes(data)
+    return data, ctypes.cast(ctypes.c_char_p(data), P) if data else None
+
+
+def lkv_export(caches, fingerprint="", created_at_unix=0, position=0, prefix_tokens=(),
+               last_token=None, is_deep=False, stream=None):
+    """An LKV2 snapshot (bytes) whose layers are the given caches."""
+    toks = np.ascontiguousarray(np.asarray(prefix_tokens, np.uint32))
+    info = LkvInfo(fingerprint.encode(), created_at_unix, position,
+                   toks.ctypes.data if toks.size else None, toks.size,
+                   int(last_token is not None), 0 if last_token is None else last_token,
+                   int(is_deep))
+    arr = (P * max(len(caches), 1))(*[c.h for c in caches])
+    n = SZ(0)
+    check(lib().tqkv_lkv_export(arr, len(caches), ctypes.byref(info), None, 0, ctypes.byref(n),
+                                stream))
+    out = np.empty(n.value, np.uint8)
+    check(lib().tqkv_lkv_export(arr, len(caches), ctypes.byref(info), out.ctypes.data, out.size,
+                                ctypes.byref(n), stream))
+    return out.tobytes()
+
+
+def lkv_check(data):
+    """Raises TqkvError (ECORRUPT) where the reference's read_lkv errs."""
+    data, p = _buf(data)
+    check(lib().tqkv_lkv_check(p, len(data)))
+
+
+def lkv_manifest(data):
+    """(manifest JSON text, layer count, record count)."""
+    data, p = _buf(data)
+    n = SZ(0)
+    nl, nr = I32(0), I32(0)
+    check(lib().tqkv_lkv_manifest(p, len(data), None, 0, ctypes.byref(n), ctypes.byref(nl),
+                                  ctypes.byref(nr)))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    check(lib().tqkv_lkv_manifest(p, len(data), buf, n.value + 1, ctypes.byref(n),
+                                  ctypes.byref(nl), ctypes.byref(nr)))
+    return buf.raw[:n.value].decode(), nl.value, nr.value
+
+
+def lkv_import(data, layer, seed=42, stream=None):
+    """A new device cache from layer `layer` of an LKV2 snapshot."""
+    data, p = _buf(data)
+    h = P()
+    check(lib().tqkv_lkv_import(p, len(data), layer, seed, ctypes.byref(h), stream))
+    return Cache.adopt(h.value)
+
+
+def lkv_rewrite(data):
+    """read_lkv then write_lkv, on the host."""
+    data, p = _buf(data)
+    n = SZ(0)
+    check(lib().tqkv_lkv_rewrite(p, len(data), None, 0, ctypes.byref(n)))
+    out = ctypes.create_string_buffer(max(n.value, 1))
+    check(lib().tqkv_lkv_rewrite(p, len(data), out, n.value, ctypes.byref(n)))
+    return out.raw[:n.value]
+
+
+def crc32(data):
+    data, p = _buf(data)
+    out = ctypes.c_uint32(0)
+    check(lib().tqkv_crc32(p, len(data), ctypes.byref(out)))
+    return out.value
