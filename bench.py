@@ -47,9 +47,15 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget for the baseline sample")
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
-                    help="decode: config 2 (the headline); prefill: config 3's "
-                         "2048-token chunk attention")
+    ap.add_argument("--workload", choices=("decode", "prefill", "append", "decode1", "prefix",
+                                           "layers"), default="decode",
+                    help="decode: config 2 (the headline); prefill: config 3's 2048-token "
+                         "chunk attention; append: config 0's quantize round trip (affine, "
+                         "affine+rotation, TurboQuant codebook); decode1: config 1's "
+                         "single-sequence decode; layers: config 3's 30-layer stack (chunked "
+                         "prefill, then decode steps); prefix: config 4's shared-prefix decode")
+    ap.add_argument("--decode-steps", type=int, default=512,
+                    help="decode steps of the layers workload (config 3: 512)")
     return ap.parse_args()
 
 
@@ -64,8 +70,10 @@ def main():
 
     hip = T.hip()
     hip._ok(hip.h.hipSetDevice(0), "hipSetDevice")
-    if args.workload == "prefill":
-        prefill_main(T, hip, args)
+    others = {"prefill": prefill_main, "append": append_main, "decode1": decode1_main,
+              "prefix": prefix_main, "layers": layers_main}
+    if args.workload in others:
+        others[args.workload](T, hip, args)
         return
     B, H, HKV, D, N, GS, BITS = args.batch, 16, 8, 256, args.context, 64, 3
     scale = D ** -0.5
@@ -377,6 +385,382 @@ def prefill_cpu_baseline(T, cg, q, B, H, HKV, D, L, N, GS, BITS, q_start):
         "sample": f"last {rows} query rows of batch row 0, {H} heads x {N} keys "
                   f"({dt:.2f} s); C++ restatement of dequantize(bf16)-then-attend",
     }
+
+
+# ------------------------------------------------------------ other configs
+def _timed(hip, stream, fn, n):
+    """Per-call milliseconds of n calls of fn, each bracketed by events."""
+    evs = [(hip.event(), hip.event()) for _ in range(n)]
+    for a, b in evs:
+        hip.record(a, stream)
+        fn()
+        hip.record(b, stream)
+    hip.sync()
+    return [hip.elapsed_ms(a, b) for a, b in evs]
+
+
+def _line(metric, value, unit, ms, args, dtype, config, roofline, extra=None, settle=0):
+    out = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "settle_steps": settle,
+           "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config,
+           "roofline": roofline}
+    if extra:
+        out.update(extra)
+    return out
+
+
+def _hbm(achieved, kernel, alg, ms, traffic=None):
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kernel,
+            "alg_bytes_per_launch": int(alg), "avg_launch_ms": round(ms, 5)}
+
+
+def _oracle():
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    return O, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def append_main(T, hip, args):
+    """one layer's append-quantize round trip, B=1, 8 KV
+    heads, D=128, 4,096 tokens, bf16 N(0,1) with 2% of channels x8, 4-bit
+    gs64, seed-42 rotation. Timed: quantize K and V (mlx affine), the
+    dequantize back, the affine+rotation mode (rotate, then quantize;
+    gemma4_moe.rs:4162-4173) and the TurboQuant codebook encode
+    (compress_one, QJL m=64). value = tokens/s of the affine K+V quantize."""
+    B, HKV, D, S, GS, BITS, M = 1, 8, 128, 4096, 64, 4, 64
+    stream = hip.stream()
+    slabs, words, groups = B * HKV, D * BITS // 32, D // GS
+    x = {n: T.DeviceArray((slabs, S, D), np.uint16) for n in ("k", "v")}
+    T.synth_bf16(x["k"].ptr, slabs * S, D, 101, 0.02, 8.0, stream)
+    T.synth_bf16(x["v"].ptr, slabs * S, D, 102, 0.02, 8.0, stream)
+    q3 = {n: (T.DeviceArray((slabs, S, words), np.uint32), T.DeviceArray((slabs, S, groups), np.uint16),
+              T.DeviceArray((slabs, S, groups), np.uint16)) for n in ("k", "v")}
+    deq = {n: T.DeviceArray((slabs, S, D), np.uint16) for n in ("k", "v")}
+    rot = {n: T.DeviceArray((slabs, S, D), np.uint16) for n in ("k", "v")}
+    R = T.DeviceArray.of(T.rotation_matrix(D, 42))
+    bnd, cen = T.lloyd_max(BITS)
+    dbnd, dcen = T.DeviceArray.of(bnd), T.DeviceArray.of(cen.astype(np.float32))
+    phi = T.DeviceArray.of(T.qjl_matrix(D, M, 43))
+    codes = {n: T.DeviceArray((slabs, S, D), np.uint8) for n in ("k", "v")}
+    sig = {n: T.DeviceArray((slabs, S), np.float32) for n in ("k", "v")}
+    sgn = {n: T.DeviceArray((slabs, S, M // 32), np.uint32) for n in ("k", "v")}
+    rn = {n: T.DeviceArray((slabs, S), np.float32) for n in ("k", "v")}
+
+    def quant():
+        for n in ("k", "v"):
+            T.affine_quantize(x[n].ptr, slabs, S, D, GS, BITS, *(a.ptr for a in q3[n]),
+                              stream=stream)
+
+    def dequant():
+        for n in ("k", "v"):
+            T.affine_dequantize(*(a.ptr for a in q3[n]), slabs * S, D, GS, BITS, deq[n].ptr, stream)
+
+    def rotq():
+        for n in ("k", "v"):
+            T.rotate_bf16(x[n].ptr, slabs * S, D, R.ptr, False, rot[n].ptr, stream)
+            T.affine_quantize(rot[n].ptr, slabs, S, D, GS, BITS, *(a.ptr for a in q3[n]),
+                              stream=stream)
+
+    def tq():
+        for n in ("k", "v"):
+            T.tq_encode(x[n].ptr, True, slabs, S, D, R.ptr, dbnd.ptr, dcen.ptr, BITS, phi.ptr, M,
+                        codes[n].ptr, sig[n].ptr, sgn[n].ptr, rn[n].ptr, stream=stream)
+
+    settle = 16 if args.settle is None else max(0, args.settle)
+    for _ in range(settle + args.warmup):
+        quant(), dequant(), rotq(), tq()
+    hip.sync()
+    n = args.steps
+    ms_q = float(np.mean(_timed(hip, stream, quant, n)))
+    ms_d = float(np.mean(_timed(hip, stream, dequant, n)))
+    ms_r = float(np.mean(_timed(hip, stream, rotq, n)))
+    ms_t = float(np.mean(_timed(hip, stream, tq, max(3, n // 5))))
+    in_bytes = 2 * slabs * S * D * 2
+    q_bytes = 2 * slabs * S * (words * 4 + 2 * groups * 2)
+    tq_bytes = 2 * slabs * S * (D + 4 + M // 8 + 4)
+    result = _line(
+        "append-quantize round trip tokens/s (one layer, K and V)", S / (ms_q * 1e-3), "tokens/s",
+        ms_q, args, "bf16->u32",
+        {"workload": "BASELINE config 0: quantize-on-append of one layer's K and V "
+                     "(B=1, 8 KV heads, D=128, 4,096 tokens, 4-bit gs64)",
+         "batch": B, "kv_heads": HKV, "head_dim": D, "tokens": S, "bits": BITS, "group_size": GS},
+        _hbm((in_bytes + q_bytes) / (ms_q * 1e-3) / 1e9, "affine_quantize_kernel (K then V)",
+             in_bytes + q_bytes, ms_q / 2),
+        {"dequantize": {"ms": round(ms_d, 5), "gbps": round((q_bytes + in_bytes) / (ms_d * 1e-3) / 1e9, 1)},
+         "affine_rotation": {"ms": round(ms_r, 5),
+                             "tokens_per_s": round(S / (ms_r * 1e-3), 1),
+                             "rotation_flop": 2 * 2 * slabs * S * D * D},
+         "turboquant_encode": {"ms": round(ms_t, 5), "tokens_per_s": round(S / (ms_t * 1e-3), 1),
+                               "bytes": in_bytes + tq_bytes, "qjl_m": M,
+                               "note": "compress_one restated bit-exactly: sequential f32 "
+                                       "sums, one wavefront per vector; latency-bound"}},
+        settle)
+    if not args.no_cpu_baseline:
+        O, threads = _oracle()
+        kh = x["k"].numpy()
+        t = time.perf_counter()
+        O.affine_quantize(kh, GS, BITS)
+        dt = time.perf_counter() - t
+        comp = O.Compressor(D, BITS, M, T.rotation_matrix(D, 42), T.qjl_matrix(D, M, 43))
+        sample = (kh[0, :256].astype(np.uint32) << 16).view(np.float32)
+        t = time.perf_counter()
+        comp.compress(sample)
+        dtq = time.perf_counter() - t
+        result["cpu_baseline"] = {
+            "value": round(S / (2 * dt), 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle affine quantize of K ({slabs} heads x {S} tokens, {dt:.3f} s; "
+                      f"K+V counted as twice that); TurboQuant compress_one of 256 vectors: "
+                      f"{256 / dtq:.0f} vectors/s single-threaded"}
+    print(json.dumps(result))
+
+
+def _fill_affine(T, stream, slabs, N, D, GS, bits, cap, seed, start=0):
+    words, groups = D * bits // 32, D // GS
+    t3 = (T.DeviceArray((slabs, cap, words), np.uint32), T.DeviceArray((slabs, cap, groups), np.uint16),
+          T.DeviceArray((slabs, cap, groups), np.uint16))
+    tmp = T.DeviceArray((slabs, 1024, D), np.uint16)
+    for c0 in range(0, N, 1024):
+        n = min(1024, N - c0)
+        T.synth_bf16(tmp.ptr, slabs * n, D, seed * 1000003 + c0, 0.01, 10.0, stream)
+        T.affine_quantize(tmp.ptr, slabs, n, D, GS, bits, *(a.ptr for a in t3), cap, start + c0,
+                          stream)
+    return t3
+
+
+def decode1_main(T, hip, args):
+    """one sequence, 32 query / 8 KV heads, D=128, 4-bit
+    gs64, context 8,192; a step appends one K and V token and decodes. The
+    decode splits the keys over enough workgroups to fill the chip and
+    merges the splits (two launches); the line is latency-bound."""
+    B, H, HKV, D, N, GS, BITS = 1, 32, 8, 128, 8192, 64, 4
+    stream = hip.stream()
+    slabs = B * HKV
+    settle = 64 if args.settle is None else max(0, args.settle)
+    steps = 256
+    cap = N + settle + args.warmup + steps + 1
+    kc = _fill_affine(T, stream, slabs, N, D, GS, BITS, cap, 7)
+    vc = _fill_affine(T, stream, slabs, N, D, GS, BITS, cap, 8)
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H, D, 9, 0.0, 1.0, stream)
+    nk, nv = T.DeviceArray((slabs, 1, D), np.uint16), T.DeviceArray((slabs, 1, D), np.uint16)
+    T.synth_bf16(nk.ptr, slabs, D, 10, 0.02, 8.0, stream)
+    T.synth_bf16(nv.ptr, slabs, D, 11, 0.02, 8.0, stream)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    wsb = T.decode_workspace_size(B, H, HKV, D, cap)
+    ws = T.DeviceArray((wsb,), np.uint8)
+    kp, vp = tuple(a.ptr for a in kc), tuple(a.ptr for a in vc)
+    pos = [N]
+
+    def append():
+        T.affine_quantize(nk.ptr, slabs, 1, D, GS, BITS, *kp, cap, pos[0], stream)
+        T.affine_quantize(nv.ptr, slabs, 1, D, GS, BITS, *vp, cap, pos[0], stream)
+        pos[0] += 1
+
+    def decode():
+        seg = T.affine_seg(kp, vp, cap, pos[0])
+        T.decode_attend_affine(q.ptr, B, H, HKV, D, GS, BITS, BITS, D ** -0.5, [seg], out.ptr,
+                               ws.ptr, wsb, stream)
+
+    for _ in range(settle + args.warmup):
+        append(), decode()
+    hip.sync()
+    ctx0 = pos[0]
+    evs = [(hip.event(), hip.event(), hip.event()) for _ in range(steps)]
+    for a, b, c in evs:
+        hip.record(a, stream)
+        append()
+        hip.record(b, stream)
+        decode()
+        hip.record(c, stream)
+    hip.sync()
+    step_ms = float(np.mean([hip.elapsed_ms(a, c) for a, b, c in evs]))
+    dec_ms = float(np.mean([hip.elapsed_ms(b, c) for a, b, c in evs]))
+    row = D * BITS // 32 * 4 + 2 * (D // GS) * 2
+    ctx = ctx0 + (steps + 1) / 2.0
+    alg = 2 * slabs * ctx * row + 2 * B * H * D * 2
+    result = _line(
+        "single-sequence quantized-KV decode tokens/s", 1.0 / (step_ms * 1e-3), "tokens/s", step_ms,
+        args, "f32",
+        {"workload": "BASELINE config 1: 1 sequence, 32/8 heads, D=128, 4-bit gs64, 8,192 "
+                     "context, 256 steps each appending one token",
+         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N, "steps": steps},
+        _hbm(alg / (dec_ms * 1e-3) / 1e9, T.decode_kernel_name(H, HKV, D, GS, BITS, BITS) +
+             " split + merge", alg, dec_ms),
+        {"decode_us": round(dec_ms * 1e3, 2), "step_us": round(step_ms * 1e3, 2)}, settle)
+    if not args.no_cpu_baseline:
+        O, threads = _oracle()
+        kt = tuple(a.numpy()[:, :pos[0]].reshape(B, HKV, pos[0], -1) for a in kc)
+        vt = tuple(a.numpy()[:, :pos[0]].reshape(B, HKV, pos[0], -1) for a in vc)
+        t = time.perf_counter()
+        O.attend_affine(q.numpy(), kt, vt, GS, BITS, BITS, D ** -0.5)
+        dt = time.perf_counter() - t
+        result["cpu_baseline"] = {"value": round(1.0 / dt, 2), "unit": "tokens/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"oracle dequantize-then-attend of one decode step "
+                                            f"({pos[0]} keys, {dt:.3f} s)"}
+    print(json.dumps(result))
+
+
+def prefix_main(T, hip, args):
+    """8 sequences over one shared 65,536-token prefix
+    (stored once, batch stride 0) plus 4,096 tokens of their own, 32 query
+    / 8 KV heads, D=128, 8-bit keys and 4-bit values, gs64; a step appends
+    one token per sequence and decodes over prefix + suffix in one softmax.
+    Achieved bandwidth is priced on the unique bytes (the prefix once)."""
+    B, H, HKV, D, P, S0, GS, BK, BV = 8, 32, 8, 128, 65536, 4096, 64, 8, 4
+    stream = hip.stream()
+    settle = 32 if args.settle is None else max(0, args.settle)
+    steps = 128
+    cap = S0 + settle + args.warmup + steps + 1
+    pk = _fill_affine(T, stream, HKV, P, D, GS, BK, P, 21)
+    pv = _fill_affine(T, stream, HKV, P, D, GS, BV, P, 22)
+    sk = _fill_affine(T, stream, B * HKV, S0, D, GS, BK, cap, 23)
+    sv = _fill_affine(T, stream, B * HKV, S0, D, GS, BV, cap, 24)
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H, D, 25, 0.0, 1.0, stream)
+    nk, nv = T.DeviceArray((B * HKV, 1, D), np.uint16), T.DeviceArray((B * HKV, 1, D), np.uint16)
+    T.synth_bf16(nk.ptr, B * HKV, D, 26, 0.0, 1.0, stream)
+    T.synth_bf16(nv.ptr, B * HKV, D, 27, 0.0, 1.0, stream)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    wsb = T.decode_workspace_size(B, H, HKV, D, P + cap)
+    ws = T.DeviceArray((wsb,), np.uint8)
+    pkp, pvp = tuple(a.ptr for a in pk), tuple(a.ptr for a in pv)
+    skp, svp = tuple(a.ptr for a in sk), tuple(a.ptr for a in sv)
+    pos = [S0]
+
+    def step(events=None):
+        T.affine_quantize(nk.ptr, B * HKV, 1, D, GS, BK, *skp, cap, pos[0], stream)
+        T.affine_quantize(nv.ptr, B * HKV, 1, D, GS, BV, *svp, cap, pos[0], stream)
+        pos[0] += 1
+        segs = [T.affine_seg(pkp, pvp, P, P, shared=True), T.affine_seg(skp, svp, cap, pos[0])]
+        if events:
+            hip.record(events[0], stream)
+        T.decode_attend_affine(q.ptr, B, H, HKV, D, GS, BK, BV, D ** -0.5, segs, out.ptr, ws.ptr,
+                               wsb, stream)
+        if events:
+            hip.record(events[1], stream)
+
+    for _ in range(settle + args.warmup):
+        step()
+    hip.sync()
+    ctx0 = pos[0]
+    evs = [(hip.event(), hip.event()) for _ in range(steps)]
+    t0, t1 = hip.event(), hip.event()
+    hip.record(t0, stream)
+    for e in evs:
+        step(e)
+    hip.record(t1, stream)
+    total = hip.elapsed_ms(t0, t1)
+    hip.sync()
+    dec_ms = float(np.mean([hip.elapsed_ms(a, b) for a, b in evs]))
+    row = (D * BK // 32 * 4 + 2 * (D // GS) * 2) + (D * BV // 32 * 4 + 2 * (D // GS) * 2)  # 208
+    ctx = ctx0 + (steps + 1) / 2.0
+    unique = P * HKV * row + B * HKV * ctx * row + 2 * B * H * D * 2
+    naive = B * HKV * (P + ctx) * row + 2 * B * H * D * 2
+    result = _line(
+        "prefix-shared quantized-KV decode tokens/s", B / (total / steps * 1e-3), "tokens/s",
+        total / steps, args, "f32",
+        {"workload": "BASELINE config 4: 8 sequences sharing a 65,536-token prefix plus 4,096 "
+                     "own tokens, 32/8 heads, D=128, K 8-bit / V 4-bit gs64, 128 decode steps",
+         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "prefix": P, "suffix": S0,
+         "bits_k": BK, "bits_v": BV, "group_size": GS},
+        _hbm(unique / (dec_ms * 1e-3) / 1e9, T.decode_kernel_name(H, HKV, D, GS, BK, BV) +
+             " (two segments)", unique, dec_ms),
+        {"naive_bytes_per_step": int(naive),
+         "naive_gbps": round(naive / (dec_ms * 1e-3) / 1e9, 1)}, settle)
+    if not args.no_cpu_baseline:
+        O, threads = _oracle()
+        cat = lambda a, b: np.concatenate([a.numpy()[:, :P].reshape(1, HKV, P, -1),
+                                           b.numpy()[:HKV, :pos[0]].reshape(1, HKV, pos[0], -1)], axis=2)
+        kt = tuple(cat(a, b) for a, b in zip(pk, sk))
+        vt = tuple(cat(a, b) for a, b in zip(pv, sv))
+        t = time.perf_counter()
+        O.attend_affine(q.numpy()[:1], kt, vt, GS, BK, BV, D ** -0.5)
+        dt = time.perf_counter() - t
+        result["cpu_baseline"] = {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"oracle dequantize-then-attend of sequence 0 over "
+                                            f"prefix + suffix ({P + pos[0]} keys, {dt:.2f} s)"}
+    print(json.dumps(result))
+
+
+def layers_main(T, hip, args):
+    """BASELINE config 3 end to end through the cache objects: 30 layers
+    (global at 5, 11, 17, 23, 29; the rest sliding with a 1,024-token ring,
+    keep 0), B=4, 32 / 8 heads, D=128, 4-bit gs64, scale 1. Prefill: a
+    16,384-token prompt in 8 chunks of 2,048 (per chunk and layer: append,
+    then chunk attention with the layer's mask). Decode: steps appending one
+    token per layer and attending; a step = all 30 layers. tokens/s = B /
+    step time (the survey's B / sum over 30 layers)."""
+    B, H, HKV, D, GS, BITS, L, CH, W = 4, 32, 8, 128, 64, 4, 16384, 2048, 1024
+    n_layers = 30
+    glob = {5, 11, 17, 23, 29}
+    stream = hip.stream()
+    slabs = B * HKV
+    caches = [T.Cache(T.CACHE_AFFINE, B, HKV, D, D, GS, BITS, BITS, prealloc=True,
+                      max_size=0 if i in glob else W, keep=0) for i in range(n_layers)]
+    kc, vc = T.DeviceArray((slabs, CH, D), np.uint16), T.DeviceArray((slabs, CH, D), np.uint16)
+    qc = T.DeviceArray((B, H, CH, D), np.uint16)
+    oc = T.DeviceArray((B, H, CH, D), np.uint16)
+    T.synth_bf16(qc.ptr, B * H * CH, D, 5, 0.0, 1.0, stream)
+
+    def prefill():
+        for c0 in range(0, L, CH):
+            T.synth_bf16(kc.ptr, slabs * CH, D, 1000 + c0, 0.02, 8.0, stream)
+            T.synth_bf16(vc.ptr, slabs * CH, D, 2000 + c0, 0.02, 8.0, stream)
+            for i, c in enumerate(caches):
+                c.append(kc.ptr, vc.ptr, CH, stream)
+                c.prefill_attend(qc.ptr, H, CH, 1.0, oc.ptr, window=-1 if i in glob else W,
+                                 stream=stream)
+
+    hip.sync()
+    t0, t1 = hip.event(), hip.event()
+    hip.record(t0, stream)
+    prefill()
+    hip.record(t1, stream)
+    prefill_ms = hip.elapsed_ms(t0, t1)
+    nk, nv = T.DeviceArray((slabs, 1, D), np.uint16), T.DeviceArray((slabs, 1, D), np.uint16)
+    T.synth_bf16(nk.ptr, slabs, D, 31, 0.02, 8.0, stream)
+    T.synth_bf16(nv.ptr, slabs, D, 32, 0.02, 8.0, stream)
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H, D, 33, 0.0, 1.0, stream)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    wsb = T.decode_workspace_size(B, H, HKV, D, L + args.decode_steps + 64)
+    ws = T.DeviceArray((wsb,), np.uint8)
+
+    def step():
+        for c in caches:
+            c.append(nk.ptr, nv.ptr, 1, stream)
+            c.decode_attend(q.ptr, H, 1.0, out.ptr, ws.ptr, wsb, stream)
+
+    settle = 16 if args.settle is None else max(0, args.settle)
+    for _ in range(settle + args.warmup):
+        step()
+    hip.sync()
+    views0 = [c.state().view for c in caches]
+    steps = args.decode_steps
+    ms = _timed(hip, stream, step, steps)
+    views1 = [c.state().view for c in caches]
+    step_ms = float(np.mean(ms))
+    row = D * BITS // 32 * 4 + 2 * (D // GS) * 2  # 72
+    avg_view = [(a + b) / 2.0 for a, b in zip(views0, views1)]
+    alg = sum(2 * slabs * v * row for v in avg_view) + n_layers * 2 * B * H * D * 2
+    result = _line(
+        "30-layer rotating-window decode tokens/s", B / (step_ms * 1e-3), "tokens/s", step_ms, args,
+        "f32",
+        {"workload": "BASELINE config 3: 30 layers (5 global, 25 sliding ring 1024), B=4, "
+                     "32/8 heads, D=128, 4-bit gs64; 16,384-token prefill in 2,048 chunks "
+                     "(MFMA chunk attention), then decode steps over all layers",
+         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "layers": n_layers,
+         "prompt": L, "chunk": CH, "window": W, "decode_steps": steps},
+        _hbm(alg / (step_ms * 1e-3) / 1e9, "30 x (append + decode) per step", alg, step_ms),
+        {"prefill_ms": round(prefill_ms, 2),
+         "prefill_tokens_per_s": round(B * L / (prefill_ms * 1e-3), 1),
+         "decode_bytes_per_step": int(alg),
+         "views_at_end": {"global": int(views1[5]), "sliding": int(views1[0])}}, settle)
+    print(json.dumps(result))
 
 
 if __name__ == "__main__":
