@@ -36,7 +36,9 @@ PEAK_HBM_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 50; the config workloads use their config's "
+                         "own step count: decode1 256, prefix 128, layers --decode-steps)")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--settle", type=int, default=None,
                     help="untimed steps before the warm-up (default: 128 decode steps, "
@@ -63,8 +65,11 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(the multi-GPU sharding is a design in DESIGN.md)"}))
+                          "(how the path shards over GPUs is a written design, not built)"}))
         sys.exit(2)
+
+    if args.steps is None and args.workload in ("decode", "prefill", "append"):
+        args.steps = 50
 
     import tqkv as T
 
@@ -136,14 +141,19 @@ def main():
     for i in range(warmup):
         step(settle + i)
     hip._ok(hip.h.hipStreamSynchronize(stream), "sync")
+    # The K timed steps, one event pair around all of them (the throughput).
     t0, t1 = hip.event(), hip.event()
     hip.record(t0, stream)
     wall0 = time.perf_counter()
     for i in range(steps):
-        step(settle + warmup + i, ev[i])
+        step(settle + warmup + i)
     hip.record(t1, stream)
     total_ms = hip.elapsed_ms(t0, t1)
     wall = time.perf_counter() - wall0
+    # The same K steps again (same rows rewritten with the same tokens), each
+    # decode launch bracketed by events: the kernel's launch duration.
+    for i in range(steps):
+        step(settle + warmup + i, ev[i])
     hip.sync()
     dec_ms = [hip.elapsed_ms(a, b) for a, b in ev]
     dec_avg_ms = float(np.mean(dec_ms))
@@ -388,20 +398,26 @@ def prefill_cpu_baseline(T, cg, q, B, H, HKV, D, L, N, GS, BITS, q_start):
 
 
 # ------------------------------------------------------------ other configs
-def _timed(hip, stream, fn, n):
-    """Per-call milliseconds of n calls of fn, each bracketed by events."""
-    evs = [(hip.event(), hip.event()) for _ in range(n)]
-    for a, b in evs:
-        hip.record(a, stream)
+def _loop_ms(hip, stream, fn, n):
+    """Milliseconds per call of n back-to-back calls of fn, timed by one
+    event pair around the whole loop (events between calls cost the stream
+    a few microseconds each, which per-call brackets would count)."""
+    t0, t1 = hip.event(), hip.event()
+    hip.record(t0, stream)
+    for _ in range(n):
         fn()
-        hip.record(b, stream)
+    hip.record(t1, stream)
     hip.sync()
-    return [hip.elapsed_ms(a, b) for a, b in evs]
+    return hip.elapsed_ms(t0, t1) / n
 
 
-def _line(metric, value, unit, ms, args, dtype, config, roofline, extra=None, settle=0):
+def _line(metric, value, unit, ms, args, dtype, config, roofline, extra=None, settle=0,
+          steps=None):
+    """One result line; `steps` is the count actually timed (the workloads
+    that follow a BASELINE config's own step count pass it)."""
     out = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1,
-           "steps": args.steps, "warmup": args.warmup, "settle_steps": settle,
+           "steps": args.steps if steps is None else steps, "warmup": args.warmup,
+           "settle_steps": settle,
            "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config,
            "roofline": roofline}
@@ -473,10 +489,10 @@ def append_main(T, hip, args):
         quant(), dequant(), rotq(), tq()
     hip.sync()
     n = args.steps
-    ms_q = float(np.mean(_timed(hip, stream, quant, n)))
-    ms_d = float(np.mean(_timed(hip, stream, dequant, n)))
-    ms_r = float(np.mean(_timed(hip, stream, rotq, n)))
-    ms_t = float(np.mean(_timed(hip, stream, tq, max(3, n // 5))))
+    ms_q = _loop_ms(hip, stream, quant, n)
+    ms_d = _loop_ms(hip, stream, dequant, n)
+    ms_r = _loop_ms(hip, stream, rotq, n)
+    ms_t = _loop_ms(hip, stream, tq, max(3, n // 5))
     in_bytes = 2 * slabs * S * D * 2
     q_bytes = 2 * slabs * S * (words * 4 + 2 * groups * 2)
     tq_bytes = 2 * slabs * S * (D + 4 + M // 8 + 4)
@@ -538,7 +554,7 @@ def decode1_main(T, hip, args):
     stream = hip.stream()
     slabs = B * HKV
     settle = 64 if args.settle is None else max(0, args.settle)
-    steps = 256
+    steps = 256 if args.steps is None else args.steps
     cap = N + settle + args.warmup + steps + 1
     kc = _fill_affine(T, stream, slabs, N, D, GS, BITS, cap, 7)
     vc = _fill_affine(T, stream, slabs, N, D, GS, BITS, cap, 8)
@@ -567,16 +583,18 @@ def decode1_main(T, hip, args):
         append(), decode()
     hip.sync()
     ctx0 = pos[0]
-    evs = [(hip.event(), hip.event(), hip.event()) for _ in range(steps)]
-    for a, b, c in evs:
-        hip.record(a, stream)
+    step_ms = _loop_ms(hip, stream, lambda: (append(), decode()), steps)
+    # The same steps again (rows rewritten with the same tokens), each decode
+    # bracketed by events.
+    pos[0] = ctx0
+    evs = [(hip.event(), hip.event()) for _ in range(steps)]
+    for b, c in evs:
         append()
         hip.record(b, stream)
         decode()
         hip.record(c, stream)
     hip.sync()
-    step_ms = float(np.mean([hip.elapsed_ms(a, c) for a, b, c in evs]))
-    dec_ms = float(np.mean([hip.elapsed_ms(b, c) for a, b, c in evs]))
+    dec_ms = float(np.mean([hip.elapsed_ms(b, c) for b, c in evs]))
     row = D * BITS // 32 * 4 + 2 * (D // GS) * 2
     ctx = ctx0 + (steps + 1) / 2.0
     alg = 2 * slabs * ctx * row + 2 * B * H * D * 2
@@ -588,7 +606,7 @@ def decode1_main(T, hip, args):
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N, "steps": steps},
         _hbm(alg / (dec_ms * 1e-3) / 1e9, T.decode_kernel_name(H, HKV, D, GS, BITS, BITS) +
              " split + merge", alg, dec_ms),
-        {"decode_us": round(dec_ms * 1e3, 2), "step_us": round(step_ms * 1e3, 2)}, settle)
+        {"decode_us": round(dec_ms * 1e3, 2), "step_us": round(step_ms * 1e3, 2)}, settle, steps)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
         kt = tuple(a.numpy()[:, :pos[0]].reshape(B, HKV, pos[0], -1) for a in kc)
@@ -612,7 +630,7 @@ def prefix_main(T, hip, args):
     B, H, HKV, D, P, S0, GS, BK, BV = 8, 32, 8, 128, 65536, 4096, 64, 8, 4
     stream = hip.stream()
     settle = 32 if args.settle is None else max(0, args.settle)
-    steps = 128
+    steps = 128 if args.steps is None else args.steps
     cap = S0 + settle + args.warmup + steps + 1
     pk = _fill_affine(T, stream, HKV, P, D, GS, BK, P, 21)
     pv = _fill_affine(T, stream, HKV, P, D, GS, BV, P, 22)
@@ -646,15 +664,23 @@ def prefix_main(T, hip, args):
         step()
     hip.sync()
     ctx0 = pos[0]
+    total = _loop_ms(hip, stream, step, steps) * steps
+    # The same steps again (rows rewritten with the same tokens), each
+    # attention call bracketed by events.
+    pos[0] = ctx0
     evs = [(hip.event(), hip.event()) for _ in range(steps)]
-    t0, t1 = hip.event(), hip.event()
-    hip.record(t0, stream)
     for e in evs:
         step(e)
-    hip.record(t1, stream)
-    total = hip.elapsed_ms(t0, t1)
     hip.sync()
     dec_ms = float(np.mean([hip.elapsed_ms(a, b) for a, b in evs]))
+    # And with the prefix read once per sequence (the library's
+    # TQKV_SHARED_PREFIX=0 switch), for comparison.
+    pos[0] = ctx0
+    os.environ["TQKV_SHARED_PREFIX"] = "0"
+    try:
+        per_seq_ms = _loop_ms(hip, stream, step, steps)
+    finally:
+        del os.environ["TQKV_SHARED_PREFIX"]
     row = (D * BK // 32 * 4 + 2 * (D // GS) * 2) + (D * BV // 32 * 4 + 2 * (D // GS) * 2)  # 208
     ctx = ctx0 + (steps + 1) / 2.0
     unique = P * HKV * row + B * HKV * ctx * row + 2 * B * H * D * 2
@@ -666,10 +692,12 @@ def prefix_main(T, hip, args):
                      "own tokens, 32/8 heads, D=128, K 8-bit / V 4-bit gs64, 128 decode steps",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "prefix": P, "suffix": S0,
          "bits_k": BK, "bits_v": BV, "group_size": GS},
-        _hbm(unique / (dec_ms * 1e-3) / 1e9, T.decode_kernel_name(H, HKV, D, GS, BK, BV) +
-             " (two segments)", unique, dec_ms),
+        _hbm(unique / (dec_ms * 1e-3) / 1e9,
+             "shared-prefix decode call: prefix pass (prefill kernel, f16 tiles) + suffix "
+             "decode (" + T.decode_kernel_name(H, HKV, D, GS, BK, BV) + ") + merge", unique, dec_ms),
         {"naive_bytes_per_step": int(naive),
-         "naive_gbps": round(naive / (dec_ms * 1e-3) / 1e9, 1)}, settle)
+         "naive_gbps": round(naive / (dec_ms * 1e-3) / 1e9, 1),
+         "per_sequence_path_ms_per_step": round(per_seq_ms, 5)}, settle, steps)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
         cat = lambda a, b: np.concatenate([a.numpy()[:, :P].reshape(1, HKV, P, -1),
@@ -740,10 +768,9 @@ def layers_main(T, hip, args):
         step()
     hip.sync()
     views0 = [c.state().view for c in caches]
-    steps = args.decode_steps
-    ms = _timed(hip, stream, step, steps)
+    steps = args.decode_steps if args.steps is None else args.steps
+    step_ms = _loop_ms(hip, stream, step, steps)
     views1 = [c.state().view for c in caches]
-    step_ms = float(np.mean(ms))
     row = D * BITS // 32 * 4 + 2 * (D // GS) * 2  # 72
     avg_view = [(a + b) / 2.0 for a, b in zip(views0, views1)]
     alg = sum(2 * slabs * v * row for v in avg_view) + n_layers * 2 * B * H * D * 2
@@ -759,7 +786,7 @@ def layers_main(T, hip, args):
         {"prefill_ms": round(prefill_ms, 2),
          "prefill_tokens_per_s": round(B * L / (prefill_ms * 1e-3), 1),
          "decode_bytes_per_step": int(alg),
-         "views_at_end": {"global": int(views1[5]), "sliding": int(views1[0])}}, settle)
+         "views_at_end": {"global": int(views1[5]), "sliding": int(views1[0])}}, settle, steps)
     print(json.dumps(result))
 
 

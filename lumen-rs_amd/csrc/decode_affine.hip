@@ -6,32 +6,83 @@
 #include "decode_mfma.hpp"
 
 namespace tqkv {
+namespace prefill {
+int32_t shared_prefix_partials(const uint16_t* q, int B, int H, int H_kv, int D, int gs, int bk,
+                               int bv, float scale, const tqkv_affine_seg& prefix, int n_splits,
+                               int split_len, int n_part, float* part_o, float* part_m,
+                               float* part_l, hipStream_t st);
+int shared_prefix_block_rows(int D);
+}  // namespace prefill
 namespace decode {
 namespace {
 
 // Merges the splits of one (batch row, query head):
-// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), as bf16.
-__global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_o,
-                                                           const float* __restrict__ part_m,
-                                                           const float* __restrict__ part_l,
-                                                           int n_splits, int D,
-                                                           uint16_t* __restrict__ out) {
+// out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), as bf16. Each split's
+// weight 2^(m_s - M) is computed once (into LDS), then every thread sums
+// its channel over the splits with coalesced reads of the partials.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeChunk = 1024;
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int w = threadIdx.x / 64;
+  __syncthreads();
+  if (threadIdx.x % 64 == 0) red[w] = v;
+  __syncthreads();
+  v = red[0];
+  for (int i = 1; i < kMergeThreads / 64; ++i) v = fmaxf(v, red[i]);
+  return v;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int w = threadIdx.x / 64;
+  __syncthreads();
+  if (threadIdx.x % 64 == 0) red[w] = v;
+  __syncthreads();
+  v = red[0];
+  for (int i = 1; i < kMergeThreads / 64; ++i) v += red[i];
+  return v;
+}
+
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_m,
+    const float* __restrict__ part_l, int n_splits, int D, uint16_t* __restrict__ out) {
+  __shared__ float wgt[kMergeChunk];
+  __shared__ float red[kMergeThreads / 64];
   const int64_t bh = blockIdx.x;
   const float* pm = part_m + bh * n_splits;
   const float* pl = part_l + bh * n_splits;
   float mx = -INFINITY;
-  for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, pm[s]);
+  for (int s = threadIdx.x; s < n_splits; s += kMergeThreads) mx = fmaxf(mx, pm[s]);
+  mx = block_max(mx, red);
   float ls = 0.0f;
-  for (int s = 0; s < n_splits; ++s)
-    if (pm[s] != -INFINITY) ls += pl[s] * exp2f(pm[s] - mx);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float os = 0.0f;
-    for (int s = 0; s < n_splits; ++s)
-      if (pm[s] != -INFINITY) os += part_o[(bh * n_splits + s) * D + d] * exp2f(pm[s] - mx);
-    out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
+  float os[2] = {0.0f, 0.0f};  // channels threadIdx.x and + 256 (D <= 512)
+  for (int c0 = 0; c0 < n_splits; c0 += kMergeChunk) {
+    const int n = n_splits - c0 < kMergeChunk ? n_splits - c0 : kMergeChunk;
+    __syncthreads();  // the previous chunk's weights are used up
+    for (int s = threadIdx.x; s < n; s += kMergeThreads) {
+      const float m = pm[c0 + s];
+      const float w = m == -INFINITY ? 0.0f : exp2f(m - mx);
+      wgt[s] = w;
+      ls += w * pl[c0 + s];
+    }
+    __syncthreads();
+    for (int k = 0; k < 2; ++k) {
+      const int d = threadIdx.x + k * kMergeThreads;
+      if (d >= D) break;
+      const float* po = part_o + (bh * n_splits + c0) * D + d;
+      float acc = os[k];
+      for (int s = 0; s < n; ++s) acc += wgt[s] * po[int64_t(s) * D];
+      os[k] = acc;
+    }
+  }
+  ls = block_sum(ls, red);
+  for (int k = 0; k < 2; ++k) {
+    const int d = threadIdx.x + k * kMergeThreads;
+    if (d < D) out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os[k] / ls : 0.0f);
   }
 }
-
 
 // Splits per (batch row, KV head). With at least ~2048 wavefronts of whole
 // (batch row, KV head) units the chip is full and each workgroup owns its
@@ -73,6 +124,34 @@ int max_splits(int B, int H_kv, int64_t total) {
 }
 
 int waves_for_shape(int G, int D) { return G * D <= 1024 ? 8 : 4; }
+
+// Workgroups of the shared-prefix pass: one per CU of an MI355X (256). The
+// pass holds one workgroup per CU, and each workgroup's fixed costs (query
+// load, first tile, partials) favour one long key range per CU over several
+// short ones (measured: 54 us at 256 against 57, 70, 74 and 102 us at 512,
+// 192, 384 and 1,024 on config 4's 65,536-token prefix).
+constexpr int kPrefixWgs = 256;
+
+// Prefix splits of the shared-prefix path: about kPrefixWgs workgroups over
+// the (KV head, row block) units, never under 256 keys a split.
+int prefix_splits(int H_kv, int64_t rows, int block_rows, int64_t P, int* split_len) {
+  const int64_t units = int64_t(H_kv) * ((rows + block_rows - 1) / block_rows);
+  int64_t want = (kPrefixWgs + units - 1) / units;
+  const int64_t most = (P + 255) / 256;
+  if (want > most) want = most;
+  if (want < 1) want = 1;
+  int64_t len = (P + want - 1) / want;
+  len = (len + 63) / 64 * 64;
+  *split_len = int(len);
+  return int((P + len - 1) / len);
+}
+
+int prefix_splits_max(int H_kv, int64_t total) {
+  int64_t want = (kPrefixWgs + H_kv - 1) / H_kv;
+  const int64_t most = (total + 255) / 256;
+  if (want > most) want = most;
+  return want < 1 ? 1 : int(want);
+}
 
 // The MFMA-scored kernel where its layout applies, else the dot2 kernel.
 // TQKV_DECODE_KERNEL=dot2 forces the dot2 kernel (tests cover both).
@@ -125,7 +204,10 @@ extern "C" const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t 
 extern "C" size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
                                              int64_t total_tokens) {
   if (B <= 0 || H <= 0 || H_kv <= 0 || D <= 0 || total_tokens <= 0) return 0;
-  const size_t ns = size_t(max_splits(B, H_kv, total_tokens));
+  // Enough for either path: per-sequence splits, or prefix splits plus the
+  // suffix's splits.
+  const size_t ns = size_t(max_splits(B, H_kv, total_tokens)) +
+                    size_t(prefix_splits_max(H_kv, total_tokens));
   return size_t(B) * H * ns * (size_t(D) + 2) * sizeof(float);
 }
 
@@ -173,8 +255,65 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
   if (a.total <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
 
   const int waves = waves_for_shape(G, D);
-  plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
   a.out = out;
+
+  // A prefix shared by B >= 2 sequences: read it once per KV head for all of
+  // them (the prefill kernel with the sequences as query rows, split over
+  // the prefix, into partials), each sequence's own suffix with the decode
+  // kernel into further partial slots, then one merge. TQKV_SHARED_PREFIX=0
+  // reads the prefix per sequence instead (tests compare the two).
+  const char* sp_env = getenv("TQKV_SHARED_PREFIX");
+  const bool shared_path = n_segs == 2 && segs[0].shared && B >= 2 && segs[0].n > 0 &&
+                           (D == 64 || D == 128 || D == 256) &&
+                           !(sp_env && strcmp(sp_env, "0") == 0);
+  if (shared_path) {
+    int split_len_p = 0;
+    const int sp_p = prefix_splits(H_kv, int64_t(B) * G, prefill::shared_prefix_block_rows(D),
+                                   segs[0].n, &split_len_p);
+    const int64_t S = segs[1].n;
+    Args s = a;
+    s.seg[0] = a.seg[1];
+    s.n0 = S;
+    s.total = S;
+    int sp_s = 0;
+    if (S > 0) plan_splits(B, H_kv, waves, S, &sp_s, &s.split_len);
+    const int n_part = sp_p + sp_s;
+    const size_t need = size_t(B) * H * n_part * (size_t(D) + 2) * sizeof(float);
+    void* ws = workspace;
+    if (!ws) {
+      if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+    } else if (workspace_bytes < need) {
+      return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+    }
+    float* po = static_cast<float*>(ws);
+    float* pm = po + size_t(B) * H * n_part * D;
+    float* pl = pm + size_t(B) * H * n_part;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (int32_t rc = prefill::shared_prefix_partials(q, B, H, H_kv, D, group_size, bits_k, bits_v,
+                                                     scale, segs[0], sp_p, split_len_p, n_part,
+                                                     po, pm, pl, st))
+      return rc;
+    if (sp_s > 0) {
+      KernelFn sfn = pick(D, bits_k, bits_v, G, group_size, S);
+      s.n_splits = sp_s;
+      s.split_base = sp_p;
+      s.n_part = n_part;
+      s.part_o = po;
+      s.part_m = pm;
+      s.part_l = pl;
+      hipLaunchKernelGGL(sfn, dim3(unsigned(sp_s), unsigned(H_kv), unsigned(B)),
+                         dim3(kWave * waves), 0, st, s);
+      TQKV_LAUNCHED();
+    }
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(kMergeThreads), 0, st,
+                       po, pm, pl, n_part, D, out);
+    TQKV_LAUNCHED();
+    return ok();
+  }
+
+  plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
+  a.split_base = 0;
+  a.n_part = a.n_splits;
   if (a.n_splits > 1) {
     const size_t need = size_t(B) * H * a.n_splits * (size_t(D) + 2) * sizeof(float);
     void* ws = workspace;
@@ -193,8 +332,8 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
                      dim3(kWave * waves), 0, st, a);
   TQKV_LAUNCHED();
   if (a.n_splits > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256), 0,
-                       st, a.part_o, a.part_m, a.part_l, a.n_splits, D, out);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(kMergeThreads), 0, st,
+                       a.part_o, a.part_m, a.part_l, a.n_splits, D, out);
     TQKV_LAUNCHED();
   }
   return ok();

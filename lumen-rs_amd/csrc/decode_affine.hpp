@@ -65,10 +65,13 @@ struct Args {
   int64_t n0, total;
   int64_t split_len;
   int n_splits;
-  uint16_t* out;  // [B, H, 1, D], written directly when n_splits == 1
-  float* part_o;  // [B, H, n_splits, D]
-  float* part_m;  // [B, H, n_splits]
-  float* part_l;  // [B, H, n_splits]
+  // Partial slots per (batch row, query head): split s writes slot
+  // split_base + s of n_part (other slots belong to other launches).
+  int split_base, n_part;
+  uint16_t* out;  // [B, H, 1, D], written directly when n_part == 1
+  float* part_o;  // [B, H, n_part, D]
+  float* part_m;  // [B, H, n_part]
+  float* part_l;  // [B, H, n_part]
 };
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
@@ -431,10 +434,10 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       os += s_acc[w][h][d] * f;
     }
     const int64_t bh = int64_t(b) * a.H + kvh * G + h;
-    if (a.n_splits == 1) {
+    if (a.n_part == 1) {
       a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
     } else {
-      const int64_t row = bh * a.n_splits + split;
+      const int64_t row = bh * a.n_part + a.split_base + split;
       a.part_o[row * D + d] = os;
       if (d == 0) {
         a.part_m[row] = mx;

@@ -547,10 +547,10 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       os += s_acc[w][h][d] * f;
     }
     const int64_t bh = int64_t(b) * a.H + kvh * G + h;
-    if (a.n_splits == 1) {
+    if (a.n_part == 1) {
       a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
     } else {
-      const int64_t row = bh * a.n_splits + split;
+      const int64_t row = bh * a.n_part + a.split_base + split;
       a.part_o[row * D + d] = os;
       if (d == 0) {
         a.part_m[row] = mx;

@@ -5,25 +5,97 @@
 
 #include "prefill_affine.hpp"
 
-using namespace tqkv;
-using namespace tqkv::prefill;
-
+namespace tqkv {
+namespace prefill {
 namespace {
 
 bool valid_bits(int bits) {
   return bits == 2 || bits == 3 || bits == 4 || bits == 5 || bits == 6 || bits == 8;
 }
 
-KernelFn pick(int D, int bk, int bv) {
+KernelFn pick(int D, int bk, int bv, bool h16 = false) {
   switch (D) {
-    case 64: return pick_d64(bk, bv);
-    case 128: return pick_d128(bk, bv);
-    case 256: return pick_d256(bk, bv);
+    case 64: return pick_d64(bk, bv, h16);
+    case 128: return pick_d128(bk, bv, h16);
+    case 256: return pick_d256(bk, bv, h16);
   }
   return nullptr;
 }
 
 }  // namespace
+}  // namespace prefill
+}  // namespace tqkv
+
+using namespace tqkv;
+using namespace tqkv::prefill;
+
+namespace tqkv {
+namespace prefill {
+
+// The shared-prefix half of a decode step: the queries of all B sequences
+// (one position each) against a prefix every sequence shares, read once per
+// KV head. The B sequences act as B query positions of one batch row
+// (rows (b, g) of a KV head), the prefix's keys are split over the grid,
+// and each split's (o, m, l) go to slots [0, n_splits) of the decode's
+// partials [B, H, n_part]. Rows b * H + h line up with the decode kernel's.
+int shared_prefix_block_rows(int D) {
+  switch (D) {
+    case 64: return Shape<64, true>::kRows;
+    case 128: return Shape<128, true>::kRows;
+    default: return Shape<256, true>::kRows;
+  }
+}
+
+int32_t shared_prefix_partials(const uint16_t* q, int B, int H, int H_kv, int D, int gs, int bk,
+                               int bv, float scale, const tqkv_affine_seg& prefix, int n_splits,
+                               int split_len, int n_part, float* part_o, float* part_m,
+                               float* part_l, hipStream_t st) {
+  // f16 operands: decode's bar is the exact dequantization, and f16's
+  // three more significand bits keep the shared-prefix path within it.
+  KernelFn fn = pick(D, bk, bv, true);
+  if (!fn) return fail(TQKV_EUNSUPPORTED, "shared-prefix decode D=%d bits %d/%d", D, bk, bv);
+  Args a{};
+  a.q = q;
+  a.out = nullptr;
+  a.qs_b = 0;
+  a.qs_h = D;
+  a.qs_l = int64_t(H) * D;  // position l of the one batch row = sequence l
+  a.H = H;
+  a.H_kv = H_kv;
+  a.G = H / H_kv;
+  a.L = B;
+  a.gs = gs;
+  a.causal = 0;
+  a.qscale = scale * kLog2e;
+  a.seg[0] = Seg{prefix.k_packed, prefix.k_scales, prefix.k_biases, prefix.v_packed,
+                 prefix.v_scales, prefix.v_biases, prefix.cap, 0};
+  a.seg[1] = a.seg[0];
+  a.n0 = prefix.n;
+  a.total = prefix.n;
+  a.n_splits = n_splits;
+  a.split_len = split_len;
+  a.split_base = 0;
+  a.n_part = n_part;
+  a.part_o = part_o;
+  a.part_m = part_m;
+  a.part_l = part_l;
+  int rows_per_block = 0, threads = 0;
+  switch (D) {
+    case 64: rows_per_block = Shape<64, true>::kRows, threads = Shape<64, true>::kThreads; break;
+    case 128: rows_per_block = Shape<128, true>::kRows, threads = Shape<128, true>::kThreads; break;
+    default: rows_per_block = Shape<256, true>::kRows, threads = Shape<256, true>::kThreads; break;
+  }
+  const int64_t blocks = (int64_t(B) * a.G + rows_per_block - 1) / rows_per_block;
+  a.n_blocks = int(blocks);
+  const int64_t grid = blocks * n_splits * H_kv;
+  if (grid > 0x7fffffff) return fail(TQKV_EINVAL_SHAPE, "grid too large");
+  hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(threads), 0, st, a);
+  TQKV_LAUNCHED();
+  return TQKV_OK;
+}
+
+}  // namespace prefill
+}  // namespace tqkv
 
 extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H,
                                               int32_t H_kv, int32_t L, int32_t D,
@@ -52,6 +124,9 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   Args a{};
   a.q = q;
   a.out = out;
+  a.qs_l = D;
+  a.qs_h = int64_t(L) * D;
+  a.qs_b = int64_t(H) * L * D;
   a.H = H;
   a.H_kv = H_kv;
   a.G = H / H_kv;
@@ -83,15 +158,19 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   a.q_start = q_start;
   a.k_start = k_start;
   a.window = window < 0 ? -1 : window;
+  a.n_splits = 1;
+  a.split_len = int(a.total + kTile - 1) / kTile * kTile;
+  a.split_base = 0;
+  a.n_part = 1;
 
   int rows_per_block = 0, threads = 0;
   switch (D) {
-    case 64: rows_per_block = Shape<64>::kRows, threads = Shape<64>::kThreads; break;
-    case 128: rows_per_block = Shape<128>::kRows, threads = Shape<128>::kThreads; break;
-    default: rows_per_block = Shape<256>::kRows, threads = Shape<256>::kThreads; break;
+    case 64: rows_per_block = Shape<64, false>::kRows, threads = Shape<64, false>::kThreads; break;
+    case 128: rows_per_block = Shape<128, false>::kRows, threads = Shape<128, false>::kThreads; break;
+    default: rows_per_block = Shape<256, false>::kRows, threads = Shape<256, false>::kThreads; break;
   }
   const int64_t blocks = (int64_t(L) * a.G + rows_per_block - 1) / rows_per_block;
-  const int64_t grid = blocks * H_kv * B;
+  const int64_t grid = blocks * a.n_splits * H_kv * B;
   if (grid > 0x7fffffff) return fail(TQKV_EINVAL_SHAPE, "grid too large");
   a.n_blocks = int(blocks);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -39,6 +39,7 @@
 #pragma once
 
 #include <cmath>
+#include <type_traits>
 #include <utility>
 
 #include "common.hpp"
@@ -60,6 +61,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kTau = 8.0f;
 
 typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
 typedef float f2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -79,8 +82,9 @@ struct Seg {
 };
 
 struct Args {
-  const uint16_t* q;  // [B, H, L, D] bf16
-  uint16_t* out;      // [B, H, L, D] bf16
+  const uint16_t* q;  // bf16; row (b, h, l) at b * qs_b + h * qs_h + l * qs_l
+  uint16_t* out;      // bf16, same strides as q (normalized output mode)
+  int64_t qs_b, qs_h, qs_l;
   int H, H_kv, G, L, gs;
   int n_blocks;   // row blocks per (batch row, KV head)
   int causal;
@@ -88,6 +92,13 @@ struct Args {
   Seg seg[2];
   int64_t n0, total;  // keys in segment 0; keys in all
   int64_t q_start, k_start, window;
+  // Key splits: split s covers keys [s * split_len, (s + 1) * split_len).
+  // With part_o set, a row's (o unnormalized, max in log2 units, sum) go to
+  // slot split_base + s of n_part, row index (b * L + l) * H + h.
+  int n_splits, split_len, split_base, n_part;
+  float* part_o;
+  float* part_m;
+  float* part_l;
 };
 
 // Launch shape per head dim: wavefronts per workgroup and query rows per
@@ -95,13 +106,20 @@ struct Args {
 // more matrix-core work; the O accumulators (RW rows x D channels a
 // wavefront) and two wavefronts per SIMD bound RW; D = 256 stays at 128 rows.
 // Loader tasks: 64 keys x D/32 runs x {K, V}, kPer a thread.
-template <int D>
+// The f16 variant serves decode over a shared prefix, where a block holds
+// only the B x G query rows of a KV head: 16 rows a wavefront there spread
+// those rows' products over more SIMDs.
+template <int D, bool H16>
 struct Shape {
   static constexpr int kWaves = D == 64 ? 4 : 8;
-  static constexpr int kRW = D == 256 ? 16 : 32;
+  static constexpr int kRW = (D == 256 || H16) ? 16 : 32;
   static constexpr int kRows = kWaves * kRW;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kPer = 4 * D / kThreads;
+  // Tiles whose raw words are in flight in registers while a tile is
+  // computed. The f16 (decode) variant serves few query rows, so a tile's
+  // compute is short and the loads must run further ahead to keep HBM busy.
+  static constexpr int kSets = H16 ? 2 : 1;
   static_assert(kPer * kThreads == 4 * D, "whole loader tasks per thread");
 };
 
@@ -151,6 +169,17 @@ __device__ __forceinline__ void load_words(uint32_t* dst, const uint32_t* src) {
 // Takes the word by value: hipcc (clang 22) miscompiles __builtin_bit_cast
 // of an ext_vector element expression such as w[1] (it reads element 0).
 __device__ __forceinline__ bf2_t as_bf2(uint32_t x) { return __builtin_bit_cast(bf2_t, x); }
+
+__device__ __forceinline__ uint32_t pack_h16(float lo, float hi) {
+  const f2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, h2_t));
+}
+__device__ __forceinline__ h2_t as_h2(uint32_t x) { return __builtin_bit_cast(h2_t, x); }
+
+// Operand packing of a kernel variant: bf16 (the reference's prefill
+// arithmetic) or f16 (three more significand bits, for decode use).
+template <bool H16>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi);
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   const f2_t f = {lo, hi};
@@ -242,30 +271,84 @@ __device__ __forceinline__ void run_codes(const uint32_t* w, float* f) {
   }
 }
 
-// mlx::dequantize for bf16: bf16(bf16(scale * code) + bias), two codes at a
-// time; out[i] holds codes 2i (low half) and 2i + 1. scale * code is exact in
-// f32 (8-bit by at most 8-bit significands), so each rounding is a single
-// RNE conversion, as in MLX's bf16 arithmetic.
+template <>
+__device__ __forceinline__ uint32_t pack2<false>(float lo, float hi) { return pack_bf16(lo, hi); }
+template <>
+__device__ __forceinline__ uint32_t pack2<true>(float lo, float hi) { return pack_h16(lo, hi); }
+
+// Dequantization of a run, two codes at a time; out[i] holds codes 2i (low
+// half) and 2i + 1. bf16: mlx::dequantize, bf16(bf16(scale * code) + bias):
+// scale * code is exact in f32 (8-bit by at most 8-bit significands), so
+// each rounding is a single RNE conversion, as in MLX's bf16 arithmetic.
+// f16: scale * code + bias in f32 (one rounding), then to f16.
+// f16 dequantization of 8- and 4-bit runs in packed f16 arithmetic, two
+// codes an instruction: a byte permute puts code c under the f16 exponent of
+// 1024 (bits 0x6400 | c is 1024 + c exactly; a 4-bit pair's high code lands
+// as 1024 + 16 c), one packed FMA takes the offset off exactly, and one more
+// gives s * c + b rounded once to f16. Scale and bias convert exactly from
+// bf16 to f16 in f16's normal range.
 template <int BITS>
+__device__ __forceinline__ void dequant_run_h16(const uint32_t* w, uint32_t sb, uint32_t* out) {
+  const _Float16 s = _Float16(__uint_as_float(sb << 16));
+  const _Float16 bias = _Float16(__uint_as_float(sb & 0xffff0000u));
+  const h2_t s2 = {s, s}, b2 = {bias, bias};
+  constexpr uint32_t kExp = 0x64646464u;
+  if constexpr (BITS == 8) {
+    const h2_t one = {_Float16(1.0f), _Float16(1.0f)};
+    const h2_t off = {_Float16(-1024.0f), _Float16(-1024.0f)};
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t sel = (4u + 2 * j) | ((5u + 2 * j) << 16);
+        const h2_t c = __builtin_elementwise_fma(as_h2(__builtin_amdgcn_perm(w[k], kExp, sel)),
+                                                 one, off);
+        out[2 * k + j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2, b2));
+      }
+  } else {
+    static_assert(BITS == 4, "packed f16 dequantization takes 8- or 4-bit codes");
+    const h2_t mul = {_Float16(1.0f), _Float16(0.0625f)};
+    const h2_t off = {_Float16(-1024.0f), _Float16(-64.0f)};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t sel = (4u + j) | ((4u + j) << 16);
+        const uint32_t x = __builtin_amdgcn_perm(w[k], kExp, sel) & 0x64F0640Fu;
+        const h2_t c = __builtin_elementwise_fma(as_h2(x), mul, off);
+        out[4 * k + j] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s2, b2));
+      }
+  }
+}
+
+template <int BITS, bool H16>
 __device__ __forceinline__ void dequant_run(const uint32_t* w, uint32_t sb, uint32_t* out) {
+  if constexpr (H16 && (BITS == 8 || BITS == 4)) {
+    dequant_run_h16<BITS>(w, sb, out);
+    return;
+  }
   float f[32];
   run_codes<BITS>(w, f);
   const float s = __uint_as_float(sb << 16), bias = __uint_as_float(sb & 0xffff0000u);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const uint32_t m = pack_bf16(s * f[2 * i], s * f[2 * i + 1]);
-    out[i] = pack_bf16(__uint_as_float(m << 16) + bias, __uint_as_float(m & 0xffff0000u) + bias);
+    if constexpr (H16) {
+      out[i] = pack_h16(s * f[2 * i] + bias, s * f[2 * i + 1] + bias);
+    } else {
+      const uint32_t m = pack_bf16(s * f[2 * i], s * f[2 * i + 1]);
+      out[i] = pack_bf16(__uint_as_float(m << 16) + bias, __uint_as_float(m & 0xffff0000u) + bias);
+    }
   }
 }
 
 // Writes a K task into LDS: row `key` of K at channels [32 run, 32 run + 32).
 // Keys past the end are zero (their scores are masked).
-template <int D, int BITS, int NW>
+template <int D, int BITS, bool H16, int NW>
 __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int key, int run) {
   constexpr int KSTR = kKStride<D>;
   uint32_t v[16];
   if (st.ok) {
-    dequant_run<BITS>(st.w, st.s | (st.b << 16), v);
+    dequant_run<BITS, H16>(st.w, st.s | (st.b << 16), v);
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = 0u;
@@ -277,12 +360,12 @@ __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int k
 
 // Writes a V task into column `key` of V^T, channels [32 run, 32 run + 32).
 // Keys past the end are zero (0 * v stays finite).
-template <int D, int BITS, int NW>
+template <int D, int BITS, bool H16, int NW>
 __device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vt, int key, int run) {
   constexpr int VSTR = kVStride;
   uint32_t v[16];
   if (st.ok) {
-    dequant_run<BITS>(st.w, st.s | (st.b << 16), v);
+    dequant_run<BITS, H16>(st.w, st.s | (st.b << 16), v);
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = 0u;
@@ -295,16 +378,45 @@ __device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vt, int k
   }
 }
 
+// The V tasks' stage registers: their own set, or the K tasks' set.
+template <bool Split, typename K, typename V>
+__device__ __forceinline__ decltype(auto) v_stages(K& k, V& v) {
+  if constexpr (Split)
+    return (v);
+  else
+    return (k);
+}
+
+// The 16x16x32 matrix-core product of the variant's operand type.
+template <bool H16, typename V>
+__device__ __forceinline__ f4_t mma(V a, V b, f4_t c) {
+  if constexpr (H16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// acc + both halves of a packed pair (v_dot2 against a (1, 1) splat).
+template <bool H16>
+__device__ __forceinline__ float sum2(uint32_t w, float acc) {
+  if constexpr (H16) {
+    const h2_t one = {_Float16(1.0f), _Float16(1.0f)};
+    return __builtin_amdgcn_fdot2(as_h2(w), one, acc, false);
+  } else {
+    const bf2_t one = {__bf16(1.0f), __bf16(1.0f)};
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w), one, acc, false);
+  }
+}
+
 // Two wavefronts per SIMD (at most 256 registers a lane): one wavefront's
 // softmax and dequantization then overlap the other's matrix-core work.
-template <int D, int BK, int BV>
-__global__ __launch_bounds__(Shape<D>::kWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
+template <int D, int BK, int BV, bool H16>
+__global__ __launch_bounds__((Shape<D, H16>::kThreads)) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_affine_kernel(const Args a) {
-  constexpr int kWaves = Shape<D>::kWaves, RW = Shape<D>::kRW, kRows = Shape<D>::kRows;
+  constexpr int kWaves = Shape<D, H16>::kWaves, RW = Shape<D, H16>::kRW, kRows = Shape<D, H16>::kRows;
   constexpr int NR = RW / 16, ND = D / 32, NT = D / 16;
   constexpr int KSTR = kKStride<D>, VSTR = kVStride;
-  constexpr int kPer = Shape<D>::kPer, kThreads = Shape<D>::kThreads;
-  constexpr int NW = BK > BV ? BK : BV;
+  constexpr int kPer = Shape<D, H16>::kPer, kThreads = Shape<D, H16>::kThreads;
   // Two tile buffers: tile t is read from one while tile t + 1 is written
   // into the other, so a tile costs one barrier.
   __shared__ __attribute__((aligned(16))) uint16_t Ks2[2][kTile * KSTR];
@@ -319,22 +431,26 @@ void prefill_affine_kernel(const Args a) {
   const int n_wg = int(gridDim.x);
   int lin = int(blockIdx.x);
   if (n_wg % kXcds == 0) lin = (lin % kXcds) * (n_wg / kXcds) + lin / kXcds;
+  const int per_unit = a.n_blocks * a.n_splits;
   const int blk = a.n_blocks - 1 - lin % a.n_blocks;
-  const int kvh = (lin / a.n_blocks) % a.H_kv, b = lin / (a.n_blocks * a.H_kv);
+  const int split = (lin % per_unit) / a.n_blocks;
+  const int kvh = (lin / per_unit) % a.H_kv, b = lin / (per_unit * a.H_kv);
   const int64_t rows = int64_t(a.L) * a.G;
   const int64_t row0 = int64_t(blk) * kRows;
   const int64_t row_end = row0 + kRows < rows ? row0 + kRows : rows;
   const int64_t qa_lo = a.q_start + row0 / a.G, qa_hi = a.q_start + (row_end - 1) / a.G;
 
-  // Visible key indices of the block.
-  int64_t kk_lo = 0, kk_hi = a.total - 1;
+  // Visible key indices of the block, within its split.
+  int64_t kk_lo = int64_t(split) * a.split_len, kk_hi = a.total - 1;
+  if (kk_lo + a.split_len - 1 < kk_hi) kk_hi = kk_lo + a.split_len - 1;
   if (a.causal) {
     if (qa_hi - a.k_start < kk_hi) kk_hi = qa_hi - a.k_start;
     if (a.window >= 0 && qa_lo - a.window + 1 - a.k_start > kk_lo)
       kk_lo = qa_lo - a.window + 1 - a.k_start;
   }
 
-  bf8_t qf[NR][ND];
+  using op8_t = std::conditional_t<H16, h8_t, bf8_t>;
+  op8_t qf[NR][ND];
   int64_t qabs[NR], orow[NR];
   bool rvalid[NR];
 #pragma unroll
@@ -344,10 +460,19 @@ void prefill_affine_kernel(const Args a) {
     const int64_t rr = rvalid[j] ? r : rows - 1;
     const int64_t l = rr / a.G, g = rr % a.G;
     qabs[j] = a.q_start + l;
-    orow[j] = ((int64_t(b) * a.H + int64_t(kvh) * a.G + g) * a.L + l) * D;
+    orow[j] = int64_t(b) * a.qs_b + (int64_t(kvh) * a.G + g) * a.qs_h + l * a.qs_l;
 #pragma unroll
     for (int s = 0; s < ND; ++s)
-      qf[j][s] = *reinterpret_cast<const bf8_t*>(a.q + orow[j] + 32 * s + 8 * lg);
+    {
+      const bf8_t x = *reinterpret_cast<const bf8_t*>(a.q + orow[j] + 32 * s + 8 * lg);
+      if constexpr (H16) {
+        // bf16 -> f16 is exact for |q| in f16's normal range.
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[j][s][e] = _Float16(float(x[e]));
+      } else {
+        qf[j][s] = x;
+      }
+    }
   }
 
   float m[NR], lsum[NR];
@@ -371,7 +496,17 @@ void prefill_affine_kernel(const Args a) {
     // Task i of this thread: tid + i * kThreads; the first 2D tasks are K
     // runs, the rest V runs (a whole wavefront takes one kind, so the kind
     // and its pointers are uniform).
-    Stage<NW> st[kPer];
+    constexpr int NS = Shape<D, H16>::kSets;
+    // K and V tasks keep their words in separate registers: with one shared
+    // set the two load paths meet in register copies that must wait for the
+    // loads to land, which would expose the full memory latency at issue.
+    // (The bf16 prefill variant shares one set: it has no registers to
+    // spare, and its long tiles hide the wait behind the other wavefront.)
+    constexpr bool kSplit = H16;
+    constexpr int NW = BK > BV ? BK : BV;
+    Stage<kSplit ? BK : NW> stk[NS][kPer];
+    Stage<kSplit ? BV : NW> stv_own[kSplit ? NS : 1][kPer];
+    auto& stv = v_stages<kSplit>(stk, stv_own);
     SlabPtrs tp[kPer];
     bool tv[kPer];
     int tkey[kPer], trun[kPer];
@@ -388,153 +523,173 @@ void prefill_affine_kernel(const Args a) {
       tp[i].b0 = tv[i] ? vp.b0 : kp.b0;
       tp[i].b1 = tv[i] ? vp.b1 : kp.b1;
     }
-#define TQKV_LOAD_TILE(T)                                                        \
+#define TQKV_LOAD_TILE(S, T)                                                     \
   _Pragma("unroll") for (int i = 0; i < kPer; ++i) {                             \
     if (tv[i])                                                                   \
-      load_stage<D, BV>(st[i], tp[i], a, (T) * kTile + tkey[i], trun[i]);        \
+      load_stage<D, BV>(stv[S][i], tp[i], a, (T) * kTile + tkey[i], trun[i]);    \
     else                                                                         \
-      load_stage<D, BK>(st[i], tp[i], a, (T) * kTile + tkey[i], trun[i]);        \
+      load_stage<D, BK>(stk[S][i], tp[i], a, (T) * kTile + tkey[i], trun[i]);    \
   }
-#define TQKV_STORE_TILE(BUF)                                                     \
+#define TQKV_STORE_TILE(S, BUF)                                                  \
   _Pragma("unroll") for (int i = 0; i < kPer; ++i) {                             \
     if (tv[i])                                                                   \
-      store_v<D, BV>(st[i], Vt2[BUF], tkey[i], trun[i]);                         \
+      store_v<D, BV, H16>(stv[S][i], Vt2[BUF], tkey[i], trun[i]);                \
     else                                                                         \
-      store_k<D, BK>(st[i], Ks2[BUF], tkey[i], trun[i]);                         \
+      store_k<D, BK, H16>(stk[S][i], Ks2[BUF], tkey[i], trun[i]);                \
   }
-    TQKV_LOAD_TILE(int(t_lo))
+    TQKV_LOAD_TILE(0, int(t_lo))
     // Everything loaded so far (the Q fragments, the first tile) has landed:
     // without this the compiler's loop-carried wait analysis keeps the Q
     // loads pending and makes every tile's MFMAs wait for the next tile's
     // prefetch. (vmcnt(0); expcnt and lgkmcnt unchanged.)
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    TQKV_STORE_TILE(0)
-    if (t_lo < t_hi) {
-      TQKV_LOAD_TILE(int(t_lo) + 1)
-    }
+    TQKV_STORE_TILE(0, 0)
+    // Tile t_lo + 1 + k into set (k + 1) % NS: tile x sits in set
+    // (x - t_lo) % NS until it is dequantized.
+    static_for<NS>([&](auto k) {
+      if (t_lo + 1 + k.value <= t_hi) {
+        TQKV_LOAD_TILE((k.value + 1) % NS, int(t_lo) + 1 + k.value)
+      }
+    });
     __syncthreads();
     // The two wavefronts on a SIMD (w and w + kWaves / 2) take the tile's
     // work in opposite orders, so one's dequantization (VALU) runs while the
     // other's products (MFMA) do.
     const bool dequant_first = wave >= kWaves / 2;
-    int cur = 0;
-    for (int t = int(t_lo); t <= int(t_hi); ++t, cur ^= 1) {
-      // Tile t + 1 into the other buffer (last read in iteration t - 1,
-      // before the barrier that ended it), then fetch tile t + 2.
+    const bool live = row0 + int64_t(wave) * RW < rows;
+    // One tile: S holds tile t + 1's words, which go into the other LDS
+    // buffer (last read in the previous tile, before the barrier that ended
+    // it); S then fetches tile t + 1 + NS.
+    auto tile = [&](int t, int cur, auto set) __attribute__((always_inline)) {
+      constexpr int S = decltype(set)::value;
       if (dequant_first && t < t_hi) {
-        TQKV_STORE_TILE(cur ^ 1)
-        if (t + 1 < t_hi) {
-          TQKV_LOAD_TILE(t + 2)
+        TQKV_STORE_TILE(S, cur ^ 1)
+        if (t + NS < t_hi + 1) {
+          TQKV_LOAD_TILE(S, t + 1 + NS)
         }
       }
       const uint16_t* Ks = Ks2[cur];
       const uint16_t* Vt = Vt2[cur];
+      // A wavefront whose rows are all past the end (a short block) only
+      // dequantizes.
+      if (live) {
 
-      f4_t sc[4][NR];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < NR; ++j) sc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int s = 0; s < ND; ++s)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bf8_t ka = *reinterpret_cast<const bf8_t*>(Ks + (16 * i + lr) * KSTR + 32 * s + 8 * lg);
-#pragma unroll
-          for (int j = 0; j < NR; ++j)
-            sc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qf[j][s], sc[i][j], 0, 0, 0);
-        }
-
-      // Mask: only on tiles some row of the block sees in part. Key offset
-      // o in the tile is visible to a row iff lo <= o <= hi.
-      const int64_t kbase = a.k_start + int64_t(t) * kTile;
-      const int rem = a.total - int64_t(t) * kTile < kTile ? int(a.total - int64_t(t) * kTile) : kTile;
-      const bool full = rem == kTile &&
-                        (!a.causal || (kbase + kTile - 1 <= qa_lo &&
-                                       (a.window < 0 || qa_hi < kbase + a.window)));
-      if (!full) {
-#pragma unroll
-        for (int j = 0; j < NR; ++j) {
-          int hi = rem - 1, lo = 0;
-          if (a.causal) {
-            const int64_t dq = qabs[j] - kbase;  // the row's own offset
-            if (dq < hi) hi = dq < -1 ? -1 : int(dq);
-            if (a.window >= 0) {
-              const int64_t first = dq - a.window + 1;
-              lo = first < 0 ? 0 : (first > kTile ? kTile : int(first));
-            }
+        f4_t sc[4][NR];
+  #pragma unroll
+        for (int i = 0; i < 4; ++i)
+  #pragma unroll
+          for (int j = 0; j < NR; ++j) sc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+        for (int s = 0; s < ND; ++s)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const op8_t ka = *reinterpret_cast<const op8_t*>(Ks + (16 * i + lr) * KSTR + 32 * s + 8 * lg);
+  #pragma unroll
+            for (int j = 0; j < NR; ++j)
+              sc[i][j] = mma<H16>(ka, qf[j][s], sc[i][j]);
           }
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int o = 16 * i + 4 * lg + r;
-              if (o < lo || o > hi) sc[i][j][r] = -INFINITY;
+
+        // Mask: only on tiles some row of the block sees in part. Key offset
+        // o in the tile is visible to a row iff lo <= o <= hi.
+        const int64_t kbase = a.k_start + int64_t(t) * kTile;
+        const int rem = a.total - int64_t(t) * kTile < kTile ? int(a.total - int64_t(t) * kTile) : kTile;
+        const bool full = rem == kTile &&
+                          (!a.causal || (kbase + kTile - 1 <= qa_lo &&
+                                         (a.window < 0 || qa_hi < kbase + a.window)));
+        if (!full) {
+  #pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            int hi = rem - 1, lo = 0;
+            if (a.causal) {
+              const int64_t dq = qabs[j] - kbase;  // the row's own offset
+              if (dq < hi) hi = dq < -1 ? -1 : int(dq);
+              if (a.window >= 0) {
+                const int64_t first = dq - a.window + 1;
+                lo = first < 0 ? 0 : (first > kTile ? kTile : int(first));
+              }
             }
+  #pragma unroll
+            for (int i = 0; i < 4; ++i)
+  #pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int o = 16 * i + 4 * lg + r;
+                if (o < lo || o > hi) sc[i][j][r] = -INFINITY;
+              }
+          }
         }
-      }
-#pragma unroll
-      for (int j = 0; j < NR; ++j) {
-        float mx = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[i][j][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        mx *= a.qscale;  // qscale > 0: the max of the scaled scores
-        const bool up = mx > m[j] + kTau;
-        if (__any(up)) {
-          const float mn = up ? mx : m[j];
-          const float alpha = up ? __builtin_amdgcn_exp2f(m[j] - mn) : 1.0f;
-          lsum[j] *= alpha;
-#pragma unroll
-          for (int t2 = 0; t2 < NT; ++t2) o[t2][j] *= alpha;
-          m[j] = mn;
-        }
-        const float nm = m[j] == -INFINITY ? 0.0f : -m[j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm));
-      }
-
-      const bf2_t kOnes = {__bf16(1.0f), __bf16(1.0f)};
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        bf8_t pb[NR];
-#pragma unroll
+  #pragma unroll
         for (int j = 0; j < NR; ++j) {
-          const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
-          const u32x4_t w = {pack_bf16(p0[0], p0[1]), pack_bf16(p0[2], p0[3]),
-                             pack_bf16(p1[0], p1[1]), pack_bf16(p1[2], p1[3])};
-          pb[j] = __builtin_bit_cast(bf8_t, w);
-          // The row sum counts the weights as rounded for the matrix cores,
-          // so the output stays an exact convex combination of them.
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            lsum[j] = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w[e]), kOnes, lsum[j], false);
+          float mx = -INFINITY;
+  #pragma unroll
+          for (int i = 0; i < 4; ++i)
+  #pragma unroll
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[i][j][r]);
+          mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+          mx *= a.qscale;  // qscale > 0: the max of the scaled scores
+          const bool up = mx > m[j] + kTau;
+          if (__any(up)) {
+            const float mn = up ? mx : m[j];
+            const float alpha = up ? __builtin_amdgcn_exp2f(m[j] - mn) : 1.0f;
+            lsum[j] *= alpha;
+  #pragma unroll
+            for (int t2 = 0; t2 < NT; ++t2) o[t2][j] *= alpha;
+            m[j] = mn;
+          }
+          const float nm = m[j] == -INFINITY ? 0.0f : -m[j];
+  #pragma unroll
+          for (int i = 0; i < 4; ++i)
+  #pragma unroll
+            for (int r = 0; r < 4; ++r)
+              sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm));
         }
-#pragma unroll
-        for (int t2 = 0; t2 < NT; ++t2) {
-          const uint16_t* vrow = Vt + (16 * t2 + lr) * VSTR + 32 * u + 4 * lg;
-          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
-          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
-          const bf8_t va = __builtin_bit_cast(bf8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-          for (int j = 0; j < NR; ++j)
-            o[t2][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[j], o[t2][j], 0, 0, 0);
+
+
+  #pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          op8_t pb[NR];
+  #pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
+            const u32x4_t w = {pack2<H16>(p0[0], p0[1]), pack2<H16>(p0[2], p0[3]),
+                               pack2<H16>(p1[0], p1[1]), pack2<H16>(p1[2], p1[3])};
+            pb[j] = __builtin_bit_cast(op8_t, w);
+            // The row sum counts the weights as rounded for the matrix cores,
+            // so the output stays an exact convex combination of them.
+  #pragma unroll
+            for (int e = 0; e < 4; ++e)
+              lsum[j] = sum2<H16>(w[e], lsum[j]);
+          }
+  #pragma unroll
+          for (int t2 = 0; t2 < NT; ++t2) {
+            const uint16_t* vrow = Vt + (16 * t2 + lr) * VSTR + 32 * u + 4 * lg;
+            const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
+            const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
+            const op8_t va = __builtin_bit_cast(op8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
+  #pragma unroll
+            for (int j = 0; j < NR; ++j)
+              o[t2][j] = mma<H16>(va, pb[j], o[t2][j]);
+          }
         }
       }
-
       if (!dequant_first && t < t_hi) {
-        TQKV_STORE_TILE(cur ^ 1)
-        if (t + 1 < t_hi) {
-          TQKV_LOAD_TILE(t + 2)
+        TQKV_STORE_TILE(S, cur ^ 1)
+        if (t + NS < t_hi + 1) {
+          TQKV_LOAD_TILE(S, t + 1 + NS)
         }
       }
       __syncthreads();
+    };
+    // Unrolled over the stage sets so each one stays in named registers.
+    int t = int(t_lo), cur = 0;
+    while (t <= int(t_hi)) {
+      static_for<NS>([&](auto k) {
+        if (t <= int(t_hi)) {
+          tile(t, cur, std::integral_constant<int, (k.value + 1) % NS>{});
+          ++t;
+          cur ^= 1;
+        }
+      });
     }
   }
 #undef TQKV_STORE_TILE
@@ -545,8 +700,21 @@ void prefill_affine_kernel(const Args a) {
     float tot = lsum[j];
     tot += __shfl_xor(tot, 16, kWave);
     tot += __shfl_xor(tot, 32, kWave);
-    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-    if (rvalid[j]) {
+    if (!rvalid[j]) continue;
+    if (a.part_o) {
+      const int64_t r = row0 + wave * RW + 16 * j + lr;
+      const int64_t l = r / a.G, h = int64_t(kvh) * a.G + r % a.G;
+      const int64_t slot = ((int64_t(b) * a.L + l) * a.H + h) * a.n_part + a.split_base + split;
+      float* po = a.part_o + slot * D;
+#pragma unroll
+      for (int t2 = 0; t2 < NT; ++t2)
+        *reinterpret_cast<f4_t*>(po + 16 * t2 + 4 * lg) = o[t2][j];
+      if (lg == 0) {
+        a.part_m[slot] = m[j];
+        a.part_l[slot] = tot;
+      }
+    } else {
+      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2) {
         const f4_t v = o[t2][j] * inv;
@@ -560,33 +728,33 @@ void prefill_affine_kernel(const Args a) {
 typedef void (*KernelFn)(Args);
 
 // The kernel for (D, bits_k, bits_v), bits in {2, 3, 4, 5, 6, 8}; null if
-// unsupported.
-KernelFn pick_d64(int bk, int bv);
-KernelFn pick_d128(int bk, int bv);
-KernelFn pick_d256(int bk, int bv);
+// unsupported. h16: the f16-operand variant.
+KernelFn pick_d64(int bk, int bv, bool h16);
+KernelFn pick_d128(int bk, int bv, bool h16);
+KernelFn pick_d256(int bk, int bv, bool h16);
 
-template <int D, int BK>
+template <int D, int BK, bool H16>
 KernelFn pick_bv(int bv) {
   switch (bv) {
-    case 2: return prefill_affine_kernel<D, BK, 2>;
-    case 3: return prefill_affine_kernel<D, BK, 3>;
-    case 4: return prefill_affine_kernel<D, BK, 4>;
-    case 5: return prefill_affine_kernel<D, BK, 5>;
-    case 6: return prefill_affine_kernel<D, BK, 6>;
-    case 8: return prefill_affine_kernel<D, BK, 8>;
+    case 2: return prefill_affine_kernel<D, BK, 2, H16>;
+    case 3: return prefill_affine_kernel<D, BK, 3, H16>;
+    case 4: return prefill_affine_kernel<D, BK, 4, H16>;
+    case 5: return prefill_affine_kernel<D, BK, 5, H16>;
+    case 6: return prefill_affine_kernel<D, BK, 6, H16>;
+    case 8: return prefill_affine_kernel<D, BK, 8, H16>;
   }
   return nullptr;
 }
 
-template <int D>
+template <int D, bool H16>
 KernelFn pick_for(int bk, int bv) {
   switch (bk) {
-    case 2: return pick_bv<D, 2>(bv);
-    case 3: return pick_bv<D, 3>(bv);
-    case 4: return pick_bv<D, 4>(bv);
-    case 5: return pick_bv<D, 5>(bv);
-    case 6: return pick_bv<D, 6>(bv);
-    case 8: return pick_bv<D, 8>(bv);
+    case 2: return pick_bv<D, 2, H16>(bv);
+    case 3: return pick_bv<D, 3, H16>(bv);
+    case 4: return pick_bv<D, 4, H16>(bv);
+    case 5: return pick_bv<D, 5, H16>(bv);
+    case 6: return pick_bv<D, 6, H16>(bv);
+    case 8: return pick_bv<D, 8, H16>(bv);
   }
   return nullptr;
 }

@@ -3,6 +3,8 @@
 
 namespace tqkv {
 namespace prefill {
-KernelFn pick_d128(int bk, int bv) { return pick_for<128>(bk, bv); }
+KernelFn pick_d128(int bk, int bv, bool h16) {
+  return h16 ? pick_for<128, true>(bk, bv) : pick_for<128, false>(bk, bv);
+}
 }  // namespace prefill
 }  // namespace tqkv

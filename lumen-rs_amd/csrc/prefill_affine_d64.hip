@@ -3,6 +3,8 @@
 
 namespace tqkv {
 namespace prefill {
-KernelFn pick_d64(int bk, int bv) { return pick_for<64>(bk, bv); }
+KernelFn pick_d64(int bk, int bv, bool h16) {
+  return h16 ? pick_for<64, true>(bk, bv) : pick_for<64, false>(bk, bv);
+}
 }  // namespace prefill
 }  // namespace tqkv

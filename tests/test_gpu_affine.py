@@ -239,6 +239,43 @@ def test_decode_shared_prefix_plus_suffix(T, kernel):
     check_close(got, wf, wm)
 
 
+@pytest.mark.parametrize("B,H,Hkv,D,P,S,bk,bv,gs", [
+    (8, 32, 8, 128, 5000, 300, 8, 4, 64),   # config 4 widths, shorter prefix
+    (2, 16, 8, 256, 1000, 0, 3, 3, 64),     # prefix only
+    (4, 8, 8, 64, 777, 65, 4, 4, 32),
+    (5, 12, 4, 128, 2049, 1, 4, 8, 128),    # odd batch, G = 3
+])
+def test_decode_shared_prefix_read_once(T, monkeypatch, B, H, Hkv, D, P, S, bk, bv, gs):
+    # With B >= 2 sequences over a shared prefix the prefix is read once per
+    # KV head for all of them (MFMA over the sequences' query rows, split
+    # over the prefix) and merged with each suffix's partials; the
+    # per-sequence path (TQKV_SHARED_PREFIX=0) must agree, and both meet the
+    # oracle's bar.
+    print(f"[decode-shared] B={B} H={H}/{Hkv} D={D} P={P} S={S} bits={bk}/{bv} gs={gs}",
+          flush=True)
+    seed = B * 131 + D + P + S
+    q = kv_bf16((B, H, 1, D), seed, std=D ** -0.5 * 4)
+    kp, vp = kv_bf16((1, Hkv, P, D), seed + 1), kv_bf16((1, Hkv, P, D), seed + 2)
+    ks, vs = kv_bf16((B, Hkv, S, D), seed + 3), kv_bf16((B, Hkv, S, D), seed + 4)
+    (kph, kpd), (vph, vpd) = _cache(kp, gs, bk), _cache(vp, gs, bv)
+    (ksh, ksd), (vsh, vsd) = _cache(ks, gs, bk, S + 3), _cache(vs, gs, bv, S + 3)
+    segs = [(kpd, vpd, P, P, True), (ksd, vsd, S + 3, S, False)]
+    monkeypatch.delenv("TQKV_SHARED_PREFIX", raising=False)
+    got = run_decode(T, q, segs, B, H, Hkv, D, gs, bk, bv, 1.0)
+    monkeypatch.setenv("TQKV_SHARED_PREFIX", "0")
+    per_seq = run_decode(T, q, segs, B, H, Hkv, D, gs, bk, bv, 1.0)
+    kfull = tuple(np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
+                  for a, b in zip(kph, ksh))
+    vfull = tuple(np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
+                  for a, b in zip(vph, vsh))
+    wf, _, _ = O.attend_affine(q, kfull, vfull, gs, bk, bv, 1.0)
+    wm, _, _ = O.attend_affine(q, kfull, vfull, gs, bk, bv, 1.0, dequant="bf16")
+    check_close(got, wf, wm)
+    check_close(per_seq, wf, wm)
+    d = np.abs(O.bf16_to_f32(got) - O.bf16_to_f32(per_seq))
+    print(f"[decode-shared] shared vs per-sequence max={d.max():.3e}", flush=True)
+
+
 def test_decode_rejects_unreadable_layouts(T):
     q = T.DeviceArray((1, 12, 1, 128), np.uint16)
     out = T.DeviceArray((1, 12, 1, 128), np.uint16)
