@@ -124,8 +124,8 @@ def main():
 
     def step(i, events=None):
         pos = N + i  # the new token's row
-        T.affine_quantize(newk.ptr, slabs, 1, D, GS, BITS, *kp, cap, pos, stream)
-        T.affine_quantize(newv.ptr, slabs, 1, D, GS, BITS, *vp, cap, pos, stream)
+        T.affine_quantize_kv(newk.ptr, newv.ptr, slabs, 1, D, GS, BITS, BITS, kp, vp, cap, pos,
+                             stream)
         seg = T.affine_seg(kp, vp, cap, pos + 1)
         if events:
             hip.record(events[0], stream)
@@ -464,10 +464,10 @@ def append_main(T, hip, args):
     sgn = {n: T.DeviceArray((slabs, S, M // 32), np.uint32) for n in ("k", "v")}
     rn = {n: T.DeviceArray((slabs, S), np.float32) for n in ("k", "v")}
 
-    def quant():
-        for n in ("k", "v"):
-            T.affine_quantize(x[n].ptr, slabs, S, D, GS, BITS, *(a.ptr for a in q3[n]),
-                              stream=stream)
+    def quant():  # K and V in one launch, as a cache append issues them
+        T.affine_quantize_kv(x["k"].ptr, x["v"].ptr, slabs, S, D, GS, BITS, BITS,
+                             tuple(a.ptr for a in q3["k"]), tuple(a.ptr for a in q3["v"]),
+                             stream=stream)
 
     def dequant():
         for n in ("k", "v"):
@@ -476,8 +476,9 @@ def append_main(T, hip, args):
     def rotq():
         for n in ("k", "v"):
             T.rotate_bf16(x[n].ptr, slabs * S, D, R.ptr, False, rot[n].ptr, stream)
-            T.affine_quantize(rot[n].ptr, slabs, S, D, GS, BITS, *(a.ptr for a in q3[n]),
-                              stream=stream)
+        T.affine_quantize_kv(rot["k"].ptr, rot["v"].ptr, slabs, S, D, GS, BITS, BITS,
+                             tuple(a.ptr for a in q3["k"]), tuple(a.ptr for a in q3["v"]),
+                             stream=stream)
 
     def tq():
         for n in ("k", "v"):
@@ -502,8 +503,8 @@ def append_main(T, hip, args):
         {"workload": "BASELINE config 0: quantize-on-append of one layer's K and V "
                      "(B=1, 8 KV heads, D=128, 4,096 tokens, 4-bit gs64)",
          "batch": B, "kv_heads": HKV, "head_dim": D, "tokens": S, "bits": BITS, "group_size": GS},
-        _hbm((in_bytes + q_bytes) / (ms_q * 1e-3) / 1e9, "affine_quantize_kernel (K then V)",
-             in_bytes + q_bytes, ms_q / 2),
+        _hbm((in_bytes + q_bytes) / (ms_q * 1e-3) / 1e9,
+             "affine_quantize_kernel<128> (K and V in one launch)", in_bytes + q_bytes, ms_q),
         {"dequantize": {"ms": round(ms_d, 5), "gbps": round((q_bytes + in_bytes) / (ms_d * 1e-3) / 1e9, 1)},
          "affine_rotation": {"ms": round(ms_r, 5),
                              "tokens_per_s": round(S / (ms_r * 1e-3), 1),
@@ -570,8 +571,8 @@ def decode1_main(T, hip, args):
     pos = [N]
 
     def append():
-        T.affine_quantize(nk.ptr, slabs, 1, D, GS, BITS, *kp, cap, pos[0], stream)
-        T.affine_quantize(nv.ptr, slabs, 1, D, GS, BITS, *vp, cap, pos[0], stream)
+        T.affine_quantize_kv(nk.ptr, nv.ptr, slabs, 1, D, GS, BITS, BITS, kp, vp, cap, pos[0],
+                             stream)
         pos[0] += 1
 
     def decode():
@@ -649,8 +650,8 @@ def prefix_main(T, hip, args):
     pos = [S0]
 
     def step(events=None):
-        T.affine_quantize(nk.ptr, B * HKV, 1, D, GS, BK, *skp, cap, pos[0], stream)
-        T.affine_quantize(nv.ptr, B * HKV, 1, D, GS, BV, *svp, cap, pos[0], stream)
+        T.affine_quantize_kv(nk.ptr, nv.ptr, B * HKV, 1, D, GS, BK, BV, skp, svp, cap, pos[0],
+                             stream)
         pos[0] += 1
         segs = [T.affine_seg(pkp, pvp, P, P, shared=True), T.affine_seg(skp, svp, cap, pos[0])]
         if events:

@@ -76,6 +76,18 @@ int32_t tqkv_affine_quantize(const uint16_t* x, int64_t n_slabs, int64_t s, int3
                              int64_t dst_start, tqkv_stream stream);
 
 /*
+ * Both quantize calls of one cache append (K with bits_k, V with bits_v;
+ * native_cache.rs:968-971 and 1445-1448 quantize keys, then values) in one
+ * launch, each bit-exact with tqkv_affine_quantize on the same arguments.
+ * K and V share n_slabs, s, dim, group_size, dst_cap and dst_start.
+ */
+int32_t tqkv_affine_quantize_kv(const uint16_t* k, const uint16_t* v, int64_t n_slabs, int64_t s,
+                                int32_t dim, int32_t group_size, int32_t bits_k, int32_t bits_v,
+                                uint32_t* k_packed, uint16_t* k_scales, uint16_t* k_biases,
+                                uint32_t* v_packed, uint16_t* v_scales, uint16_t* v_biases,
+                                int64_t dst_cap, int64_t dst_start, tqkv_stream stream);
+
+/*
  * mlx::dequantize(packed, scales, biases, group_size, bits) to bf16, as the
  * reference's prefill fallback uses it (gemma4_moe.rs:2394-2399):
  * out = bf16(bf16(scale * code) + bias). rows = number of [dim] rows.

@@ -1,11 +1,15 @@
 // Quantize-on-append in MLX's affine format, bit-exact with its Metal kernel,
 // and the matching dequantize.
 //
-// One wavefront per row. Each lane owns EPL = dim / 64 consecutive elements
-// (all lanes of a group hold the same group), so a group's min and max are a
-// butterfly over gs / EPL lanes. Codes go through LDS as bytes and are packed
-// into the LSB-first u32 stream one output word per lane, which handles
-// widths whose codes straddle words (3, 5, 6 bits) without special cases.
+// Layout of the work: each lane owns EPL = 8 consecutive elements of a row
+// (16 at dim 1024), read as one 16-byte load, so a row takes dim / EPL
+// lanes and a wavefront holds several rows (4 at dim 128); a 256-thread
+// workgroup takes a block of rows of one tensor, and the grid covers K and
+// V in one launch. A group's lanes are adjacent, so its min and max are a
+// butterfly over gs / EPL lanes. Each lane packs its codes into a 64-bit
+// chunk (8 x bits bits), the chunks go through LDS, and each output word is
+// cut from the one or two chunks it overlaps: LSB-first u32 words for every
+// width, including those whose codes straddle words (3, 5, 6 bits).
 //
 // Arithmetic follows MLX's affine_quantize exactly (see the oracle's
 // affine.cpp for the statement): f32 throughout, IEEE division (hipcc's
@@ -19,77 +23,126 @@ namespace tqkv {
 namespace {
 
 constexpr int kWave = 64;
+constexpr int kQThreads = 256;
+constexpr int kQWaves = kQThreads / kWave;
 
-template <int EPL>
-__global__ __launch_bounds__(kWave) void affine_quantize_kernel(
-    const uint16_t* __restrict__ x, int64_t s, int dim, int gs, int bits,
-    uint32_t* __restrict__ packed, uint16_t* __restrict__ scales,
-    uint16_t* __restrict__ biases, int64_t dst_cap, int64_t dst_start) {
-  __shared__ uint8_t codes[1024];
-  const int lane = threadIdx.x;
-  const int64_t r = blockIdx.x;
-  const int64_t slab = r / s, j = r % s;
-  const int64_t dst = slab * dst_cap + dst_start + j;
-  const uint16_t* xr = x + r * dim;
-  const int base = lane * EPL;
-  const bool active = base < dim;  // dim = 32 leaves half the wave idle
+// One tensor of a quantize launch: rows [n_slabs * s] of bf16 x into a
+// cache buffer at rows slab * dst_cap + dst_start + j.
+struct QTensor {
+  const uint16_t* x;
+  uint32_t* packed;
+  uint16_t* scales;
+  uint16_t* biases;
+  int bits;
+};
 
-  float v[EPL];
+struct QArgs {
+  QTensor t[2];
+  int64_t s, rows, dst_cap, dst_start;
+  int gs;
+  int blocks_per_tensor;  // row blocks of one tensor
+  int n_blocks;           // over all tensors
+};
+
+template <int D>
+struct QShape {
+  static constexpr int kEpl = D > 512 ? 16 : 8;   // elements a lane
+  static constexpr int kLpr = D / kEpl;           // lanes a row
+  static constexpr int kRpw = kWave / kLpr;       // rows a wavefront
+  static constexpr int kRows = kQWaves * kRpw;    // rows a block
+  static constexpr int kUnits = kEpl / 8;         // 8-code chunks a lane
+};
+
+template <int D>
+__global__ __launch_bounds__(kQThreads) void affine_quantize_kernel(const QArgs a) {
+  using S = QShape<D>;
+  constexpr int EPL = S::kEpl, LPR = S::kLpr;
+  __shared__ uint64_t chunks[kQWaves][kWave * S::kUnits];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lir = lane % LPR;                // lane in its row
+  const int rw = lane / LPR;                 // row in the wavefront
+  uint64_t* ch = chunks[wave] + rw * (D / 8);
+
+  for (int blk = blockIdx.x; blk < a.n_blocks; blk += gridDim.x) {
+    const int ti = blk / a.blocks_per_tensor;  // uniform: K then V
+    const QTensor& t = a.t[ti];
+    const int64_t r = int64_t(blk % a.blocks_per_tensor) * S::kRows + wave * S::kRpw + rw;
+    const bool live = r < a.rows;
+    const int64_t rr = live ? r : a.rows - 1;  // dead rows recompute the last one
+    const int64_t slab = rr / a.s, j = rr % a.s;
+    const int64_t dst = slab * a.dst_cap + a.dst_start + j;
+
+    float v[EPL];
+    const uint16_t* xr = t.x + rr * D + lir * EPL;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) v[e] = active ? bf16_to_f32(xr[base + e]) : 0.0f;
-
-  // The Metal kernel starts w_min at the dtype's max and w_max at 0.
-  float w_min = __uint_as_float(0x7f7f0000u);
-  float w_max = 0.0f;
+    for (int h = 0; h < EPL / 8; ++h) {
+      const uint4 w = *reinterpret_cast<const uint4*>(xr + 8 * h);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    w_min = fminf(w_min, v[e]);
-    w_max = fmaxf(w_max, v[e]);
-  }
-  const int lanes_per_group = gs / EPL;  // power of two, <= 64
-  for (int off = 1; off < lanes_per_group; off <<= 1) {
-    w_min = fminf(w_min, __shfl_xor(w_min, off, kWave));
-    w_max = fmaxf(w_max, __shfl_xor(w_max, off, kWave));
-  }
+      for (int e = 0; e < 4; ++e) {
+        v[8 * h + 2 * e] = __uint_as_float(ws[e] << 16);
+        v[8 * h + 2 * e + 1] = __uint_as_float(ws[e] & 0xffff0000u);
+      }
+    }
 
-  const float n_bins = float((1 << bits) - 1);
-  float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
-  const bool side = fabsf(w_min) > fabsf(w_max);
-  scale = side ? scale : -scale;
-  const float edge = side ? w_min : w_max;
-  const float q0 = roundf(edge / scale);
-  const bool at_zero = q0 == 0.0f;
-  scale = at_zero ? scale : edge / q0;
-  const float bias = at_zero ? 0.0f : edge;
-
-  const int groups = dim / gs;
-  if (active && (base % gs) == 0) {
-    const int g = base / gs;
-    scales[dst * groups + g] = f32_to_bf16(scale);
-    biases[dst * groups + g] = f32_to_bf16(bias);
-  }
-  if (active) {
+    // The Metal kernel starts w_min at the dtype's max and w_max at 0.
+    float w_min = __uint_as_float(0x7f7f0000u);
+    float w_max = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-      float q = fminf(roundf((v[e] - bias) / scale), n_bins);
-      codes[base + e] = q <= 0.0f ? uint8_t(0) : uint8_t(q);
+      w_min = fminf(w_min, v[e]);
+      w_max = fmaxf(w_max, v[e]);
     }
-  }
-  __syncthreads();
+    const int lpg = a.gs / EPL;  // lanes a group: a power of two, <= LPR
+    for (int off = 1; off < lpg; off <<= 1) {
+      w_min = fminf(w_min, __shfl_xor(w_min, off, kWave));
+      w_max = fmaxf(w_max, __shfl_xor(w_max, off, kWave));
+    }
 
-  const int words = dim * bits / 32;
-  uint32_t* out = packed + dst * words;
-  for (int w = lane; w < words; w += kWave) {
-    const int bit0 = 32 * w;
-    const int e0 = bit0 / bits;
-    const int e1 = (bit0 + 31) / bits;
-    uint32_t word = 0;
-    for (int e = e0; e <= e1 && e < dim; ++e) {
-      const int sh = e * bits - bit0;
-      const uint32_t c = codes[e];
-      word |= sh >= 0 ? (c << sh) : (c >> (-sh));
+    const int bits = t.bits;
+    const float n_bins = float((1 << bits) - 1);
+    float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
+    const bool side = fabsf(w_min) > fabsf(w_max);
+    scale = side ? scale : -scale;
+    const float edge = side ? w_min : w_max;
+    const float q0 = roundf(edge / scale);
+    const bool at_zero = q0 == 0.0f;
+    scale = at_zero ? scale : edge / q0;
+    const float bias = at_zero ? 0.0f : edge;
+
+    const int groups = D / a.gs;
+    if (live && lir % lpg == 0) {
+      const int g = lir / lpg;
+      t.scales[dst * groups + g] = f32_to_bf16(scale);
+      t.biases[dst * groups + g] = f32_to_bf16(bias);
     }
-    out[w] = word;
+#pragma unroll
+    for (int h = 0; h < S::kUnits; ++h) {
+      uint64_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = fminf(roundf((v[8 * h + e] - bias) / scale), n_bins);
+        const uint32_t code = q <= 0.0f ? 0u : uint32_t(q);
+        c |= uint64_t(code) << (bits * e);
+      }
+      ch[lir * S::kUnits + h] = c;
+    }
+    __syncthreads();
+
+    // Output word w of the row covers bits [32 w, 32 w + 32): chunk k =
+    // 32 w / (8 bits) from bit `off`, and chunk k + 1 when it runs past.
+    const int ub = 8 * bits;
+    const int words = D * bits / 32;
+    if (live) {
+      uint32_t* out = t.packed + dst * words;
+      for (int w = lir; w < words; w += LPR) {
+        const int bit0 = 32 * w, k = bit0 / ub, off = bit0 - k * ub;
+        uint64_t word = ch[k] >> off;
+        if (off + 32 > ub) word |= ch[k + 1] << (ub - off);
+        out[w] = uint32_t(word);
+      }
+    }
+    __syncthreads();  // the chunks are reused by the next block
   }
 }
 
@@ -128,6 +181,47 @@ int32_t check_affine_shape(int32_t dim, int32_t gs, int32_t bits) {
   return TQKV_OK;
 }
 
+// Launches the quantize kernel over one or two tensors of the same shape.
+int32_t launch_quantize(const QArgs& a0, int dim, tqkv_stream stream) {
+  QArgs a = a0;
+  int rows_per_block = 0;
+  switch (dim) {
+    case 32: rows_per_block = QShape<32>::kRows; break;
+    case 64: rows_per_block = QShape<64>::kRows; break;
+    case 128: rows_per_block = QShape<128>::kRows; break;
+    case 256: rows_per_block = QShape<256>::kRows; break;
+    case 512: rows_per_block = QShape<512>::kRows; break;
+    case 1024: rows_per_block = QShape<1024>::kRows; break;
+    default: return fail(TQKV_EUNSUPPORTED, "dim=%d", dim);
+  }
+  const int n_t = a.t[1].x ? 2 : 1;
+  const int64_t bpt = (a.rows + rows_per_block - 1) / rows_per_block;
+  if (bpt * n_t > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "%lld rows exceed one launch", (long long)a.rows);
+  a.blocks_per_tensor = int(bpt);
+  a.n_blocks = int(bpt * n_t);
+  // Enough workgroups to fill the chip several times over; larger inputs
+  // loop (grid stride).
+  const int grid = a.n_blocks < 8192 ? a.n_blocks : 8192;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (dim) {
+    case 32: hipLaunchKernelGGL(affine_quantize_kernel<32>, dim3(grid), dim3(kQThreads), 0, st, a); break;
+    case 64: hipLaunchKernelGGL(affine_quantize_kernel<64>, dim3(grid), dim3(kQThreads), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(affine_quantize_kernel<128>, dim3(grid), dim3(kQThreads), 0, st, a); break;
+    case 256: hipLaunchKernelGGL(affine_quantize_kernel<256>, dim3(grid), dim3(kQThreads), 0, st, a); break;
+    case 512: hipLaunchKernelGGL(affine_quantize_kernel<512>, dim3(grid), dim3(kQThreads), 0, st, a); break;
+    default: hipLaunchKernelGGL(affine_quantize_kernel<1024>, dim3(grid), dim3(kQThreads), 0, st, a); break;
+  }
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+int32_t check_rows(int64_t n_slabs, int64_t s, int64_t dst_cap, int64_t dst_start) {
+  if (n_slabs < 0 || s < 0 || dst_start < 0 || dst_start + s > dst_cap)
+    return fail(TQKV_EINVAL_SHAPE, "rows [%lld, %lld) do not fit a buffer of %lld",
+                (long long)dst_start, (long long)(dst_start + s), (long long)dst_cap);
+  return TQKV_OK;
+}
+
 }  // namespace
 }  // namespace tqkv
 
@@ -139,28 +233,41 @@ extern "C" int32_t tqkv_affine_quantize(const uint16_t* x, int64_t n_slabs, int6
                                         int64_t dst_cap, int64_t dst_start,
                                         tqkv_stream stream) {
   if (int32_t rc = check_affine_shape(dim, group_size, bits)) return rc;
-  if (n_slabs < 0 || s < 0 || dst_start < 0 || dst_start + s > dst_cap)
-    return fail(TQKV_EINVAL_SHAPE, "rows [%lld, %lld) do not fit a buffer of %lld",
-                (long long)dst_start, (long long)(dst_start + s), (long long)dst_cap);
+  if (int32_t rc = check_rows(n_slabs, s, dst_cap, dst_start)) return rc;
   if (n_slabs == 0 || s == 0) return ok();
   if (!x || !packed || !scales || !biases) return fail(TQKV_EINVAL_ARG, "null pointer");
-  const int64_t rows = n_slabs * s;
-  if (rows > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "%lld rows exceed one launch", (long long)rows);
-  const int epl = dim < 64 ? 1 : dim / 64;
-  const dim3 grid{unsigned(rows)}, block{64u};
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define TQKV_Q(E)                                                                        \
-  case E:                                                                               \
-    hipLaunchKernelGGL(affine_quantize_kernel<E>, grid, block, 0, st, x, s, dim,        \
-                       group_size, bits, packed, scales, biases, dst_cap, dst_start);   \
-    break;
-  switch (epl) {
-    TQKV_Q(1) TQKV_Q(2) TQKV_Q(4) TQKV_Q(8) TQKV_Q(16)
-    default: return fail(TQKV_EUNSUPPORTED, "dim=%d", dim);
-  }
-#undef TQKV_Q
-  TQKV_LAUNCHED();
-  return ok();
+  QArgs a{};
+  a.t[0] = QTensor{x, packed, scales, biases, bits};
+  a.s = s;
+  a.rows = n_slabs * s;
+  a.dst_cap = dst_cap;
+  a.dst_start = dst_start;
+  a.gs = group_size;
+  return launch_quantize(a, dim, stream);
+}
+
+extern "C" int32_t tqkv_affine_quantize_kv(const uint16_t* k, const uint16_t* v, int64_t n_slabs,
+                                           int64_t s, int32_t dim, int32_t group_size,
+                                           int32_t bits_k, int32_t bits_v, uint32_t* k_packed,
+                                           uint16_t* k_scales, uint16_t* k_biases,
+                                           uint32_t* v_packed, uint16_t* v_scales,
+                                           uint16_t* v_biases, int64_t dst_cap,
+                                           int64_t dst_start, tqkv_stream stream) {
+  if (int32_t rc = check_affine_shape(dim, group_size, bits_k)) return rc;
+  if (int32_t rc = check_affine_shape(dim, group_size, bits_v)) return rc;
+  if (int32_t rc = check_rows(n_slabs, s, dst_cap, dst_start)) return rc;
+  if (n_slabs == 0 || s == 0) return ok();
+  if (!k || !v || !k_packed || !k_scales || !k_biases || !v_packed || !v_scales || !v_biases)
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  QArgs a{};
+  a.t[0] = QTensor{k, k_packed, k_scales, k_biases, bits_k};
+  a.t[1] = QTensor{v, v_packed, v_scales, v_biases, bits_v};
+  a.s = s;
+  a.rows = n_slabs * s;
+  a.dst_cap = dst_cap;
+  a.dst_start = dst_start;
+  a.gs = group_size;
+  return launch_quantize(a, dim, stream);
 }
 
 extern "C" int32_t tqkv_affine_dequantize(const uint32_t* packed, const uint16_t* scales,

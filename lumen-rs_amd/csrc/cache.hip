@@ -567,6 +567,20 @@ int32_t tqkv_cache_append(tqkv_cache* c, const uint16_t* k, const uint16_t* v, i
   const cacheplan::Plan p = cacheplan::update(next, c->pc, s);
   if (int32_t rc = execute(c, p, old_len, st)) return rc;
   const tqkv_cache_config& g = c->cfg;
+  if (g.k_dim == g.v_dim && c->cur[0].cap == c->cur[3].cap) {
+    // Keys and values in one launch.
+    if (int32_t rc = tqkv_affine_quantize_kv(
+            k, v, c->n_slabs, s, g.k_dim, g.group_size, g.bits_k, g.bits_v,
+            reinterpret_cast<uint32_t*>(c->cur[0].ptr), reinterpret_cast<uint16_t*>(c->cur[1].ptr),
+            reinterpret_cast<uint16_t*>(c->cur[2].ptr), reinterpret_cast<uint32_t*>(c->cur[3].ptr),
+            reinterpret_cast<uint16_t*>(c->cur[4].ptr), reinterpret_cast<uint16_t*>(c->cur[5].ptr),
+            c->cur[0].cap, p.write_at, stream))
+      return rc;
+    c->st = next;
+    c->view_n = p.view;
+    if (fetched) fill_view(c, p.view, fetched);
+    return ok();
+  }
   if (int32_t rc = tqkv_affine_quantize(
           k, c->n_slabs, s, g.k_dim, g.group_size, g.bits_k,
           reinterpret_cast<uint32_t*>(c->cur[0].ptr), reinterpret_cast<uint16_t*>(c->cur[1].ptr),

@@ -81,6 +81,8 @@ _SIGS = {
     "tqkv_last_error": (ctypes.c_char_p, []),
     "tqkv_version": (I32, []),
     "tqkv_affine_quantize": (I32, [P, I64, I64, I32, I32, I32, P, P, P, I64, I64, P]),
+    "tqkv_affine_quantize_kv": (I32, [P, P, I64, I64, I32, I32, I32, I32, P, P, P, P, P, P, I64,
+                                      I64, P]),
     "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
@@ -304,6 +306,14 @@ def affine_quantize(x, n_slabs, s, dim, gs, bits, packed, scales, biases, dst_ca
     """x, packed, scales, biases: device pointers."""
     check(lib().tqkv_affine_quantize(x, n_slabs, s, dim, gs, bits, packed, scales, biases,
                                      s if dst_cap is None else dst_cap, dst_start, stream))
+
+
+def affine_quantize_kv(k, v, n_slabs, s, dim, gs, bits_k, bits_v, kt, vt, dst_cap=None,
+                       dst_start=0, stream=None):
+    """K and V in one launch; kt, vt: (packed, scales, biases) device
+    pointers of each."""
+    check(lib().tqkv_affine_quantize_kv(k, v, n_slabs, s, dim, gs, bits_k, bits_v, *kt, *vt,
+                                        s if dst_cap is None else dst_cap, dst_start, stream))
 
 
 def affine_dequantize(packed, scales, biases, rows, dim, gs, bits, out, stream=None):

@@ -64,6 +64,47 @@ def test_quantize_writes_only_its_rows(T):
     assert np.all(sc[:, :9] == 0x7777) and np.all(bi[:, 14:] == 0x7777)
 
 
+def device_triple(T, slabs, cap, dim, gs, bits):
+    words, groups = dim * bits // 32, dim // gs
+    return (T.DeviceArray((slabs, cap, words), np.uint32,
+                          np.full((slabs, cap, words), 0xDEADBEEF, np.uint32)),
+            T.DeviceArray((slabs, cap, groups), np.uint16,
+                          np.full((slabs, cap, groups), 0x7777, np.uint16)),
+            T.DeviceArray((slabs, cap, groups), np.uint16,
+                          np.full((slabs, cap, groups), 0x7777, np.uint16)))
+
+
+@pytest.mark.parametrize("dim,gs,bk,bv,slabs,s", [
+    (128, 64, 8, 4, 3, 37), (256, 64, 3, 3, 2, 29), (64, 32, 4, 2, 5, 1), (1024, 128, 8, 5, 2, 9),
+    (32, 32, 6, 4, 7, 3), (128, 64, 4, 4, 4, 33000),  # the last loops over its grid
+])
+def test_quantize_kv_one_launch_matches_two(T, dim, gs, bk, bv, slabs, s):
+    """tqkv_affine_quantize_kv: K and V bit-exact with the oracle (and so with
+    two tqkv_affine_quantize calls), rows outside [start, start + s) untouched."""
+    start, cap = 3, s + 5
+    k = kv_bf16((slabs, s, dim), 300 + dim + bk, frac=0.02, mult=8.0)
+    v = kv_bf16((slabs, s, dim), 400 + dim + bv, frac=0.02, mult=8.0)
+    dk, dv = T.DeviceArray.of(k), T.DeviceArray.of(v)
+    kt, vt = device_triple(T, slabs, cap, dim, gs, bk), device_triple(T, slabs, cap, dim, gs, bv)
+    print(f"[quantize_kv] slabs={slabs} s={s} dim={dim} gs={gs} bits={bk}/{bv}", flush=True)
+    T.affine_quantize_kv(dk.ptr, dv.ptr, slabs, s, dim, gs, bk, bv, tuple(a.ptr for a in kt),
+                         tuple(a.ptr for a in vt), cap, start)
+    T.hip().sync()
+    for x, trip, bits in ((k, kt, bk), (v, vt, bv)):
+        got = [a.numpy() for a in trip]
+        want = O.affine_quantize(x, gs, bits)
+        for g, w, fill in zip(got, want, (0xDEADBEEF, 0x7777, 0x7777)):
+            assert np.array_equal(g[:, start:start + s], w)
+            assert np.all(g[:, :start] == fill) and np.all(g[:, start + s:] == fill)
+
+
+def test_quantize_kv_rejects_either_bad_width(T):
+    for bk, bv in ((7, 4), (4, 7)):
+        with pytest.raises(T.TqkvError) as e:
+            T.affine_quantize_kv(0, 0, 1, 1, 128, 64, bk, bv, (0, 0, 0), (0, 0, 0))
+        assert e.value.status == T.EUNSUPPORTED
+
+
 def test_quantize_rejects_bad_layouts(T):
     with pytest.raises(T.TqkvError) as e:
         T.affine_quantize(0, 1, 1, 96, 64, 4, 0, 0, 0)
