@@ -1,13 +1,13 @@
 // Quantize-on-append in MLX's affine format, bit-exact with its Metal kernel,
 // and the matching dequantize.
 //
-// Layout of the work: each lane owns EPL = 8 consecutive elements of a row
-// (16 at dim 1024), read as one 16-byte load, so a row takes dim / EPL
-// lanes and a wavefront holds several rows (4 at dim 128); a 256-thread
+// Layout of the work: each lane owns EPL = 16 consecutive elements of a row,
+// read as two 16-byte loads, so a row takes dim / EPL lanes and a
+// wavefront holds several rows (8 at dim 128); a 256-thread
 // workgroup takes a block of rows of one tensor, and the grid covers K and
 // V in one launch. A group's lanes are adjacent, so its min and max are a
-// butterfly over gs / EPL lanes. Each lane packs its codes into a 64-bit
-// chunk (8 x bits bits), the chunks go through LDS, and each output word is
+// butterfly over gs / EPL lanes. Each lane packs every 8 codes into a
+// 64-bit chunk (8 x bits bits), the chunks go through LDS, and each output word is
 // cut from the one or two chunks it overlaps: LSB-first u32 words for every
 // width, including those whose codes straddle words (3, 5, 6 bits).
 //
@@ -46,7 +46,7 @@ struct QArgs {
 
 template <int D>
 struct QShape {
-  static constexpr int kEpl = D > 512 ? 16 : 8;   // elements a lane
+  static constexpr int kEpl = 16;                 // elements a lane
   static constexpr int kLpr = D / kEpl;           // lanes a row
   static constexpr int kRpw = kWave / kLpr;       // rows a wavefront
   static constexpr int kRows = kQWaves * kRpw;    // rows a block
@@ -69,8 +69,9 @@ __global__ __launch_bounds__(kQThreads) void affine_quantize_kernel(const QArgs 
     const int64_t r = int64_t(blk % a.blocks_per_tensor) * S::kRows + wave * S::kRpw + rw;
     const bool live = r < a.rows;
     const int64_t rr = live ? r : a.rows - 1;  // dead rows recompute the last one
-    const int64_t slab = rr / a.s, j = rr % a.s;
-    const int64_t dst = slab * a.dst_cap + a.dst_start + j;
+    // 32-bit division: the host keeps rows (and so s) below 2^31.
+    const uint32_t slab = uint32_t(rr) / uint32_t(a.s), j = uint32_t(rr) - slab * uint32_t(a.s);
+    const int64_t dst = int64_t(slab) * a.dst_cap + a.dst_start + j;
 
     float v[EPL];
     const uint16_t* xr = t.x + rr * D + lir * EPL;
@@ -195,8 +196,9 @@ int32_t launch_quantize(const QArgs& a0, int dim, tqkv_stream stream) {
     default: return fail(TQKV_EUNSUPPORTED, "dim=%d", dim);
   }
   const int n_t = a.t[1].x ? 2 : 1;
+  if (a.rows > 0x7fffffffLL)
+    return fail(TQKV_EINVAL_SHAPE, "%lld rows exceed one launch", (long long)a.rows);
   const int64_t bpt = (a.rows + rows_per_block - 1) / rows_per_block;
-  if (bpt * n_t > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "%lld rows exceed one launch", (long long)a.rows);
   a.blocks_per_tensor = int(bpt);
   a.n_blocks = int(bpt * n_t);
   // Enough workgroups to fill the chip several times over; larger inputs
