@@ -50,12 +50,13 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget for the baseline sample")
     ap.add_argument("--workload", choices=("decode", "prefill", "append", "decode1", "prefix",
-                                           "layers"), default="decode",
+                                           "layers", "sparse"), default="decode",
                     help="decode: config 2 (the headline); prefill: config 3's 2048-token "
                          "chunk attention; append: config 0's quantize round trip (affine, "
                          "affine+rotation, TurboQuant codebook); decode1: config 1's "
                          "single-sequence decode; layers: config 3's 30-layer stack (chunked "
-                         "prefill, then decode steps); prefix: config 4's shared-prefix decode")
+                         "prefill, then decode steps); prefix: config 4's shared-prefix decode; "
+                         "sparse: config 2's shape with page-sparse decode")
     ap.add_argument("--decode-steps", type=int, default=512,
                     help="decode steps of the layers workload (config 3: 512)")
     return ap.parse_args()
@@ -76,7 +77,7 @@ def main():
     hip = T.hip()
     hip._ok(hip.h.hipSetDevice(0), "hipSetDevice")
     others = {"prefill": prefill_main, "append": append_main, "decode1": decode1_main,
-              "prefix": prefix_main, "layers": layers_main}
+              "prefix": prefix_main, "layers": layers_main, "sparse": sparse_main}
     if args.workload in others:
         others[args.workload](T, hip, args)
         return
@@ -712,6 +713,101 @@ def prefix_main(T, hip, args):
                                   "kind": "port",
                                   "sample": f"oracle dequantize-then-attend of sequence 0 over "
                                             f"prefix + suffix ({P + pos[0]} keys, {dt:.2f} s)"}
+    print(json.dumps(result))
+
+
+def sparse_main(T, hip, args):
+    """Config 2's shape (B=32, 16 / 8 heads, D=256, 32,768-token context,
+    3-bit gs64) with page-sparse decode (sdpa_page_sparse, the reference's
+    LUMEN_SPARSE_DECODE): a step appends one token per sequence (digesting a
+    page when one fills) and attends to the keep = max(pages / 8, 64) pages
+    whose key bounds score highest, plus the first, the last four and the
+    undigested tail. Not the headline metric (it attends to fewer keys):
+    reported beside it. Bytes are the ones the sparse call reads: the digest,
+    the chosen pages' K and V, the tail, Q and O."""
+    B, H, HKV, D, N, GS, BITS = 32, 16, 8, 256, args.context, 64, 3
+    stream = hip.stream()
+    slabs = B * HKV
+    settle = 64 if args.settle is None else max(0, args.settle)
+    steps = 50 if args.steps is None else args.steps
+    cap = (N + settle + args.warmup + steps + 255) // 256 * 256
+    kc = _fill_affine(T, stream, slabs, N, D, GS, BITS, cap, 11)
+    vc = _fill_affine(T, stream, slabs, N, D, GS, BITS, cap, 22)
+    max_pages = cap // 64
+    kmin = T.DeviceArray((slabs, max_pages, D), np.uint16)
+    kmax = T.DeviceArray((slabs, max_pages, D), np.uint16)
+    kp, vp = tuple(a.ptr for a in kc), tuple(a.ptr for a in vc)
+    pages0 = N // 64
+    t0, t1 = hip.event(), hip.event()
+    hip.record(t0, stream)
+    T.page_digest_affine(kp, slabs, cap, D, GS, BITS, 0, pages0, kmin.ptr, kmax.ptr, max_pages,
+                         stream)
+    hip.record(t1, stream)
+    hip.sync()
+    digest_ms = hip.elapsed_ms(t0, t1)
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H, D, 33, 0.0, 1.0, stream)
+    nk, nv = T.DeviceArray((slabs, 1, D), np.uint16), T.DeviceArray((slabs, 1, D), np.uint16)
+    T.synth_bf16(nk.ptr, slabs, D, 44, 0.01, 10.0, stream)
+    T.synth_bf16(nv.ptr, slabs, D, 55, 0.01, 10.0, stream)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    keep_max = int(T.sparse_keep_pages(max_pages))
+    wsb = T.sparse_workspace_size(B, H, HKV, D, cap, keep_max)
+    ws = T.DeviceArray((wsb,), np.uint8)
+    pos = [N]
+    digested = [pages0]
+
+    def append():
+        T.affine_quantize_kv(nk.ptr, nv.ptr, slabs, 1, D, GS, BITS, BITS, kp, vp, cap, pos[0],
+                             stream)
+        pos[0] += 1
+        if pos[0] // 64 > digested[0]:
+            T.page_digest_affine(kp, slabs, cap, D, GS, BITS, digested[0], pos[0] // 64, kmin.ptr,
+                                 kmax.ptr, max_pages, stream)
+            digested[0] = pos[0] // 64
+
+    def attend():
+        pages = digested[0]
+        seg = T.affine_seg(kp, vp, cap, pos[0])
+        T.decode_attend_affine_sparse(q.ptr, B, H, HKV, D, GS, BITS, BITS, D ** -0.5, seg,
+                                      kmin.ptr, kmax.ptr, max_pages, pages,
+                                      int(T.sparse_keep_pages(pages)), out.ptr, ws.ptr, wsb,
+                                      stream=stream)
+
+    for _ in range(settle + args.warmup):
+        append(), attend()
+    hip.sync()
+    ctx0, dig0 = pos[0], digested[0]
+    step_ms = _loop_ms(hip, stream, lambda: (append(), attend()), steps)
+    pos[0], digested[0] = ctx0, dig0
+    evs = [(hip.event(), hip.event()) for _ in range(steps)]
+    alg = []
+    row = D * BITS // 32 * 4 + 2 * (D // GS) * 2
+    for a_, b_ in evs:
+        append()
+        pages = digested[0]
+        keep = int(T.sparse_keep_pages(pages))
+        alg.append(slabs * (2 * keep * 64 * row + 2 * (pos[0] - pages * 64) * row +
+                            2 * pages * D * 2) + 2 * B * H * D * 2)
+        hip.record(a_, stream)
+        attend()
+        hip.record(b_, stream)
+    hip.sync()
+    att_ms = float(np.mean([hip.elapsed_ms(a_, b_) for a_, b_ in evs]))
+    alg_b = float(np.mean(alg))
+    dense_b = 2 * slabs * (ctx0 + steps / 2.0) * row + 2 * B * H * D * 2
+    result = _line(
+        "page-sparse quantized-KV decode tokens/s @ B=32, 32K ctx", B / (step_ms * 1e-3),
+        "tokens/s", step_ms, args, "f32",
+        {"workload": "config 2's shape (B=32, 16/8 heads, D=256, 32K context, 3-bit gs64) with "
+                     "page-sparse decode: keep max(pages/8, 64) pages + sink + 4 recent + tail",
+         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N,
+         "bits_k": BITS, "bits_v": BITS, "group_size": GS,
+         "keep_pages": int(T.sparse_keep_pages(N // 64))},
+        _hbm(alg_b / (att_ms * 1e-3) / 1e9,
+             "page select + decode_mfma_kernel<256,3,3,2,4,8,paged> + merge", alg_b, att_ms),
+        {"digest_ms_once": round(digest_ms, 4), "dense_bytes_per_step": int(dense_b),
+         "dense_equivalent_gbps": round(dense_b / (att_ms * 1e-3) / 1e9, 1)}, settle, steps)
     print(json.dumps(result))
 
 

@@ -144,6 +144,72 @@ int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32
                                   size_t workspace_bytes, tqkv_stream stream);
 
 /*
+ * Page-sparse decode over an affine cache, after sdpa_page_sparse
+ * (native_attention.rs:210-329) and PageDigest (native_cache.rs:352-445).
+ * Pages are 64 rows; a cache segment's buffers are [B, H_kv, cap, .].
+ *
+ * tqkv_page_digest_affine: key_min / key_max [n_slabs, max_pages, dim] bf16
+ * get, for pages [page_from, page_to) of every slab, the elementwise min and
+ * max over the page's 64 mlx::dequantize'd keys (bf16(bf16(scale * code) +
+ * bias)). Digesting only the newly filled pages keeps the digest current, as
+ * page_digest does.
+ */
+int32_t tqkv_page_digest_affine(const uint32_t* k_packed, const uint16_t* k_scales,
+                                const uint16_t* k_biases, int64_t n_slabs, int64_t cap,
+                                int32_t dim, int32_t group_size, int32_t bits, int64_t page_from,
+                                int64_t page_to, uint16_t* key_min, uint16_t* key_max,
+                                int64_t max_pages, tqkv_stream stream);
+
+/* sparse_keep_pages (native_attention.rs:325-329): max(pages / 8, 64). */
+int64_t tqkv_sparse_keep_pages(int64_t pages);
+
+/*
+ * The page choice of sdpa_page_sparse (native_attention.rs:240-271): per
+ * (batch row, KV head), bound(p) = max over the query group of
+ * sum_d max(q_d * key_max[p][d], q_d * key_min[p][d]) (f32); page 0 and the
+ * last 4 of `pages` digested pages are always taken; the `keep` largest
+ * bounds win, ties to the lower page. chosen: int32 [B, H_kv, keep] in
+ * ascending page order. pages <= 4096, keep <= pages, D in {64, 128, 256,
+ * 512}.
+ */
+int32_t tqkv_page_select(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D,
+                         const uint16_t* key_min, const uint16_t* key_max, int64_t max_pages,
+                         int64_t pages, int32_t keep, int32_t* chosen, void* workspace,
+                         size_t workspace_bytes, tqkv_stream stream);
+/* Workspace of tqkv_page_select: the f32 bounds [B, H_kv, pages]. */
+size_t tqkv_page_select_workspace_size(int32_t B, int32_t H_kv, int64_t pages);
+
+/*
+ * Decode attention over the chosen pages of one (unshared) segment plus its
+ * undigested tail, rows [pages * 64, seg->n) (the attention of
+ * sdpa_page_sparse, native_attention.rs:272-291): one softmax over both, as
+ * tqkv_decode_attend_affine would give over those keys. Matrix-core layouts
+ * only (tqkv_decode_kernel_name "mfma"); TQKV_EUNSUPPORTED otherwise.
+ */
+int32_t tqkv_decode_attend_affine_pages(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
+                                        int32_t D, int32_t group_size, int32_t bits_k,
+                                        int32_t bits_v, float scale, const tqkv_affine_seg* seg,
+                                        const int32_t* chosen, int32_t keep, int64_t pages,
+                                        uint16_t* out, void* workspace, size_t workspace_bytes,
+                                        tqkv_stream stream);
+
+/*
+ * sdpa_page_sparse whole: with pages <= keep, dense tqkv_decode_attend_affine
+ * over the segment; otherwise tqkv_page_select into chosen_out (or the
+ * workspace when chosen_out is NULL), then tqkv_decode_attend_affine_pages.
+ * workspace: tqkv_sparse_workspace_size() bytes (required).
+ */
+int32_t tqkv_decode_attend_affine_sparse(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
+                                         int32_t D, int32_t group_size, int32_t bits_k,
+                                         int32_t bits_v, float scale, const tqkv_affine_seg* seg,
+                                         const uint16_t* key_min, const uint16_t* key_max,
+                                         int64_t max_pages, int64_t pages, int32_t keep,
+                                         uint16_t* out, int32_t* chosen_out, void* workspace,
+                                         size_t workspace_bytes, tqkv_stream stream);
+size_t tqkv_sparse_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
+                                  int64_t total_tokens, int32_t keep);
+
+/*
  * Which decode kernel tqkv_decode_attend_affine runs for a layout: "mfma"
  * (scores on the matrix cores; group_size 64, D in {64, 128, 256},
  * H / H_kv in {1, 2, 4, 8} with H / H_kv * D / 64 <= 16), "dot2" (every other

@@ -338,3 +338,136 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
   }
   return ok();
 }
+
+// Decode over chosen 64-row pages of one cache segment plus its undigested
+// tail (the attention half of sdpa_page_sparse, native_attention.rs:272-291):
+// rows [0, keep * 64) of the first kernel segment stand for the pages in
+// `chosen` (read through the paged kernel's page table), the second segment
+// is rows [pages * 64, n) of the same buffers. With one query and no mask,
+// attention does not depend on key order.
+extern "C" int32_t tqkv_decode_attend_affine_pages(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
+    int32_t bits_k, int32_t bits_v, float scale, const tqkv_affine_seg* seg,
+    const int32_t* chosen, int32_t keep, int64_t pages, uint16_t* out, void* workspace,
+    size_t workspace_bytes, tqkv_stream stream) {
+  if (!q || !out || !seg || !chosen) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0)
+    return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d", B, H, H_kv);
+  const tqkv_affine_seg& s = *seg;
+  if (s.shared) return fail(TQKV_EUNSUPPORTED, "page-sparse decode over a shared segment");
+  if (keep < 1 || pages < keep || pages * kPageRows > s.n || s.n > s.cap)
+    return fail(TQKV_EINVAL_SHAPE, "keep=%d pages=%lld n=%lld cap=%lld", keep, (long long)pages,
+                (long long)s.n, (long long)s.cap);
+  if (!s.k_packed || !s.k_scales || !s.k_biases || !s.v_packed || !s.v_scales || !s.v_biases)
+    return fail(TQKV_EINVAL_ARG, "null buffer");
+  const int G = H / H_kv;
+  KernelFn fn = nullptr;
+  if (s.cap * D < (int64_t(1) << 31)) {
+    switch (D) {
+      case 64: fn = pick_mfma_d64(bits_k, bits_v, G, group_size, true); break;
+      case 128: fn = pick_mfma_d128(bits_k, bits_v, G, group_size, true); break;
+      case 256: fn = pick_mfma_d256(bits_k, bits_v, G, group_size, true); break;
+    }
+  }
+  if (!fn)
+    return fail(TQKV_EUNSUPPORTED, "page-sparse decode layout D=%d bits %d/%d gqa=%d gs=%d", D,
+                bits_k, bits_v, G, group_size);
+  Args a{};
+  a.q = q;
+  a.H = H;
+  a.H_kv = H_kv;
+  a.gs = group_size;
+  a.qscale = scale * kLog2e;
+  const int64_t tail0 = pages * kPageRows;
+  const int64_t bs = int64_t(H_kv) * s.cap;
+  a.seg[0] = Seg{s.k_packed, s.k_scales, s.k_biases, s.v_packed, s.v_scales, s.v_biases,
+                 s.cap, int64_t(keep) * kPageRows, bs};
+  const int kr = D * bits_k / 32, vr = D * bits_v / 32, ng = D / group_size;
+  a.seg[1] = Seg{s.k_packed + tail0 * kr, s.k_scales + tail0 * ng, s.k_biases + tail0 * ng,
+                 s.v_packed + tail0 * vr, s.v_scales + tail0 * ng, s.v_biases + tail0 * ng,
+                 s.cap, s.n - tail0, bs};
+  a.n0 = int64_t(keep) * kPageRows;
+  a.total = a.n0 + (s.n - tail0);
+  a.pages = chosen;
+  a.n_pages = keep;
+  a.out = out;
+  const int waves = waves_for_shape(G, D);
+  plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
+  // A wavefront holds its page numbers one a lane: at most kMaxWavePages
+  // pages a wavefront, so a split spans at most waves * kMaxWavePages.
+  const int64_t most = int64_t(waves) * kMaxWavePages * kPageRows;
+  if (a.split_len > most) {
+    a.split_len = most;
+    a.n_splits = int((a.total + a.split_len - 1) / a.split_len);
+  }
+  a.split_base = 0;
+  a.n_part = a.n_splits;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (a.n_splits > 1) {
+    const size_t need = size_t(B) * H * a.n_splits * (size_t(D) + 2) * sizeof(float);
+    void* ws = workspace;
+    if (!ws) {
+      if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+    } else if (workspace_bytes < need) {
+      return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+    }
+    a.part_o = static_cast<float*>(ws);
+    a.part_m = a.part_o + size_t(B) * H * a.n_splits * D;
+    a.part_l = a.part_m + size_t(B) * H * a.n_splits;
+  }
+  hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
+                     dim3(kWave * waves), 0, st, a);
+  TQKV_LAUNCHED();
+  if (a.n_splits > 1) {
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(kMergeThreads), 0, st,
+                       a.part_o, a.part_m, a.part_l, a.n_splits, D, out);
+    TQKV_LAUNCHED();
+  }
+  return ok();
+}
+
+// Workspace of the page-sparse call: the chosen-page table, the page bounds,
+// then the decode's split partials.
+size_t sparse_table_bytes(int32_t B, int32_t H_kv, int32_t keep) {
+  return (size_t(B) * H_kv * size_t(keep) * sizeof(int32_t) + 255) / 256 * 256;
+}
+
+extern "C" size_t tqkv_sparse_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
+                                             int64_t total_tokens, int32_t keep) {
+  if (B <= 0 || H <= 0 || H_kv <= 0 || keep < 0 || total_tokens <= 0) return 0;
+  return sparse_table_bytes(B, H_kv, keep) +
+         tqkv_page_select_workspace_size(B, H_kv, total_tokens / kPageRows + 1) +
+         tqkv_decode_workspace_size(B, H, H_kv, D, total_tokens) +
+         size_t(B) * H * (size_t(D) + 2) * sizeof(float) *
+             size_t(total_tokens / (int64_t(4) * kMaxWavePages * kPageRows) + 1);
+}
+
+// sdpa_page_sparse whole (native_attention.rs:210-291): with keep or fewer
+// digested pages, dense decode over the segment; otherwise the page choice
+// into the workspace's table, then decode over the chosen pages and the tail.
+extern "C" int32_t tqkv_decode_attend_affine_sparse(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
+    int32_t bits_k, int32_t bits_v, float scale, const tqkv_affine_seg* seg,
+    const uint16_t* key_min, const uint16_t* key_max, int64_t max_pages, int64_t pages,
+    int32_t keep, uint16_t* out, int32_t* chosen_out, void* workspace, size_t workspace_bytes,
+    tqkv_stream stream) {
+  if (!seg) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (pages <= keep)
+    return tqkv_decode_attend_affine(q, B, H, H_kv, D, group_size, bits_k, bits_v, scale, seg, 1,
+                                     out, workspace, workspace_bytes, stream);
+  if (!workspace) return fail(TQKV_EINVAL_ARG, "page-sparse decode needs a workspace");
+  if (B <= 0 || H_kv <= 0 || keep < 1) return fail(TQKV_EINVAL_SHAPE, "B=%d H_kv=%d keep=%d", B, H_kv, keep);
+  const size_t table = sparse_table_bytes(B, H_kv, keep);
+  const size_t bnd = tqkv_page_select_workspace_size(B, H_kv, pages);
+  if (workspace_bytes < table + bnd)
+    return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need more than %zu", workspace_bytes,
+                table + bnd);
+  char* w = static_cast<char*>(workspace);
+  int32_t* chosen = chosen_out ? chosen_out : reinterpret_cast<int32_t*>(w);
+  if (int32_t rc = tqkv_page_select(q, B, H, H_kv, D, key_min, key_max, max_pages, pages, keep,
+                                    chosen, w + table, bnd, stream))
+    return rc;
+  return tqkv_decode_attend_affine_pages(q, B, H, H_kv, D, group_size, bits_k, bits_v, scale, seg,
+                                         chosen, keep, pages, out, w + table + bnd,
+                                         workspace_bytes - table - bnd, stream);
+}

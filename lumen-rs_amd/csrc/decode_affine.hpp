@@ -69,6 +69,11 @@ struct Args {
   // split_base + s of n_part (other slots belong to other launches).
   int split_base, n_part;
   uint16_t* out;  // [B, H, 1, D], written directly when n_part == 1
+  // Page-sparse decode (the paged kernels only): segment 0 is a whole cache
+  // slab read through this page table, rows [0, n0) standing for pages
+  // pages[(b * H_kv + kvh) * n_pages + i] (64 rows each, ascending).
+  const int32_t* pages;
+  int n_pages;
   float* part_o;  // [B, H, n_part, D]
   float* part_m;  // [B, H, n_part]
   float* part_l;  // [B, H, n_part]

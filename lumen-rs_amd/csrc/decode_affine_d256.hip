@@ -4,6 +4,8 @@
 namespace tqkv {
 namespace decode {
 KernelFn pick_d256(int bk, int bv, int G) { return pick_bits<256>(bk, bv, G); }
-KernelFn pick_mfma_d256(int bk, int bv, int G, int gs) { return pick_mfma<256>(bk, bv, G, gs); }
+KernelFn pick_mfma_d256(int bk, int bv, int G, int gs, bool paged) {
+  return paged ? pick_mfma<256, true>(bk, bv, G, gs) : pick_mfma<256, false>(bk, bv, G, gs);
+}
 }  // namespace decode
 }  // namespace tqkv

@@ -117,7 +117,17 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <int D, int BK, int BV, int G, int NG, int kWaves>
+// Rows of a page of the page-sparse decode, and the most pages one
+// wavefront may cover (one page number a lane).
+constexpr int kPageRows = 64;
+constexpr int kMaxWavePages = 64;
+
+// PAGED: segment 0's rows [0, n0) are the chosen 64-row pages of the slab
+// (Args::pages). Wavefront ranges are whole pages; a wavefront reads its
+// page numbers once (lane j holds its j-th page), and each 16-token step
+// takes its page's physical row with a readlane, so the pipeline runs
+// across pages as over contiguous rows.
+template <int D, int BK, int BV, int G, int NG, int kWaves, bool PAGED = false>
 __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   constexpr int EK = D / 4, EV = D / 8;
   constexpr int KW = EK * BK / 32, VW = EV * BV / 32;
@@ -232,7 +242,8 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   const int64_t t_begin = int64_t(split) * a.split_len;
   const int64_t t_end = t_begin + a.split_len < a.total ? t_begin + a.split_len : a.total;
   int64_t chunk = (t_end - t_begin + kWaves - 1) / kWaves;
-  chunk = (chunk + kStep - 1) / kStep * kStep;
+  constexpr int kChunkAlign = PAGED ? kPageRows : kStep;  // paged: whole pages
+  chunk = (chunk + kChunkAlign - 1) / kChunkAlign * kChunkAlign;
   const int64_t w_begin = t_begin + wave * chunk;
   const int64_t w_end = w_begin + chunk < t_end ? w_begin + chunk : t_end;
 
@@ -444,40 +455,63 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     const int64_t hi = sg == 0 ? (w_end < a.n0 ? w_end : a.n0) : w_end;
     if (lo >= hi) continue;
     const int64_t off = sg == 0 ? 0 : a.n0;
-    const int64_t row0 = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap + (lo - off);
+    const bool paged = PAGED && sg == 0;
+    const int64_t slab0 = int64_t(b) * s.b_stride + int64_t(kvh) * s.cap;
+    const int64_t row0 = paged ? slab0 : slab0 + (lo - off);
     const uint32_t nrows = uint32_t(hi - lo);
-    const uint32_t n = nrows / kStep;  // full steps
+    const uint32_t n = nrows / kStep;  // full steps (a page segment has no partial one)
     const std::integral_constant<bool, false> full{};
     const std::integral_constant<bool, true> masked{};
     if (n > 0) {
       // Iteration i: load keys of step i + 2 and values of step i + 1, score
       // step i + 1, accumulate the values of step i. Loads past the last
       // step re-read it (unconditional loads keep the buffers in place).
-      const Rsrc r = make(s, row0, n * kStep);
+      // Paged: the descriptors span the slab and step i maps to the physical
+      // step of its page.
+      const Rsrc r = make(s, row0, paged ? uint32_t(s.cap) : n * kStep);
       const uint32_t last = n - 1;
-      auto cl = [&](uint32_t x) { return x < last ? x : last; };
+      // Paged: lo is a page boundary; lane j holds the range's j-th page.
+      int my_page = 0;
+      if constexpr (PAGED) {
+        if (paged) {
+          const int64_t first = lo / kPageRows;
+          const int npg = int((hi - lo + kPageRows - 1) / kPageRows);
+          if (lane < npg) my_page = a.pages[(int64_t(b) * a.H_kv + kvh) * a.n_pages + first + lane];
+        }
+      }
+      auto cl = [&](uint32_t x) {
+        const uint32_t c = x < last ? x : last;
+        if constexpr (PAGED) {
+          if (paged) {
+            constexpr uint32_t kSteps = kPageRows / kStep;
+            const int pg = __builtin_amdgcn_readlane(my_page, int(c / kSteps));
+            return uint32_t(pg) * kSteps + c % kSteps;
+          }
+        }
+        return c;
+      };
       KBuf k0, k1;
       VBuf v0, v1;
       Pend p0, p1;
 #pragma unroll
       for (int h = 0; h < G; ++h) p1.p0[h] = p1.p1[h] = 0.0f;
-      load_k(k0, r, 0, kt);
+      load_k(k0, r, cl(0), kt);
       load_k(k1, r, cl(1), kt);
-      load_v(v0, r, 0, vp, vp + 8);
+      load_v(v0, r, cl(0), vp, vp + 8);
       score(k0, true, full, p1, p0);
       uint32_t i = 0;
       for (; i + 2 < n; i += 2) {
         load_k(k0, r, cl(i + 2), kt);
-        load_v(v1, r, i + 1, vp, vp + 8);
+        load_v(v1, r, cl(i + 1), vp, vp + 8);
         score(k1, true, full, p0, p1);
         values(v0, p0);
         load_k(k1, r, cl(i + 3), kt);
-        load_v(v0, r, i + 2, vp, vp + 8);
+        load_v(v0, r, cl(i + 2), vp, vp + 8);
         score(k0, true, full, p1, p0);
         values(v1, p1);
       }
       if (i + 1 < n) {
-        load_v(v1, r, i + 1, vp, vp + 8);
+        load_v(v1, r, cl(i + 1), vp, vp + 8);
         score(k1, true, full, p0, p1);
         values(v0, p0);
         values(v1, p1);
@@ -486,7 +520,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       }
     }
     const uint32_t left = nrows - n * kStep;
-    if (left > 0) {
+    if (left > 0 && !paged) {
       // Lanes past the range re-read its last row and are masked.
       const Rsrc r = make(s, row0 + n * kStep, left);
       const uint32_t lst = left - 1;
@@ -562,31 +596,31 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 
 // The MFMA kernel for a layout, or nullptr where it does not apply (the dot2
 // kernel serves those). Instantiated for group size 64 only.
-template <int D, int BK, int BV, int G>
+template <int D, int BK, int BV, int G, bool PAGED>
 KernelFn pick_mfma_g() {
   constexpr int NG = D / 64;
   if constexpr (NG >= 1 && mfma_layout_ok<D, BK, BV, G, NG>())
-    return decode_mfma_kernel<D, BK, BV, G, NG, waves_for<G, D>()>;
+    return decode_mfma_kernel<D, BK, BV, G, NG, waves_for<G, D>(), PAGED>;
   else
     return nullptr;
 }
 
-template <int D, int BK, int BV>
+template <int D, int BK, int BV, bool PAGED>
 KernelFn pick_mfma_bits_g(int G) {
   switch (G) {
-    case 1: return pick_mfma_g<D, BK, BV, 1>();
-    case 2: return pick_mfma_g<D, BK, BV, 2>();
-    case 4: return pick_mfma_g<D, BK, BV, 4>();
-    case 8: return pick_mfma_g<D, BK, BV, 8>();
+    case 1: return pick_mfma_g<D, BK, BV, 1, PAGED>();
+    case 2: return pick_mfma_g<D, BK, BV, 2, PAGED>();
+    case 4: return pick_mfma_g<D, BK, BV, 4, PAGED>();
+    case 8: return pick_mfma_g<D, BK, BV, 8, PAGED>();
   }
   return nullptr;
 }
 
-template <int D>
+template <int D, bool PAGED = false>
 KernelFn pick_mfma(int bk, int bv, int G, int gs) {
   if (gs != 64) return nullptr;
 #define TQKV_PAIR(K, V) \
-  if (bk == K && bv == V) return pick_mfma_bits_g<D, K, V>(G);
+  if (bk == K && bv == V) return pick_mfma_bits_g<D, K, V, PAGED>(G);
   TQKV_PAIR(3, 3) TQKV_PAIR(4, 4) TQKV_PAIR(8, 8)
   TQKV_PAIR(3, 4) TQKV_PAIR(4, 3) TQKV_PAIR(3, 8)
   TQKV_PAIR(8, 3) TQKV_PAIR(4, 8) TQKV_PAIR(8, 4)
@@ -594,9 +628,9 @@ KernelFn pick_mfma(int bk, int bv, int G, int gs) {
   return nullptr;
 }
 
-KernelFn pick_mfma_d64(int bk, int bv, int G, int gs);
-KernelFn pick_mfma_d128(int bk, int bv, int G, int gs);
-KernelFn pick_mfma_d256(int bk, int bv, int G, int gs);
+KernelFn pick_mfma_d64(int bk, int bv, int G, int gs, bool paged = false);
+KernelFn pick_mfma_d128(int bk, int bv, int G, int gs, bool paged = false);
+KernelFn pick_mfma_d256(int bk, int bv, int G, int gs, bool paged = false);
 
 }  // namespace decode
 }  // namespace tqkv

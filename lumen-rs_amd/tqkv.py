@@ -91,6 +91,15 @@ _SIGS = {
                                          P]),
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
     "tqkv_decode_kernel_name": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32]),
+    "tqkv_page_digest_affine": (I32, [P, P, P, I64, I64, I32, I32, I32, I64, I64, P, P, I64, P]),
+    "tqkv_sparse_keep_pages": (I64, [I64]),
+    "tqkv_page_select": (I32, [P, I32, I32, I32, I32, P, P, I64, I64, I32, P, P, SZ, P]),
+    "tqkv_page_select_workspace_size": (SZ, [I32, I32, I64]),
+    "tqkv_decode_attend_affine_pages": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32, P, P,
+                                              I32, I64, P, P, SZ, P]),
+    "tqkv_decode_attend_affine_sparse": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32, P, P,
+                                               P, I64, I64, I32, P, P, P, SZ, P]),
+    "tqkv_sparse_workspace_size": (SZ, [I32, I32, I32, I32, I64, I32]),
     "tqkv_synth_bf16": (I32, [P, I64, I32, ctypes.c_uint64, F32, F32, P]),
     "tqkv_lloyd_max": (I32, [ctypes.c_uint32, SZ, P, P]),
     "tqkv_rotation_matrix": (I32, [I32, ctypes.c_uint64, P]),
@@ -345,6 +354,47 @@ def prefill_attend_affine(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, segs, 
 def decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v):
     """"mfma", "dot2" or "" (unsupported) for a decode layout."""
     return lib().tqkv_decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v).decode()
+
+
+def page_digest_affine(kt, n_slabs, cap, dim, gs, bits, page_from, page_to, key_min, key_max,
+                       max_pages, stream=None):
+    """kt: (packed, scales, biases) device pointers of a K buffer."""
+    check(lib().tqkv_page_digest_affine(*kt, n_slabs, cap, dim, gs, bits, page_from, page_to,
+                                        key_min, key_max, max_pages, stream))
+
+
+def sparse_keep_pages(pages):
+    return lib().tqkv_sparse_keep_pages(pages)
+
+
+def page_select(q, B, H, H_kv, D, key_min, key_max, max_pages, pages, keep, chosen, workspace,
+                workspace_bytes, stream=None):
+    check(lib().tqkv_page_select(q, B, H, H_kv, D, key_min, key_max, max_pages, pages, keep,
+                                 chosen, workspace, workspace_bytes, stream))
+
+
+def page_select_workspace_size(B, H_kv, pages):
+    return lib().tqkv_page_select_workspace_size(B, H_kv, pages)
+
+
+def decode_attend_affine_pages(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, seg, chosen, keep,
+                               pages, out, workspace=None, workspace_bytes=0, stream=None):
+    check(lib().tqkv_decode_attend_affine_pages(q, B, H, H_kv, D, gs, bits_k, bits_v, scale,
+                                                ctypes.byref(seg), chosen, keep, pages, out,
+                                                workspace, workspace_bytes, stream))
+
+
+def decode_attend_affine_sparse(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, seg, key_min,
+                                key_max, max_pages, pages, keep, out, workspace, workspace_bytes,
+                                chosen_out=None, stream=None):
+    check(lib().tqkv_decode_attend_affine_sparse(q, B, H, H_kv, D, gs, bits_k, bits_v, scale,
+                                                 ctypes.byref(seg), key_min, key_max, max_pages,
+                                                 pages, keep, out, chosen_out, workspace,
+                                                 workspace_bytes, stream))
+
+
+def sparse_workspace_size(B, H, H_kv, D, total, keep):
+    return lib().tqkv_sparse_workspace_size(B, H, H_kv, D, total, keep)
 
 
 def decode_workspace_size(B, H, H_kv, D, total):

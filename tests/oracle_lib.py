@@ -61,6 +61,10 @@ def lib():
                                               SZ, L, P, P, P]),
             "oracle_golden_tape": (ctypes.c_int64, [ctypes.c_char_p, ctypes.c_char_p, P,
                                                     ctypes.c_int64, P, ctypes.c_int64, P, P, P]),
+            "oracle_page_digest_affine": (None, [P, P, P, SZ, SZ, I, I, I, SZ, SZ, P, P]),
+            "oracle_page_bounds": (None, [P, P, P, I, I, I, I, SZ, SZ, P]),
+            "oracle_sparse_keep_pages": (SZ, [SZ]),
+            "oracle_select_pages": (None, [P, SZ, SZ, SZ, P]),
             "oracle_fnv_num": (U64, [U64, U64]),
             "oracle_fnv_array": (U64, [U64, I, I, I, I, P]),
         }
@@ -236,3 +240,69 @@ def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0,
                                N, D, gs, bits_k, bits_v, scale, int(causal), q_start, first_held,
                                window, ptr(of), ptr(ob), ptr(lse), int(dequant == "f32"))
     return of, ob, lse
+
+
+# ------------------------------------------------------------- page-sparse
+PAGE = 64
+
+
+def page_digest_affine(kt, gs, bits, pages, max_pages=None):
+    """kt: (packed, scales, biases) [B, H_kv, cap, .]; key_min / key_max
+    bf16 [B, H_kv, max_pages, D] over pages [0, pages) (the rest zero)."""
+    kw, ks, kb = (np.ascontiguousarray(a) for a in kt)
+    B, Hkv, cap = kw.shape[:3]
+    D = kw.shape[3] * 32 // bits
+    mp = pages if max_pages is None else max_pages
+    kmin = np.zeros((B, Hkv, mp, D), np.uint16)
+    kmax = np.zeros((B, Hkv, mp, D), np.uint16)
+    lib().oracle_page_digest_affine(ptr(kw), ptr(ks), ptr(kb), B * Hkv, cap, D, gs, bits, pages,
+                                    mp, ptr(kmin), ptr(kmax))
+    return kmin, kmax
+
+
+def page_bounds(q, kmin, kmax, pages):
+    """f64 [B, H_kv, pages] page bounds (unpinned)."""
+    B, H, _, D = q.shape
+    Hkv, mp = kmin.shape[1], kmin.shape[2]
+    out = np.empty((B, Hkv, pages), np.float64)
+    lib().oracle_page_bounds(ptr(np.ascontiguousarray(q)), ptr(np.ascontiguousarray(kmin)),
+                             ptr(np.ascontiguousarray(kmax)), B, H, Hkv, D, pages, mp, ptr(out))
+    return out
+
+
+def sparse_keep_pages(pages):
+    return int(lib().oracle_sparse_keep_pages(pages))
+
+
+def select_pages(bounds, keep):
+    B, Hkv, pages = bounds.shape
+    out = np.empty((B, Hkv, keep), np.int32)
+    lib().oracle_select_pages(ptr(np.ascontiguousarray(bounds)), B * Hkv, pages, keep, ptr(out))
+    return out
+
+
+def gather_pages(t, chosen, n):
+    """Rows of the chosen pages of each (batch row, KV head), then the tail
+    [pages * 64, n) (pages = the digested count): one array per input array."""
+    B, Hkv, keep = chosen.shape
+    out = []
+    for a in t:
+        rows = []
+        for b in range(B):
+            per = []
+            for h in range(Hkv):
+                idx = (chosen[b, h][:, None] * PAGE + np.arange(PAGE)[None, :]).reshape(-1)
+                per.append(a[b, h, idx])
+            rows.append(per)
+        out.append(np.array(rows))
+    return out
+
+
+def attend_affine_pages(q, kt, vt, chosen, pages, n, gs, bits_k, bits_v, scale):
+    """sdpa_page_sparse's attention over the chosen pages plus the tail
+    [pages * 64, n), with the exact dequantization of the decode paths."""
+    kg, vg = gather_pages(kt, chosen, n), gather_pages(vt, chosen, n)
+    tail = lambda a: a[:, :, pages * PAGE:n]
+    kc = tuple(np.concatenate([g, tail(a)], axis=2) for g, a in zip(kg, kt))
+    vc = tuple(np.concatenate([g, tail(a)], axis=2) for g, a in zip(vg, vt))
+    return attend_affine(q, kc, vc, gs, bits_k, bits_v, scale)
