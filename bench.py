@@ -805,7 +805,7 @@ def sparse_main(T, hip, args):
          "bits_k": BITS, "bits_v": BITS, "group_size": GS,
          "keep_pages": int(T.sparse_keep_pages(N // 64))},
         _hbm(alg_b / (att_ms * 1e-3) / 1e9,
-             "page select + decode_mfma_kernel<256,3,3,2,4,8,paged> + merge", alg_b, att_ms),
+             "page bounds + select + decode_mfma_kernel<256,3,3,2,4,8,paged>", alg_b, att_ms),
         {"digest_ms_once": round(digest_ms, 4), "dense_bytes_per_step": int(dense_b),
          "dense_equivalent_gbps": round(dense_b / (att_ms * 1e-3) / 1e9, 1)}, settle, steps)
     print(json.dumps(result))
