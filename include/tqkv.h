@@ -239,6 +239,26 @@ int32_t tqkv_decode_attend_codebook(const uint16_t* q, int32_t B, int32_t H, int
                                     int64_t n, uint16_t* out, void* workspace,
                                     size_t workspace_bytes, tqkv_stream stream);
 size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int32_t D, int64_t total_tokens);
+/*
+ * The same attention over a codebook cache with QJL residual signs: each
+ * key's score is the two-stage estimate of estimate_inner_products
+ * (compressor.rs:122-159): stage 1 on the codes plus ||r|| sqrt(pi/2) /
+ * sqrt(m) * sum_i sign_i (Phi q)_i (qjl.rs:76-118), the QJL stage of the
+ * reference's TurboQuant attention (turboquant.rs:539-691) taken on the
+ * scores instead of materializing K_eff. k_signs u32 [B, H_kv, cap,
+ * ceil(m/32)], k_rnorm f32 [B, H_kv, cap], qjl f32 [m, D] (device),
+ * 1 <= qjl_m <= 1024.
+ */
+int32_t tqkv_decode_attend_codebook_qjl(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
+                                        int32_t D, float scale, const float* rotation,
+                                        const float* centroids_k, int32_t bits_k,
+                                        const float* centroids_v, int32_t bits_v,
+                                        const uint8_t* k_codes, const float* k_sigma,
+                                        const uint32_t* k_signs, const float* k_rnorm,
+                                        const float* qjl, int32_t qjl_m, const uint8_t* v_codes,
+                                        const float* v_sigma, int64_t cap, int64_t n,
+                                        uint16_t* out, void* workspace, size_t workspace_bytes,
+                                        tqkv_stream stream);
 
 /*
  * Prefill-chunk attention over affine-packed K/V on the matrix cores:
@@ -551,6 +571,31 @@ int32_t tqkv_tq_rotate_query(const float* rotation, const float* q, int32_t dim,
 int32_t tqkv_tq_scores(const float* rq, const uint8_t* codes, const float* sigma,
                        const float* centroids_f32, int32_t dim, int64_t n, float* scores,
                        tqkv_stream stream);
+/* QJLProjector::project_query (qjl.rs:76-84): pq[row] = Phi[row] . q, f32
+ * [m], bit-exact (sums folded from -0.0 in index order). Device. */
+int32_t tqkv_qjl_project_query(const float* qjl, int32_t m, int32_t dim, const float* q,
+                               float* pq, tqkv_stream stream);
+/* estimate_inner_products (compressor.rs:122-159): stage 1 as tqkv_tq_scores
+ * plus estimate_correction_from_projection (qjl.rs:86-118) of each key's
+ * residual signs (u32 words [n, ceil(m/32)], bit i of a key = sign of row
+ * i) and norm, bit-exact. Device. */
+int32_t tqkv_tq_scores_two_stage(const float* rq, const float* pq, const uint8_t* codes,
+                                 const float* sigma, const float* centroids_f32,
+                                 const uint32_t* signs, const float* rnorm, int32_t dim,
+                                 int32_t m, int64_t n, float* scores, tqkv_stream stream);
+/* qjl_encode_stage2_packed (turboquant.rs:592-622): residual = K_rot - K_dq
+ * (bf16 in, f32), r_norm = sqrt(sum r^2), sign bit i = (Phi[i] . r >= 0),
+ * packed LSB-first into u32 [rows, ceil(m/32)]. Sums run in index order
+ * from +0.0. Device. */
+int32_t tqkv_qjl_encode_stage2(const uint16_t* k_rot, const uint16_t* k_dq, const float* qjl,
+                               int64_t rows, int32_t dim, int32_t m, uint32_t* signs,
+                               float* rnorm, tqkv_stream stream);
+/* qjl_apply_correction_packed (turboquant.rs:624-691): K_eff = bf16(K_dq +
+ * bf16((sum_i sign_i Phi[i][d]) * (r_norm * sqrt(pi/2) / sqrt(m)))), bf16
+ * [rows, dim]. Device. */
+int32_t tqkv_qjl_apply_correction(const uint16_t* k_dq, const uint32_t* signs,
+                                  const float* rnorm, const float* qjl, int64_t rows, int32_t dim,
+                                  int32_t m, uint16_t* k_eff, tqkv_stream stream);
 /* SimpleCache::attend_values (simple.rs:40-62, 105-118): out = sum_t w_t *
  * R^T(centroid[c_t] * sigma_t), tokens with |w_t| < 1e-10 skipped, in the
  * reference's accumulation order. Device. */

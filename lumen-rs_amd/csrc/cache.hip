@@ -697,6 +697,14 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* c, const uint16_t* q, int32_t
     if (c->view_n <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
     const tqkv_cache_config& g = c->cfg;
     const int vi = g.qjl_words > 0 ? 4 : 2;
+    if (g.qjl_words > 0)  // keys' QJL residual signs correct the scores
+      return tqkv_decode_attend_codebook_qjl(
+          q, g.batch, H, g.kv_heads, g.k_dim, scale, c->R, c->cent_k, g.bits_k, c->cent_v,
+          g.bits_v, c->cur[0].ptr, reinterpret_cast<const float*>(c->cur[1].ptr),
+          reinterpret_cast<const uint32_t*>(c->cur[2].ptr),
+          reinterpret_cast<const float*>(c->cur[3].ptr), c->phi, 32 * g.qjl_words,
+          c->cur[vi].ptr, reinterpret_cast<const float*>(c->cur[vi + 1].ptr), c->cur[0].cap,
+          c->view_n, out, workspace, workspace_bytes, stream);
     return tqkv_decode_attend_codebook(
         q, g.batch, H, g.kv_heads, g.k_dim, scale, c->R, c->cent_k, g.bits_k, c->cent_v, g.bits_v,
         c->cur[0].ptr, reinterpret_cast<const float*>(c->cur[1].ptr), c->cur[vi].ptr,

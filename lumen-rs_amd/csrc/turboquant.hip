@@ -159,6 +159,116 @@ __global__ void tq_scores_kernel(const float* __restrict__ rq, const uint8_t* __
   scores[t] = mul(acc, sigma[t]);
 }
 
+// QJLProjector::project_query (qjl.rs:76-84): pq[row] = sum_j Phi[row][j] *
+// q[j], folded from -0.0 in j order.
+__global__ void tq_project_query_kernel(const float* __restrict__ phi, int m, int D,
+                                        const float* __restrict__ q, float* __restrict__ pq) {
+  for (int row = blockIdx.x * blockDim.x + threadIdx.x; row < m; row += gridDim.x * blockDim.x) {
+    const float* p = phi + int64_t(row) * D;
+    float acc = -0.0f;
+    for (int j = 0; j < D; ++j) acc = add(acc, mul(p[j], q[j]));
+    pq[row] = acc;
+  }
+}
+
+// The QJL correction of estimate_correction_from_projection (qjl.rs:86-118):
+// 0 when ||r|| < 1e-10, else ||r|| * sqrt(pi/2) / sqrt(m) * sum_i sign_i * pq_i
+// with the sum folded from +0.0 in row order; sign bit i of a key is bit
+// i % 32 of word i / 32 (the reference's u64 words, little-endian).
+__device__ __forceinline__ float qjl_correction(const float* pq, int m, const uint32_t* sg,
+                                                float rn) {
+  if (rn < 1e-10f) return 0.0f;
+  float sum = 0.0f;
+  for (int row = 0; row < m; ++row) {
+    const float sgn = ((sg[row / 32] >> (row % 32)) & 1u) ? 1.0f : -1.0f;
+    sum = add(sum, mul(sgn, pq[row]));
+  }
+  const float scale = div_rn(mul(rn, sqrt_rn(1.57079632679489661923f)), sqrt_rn(float(m)));
+  return mul(scale, sum);
+}
+
+// estimate_inner_products (compressor.rs:122-159): stage 1 as
+// tq_scores_kernel plus the QJL correction of the stored residual signs.
+__global__ void tq_scores_two_stage_kernel(const float* __restrict__ rq,
+                                           const float* __restrict__ pq,
+                                           const uint8_t* __restrict__ codes,
+                                           const float* __restrict__ sigma,
+                                           const float* __restrict__ cent_f32,
+                                           const uint32_t* __restrict__ signs,
+                                           const float* __restrict__ rnorm, int D, int m,
+                                           int64_t n, float* __restrict__ scores) {
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const uint8_t* c = codes + t * D;
+  float acc = -0.0f;
+  for (int i = 0; i < D; ++i) acc = add(acc, mul(rq[i], cent_f32[c[i]]));
+  const float s1 = mul(acc, sigma[t]);
+  const int words = (m + 31) / 32;
+  scores[t] = add(s1, qjl_correction(pq, m, signs + t * words, rnorm[t]));
+}
+
+// The GPU TurboQuant path's stage 2 (turboquant.rs:592-622): one wavefront
+// per row; residual = f32(K_rot) - f32(K_dq), r_norm = sqrt(sum r^2) in
+// channel order, sign bit i = (sum_d r_d * Phi[i][d] >= 0), sums from +0.0.
+__global__ __launch_bounds__(kWave) void qjl_encode_stage2_kernel(
+    const uint16_t* __restrict__ k_rot, const uint16_t* __restrict__ k_dq,
+    const float* __restrict__ phi, int D, int m, uint32_t* __restrict__ signs,
+    float* __restrict__ rnorm) {
+  extern __shared__ float s_r[];
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int d = lane; d < D; d += kWave)
+    s_r[d] = __fsub_rn(bf16_to_f32(k_rot[t * D + d]), bf16_to_f32(k_dq[t * D + d]));
+  __syncthreads();
+  if (lane == 0) {
+    float ss = 0.0f;
+    for (int d = 0; d < D; ++d) ss = add(ss, mul(s_r[d], s_r[d]));
+    rnorm[t] = sqrt_rn(ss);
+  }
+  const int words = (m + 31) / 32;
+  for (int base = 0; base < m; base += kWave) {
+    const int row = base + lane;
+    bool bit = false;
+    if (row < m) {
+      const float* p = phi + int64_t(row) * D;
+      float acc = 0.0f;
+      for (int d = 0; d < D; ++d) acc = add(acc, mul(s_r[d], p[d]));
+      bit = acc >= 0.0f;
+    }
+    const uint64_t ball = __ballot(bit);
+    if (lane == 0) {
+      const int w0 = base / 32;
+      signs[t * words + w0] = uint32_t(ball);
+      if (w0 + 1 < words) signs[t * words + w0 + 1] = uint32_t(ball >> 32);
+    }
+  }
+}
+
+// qjl_apply_correction_packed / _to_k_dq (turboquant.rs:624-691): one
+// thread per (row, channel); K_eff = bf16(K_dq + bf16((sum_i sign_i *
+// Phi[i][d]) * (r_norm * sqrt(pi/2) / sqrt(m)))), the sum from +0.0 in i
+// order.
+__global__ void qjl_apply_correction_kernel(const uint16_t* __restrict__ k_dq,
+                                            const uint32_t* __restrict__ signs,
+                                            const float* __restrict__ rnorm,
+                                            const float* __restrict__ phi, int D, int m,
+                                            int64_t rows, uint16_t* __restrict__ k_eff) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * D) return;
+  const int64_t t = i / D;
+  const int d = int(i % D);
+  const int words = (m + 31) / 32;
+  const uint32_t* sg = signs + t * words;
+  float acc = 0.0f;
+  for (int row = 0; row < m; ++row) {
+    const float p = phi[int64_t(row) * D + d];
+    acc = add(acc, ((sg[row / 32] >> (row % 32)) & 1u) ? p : -p);
+  }
+  const float sc = div_rn(sqrt_rn(1.57079632679489661923f), sqrt_rn(float(m)));
+  const float corr = bf16_to_f32(f32_to_bf16(mul(acc, mul(rnorm[t], sc))));
+  k_eff[i] = f32_to_bf16(add(bf16_to_f32(k_dq[i]), corr));
+}
+
 // attend_values: output channel i sums, token by token in order and channel
 // j by channel j, R[j][i] * (centroid * (scale * w)); tokens with |w| < 1e-10
 // are skipped (simple.rs:40-62, 105-118).
@@ -248,6 +358,64 @@ extern "C" int32_t tqkv_tq_rotate_query(const float* rotation, const float* q, i
   return ok();
 }
 
+extern "C" int32_t tqkv_qjl_project_query(const float* qjl, int32_t m, int32_t dim,
+                                          const float* q, float* pq, tqkv_stream stream) {
+  if (!qjl || !q || !pq) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (m <= 0 || dim <= 0) return fail(TQKV_EINVAL_SHAPE, "m=%d dim=%d", m, dim);
+  hipLaunchKernelGGL(tq_project_query_kernel, dim3(unsigned((m + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), qjl, m, dim, q, pq);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_scores_two_stage(const float* rq, const float* pq,
+                                            const uint8_t* codes, const float* sigma,
+                                            const float* centroids_f32, const uint32_t* signs,
+                                            const float* rnorm, int32_t dim, int32_t m, int64_t n,
+                                            float* scores, tqkv_stream stream) {
+  if (n == 0) return ok();
+  if (!rq || !pq || !codes || !sigma || !centroids_f32 || !signs || !rnorm || !scores)
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (dim <= 0 || m <= 0 || n < 0)
+    return fail(TQKV_EINVAL_SHAPE, "dim=%d m=%d n=%lld", dim, m, (long long)n);
+  hipLaunchKernelGGL(tq_scores_two_stage_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), rq, pq, codes, sigma, centroids_f32,
+                     signs, rnorm, dim, m, n, scores);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_qjl_encode_stage2(const uint16_t* k_rot, const uint16_t* k_dq,
+                                          const float* qjl, int64_t rows, int32_t dim, int32_t m,
+                                          uint32_t* signs, float* rnorm, tqkv_stream stream) {
+  if (rows == 0) return ok();
+  if (!k_rot || !k_dq || !qjl || !signs || !rnorm) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (rows < 0 || rows > 0x7fffffffLL || dim <= 0 || dim > 4096 || m <= 0)
+    return fail(TQKV_EINVAL_SHAPE, "rows=%lld dim=%d m=%d", (long long)rows, dim, m);
+  hipLaunchKernelGGL(qjl_encode_stage2_kernel, dim3(unsigned(rows)), dim3(kWave),
+                     size_t(dim) * sizeof(float), reinterpret_cast<hipStream_t>(stream), k_rot,
+                     k_dq, qjl, dim, m, signs, rnorm);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_qjl_apply_correction(const uint16_t* k_dq, const uint32_t* signs,
+                                             const float* rnorm, const float* qjl, int64_t rows,
+                                             int32_t dim, int32_t m, uint16_t* k_eff,
+                                             tqkv_stream stream) {
+  if (rows == 0) return ok();
+  if (!k_dq || !signs || !rnorm || !qjl || !k_eff) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (rows < 0 || dim <= 0 || m <= 0)
+    return fail(TQKV_EINVAL_SHAPE, "rows=%lld dim=%d m=%d", (long long)rows, dim, m);
+  const int64_t blocks = (rows * dim + 255) / 256;
+  if (blocks > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "too many rows");
+  hipLaunchKernelGGL(qjl_apply_correction_kernel, dim3(unsigned(blocks)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), k_dq, signs, rnorm, qjl, dim, m, rows,
+                     k_eff);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
 extern "C" int32_t tqkv_tq_scores(const float* rq, const uint8_t* codes, const float* sigma,
                                   const float* centroids_f32, int32_t dim, int64_t n,
                                   float* scores, tqkv_stream stream) {
@@ -311,26 +479,52 @@ __global__ void cb_rotate_q_kernel(const uint16_t* __restrict__ q, const float* 
   }
 }
 
+// pq = Phi q for every (batch row, head): the query's QJL projection
+// (QJLProjector::project_query, qjl.rs:76-84) for the score correction.
+__global__ void cb_project_q_kernel(const uint16_t* __restrict__ q, const float* __restrict__ phi,
+                                    int D, int m, float* __restrict__ pq) {
+  const int64_t bh = blockIdx.x;
+  for (int row = threadIdx.x; row < m; row += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < D; ++j) acc = fmaf(phi[int64_t(row) * D + j], bf16_to_f32(q[bh * D + j]), acc);
+    pq[bh * m + row] = acc;
+  }
+}
+
+// Most QJL rows the fused decode takes (m = 32 * qjl_words).
+constexpr int kMaxQjl = 1024;
+
 // One workgroup of one wavefront per (split, KV head, batch row): partial
 // softmax state over its tokens for the G query heads. Scores: lane = token;
-// values: lane = channels (D / 64 each).
-template <int D, int G>
+// values: lane = channels (D / 64 each). QJL: each key's score gains the
+// QJL estimate of q . r from its residual signs (estimate_correction,
+// qjl.rs:86-118; the two-stage scores of compressor.rs:122-159), with the
+// query's projection in LDS.
+template <int D, int G, bool QJL>
 __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     const float* __restrict__ qr, int H, const uint8_t* __restrict__ kc,
     const float* __restrict__ ks, const uint8_t* __restrict__ vc, const float* __restrict__ vs,
     int64_t cap, int64_t n, int H_kv, const float* __restrict__ cent_k,
     const float* __restrict__ cent_v, int n_k, int n_v, float qscale, int64_t split_len,
     int n_splits, float* __restrict__ part_o, float* __restrict__ part_m,
-    float* __restrict__ part_l) {
+    float* __restrict__ part_l, const uint32_t* __restrict__ ksg, const float* __restrict__ krn,
+    const float* __restrict__ pq, int qm) {
   constexpr int PER = D / kWave;
   __shared__ float s_q[G][D];
   __shared__ float s_ck[256], s_cv[256];
   __shared__ float s_p[G][kCbTile];
+  __shared__ float s_pq[QJL ? G : 1][QJL ? kMaxQjl : 1];
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int lane = threadIdx.x;
   for (int i = lane; i < G * D; i += kWave) {
     const int h = i / D, d = i % D;
     s_q[h][d] = qr[(int64_t(b) * H + kvh * G + h) * D + d] * qscale;
+  }
+  if constexpr (QJL) {
+    for (int i = lane; i < G * qm; i += kWave) {
+      const int h = i / qm, r = i % qm;
+      s_pq[h][r] = pq[(int64_t(b) * H + kvh * G + h) * qm + r];
+    }
   }
   for (int i = lane; i < 256; i += kWave) {
     s_ck[i] = i < n_k ? cent_k[i] : 0.0f;
@@ -369,6 +563,31 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
       const float sg = ks[slab + t];
 #pragma unroll
       for (int h = 0; h < G; ++h) sc[h] *= sg;
+      if constexpr (QJL) {
+        const float rn = krn[slab + t];
+        if (rn >= 1e-10f) {
+          const int words = (qm + 31) / 32;
+          const uint32_t* sw = ksg + (slab + t) * words;
+          float corr[G];
+#pragma unroll
+          for (int h = 0; h < G; ++h) corr[h] = 0.0f;
+          for (int w = 0; w < words; ++w) {
+            const uint32_t bits = sw[w];
+            const int nb = qm - 32 * w < 32 ? qm - 32 * w : 32;
+            for (int j = 0; j < nb; ++j) {
+              const bool pos = (bits >> j) & 1u;
+#pragma unroll
+              for (int h = 0; h < G; ++h) {
+                const float p = s_pq[h][32 * w + j];
+                corr[h] += pos ? p : -p;
+              }
+            }
+          }
+          const float cm = rn * (1.2533141373155001f / sqrtf(float(qm)));  // sqrt(pi/2) / sqrt(m)
+#pragma unroll
+          for (int h = 0; h < G; ++h) sc[h] = fmaf(corr[h] * cm, qscale, sc[h]);
+        }
+      }
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -445,12 +664,18 @@ template <int D>
 int32_t launch_cb(int G, dim3 grid, hipStream_t st, const float* qr, int H, const uint8_t* kc,
                   const float* ks, const uint8_t* vc, const float* vs, int64_t cap, int64_t n,
                   int H_kv, const float* ck, const float* cv, int nk, int nv, float qscale,
-                  int64_t split_len, int n_splits, float* po, float* pm, float* pl) {
-#define TQKV_CB(GG)                                                                          \
-  case GG:                                                                                  \
-    hipLaunchKernelGGL((cb_decode_kernel<D, GG>), grid, dim3(kWave), 0, st, qr, H, kc, ks, vc, \
-                       vs, cap, n, H_kv, ck, cv, nk, nv, qscale, split_len, n_splits, po, pm, \
-                       pl);                                                                   \
+                  int64_t split_len, int n_splits, float* po, float* pm, float* pl,
+                  const uint32_t* ksg, const float* krn, const float* pq, int m) {
+#define TQKV_CB(GG)                                                                           \
+  case GG:                                                                                   \
+    if (ksg)                                                                                 \
+      hipLaunchKernelGGL((cb_decode_kernel<D, GG, true>), grid, dim3(kWave), 0, st, qr, H, kc, \
+                         ks, vc, vs, cap, n, H_kv, ck, cv, nk, nv, qscale, split_len, n_splits, \
+                         po, pm, pl, ksg, krn, pq, m);                                        \
+    else                                                                                     \
+      hipLaunchKernelGGL((cb_decode_kernel<D, GG, false>), grid, dim3(kWave), 0, st, qr, H, kc,\
+                         ks, vc, vs, cap, n, H_kv, ck, cv, nk, nv, qscale, split_len, n_splits, \
+                         po, pm, pl, ksg, krn, pq, m);                                        \
     break;
   switch (G) {
     TQKV_CB(1) TQKV_CB(2) TQKV_CB(4) TQKV_CB(8)
@@ -469,18 +694,25 @@ extern "C" size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int3
                                                        int64_t total_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || total_tokens <= 0) return 0;
   const int64_t splits = (total_tokens + 511) / 512 < 64 ? (total_tokens + 511) / 512 : 64;
-  return size_t(B) * H * (size_t(D) + size_t(splits) * (size_t(D) + 2)) * sizeof(float);
+  return size_t(B) * H * (size_t(D) + size_t(tq::kMaxQjl) + size_t(splits) * (size_t(D) + 2)) *
+         sizeof(float);
 }
 
-extern "C" int32_t tqkv_decode_attend_codebook(
-    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,
-    const float* rotation, const float* centroids_k, int32_t bits_k, const float* centroids_v,
-    int32_t bits_v, const uint8_t* k_codes, const float* k_sigma, const uint8_t* v_codes,
-    const float* v_sigma, int64_t cap, int64_t n, uint16_t* out, void* workspace,
-    size_t workspace_bytes, tqkv_stream stream) {
+namespace {
+int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D,
+                        float scale, const float* rotation, const float* centroids_k,
+                        int32_t bits_k, const float* centroids_v, int32_t bits_v,
+                        const uint8_t* k_codes, const float* k_sigma, const uint32_t* k_signs,
+                        const float* k_rnorm, const float* qjl, int32_t qjl_m,
+                        const uint8_t* v_codes, const float* v_sigma, int64_t cap, int64_t n,
+                        uint16_t* out, void* workspace, size_t workspace_bytes,
+                        tqkv_stream stream) {
   if (!q || !rotation || !centroids_k || !centroids_v || !k_codes || !k_sigma || !v_codes ||
       !v_sigma || !out)
     return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (qjl_m != 0 && (!k_signs || !k_rnorm || !qjl || qjl_m < 0 || qjl_m > tq::kMaxQjl))
+    return fail(TQKV_EINVAL_ARG, "qjl_m=%d needs signs, residual norms and the QJL matrix "
+                "(m <= %d)", qjl_m, tq::kMaxQjl);
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n <= 0 || n > cap)
     return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d n=%lld cap=%lld", B, H, H_kv, (long long)n,
                 (long long)cap);
@@ -498,20 +730,27 @@ extern "C" int32_t tqkv_decode_attend_codebook(
     return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
   }
   float* qr = static_cast<float*>(ws);
-  float* po = qr + size_t(B) * H * D;
+  float* pq = qr + size_t(B) * H * D;
+  float* po = pq + size_t(B) * H * tq::kMaxQjl;
   float* pm = po + size_t(B) * H * n_splits * D;
   float* pl = pm + size_t(B) * H * n_splits;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(tq::cb_rotate_q_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256), 0,
                      st, q, rotation, D, qr);
   TQKV_LAUNCHED();
+  if (qjl_m > 0) {
+    hipLaunchKernelGGL(tq::cb_project_q_kernel, dim3(unsigned(B * H)), dim3(256), 0, st, q, qjl,
+                       D, qjl_m, pq);
+    TQKV_LAUNCHED();
+  }
+  const uint32_t* sg = qjl_m > 0 ? k_signs : nullptr;
   const dim3 grid{unsigned(n_splits), unsigned(H_kv), unsigned(B)};
   const float qscale = scale * 1.4426950408889634f;
   int32_t rc = TQKV_OK;
   switch (D) {
-    case 64: rc = tq::launch_cb<64>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl); break;
-    case 128: rc = tq::launch_cb<128>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl); break;
-    case 256: rc = tq::launch_cb<256>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl); break;
+    case 64: rc = tq::launch_cb<64>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
+    case 128: rc = tq::launch_cb<128>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
+    case 256: rc = tq::launch_cb<256>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
     default: return fail(TQKV_EUNSUPPORTED, "codebook decode D=%d not in {64,128,256}", D);
   }
   if (rc) return rc;
@@ -519,4 +758,29 @@ extern "C" int32_t tqkv_decode_attend_codebook(
                      size_t(D) * sizeof(float), st, po, pm, pl, n_splits, D, rotation, out);
   TQKV_LAUNCHED();
   return ok();
+}
+}  // namespace
+
+extern "C" int32_t tqkv_decode_attend_codebook(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,
+    const float* rotation, const float* centroids_k, int32_t bits_k, const float* centroids_v,
+    int32_t bits_v, const uint8_t* k_codes, const float* k_sigma, const uint8_t* v_codes,
+    const float* v_sigma, int64_t cap, int64_t n, uint16_t* out, void* workspace,
+    size_t workspace_bytes, tqkv_stream stream) {
+  return decode_codebook(q, B, H, H_kv, D, scale, rotation, centroids_k, bits_k, centroids_v,
+                         bits_v, k_codes, k_sigma, nullptr, nullptr, nullptr, 0, v_codes, v_sigma,
+                         cap, n, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int32_t tqkv_decode_attend_codebook_qjl(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,
+    const float* rotation, const float* centroids_k, int32_t bits_k, const float* centroids_v,
+    int32_t bits_v, const uint8_t* k_codes, const float* k_sigma, const uint32_t* k_signs,
+    const float* k_rnorm, const float* qjl, int32_t qjl_m, const uint8_t* v_codes,
+    const float* v_sigma, int64_t cap, int64_t n, uint16_t* out, void* workspace,
+    size_t workspace_bytes, tqkv_stream stream) {
+  if (qjl_m <= 0) return fail(TQKV_EINVAL_ARG, "qjl_m=%d", qjl_m);
+  return decode_codebook(q, B, H, H_kv, D, scale, rotation, centroids_k, bits_k, centroids_v,
+                         bits_v, k_codes, k_sigma, k_signs, k_rnorm, qjl, qjl_m, v_codes, v_sigma,
+                         cap, n, out, workspace, workspace_bytes, stream);
 }

@@ -108,6 +108,12 @@ _SIGS = {
                              P]),
     "tqkv_tq_rotate_query": (I32, [P, P, I32, P, P]),
     "tqkv_tq_scores": (I32, [P, P, P, P, I32, I64, P, P]),
+    "tqkv_qjl_project_query": (I32, [P, I32, I32, P, P, P]),
+    "tqkv_tq_scores_two_stage": (I32, [P, P, P, P, P, P, P, I32, I32, I64, P, P]),
+    "tqkv_qjl_encode_stage2": (I32, [P, P, P, I64, I32, I32, P, P, P]),
+    "tqkv_qjl_apply_correction": (I32, [P, P, P, P, I64, I32, I32, P, P]),
+    "tqkv_decode_attend_codebook_qjl": (I32, [P, I32, I32, I32, I32, F32, P, P, I32, P, I32, P, P,
+                                              P, P, P, I32, P, P, I64, I64, P, P, SZ, P]),
     "tqkv_tq_values": (I32, [P, P, P, P, P, I32, I64, P, P]),
     "tqkv_rotate_bf16": (I32, [P, I64, I32, P, I32, P, P]),
     "tqkv_kvcache_create": (I32, [ctypes.POINTER(TqConfig), P, P, I32, I32, ctypes.POINTER(P)]),
@@ -395,6 +401,28 @@ def decode_attend_affine_sparse(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, seg
 
 def sparse_workspace_size(B, H, H_kv, D, total, keep):
     return lib().tqkv_sparse_workspace_size(B, H, H_kv, D, total, keep)
+
+
+def tq_rotate_query(rotation, q, dim, rq, stream=None):
+    check(lib().tqkv_tq_rotate_query(rotation, q, dim, rq, stream))
+
+
+def qjl_project_query(qjl, m, dim, q, pq, stream=None):
+    check(lib().tqkv_qjl_project_query(qjl, m, dim, q, pq, stream))
+
+
+def tq_scores_two_stage(rq, pq, codes, sigma, centroids, signs, rnorm, dim, m, n, scores,
+                        stream=None):
+    check(lib().tqkv_tq_scores_two_stage(rq, pq, codes, sigma, centroids, signs, rnorm, dim, m,
+                                         n, scores, stream))
+
+
+def qjl_encode_stage2(k_rot, k_dq, qjl, rows, dim, m, signs, rnorm, stream=None):
+    check(lib().tqkv_qjl_encode_stage2(k_rot, k_dq, qjl, rows, dim, m, signs, rnorm, stream))
+
+
+def qjl_apply_correction(k_dq, signs, rnorm, qjl, rows, dim, m, k_eff, stream=None):
+    check(lib().tqkv_qjl_apply_correction(k_dq, signs, rnorm, qjl, rows, dim, m, k_eff, stream))
 
 
 def decode_workspace_size(B, H, H_kv, D, total):

@@ -65,6 +65,10 @@ def lib():
             "oracle_page_bounds": (None, [P, P, P, I, I, I, I, SZ, SZ, P]),
             "oracle_sparse_keep_pages": (SZ, [SZ]),
             "oracle_select_pages": (None, [P, SZ, SZ, SZ, P]),
+            "oracle_qjl_encode_stage2": (None, [P, P, P, SZ, I, I, P, P]),
+            "oracle_qjl_apply_correction": (None, [P, P, P, P, SZ, I, I, P]),
+            "oracle_attend_codebook_qjl": (None, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, SZ,
+                                                  I, I, F, P]),
             "oracle_fnv_num": (U64, [U64, U64]),
             "oracle_fnv_array": (U64, [U64, I, I, I, I, P]),
         }
@@ -124,6 +128,14 @@ def pack_codes(codes, bits):
     c = np.ascontiguousarray(codes, np.uint8)
     out = np.zeros(lib().oracle_packed_words(c.size, bits), np.uint64)
     lib().oracle_pack_codes(ptr(c), c.size, bits, ptr(out))
+    return out
+
+
+def unpack_codes(packed, n, bits):
+    """bitpack::unpack_codes (bitpack.rs:35-52): u64 words -> n u8 codes."""
+    p = np.ascontiguousarray(packed, np.uint64)
+    out = np.zeros(n, np.uint8)
+    lib().oracle_unpack_codes(ptr(p), n, bits, ptr(out))
     return out
 
 
@@ -306,3 +318,46 @@ def attend_affine_pages(q, kt, vt, chosen, pages, n, gs, bits_k, bits_v, scale):
     kc = tuple(np.concatenate([g, tail(a)], axis=2) for g, a in zip(kg, kt))
     vc = tuple(np.concatenate([g, tail(a)], axis=2) for g, a in zip(vg, vt))
     return attend_affine(q, kc, vc, gs, bits_k, bits_v, scale)
+
+
+# ------------------------------------------------------- QJL (GPU path)
+def qjl_encode_stage2(k_rot, k_dq, phi, m):
+    """turboquant.rs:592-622 restated: (signs u32 [rows, ceil(m/32)], r_norm)."""
+    k_rot = np.ascontiguousarray(k_rot, np.uint16)
+    D = k_rot.shape[-1]
+    rows = k_rot.size // D
+    signs = np.zeros((rows, (m + 31) // 32), np.uint32)
+    rn = np.zeros(rows, np.float32)
+    lib().oracle_qjl_encode_stage2(ptr(k_rot), ptr(np.ascontiguousarray(k_dq, np.uint16)),
+                                   ptr(np.ascontiguousarray(phi, np.float32)), rows, D, m,
+                                   ptr(signs), ptr(rn))
+    return signs, rn
+
+
+def qjl_apply_correction(k_dq, signs, rnorm, phi, m):
+    """turboquant.rs:624-691 restated: K_eff bf16."""
+    k_dq = np.ascontiguousarray(k_dq, np.uint16)
+    D = k_dq.shape[-1]
+    rows = k_dq.size // D
+    out = np.zeros_like(k_dq)
+    lib().oracle_qjl_apply_correction(ptr(k_dq), ptr(np.ascontiguousarray(signs, np.uint32)),
+                                      ptr(np.ascontiguousarray(rnorm, np.float32)),
+                                      ptr(np.ascontiguousarray(phi, np.float32)), rows, D, m,
+                                      ptr(out))
+    return out
+
+
+def attend_codebook_qjl(q, kc, ks, ksg, krn, vc, vs, cent_k, cent_v, R, phi, m, scale):
+    """Codebook attention with the two-stage (QJL-corrected) scores; f32
+    [B, H, D] in the original basis."""
+    B, H, _, D = q.shape
+    Hkv, N = kc.shape[1], kc.shape[2]
+    out = np.zeros((B, H, D), np.float32)
+    c = lambda a, t: np.ascontiguousarray(a, t)
+    lib().oracle_attend_codebook_qjl(ptr(c(q, np.uint16)), ptr(c(kc, np.uint8)), ptr(c(ks, np.float32)),
+                                     ptr(c(ksg, np.uint32)), ptr(c(krn, np.float32)),
+                                     ptr(c(vc, np.uint8)), ptr(c(vs, np.float32)),
+                                     ptr(c(cent_k, np.float32)), ptr(c(cent_v, np.float32)),
+                                     ptr(c(R, np.float32)), ptr(c(phi, np.float32)), B, H, Hkv, N,
+                                     D, m, scale, ptr(out))
+    return out

@@ -320,7 +320,18 @@ def test_codebook_cache_append_and_decode(T, bits, qjl_words):
     q = kv_bf16((B, Hq, 1, D), 63)
     qf = O.bf16_to_f32(q).reshape(B, Hq, D).astype(np.float64)
     qr = qf @ R.astype(np.float64).T  # R q per head
-    want = attention_f64(qr, Kr, Vr, D ** -0.5, Hq // Hkv) @ R.astype(np.float64)  # R^T o
+    if qjl_words:
+        # The keys' QJL residual signs correct every score (two-stage scores).
+        ksg = T.view_slot(bufs, 2, B * Hkv, np.uint32, qjl_words)[:, :300]
+        krn = T.view_slot(bufs, 3, B * Hkv, np.float32, 1)[:, :300, 0]
+        _, centk = T.lloyd_max(bits)
+        cf = centk.astype(np.float32)
+        want = O.attend_codebook_qjl(q, kc.reshape(B, Hkv, 300, D), ks.reshape(B, Hkv, 300),
+                                     ksg.reshape(B, Hkv, 300, qjl_words), krn.reshape(B, Hkv, 300),
+                                     vc.reshape(B, Hkv, 300, D), vsg.reshape(B, Hkv, 300), cf, cf,
+                                     R, phi[:m], m, D ** -0.5).astype(np.float64)
+    else:
+        want = attention_f64(qr, Kr, Vr, D ** -0.5, Hq // Hkv) @ R.astype(np.float64)  # R^T o
     got = O.bf16_to_f32(decode(T, c, q, Hq, D ** -0.5)).reshape(B, Hq, D)
     err = np.abs(got - want)
     print(f"[codebook-decode] bits={bits} max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
