@@ -368,6 +368,14 @@ typedef struct tqkv_cache_state {
  * destroy frees the device buffers. */
 int32_t tqkv_cache_create(const tqkv_cache_config* cfg, tqkv_cache** out);
 int32_t tqkv_cache_destroy(tqkv_cache* cache);
+/*
+ * deep_clone (native_cache.rs:1575-1610; native_snapshot.rs:87-121 for the
+ * fork of a prompt cache): a new cache with the source's configuration,
+ * state and tables and its own copy of every buffer (stream-ordered device
+ * copies), independent of the source from then on. A shared prefix the
+ * source reads stays shared.
+ */
+int32_t tqkv_cache_clone(const tqkv_cache* src, tqkv_cache** out, tqkv_stream stream);
 
 /*
  * update_and_fetch with the slots' new rows given as they are stored

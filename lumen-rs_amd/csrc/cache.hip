@@ -13,6 +13,7 @@
 // copies are small kernels (no hipMemsetAsync, so a caller may capture the
 // update-free calls in a graph).
 #include <algorithm>
+#include <type_traits>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -483,6 +484,53 @@ int32_t tqkv_cache_create(const tqkv_cache_config* cfg, tqkv_cache** out) {
       delete c;
       return fail(TQKV_EINVAL_ARG, "kind=%d", k.kind);
   }
+  *out = c;
+  return ok();
+}
+
+int32_t tqkv_cache_clone(const tqkv_cache* src, tqkv_cache** out, tqkv_stream stream) {
+  if (!src || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  *out = nullptr;
+  tqkv_cache* c = nullptr;
+  if (int32_t rc = tqkv_cache_create(&src->cfg, &c)) return rc;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto copy = [&](void* dst, const void* from, size_t bytes) -> int32_t {
+    TQKV_HIP(hipMemcpyAsync(dst, from, bytes, hipMemcpyDeviceToDevice, st));
+    return TQKV_OK;
+  };
+  auto table = [&](auto** dst, const auto* from, size_t bytes) -> int32_t {
+    if (!from) return TQKV_OK;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return fail(TQKV_ENOMEM, "table hipMalloc");
+    *dst = static_cast<std::remove_pointer_t<decltype(dst)>>(p);
+    return copy(p, from, bytes);
+  };
+  int32_t rc = TQKV_OK;
+  for (int s = 0; s < src->n_slots && rc == TQKV_OK; ++s) {
+    const Buf& b = src->cur[s];
+    if (!b.ptr) continue;
+    rc = alloc(c, c->cur[s], b.cap, s);
+    if (rc == TQKV_OK)
+      rc = copy(c->cur[s].ptr, b.ptr, size_t(src->n_slabs) * size_t(b.cap) * size_t(src->rb[s]));
+  }
+  if (rc == TQKV_OK && src->R) {
+    const size_t D = size_t(src->cfg.k_dim), m = size_t(32) * size_t(src->cfg.qjl_words);
+    const size_t nk = size_t(1) << src->cfg.bits_k, nv = size_t(1) << src->cfg.bits_v;
+    rc = table(&c->R, src->R, D * D * sizeof(float));
+    if (rc == TQKV_OK && m) rc = table(&c->phi, src->phi, m * D * sizeof(float));
+    if (rc == TQKV_OK) rc = table(&c->bnd_k, src->bnd_k, (nk + 1) * sizeof(double));
+    if (rc == TQKV_OK) rc = table(&c->bnd_v, src->bnd_v, (nv + 1) * sizeof(double));
+    if (rc == TQKV_OK) rc = table(&c->cent_k, src->cent_k, nk * sizeof(float));
+    if (rc == TQKV_OK) rc = table(&c->cent_v, src->cent_v, nv * sizeof(float));
+  }
+  if (rc != TQKV_OK) {
+    tqkv_cache_destroy(c);
+    return rc;
+  }
+  c->st = src->st;
+  c->view_n = src->view_n;
+  c->base_offset = src->base_offset;
+  c->prefix = src->prefix;  // a shared prefix stays shared by every fork
   *out = c;
   return ok();
 }

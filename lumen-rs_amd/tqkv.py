@@ -128,6 +128,7 @@ _SIGS = {
     "tqkv_kvcache_read": (I32, [P, I32, I32, I32, I64, I64, P, P, P, P]),
     "tqkv_cache_create": (I32, [ctypes.POINTER(CacheConfig), ctypes.POINTER(P)]),
     "tqkv_cache_destroy": (I32, [P]),
+    "tqkv_cache_clone": (I32, [P, ctypes.POINTER(P), P]),
     "tqkv_cache_update": (I32, [P, ctypes.POINTER(P), I64, ctypes.POINTER(CacheView), P]),
     "tqkv_cache_append": (I32, [P, P, P, I64, ctypes.POINTER(CacheView), P]),
     "tqkv_cache_truncate": (I32, [P, I64]),
@@ -480,6 +481,14 @@ class Cache:
         c = cls.__new__(cls)
         c.cfg = None
         c.h = handle
+        return c
+
+    def clone(self, stream=None):
+        """An independent deep copy (tqkv_cache_clone)."""
+        h = P()
+        check(lib().tqkv_cache_clone(self.h, ctypes.byref(h), stream))
+        c = Cache.adopt(h.value)
+        c.cfg = self.cfg
         return c
 
     def close(self):

@@ -191,3 +191,36 @@ def test_import_rejects_inconsistent_layers(T):
     with pytest.raises(T.TqkvError) as e:
         T.lkv_import(L.write(lin, []), 0)
     assert e.value.status == T.EUNSUPPORTED
+
+
+@pytest.mark.parametrize("name,kind,kw,D,chunks", CASES, ids=[c[0] for c in CASES])
+def test_clone_is_an_independent_copy(T, name, kind, kw, D, chunks):
+    """tqkv_cache_clone (deep_clone, native_cache.rs:1575-1610): the clone
+    holds the same state and bytes, attends the same, and stays untouched
+    when the source takes further appends and is destroyed."""
+    B, Hkv, Hq = 2, 2, 4
+    print(f"[clone] {name}", flush=True)
+    c = make(T, kind, kw, B, Hkv, D)
+    fill(T, c, B, Hkv, D, chunks, 21)
+    c2 = c.clone()
+    T.hip().sync()
+    a, b = c.state(), c2.state()
+    assert (a.offset, a.idx, a.cached_len, a.base_offset, a.view) == \
+           (b.offset, b.idx, b.cached_len, b.base_offset, b.view)
+    before = download_slots(T, c, B * Hkv)
+    for x, y in zip(before, download_slots(T, c2, B * Hkv)):
+        assert np.array_equal(x, y)
+    if kind != "BF16":
+        q = kv_bf16((B, Hq, 1, D), 5)
+        dq = T.DeviceArray.of(q)
+        o1, o2 = T.DeviceArray((B, Hq, 1, D), np.uint16), T.DeviceArray((B, Hq, 1, D), np.uint16)
+        c.decode_attend(dq.ptr, Hq, D ** -0.5, o1.ptr)
+        c2.decode_attend(dq.ptr, Hq, D ** -0.5, o2.ptr)
+        T.hip().sync()
+        assert np.array_equal(o1.numpy(), o2.numpy())
+    fill(T, c, B, Hkv, D, [1, 5], 77)  # the source moves on
+    c.close()
+    for x, y in zip(before, download_slots(T, c2, B * Hkv)):
+        assert np.array_equal(x, y)
+    fill(T, c2, B, Hkv, D, [2], 78)  # the clone still appends
+    assert c2.state().offset == a.offset + 2
