@@ -504,8 +504,13 @@ def append_main(T, hip, args):
         {"workload": "BASELINE config 0: quantize-on-append of one layer's K and V "
                      "(B=1, 8 KV heads, D=128, 4,096 tokens, 4-bit gs64)",
          "batch": B, "kv_heads": HKV, "head_dim": D, "tokens": S, "bits": BITS, "group_size": GS},
+        # HBM bytes per launch from the counter passes recorded in
+        # profiles/append_quantize_config0.md (FETCH_SIZE 8,237.0 KiB x 2.000
+        # + WRITE_SIZE 4,608.0 KiB x 1.000, the read / write kernels'
+        # factors) = 1.00429 per algorithmic byte.
         _hbm((in_bytes + q_bytes) / (ms_q * 1e-3) / 1e9,
-             "affine_quantize_kernel<128> (K and V in one launch)", in_bytes + q_bytes, ms_q),
+             "affine_quantize_kernel<128> (K and V in one launch)", in_bytes + q_bytes, ms_q,
+             int((in_bytes + q_bytes) * 1.00429)),
         {"dequantize": {"ms": round(ms_d, 5), "gbps": round((q_bytes + in_bytes) / (ms_d * 1e-3) / 1e9, 1)},
          "affine_rotation": {"ms": round(ms_r, 5),
                              "tokens_per_s": round(S / (ms_r * 1e-3), 1),
