@@ -57,6 +57,10 @@ def parse():
                          "single-sequence decode; layers: config 3's 30-layer stack (chunked "
                          "prefill, then decode steps); prefix: config 4's shared-prefix decode; "
                          "sparse: config 2's shape with page-sparse decode")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="decode steps append with the quantize kernel and then attend (two "
+                         "launches) instead of the decode kernel quantizing the new token "
+                         "itself (tqkv_decode_attend_affine_append / tqkv_cache_append_decode)")
     ap.add_argument("--decode-steps", type=int, default=512,
                     help="decode steps of the layers workload (config 3: 512)")
     return ap.parse_args()
@@ -123,8 +127,20 @@ def main():
     vp = tuple(a.ptr for a in cache["v"])
     ev = [(hip.event(), hip.event()) for _ in range(steps)]
 
+    fused = not args.two_launch
+
     def step(i, events=None):
         pos = N + i  # the new token's row
+        if fused:  # the decode kernel quantizes the new token into row pos itself
+            seg = T.affine_seg(kp, vp, cap, pos)
+            if events:
+                hip.record(events[0], stream)
+            T.decode_attend_affine_append(q.ptr, B, H, HKV, D, GS, BITS, BITS, scale, [seg],
+                                          newk.ptr, newv.ptr, kp + vp, cap, pos, out.ptr,
+                                          ws.ptr, ws_bytes, stream)
+            if events:
+                hip.record(events[1], stream)
+            return
         T.affine_quantize_kv(newk.ptr, newv.ptr, slabs, 1, D, GS, BITS, BITS, kp, vp, cap, pos,
                              stream)
         seg = T.affine_seg(kp, vp, cap, pos + 1)
@@ -162,6 +178,8 @@ def main():
     row_bytes = words * 4 + 2 * groups * 2  # packed codes + bf16 scales + bf16 biases
     ctx_avg = N + settle + warmup + (steps - 1) / 2.0 + 1
     alg_bytes = 2 * slabs * ctx_avg * row_bytes + 2 * B * H * D * 2  # K+V, then Q in + O out
+    if fused:  # the launch also reads the new bf16 rows and writes their codes
+        alg_bytes += 2 * slabs * (D * 2 + row_bytes)
     achieved = alg_bytes / (dec_avg_ms * 1e-3) / 1e9
     ms_per_step = total_ms / steps
     # HBM bytes per decode launch: the two counter passes recorded in
@@ -201,7 +219,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "BASELINE config 2: batched decode over a 3-bit affine cache "
-                        "(append 1 token + fused decode attention per step)",
+                        "(append 1 token + fused decode attention per step" +
+                        (", one launch: the decode kernel quantizes the new token)" if fused
+                         else ", two launches)"),
             "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N,
             "bits_k": BITS, "bits_v": BITS, "group_size": GS,
             "layers": 1,
@@ -575,13 +595,23 @@ def decode1_main(T, hip, args):
     ws = T.DeviceArray((wsb,), np.uint8)
     kp, vp = tuple(a.ptr for a in kc), tuple(a.ptr for a in vc)
     pos = [N]
+    fused = not args.two_launch
 
     def append():
+        if fused:  # the decode launch quantizes the token itself
+            return
         T.affine_quantize_kv(nk.ptr, nv.ptr, slabs, 1, D, GS, BITS, BITS, kp, vp, cap, pos[0],
                              stream)
         pos[0] += 1
 
     def decode():
+        if fused:
+            seg = T.affine_seg(kp, vp, cap, pos[0])
+            T.decode_attend_affine_append(q.ptr, B, H, HKV, D, GS, BITS, BITS, D ** -0.5, [seg],
+                                          nk.ptr, nv.ptr, kp + vp, cap, pos[0], out.ptr, ws.ptr,
+                                          wsb, stream)
+            pos[0] += 1
+            return
         seg = T.affine_seg(kp, vp, cap, pos[0])
         T.decode_attend_affine(q.ptr, B, H, HKV, D, GS, BITS, BITS, D ** -0.5, [seg], out.ptr,
                                ws.ptr, wsb, stream)
@@ -610,9 +640,11 @@ def decode1_main(T, hip, args):
         args, "f32",
         {"workload": "BASELINE config 1: 1 sequence, 32/8 heads, D=128, 4-bit gs64, 8,192 "
                      "context, 256 steps each appending one token",
-         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N, "steps": steps},
+         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N, "steps": steps,
+         "launches_per_step": 2 if fused else 3},
         _hbm(alg / (dec_ms * 1e-3) / 1e9, T.decode_kernel_name(H, HKV, D, GS, BITS, BITS) +
-             " split + merge", alg, dec_ms),
+             (" split (quantizing the new token) + merge" if fused else " split + merge"),
+             alg, dec_ms),
         {"decode_us": round(dec_ms * 1e3, 2), "step_us": round(step_ms * 1e3, 2)}, settle, steps)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
@@ -655,7 +687,21 @@ def prefix_main(T, hip, args):
     skp, svp = tuple(a.ptr for a in sk), tuple(a.ptr for a in sv)
     pos = [S0]
 
+    fused = not args.two_launch
+
     def step(events=None):
+        if fused:  # the suffix decode launch quantizes the token itself
+            segs = [T.affine_seg(pkp, pvp, P, P, shared=True),
+                    T.affine_seg(skp, svp, cap, pos[0])]
+            if events:
+                hip.record(events[0], stream)
+            T.decode_attend_affine_append(q.ptr, B, H, HKV, D, GS, BK, BV, D ** -0.5, segs,
+                                          nk.ptr, nv.ptr, skp + svp, cap, pos[0], out.ptr,
+                                          ws.ptr, wsb, stream)
+            if events:
+                hip.record(events[1], stream)
+            pos[0] += 1
+            return
         T.affine_quantize_kv(nk.ptr, nv.ptr, B * HKV, 1, D, GS, BK, BV, skp, svp, cap, pos[0],
                              stream)
         pos[0] += 1
@@ -698,7 +744,7 @@ def prefix_main(T, hip, args):
         {"workload": "BASELINE config 4: 8 sequences sharing a 65,536-token prefix plus 4,096 "
                      "own tokens, 32/8 heads, D=128, K 8-bit / V 4-bit gs64, 128 decode steps",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "prefix": P, "suffix": S0,
-         "bits_k": BK, "bits_v": BV, "group_size": GS},
+         "bits_k": BK, "bits_v": BV, "group_size": GS, "launches_per_step": 3 if fused else 4},
         _hbm(unique / (dec_ms * 1e-3) / 1e9,
              "shared-prefix decode call: prefix pass (prefill kernel, f16 tiles) + suffix "
              "decode (" + T.decode_kernel_name(H, HKV, D, GS, BK, BV) + ") + merge", unique, dec_ms),
@@ -860,10 +906,15 @@ def layers_main(T, hip, args):
     wsb = T.decode_workspace_size(B, H, HKV, D, L + args.decode_steps + 64)
     ws = T.DeviceArray((wsb,), np.uint8)
 
+    fused = not args.two_launch
+
     def step():
         for c in caches:
-            c.append(nk.ptr, nv.ptr, 1, stream)
-            c.decode_attend(q.ptr, H, 1.0, out.ptr, ws.ptr, wsb, stream)
+            if fused:  # one decode launch (+ merge) quantizes the token itself
+                c.append_decode(nk.ptr, nv.ptr, q.ptr, H, 1.0, out.ptr, ws.ptr, wsb, stream)
+            else:
+                c.append(nk.ptr, nv.ptr, 1, stream)
+                c.decode_attend(q.ptr, H, 1.0, out.ptr, ws.ptr, wsb, stream)
 
     settle = 16 if args.settle is None else max(0, args.settle)
     for _ in range(settle + args.warmup):
@@ -883,7 +934,8 @@ def layers_main(T, hip, args):
                      "32/8 heads, D=128, 4-bit gs64; 16,384-token prefill in 2,048 chunks "
                      "(MFMA chunk attention), then decode steps over all layers",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "layers": n_layers,
-         "prompt": L, "chunk": CH, "window": W, "decode_steps": steps},
+         "prompt": L, "chunk": CH, "window": W, "decode_steps": steps,
+         "append": "in the decode kernel" if fused else "own launch"},
         _hbm(alg / (step_ms * 1e-3) / 1e9, "30 x (append + decode) per step", alg, step_ms),
         {"prefill_ms": round(prefill_ms, 2),
          "prefill_tokens_per_s": round(B * L / (prefill_ms * 1e-3), 1),

@@ -144,6 +144,28 @@ int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32
                                   size_t workspace_bytes, tqkv_stream stream);
 
 /*
+ * A decode step's append and attention in one kernel: the reference's
+ * update_and_fetch of one token followed by quantized_decode_attention over
+ * the fetched view (gemma4_moe.rs:4081, 4125). Same result as
+ * tqkv_affine_quantize_kv(k, v, B * H_kv slabs, s = 1, ..., dst_cap,
+ * dst_row) and then tqkv_decode_attend_affine over `segs` plus the new row:
+ * the new K and V rows (bf16 [B, H_kv, 1, D], 16-byte aligned) are quantized
+ * bit-exactly as that call would, written at row dst_row of every slab of
+ * the destination buffers ([B, H_kv, dst_cap, .]), and enter the softmax as
+ * one more key. `segs` must not hold that row (they may hold no rows at all).
+ * Layouts of the MFMA decode kernel only (group_size 64, D in {64, 128, 256},
+ * tqkv_decode_kernel_name() == "mfma"); TQKV_EUNSUPPORTED otherwise, and the
+ * caller appends and attends in two calls.
+ */
+int32_t tqkv_decode_attend_affine_append(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
+    int32_t bits_k, int32_t bits_v, float scale, const tqkv_affine_seg* segs, int32_t n_segs,
+    const uint16_t* k, const uint16_t* v, uint32_t* k_packed, uint16_t* k_scales,
+    uint16_t* k_biases, uint32_t* v_packed, uint16_t* v_scales, uint16_t* v_biases,
+    int64_t dst_cap, int64_t dst_row, uint16_t* out, void* workspace, size_t workspace_bytes,
+    tqkv_stream stream);
+
+/*
  * Page-sparse decode over an affine cache, after sdpa_page_sparse
  * (native_attention.rs:210-329) and PageDigest (native_cache.rs:352-445).
  * Pages are 64 rows; a cache segment's buffers are [B, H_kv, cap, .].
@@ -444,6 +466,19 @@ int32_t tqkv_cache_attach_prefix(tqkv_cache* cache, const tqkv_cache* prefix);
 int32_t tqkv_cache_decode_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
                                  float scale, uint16_t* out, void* workspace,
                                  size_t workspace_bytes, tqkv_stream stream);
+
+/*
+ * One decode step: tqkv_cache_append of one token (k, v: bf16 [B, H_kv, 1,
+ * dim]) then tqkv_cache_decode_attend (the reference's update_and_fetch +
+ * quantized_decode_attention, gemma4_moe.rs:4081, 4125). On an affine cache
+ * whose layout the MFMA decode kernel serves, the new token is quantized
+ * inside the decode kernel (tqkv_decode_attend_affine_append): one launch
+ * fewer, the same cache bytes. Otherwise the two calls. Growth and
+ * rotation follow tqkv_cache_append exactly.
+ */
+int32_t tqkv_cache_append_decode(tqkv_cache* cache, const uint16_t* k, const uint16_t* v,
+                                 const uint16_t* q, int32_t H, float scale, uint16_t* out,
+                                 void* workspace, size_t workspace_bytes, tqkv_stream stream);
 
 /*
  * Prefill-chunk attention over the last fetched view (plus the attached

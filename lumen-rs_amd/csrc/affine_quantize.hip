@@ -1,23 +1,17 @@
 // Quantize-on-append in MLX's affine format, bit-exact with its Metal kernel,
 // and the matching dequantize.
 //
-// Layout of the work: each lane owns EPL = 16 consecutive elements of a row,
-// read as two 16-byte loads, so a row takes dim / EPL lanes and a
-// wavefront holds several rows (8 at dim 128); a 256-thread
-// workgroup takes a block of rows of one tensor, and the grid covers K and
-// V in one launch. A group's lanes are adjacent, so its min and max are a
-// butterfly over gs / EPL lanes. Each lane packs every 8 codes into a
-// 64-bit chunk (8 x bits bits), the chunks go through LDS, and each output word is
-// cut from the one or two chunks it overlaps: LSB-first u32 words for every
-// width, including those whose codes straddle words (3, 5, 6 bits).
-//
-// Arithmetic follows MLX's affine_quantize exactly (see the oracle's
-// affine.cpp for the statement): f32 throughout, IEEE division (hipcc's
-// default correctly rounded divide), roundf = half away from zero, bf16
-// round-to-nearest-even storage of scale and bias, codes from the unrounded
-// f32 scale and bias. The reference's recorded digests pin this at 4 bits /
-// gs64 (golden_tests.rs:425-463).
-#include "common.hpp"
+// Layout of the work: each lane owns 16 consecutive elements of a row, read
+// as two 16-byte loads, so a row takes dim / 16 lanes and a wavefront holds
+// several rows (8 at dim 128); a 256-thread workgroup takes a block of rows
+// of one tensor, and the grid covers K and V in one launch. A group's lanes
+// are adjacent, so its min and max are a butterfly over gs / 16 lanes. Each
+// lane packs every 8 codes into a 64-bit chunk (8 x bits bits), the chunks go
+// through LDS, and each output word is cut from the one or two chunks it
+// overlaps: LSB-first u32 words for every width, including those whose codes
+// straddle words (3, 5, 6 bits). The per-lane arithmetic (affine_quantize.hpp)
+// is MLX's exactly.
+#include "affine_quantize.hpp"
 
 namespace tqkv {
 namespace {
@@ -74,74 +68,24 @@ __global__ __launch_bounds__(kQThreads) void affine_quantize_kernel(const QArgs 
     const int64_t dst = int64_t(slab) * a.dst_cap + a.dst_start + j;
 
     float v[EPL];
-    const uint16_t* xr = t.x + rr * D + lir * EPL;
-#pragma unroll
-    for (int h = 0; h < EPL / 8; ++h) {
-      const uint4 w = *reinterpret_cast<const uint4*>(xr + 8 * h);
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[8 * h + 2 * e] = __uint_as_float(ws[e] << 16);
-        v[8 * h + 2 * e + 1] = __uint_as_float(ws[e] & 0xffff0000u);
-      }
-    }
-
-    // The Metal kernel starts w_min at the dtype's max and w_max at 0.
-    float w_min = __uint_as_float(0x7f7f0000u);
-    float w_max = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      w_min = fminf(w_min, v[e]);
-      w_max = fmaxf(w_max, v[e]);
-    }
-    const int lpg = a.gs / EPL;  // lanes a group: a power of two, <= LPR
-    for (int off = 1; off < lpg; off <<= 1) {
-      w_min = fminf(w_min, __shfl_xor(w_min, off, kWave));
-      w_max = fmaxf(w_max, __shfl_xor(w_max, off, kWave));
-    }
-
+    aq::load_lane(t.x + rr * D + lir * EPL, v);
     const int bits = t.bits;
-    const float n_bins = float((1 << bits) - 1);
-    float scale = fmaxf((w_max - w_min) / n_bins, 1e-7f);
-    const bool side = fabsf(w_min) > fabsf(w_max);
-    scale = side ? scale : -scale;
-    const float edge = side ? w_min : w_max;
-    const float q0 = roundf(edge / scale);
-    const bool at_zero = q0 == 0.0f;
-    scale = at_zero ? scale : edge / q0;
-    const float bias = at_zero ? 0.0f : edge;
-
+    const aq::LaneCodes qc = aq::quantize_lane(v, a.gs, bits);
+    const int lpg = a.gs / EPL;  // lanes a group: a power of two, <= LPR
     const int groups = D / a.gs;
     if (live && lir % lpg == 0) {
       const int g = lir / lpg;
-      t.scales[dst * groups + g] = f32_to_bf16(scale);
-      t.biases[dst * groups + g] = f32_to_bf16(bias);
+      t.scales[dst * groups + g] = f32_to_bf16(qc.scale);
+      t.biases[dst * groups + g] = f32_to_bf16(qc.bias);
     }
 #pragma unroll
-    for (int h = 0; h < S::kUnits; ++h) {
-      uint64_t c = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float q = fminf(roundf((v[8 * h + e] - bias) / scale), n_bins);
-        const uint32_t code = q <= 0.0f ? 0u : uint32_t(q);
-        c |= uint64_t(code) << (bits * e);
-      }
-      ch[lir * S::kUnits + h] = c;
-    }
+    for (int h = 0; h < S::kUnits; ++h) ch[lir * S::kUnits + h] = qc.chunk[h];
     __syncthreads();
 
-    // Output word w of the row covers bits [32 w, 32 w + 32): chunk k =
-    // 32 w / (8 bits) from bit `off`, and chunk k + 1 when it runs past.
-    const int ub = 8 * bits;
     const int words = D * bits / 32;
     if (live) {
       uint32_t* out = t.packed + dst * words;
-      for (int w = lir; w < words; w += LPR) {
-        const int bit0 = 32 * w, k = bit0 / ub, off = bit0 - k * ub;
-        uint64_t word = ch[k] >> off;
-        if (off + 32 > ub) word |= ch[k + 1] << (ub - off);
-        out[w] = uint32_t(word);
-      }
+      for (int w = lir; w < words; w += LPR) out[w] = aq::packed_word(ch, w, bits);
     }
     __syncthreads();  // the chunks are reused by the next block
   }

@@ -772,6 +772,68 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* c, const uint16_t* q, int32_t
                                    stream);
 }
 
+int32_t tqkv_cache_append_decode(tqkv_cache* c, const uint16_t* k, const uint16_t* v,
+                                 const uint16_t* q, int32_t H, float scale, uint16_t* out,
+                                 void* workspace, size_t workspace_bytes, tqkv_stream stream) {
+  if (!c || !k || !v || !q || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  auto two_calls = [&]() -> int32_t {
+    if (int32_t rc = tqkv_cache_append(c, k, v, 1, nullptr, stream)) return rc;
+    return tqkv_cache_decode_attend(c, q, H, scale, out, workspace, workspace_bytes, stream);
+  };
+  const tqkv_cache_config& g = c->cfg;
+  if (g.kind != TQKV_CACHE_AFFINE || g.k_dim != g.v_dim || H <= 0 || H % g.kv_heads != 0)
+    return two_calls();
+  // TQKV_FUSED_APPEND=0 keeps the two calls (tests compare the paths).
+  const char* env = getenv("TQKV_FUSED_APPEND");
+  if (env && strcmp(env, "0") == 0) return two_calls();
+  if (strcmp(tqkv_decode_kernel_name(H, g.kv_heads, g.k_dim, g.group_size, g.bits_k, g.bits_v),
+             "mfma") != 0 ||
+      (reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) % 16 != 0)
+    return two_calls();
+  cacheplan::State next = c->st;
+  const cacheplan::Plan p = cacheplan::update(next, c->pc, 1);
+  // The attended rows are the new view without the new row: [0, view - 1)
+  // when the row lands last, else (a ring written in place) the rows either
+  // side of it, which with an attached prefix would be a third segment.
+  const bool has_prefix = c->prefix && c->base_offset > 0;
+  const bool last = p.write_at == p.view - 1;
+  if (p.write_at < 0 || p.write_at >= p.view || (!last && has_prefix)) return two_calls();
+  const int64_t old_len = c->st.has ? c->st.len : 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (int32_t rc = execute(c, p, old_len, st)) return rc;
+  c->st = next;
+  c->view_n = p.view;
+  tqkv_affine_seg segs[2];
+  int n = affine_segments(c, segs);
+  tqkv_affine_seg& own = segs[n - 1];  // the cache's own rows (view >= 1)
+  if (last) {
+    own.n -= 1;
+  } else {
+    // [0, write_at) and [write_at + 1, view) of the same slabs.
+    const int64_t r1 = p.write_at + 1;
+    const int kr = g.k_dim * g.bits_k / 32, vr = g.v_dim * g.bits_v / 32;
+    const int ng = g.k_dim / g.group_size;
+    tqkv_affine_seg hi = own;
+    hi.k_packed += r1 * kr;
+    hi.k_scales += r1 * ng;
+    hi.k_biases += r1 * ng;
+    hi.v_packed += r1 * vr;
+    hi.v_scales += r1 * ng;
+    hi.v_biases += r1 * ng;
+    hi.n = p.view - r1;
+    own.n = p.write_at;
+    segs[n++] = hi;
+  }
+  if (c->cur[0].cap != c->cur[3].cap)
+    return fail(TQKV_EINVAL_ARG, "K and V buffers of different capacity");
+  return tqkv_decode_attend_affine_append(
+      q, g.batch, H, g.kv_heads, g.k_dim, g.group_size, g.bits_k, g.bits_v, scale, segs, n, k, v,
+      reinterpret_cast<uint32_t*>(c->cur[0].ptr), reinterpret_cast<uint16_t*>(c->cur[1].ptr),
+      reinterpret_cast<uint16_t*>(c->cur[2].ptr), reinterpret_cast<uint32_t*>(c->cur[3].ptr),
+      reinterpret_cast<uint16_t*>(c->cur[4].ptr), reinterpret_cast<uint16_t*>(c->cur[5].ptr),
+      c->cur[0].cap, p.write_at, out, workspace, workspace_bytes, stream);
+}
+
 int32_t tqkv_cache_prefill_attend(const tqkv_cache* c, const uint16_t* q, int32_t H, int32_t L,
                                   float scale, int64_t window, uint16_t* out,
                                   tqkv_stream stream) {

@@ -211,12 +211,26 @@ extern "C" size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv,
   return size_t(B) * H * ns * (size_t(D) + 2) * sizeof(float);
 }
 
-extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H,
-                                             int32_t H_kv, int32_t D, int32_t group_size,
-                                             int32_t bits_k, int32_t bits_v, float scale,
-                                             const tqkv_affine_seg* segs, int32_t n_segs,
-                                             uint16_t* out, void* workspace,
-                                             size_t workspace_bytes, tqkv_stream stream) {
+namespace {
+
+// The cache rows a fused append writes (tqkv_decode_attend_affine_append).
+struct AppendDst {
+  const uint16_t* k;
+  const uint16_t* v;
+  uint32_t* kw;
+  uint16_t* ks;
+  uint16_t* kb;
+  uint32_t* vw;
+  uint16_t* vs;
+  uint16_t* vb;
+  int64_t cap, row;
+};
+
+int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D,
+                      int32_t group_size, int32_t bits_k, int32_t bits_v, float scale,
+                      const tqkv_affine_seg* segs, int32_t n_segs, const AppendDst* app,
+                      uint16_t* out, void* workspace, size_t workspace_bytes,
+                      tqkv_stream stream) {
   if (!q || !out || !segs) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0)
     return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d", B, H, H_kv);
@@ -252,7 +266,33 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
   if (n_segs == 1) a.seg[1] = a.seg[0];
   a.n0 = segs[0].n;
   a.total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
-  if (a.total <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
+  if (app) {
+    // Only the MFMA kernels quantize in place.
+    KernelFn mf = nullptr;
+    switch (D) {
+      case 64: mf = pick_mfma_d64(bits_k, bits_v, G, group_size); break;
+      case 128: mf = pick_mfma_d128(bits_k, bits_v, G, group_size); break;
+      case 256: mf = pick_mfma_d256(bits_k, bits_v, G, group_size); break;
+    }
+    if (fn != mf)
+      return fail(TQKV_EUNSUPPORTED, "fused append needs the MFMA decode kernel (D=%d bits %d/%d "
+                  "gqa=%d gs=%d)", D, bits_k, bits_v, G, group_size);
+    if (app->row < 0 || app->row >= app->cap)
+      return fail(TQKV_EINVAL_SHAPE, "append row %lld of %lld", (long long)app->row,
+                  (long long)app->cap);
+    a.app_k = app->k;
+    a.app_v = app->v;
+    a.app_kw = app->kw;
+    a.app_ks = app->ks;
+    a.app_kb = app->kb;
+    a.app_vw = app->vw;
+    a.app_vs = app->vs;
+    a.app_vb = app->vb;
+    a.app_cap = app->cap;
+    a.app_row = app->row;
+  } else if (a.total <= 0) {
+    return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
+  }
 
   const int waves = waves_for_shape(G, D);
   a.out = out;
@@ -277,6 +317,10 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
     s.total = S;
     int sp_s = 0;
     if (S > 0) plan_splits(B, H_kv, waves, S, &sp_s, &s.split_len);
+    if (app && sp_s == 0) {  // the new row needs a suffix launch
+      sp_s = 1;
+      s.split_len = 64;
+    }
     const int n_part = sp_p + sp_s;
     const size_t need = size_t(B) * H * n_part * (size_t(D) + 2) * sizeof(float);
     void* ws = workspace;
@@ -294,7 +338,7 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
                                                      po, pm, pl, st))
       return rc;
     if (sp_s > 0) {
-      KernelFn sfn = pick(D, bits_k, bits_v, G, group_size, S);
+      KernelFn sfn = app ? fn : pick(D, bits_k, bits_v, G, group_size, S);
       s.n_splits = sp_s;
       s.split_base = sp_p;
       s.n_part = n_part;
@@ -337,6 +381,35 @@ extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32
     TQKV_LAUNCHED();
   }
   return ok();
+}
+
+}  // namespace
+
+extern "C" int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H,
+                                             int32_t H_kv, int32_t D, int32_t group_size,
+                                             int32_t bits_k, int32_t bits_v, float scale,
+                                             const tqkv_affine_seg* segs, int32_t n_segs,
+                                             uint16_t* out, void* workspace,
+                                             size_t workspace_bytes, tqkv_stream stream) {
+  return decode_affine(q, B, H, H_kv, D, group_size, bits_k, bits_v, scale, segs, n_segs,
+                       nullptr, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int32_t tqkv_decode_attend_affine_append(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
+    int32_t bits_k, int32_t bits_v, float scale, const tqkv_affine_seg* segs, int32_t n_segs,
+    const uint16_t* k, const uint16_t* v, uint32_t* k_packed, uint16_t* k_scales,
+    uint16_t* k_biases, uint32_t* v_packed, uint16_t* v_scales, uint16_t* v_biases,
+    int64_t dst_cap, int64_t dst_row, uint16_t* out, void* workspace, size_t workspace_bytes,
+    tqkv_stream stream) {
+  if (!k || !v || !k_packed || !k_scales || !k_biases || !v_packed || !v_scales || !v_biases)
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) % 16 != 0)
+    return fail(TQKV_EINVAL_ARG, "new K/V rows must be 16-byte aligned");
+  const AppendDst app{k, v, k_packed, k_scales, k_biases, v_packed, v_scales, v_biases,
+                      dst_cap, dst_row};
+  return decode_affine(q, B, H, H_kv, D, group_size, bits_k, bits_v, scale, segs, n_segs, &app,
+                       out, workspace, workspace_bytes, stream);
 }
 
 // Decode over chosen 64-row pages of one cache segment plus its undigested

@@ -74,6 +74,20 @@ struct Args {
   // pages[(b * H_kv + kvh) * n_pages + i] (64 rows each, ascending).
   const int32_t* pages;
   int n_pages;
+  // Append fused into the decode (the MFMA kernels; app_k null: none): the
+  // new token's bf16 K and V rows ([B, H_kv, D] each) are quantized by the
+  // last wavefront of each unit's last split, written into the cache buffers
+  // at row app_row of the unit's slab (app_cap rows a slab), and attended as
+  // one more key read back from LDS. The segments do not hold that row.
+  const uint16_t* app_k;
+  const uint16_t* app_v;
+  uint32_t* app_kw;
+  uint16_t* app_ks;
+  uint16_t* app_kb;
+  uint32_t* app_vw;
+  uint16_t* app_vs;
+  uint16_t* app_vb;
+  int64_t app_cap, app_row;
   float* part_o;  // [B, H, n_part, D]
   float* part_m;  // [B, H, n_part]
   float* part_l;  // [B, H, n_part]

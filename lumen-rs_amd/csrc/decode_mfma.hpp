@@ -33,6 +33,7 @@
 // group a multiple of D/8; plans for (bits_k, D/4) and (bits_v, D/8).
 #pragma once
 
+#include "affine_quantize.hpp"
 #include "decode_affine.hpp"
 
 namespace tqkv {
@@ -237,6 +238,51 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   }
 #pragma unroll
   for (int hh = 0; hh < HPL; ++hh) hl[hh] = (4 * kj + hh * RPH) / NG;
+
+  // ---- fused append: the last wavefront of the unit's last split quantizes
+  // the new K row (lanes [0, 32)) and V row (lanes [32, 64)), D / 16 lanes a
+  // row, writes both into the cache and keeps them in LDS for one more key
+  // step after its range. LDS accesses of one wavefront complete in order,
+  // so its lanes read what its lanes wrote without a workgroup barrier.
+  __shared__ uint64_t s_ach[2][D / 8];
+  __shared__ uint32_t s_akw[KROW], s_avw[VROW];
+  __shared__ uint16_t s_aks[NG], s_akb[NG], s_avs[NG], s_avb[NG];
+  const bool app = a.app_k != nullptr && split == int(gridDim.x) - 1 && wave == kWaves - 1;
+  if (app) {
+    constexpr int LPR = D / aq::kLaneElems;
+    const int tv = lane >> 5, lir = lane & 31;
+    const int li = lir < LPR ? lir : LPR - 1;  // idle lanes repeat a live one
+    const int64_t slab = int64_t(b) * a.H_kv + kvh;
+    float x[aq::kLaneElems];
+    aq::load_lane((tv ? a.app_v : a.app_k) + slab * D + li * aq::kLaneElems, x);
+    const aq::LaneCodes qc = aq::quantize_lane(x, a.gs, tv ? BV : BK);
+    const int lpg = a.gs / aq::kLaneElems;
+    const int64_t dst = slab * a.app_cap + a.app_row;
+    if (lir < LPR) {
+      if (lir % lpg == 0) {
+        const int g = lir / lpg;
+        const uint16_t sc = f32_to_bf16(qc.scale), bi = f32_to_bf16(qc.bias);
+        (tv ? a.app_vs : a.app_ks)[dst * NG + g] = sc;
+        (tv ? a.app_vb : a.app_kb)[dst * NG + g] = bi;
+        (tv ? s_avs : s_aks)[g] = sc;
+        (tv ? s_avb : s_akb)[g] = bi;
+      }
+      s_ach[tv][2 * lir] = qc.chunk[0];
+      s_ach[tv][2 * lir + 1] = qc.chunk[1];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    for (int w = lane; w < KROW; w += kWave) {
+      const uint32_t word = aq::packed_word(s_ach[0], w, BK);
+      a.app_kw[dst * KROW + w] = word;
+      s_akw[w] = word;
+    }
+    for (int w = lane; w < VROW; w += kWave) {
+      const uint32_t word = aq::packed_word(s_ach[1], w, BV);
+      a.app_vw[dst * VROW + w] = word;
+      s_avw[w] = word;
+    }
+  }
 
   // ---- this wavefront's keys
   const int64_t t_begin = int64_t(split) * a.split_len;
@@ -534,6 +580,36 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       score(kf_, kt < left, masked, pz, pt);
       values(vf_, pt);
     }
+  }
+  if (app) {
+    // The appended token: a masked step whose one key (token 0) is the new
+    // row, every lane reading its share from LDS.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    KBuf kf_;
+    VBuf vf_;
+    Pend pz, pt;
+#pragma unroll
+    for (int h = 0; h < G; ++h) pz.p0[h] = pz.p1[h] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KW; ++i) kf_.kw[i] = s_akw[kj * KW + i];
+    const int si = (4 * kj) % NG;
+    if constexpr (NSC == 1) {
+      kf_.ks[0] = s_aks[si];
+      kf_.kb[0] = s_akb[si];
+    } else {
+#pragma unroll
+      for (int w = 0; w < NSW; ++w) {
+        kf_.ks[w] = uint32_t(s_aks[si + 2 * w]) | uint32_t(s_aks[si + 2 * w + 1]) << 16;
+        kf_.kb[w] = uint32_t(s_akb[si + 2 * w]) | uint32_t(s_akb[si + 2 * w + 1]) << 16;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VW; ++i) vf_.vw[0][i] = vf_.vw[1][i] = s_avw[vc * VW + i];
+    vf_.vs[0] = vf_.vs[1] = s_avs[vgrp];
+    vf_.vb[0] = vf_.vb[1] = s_avb[vgrp];
+    score(kf_, kt == 0, std::integral_constant<bool, true>{}, pz, pt);
+    values(vf_, pt);
   }
 
   // ---- merge: undo the code scale, add the bias term, sum the token pairs

@@ -86,6 +86,9 @@ _SIGS = {
     "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
+    "tqkv_decode_attend_affine_append": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
+                                               ctypes.POINTER(AffineSeg), I32, P, P, P, P, P,
+                                               P, P, P, I64, I64, P, P, SZ, P]),
     "tqkv_prefill_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, I32, F32,
                                          ctypes.POINTER(AffineSeg), I32, I64, I64, I32, I64, P,
                                          P]),
@@ -139,6 +142,7 @@ _SIGS = {
     "tqkv_cache_attach_prefix": (I32, [P, P]),
     "tqkv_cache_set_tables": (I32, [P, P, P]),
     "tqkv_cache_decode_attend": (I32, [P, P, I32, F32, P, P, SZ, P]),
+    "tqkv_cache_append_decode": (I32, [P, P, P, P, I32, F32, P, P, SZ, P]),
     "tqkv_cache_prefill_attend": (I32, [P, P, I32, I32, F32, I64, P, P]),
     "tqkv_read_probe": (I32, [P, SZ, P, SZ, P, P]),
     "tqkv_lkv_export": (I32, [P, I32, ctypes.POINTER(LkvInfo), P, SZ, ctypes.POINTER(SZ), P]),
@@ -349,6 +353,18 @@ def decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, out,
                                           len(segs), out, workspace, workspace_bytes, stream))
 
 
+def decode_attend_affine_append(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, k, v, dst,
+                                dst_cap, dst_row, out, workspace=None, workspace_bytes=0,
+                                stream=None):
+    """Quantize the new rows k, v into dst (six device pointers: K packed,
+    scales, biases, V packed, scales, biases) at row dst_row of every slab
+    and attend over segs plus that row, in one kernel."""
+    arr = (AffineSeg * max(len(segs), 1))(*segs)
+    check(lib().tqkv_decode_attend_affine_append(q, B, H, H_kv, D, gs, bits_k, bits_v, scale,
+                                                 arr, len(segs), k, v, *dst, dst_cap, dst_row,
+                                                 out, workspace, workspace_bytes, stream))
+
+
 def prefill_attend_affine(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, segs, out,
                           q_start=0, k_start=0, causal=True, window=-1, stream=None):
     """Chunk attention: query row l at q_start + l, key k at k_start + k."""
@@ -550,6 +566,12 @@ class Cache:
 
     def decode_attend(self, q, H, scale, out, workspace=None, workspace_bytes=0, stream=None):
         check(lib().tqkv_cache_decode_attend(self.h, q, H, scale, out, workspace,
+                                             workspace_bytes, stream))
+
+    def append_decode(self, k, v, q, H, scale, out, workspace=None, workspace_bytes=0,
+                      stream=None):
+        """One decode step: append one token, attend over the new view."""
+        check(lib().tqkv_cache_append_decode(self.h, k, v, q, H, scale, out, workspace,
                                              workspace_bytes, stream))
 
     def prefill_attend(self, q, H, L, scale, out, window=-1, stream=None):
