@@ -106,6 +106,32 @@ __device__ __forceinline__ float row_max16(float v) {
   return v;
 }
 
+// Sum over the 16 lanes of a DPP row, every lane getting it (the pairings
+// of row_max16).
+__device__ __forceinline__ float row_sum16(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x),
+                                                      decltype(ctrl)::value, 0xf, 0xf, true));
+  };
+  v += dpp(v, std::integral_constant<int, 0xb1>{});
+  v += dpp(v, std::integral_constant<int, 0x4e>{});
+  v += dpp(v, std::integral_constant<int, 0x141>{});
+  v += dpp(v, std::integral_constant<int, 0x140>{});
+  return v;
+}
+
+// The wavefront's max / sum from row-reduced values (every lane of a row
+// holding its row's result), as a wave-uniform value: one readlane a row.
+__device__ __forceinline__ float rl(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ float rows_max(float v) {
+  return fmaxf(fmaxf(rl(v, 0), rl(v, 16)), fmaxf(rl(v, 32), rl(v, 48)));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
@@ -155,7 +181,12 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   const int ve0 = vc * EV;
   const int vgrp = ve0 / GS;
 
-  // ---- queries: f32 in LDS, then per-head exponents and group sums
+  // ---- queries: f32 in LDS, then per-head exponents and group sums. A
+  // group is 64 channels, so lane l reads channel l of every group, and the
+  // G * (NG + 1) reductions run side by side (DPP within rows of 16 lanes,
+  // then one readlane a row): their results are wave-uniform and no
+  // reduction waits on another.
+  static_assert(GS == kWave, "a lane a channel of each group");
   __shared__ float s_q[G][D];
   for (int i = threadIdx.x; i < G * D; i += kWave * kWaves) {
     const int h = i / D, d = i % D;
@@ -164,24 +195,28 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   __syncthreads();
   int E[G];
   float qsum[G][NG];
+  {
+    float mx[G];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float mx = 0.0f;
-    float part[NG];
+    for (int h = 0; h < G; ++h) {
+      mx[h] = 0.0f;
 #pragma unroll
-    for (int g = 0; g < NG; ++g) part[g] = 0.0f;
-    for (int d = lane; d < D; d += kWave) {
-      mx = fmaxf(mx, fabsf(s_q[h][d]));
-#pragma unroll
-      for (int g = 0; g < NG; ++g)
-        if (d / GS == g) part[g] += s_q[h][d];
+      for (int g = 0; g < NG; ++g) {
+        const float x = s_q[h][g * kWave + lane];
+        mx[h] = fmaxf(mx[h], fabsf(x));
+        qsum[h][g] = row_sum16(x);
+      }
+      mx[h] = row_max16(mx[h]);
     }
-    mx = wave_max(mx);
-    int ex = 0;
-    if (mx > 0.0f) frexpf(mx, &ex);
-    E[h] = 15 - ex;
 #pragma unroll
-    for (int g = 0; g < NG; ++g) qsum[h][g] = wave_sum(part[g]);
+    for (int h = 0; h < G; ++h) {
+      const float m = rows_max(mx[h]);
+      int ex = 0;
+      if (m > 0.0f) frexpf(m, &ex);
+      E[h] = 15 - ex;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) qsum[h][g] = rows_sum(qsum[h][g]);
+    }
   }
 
   // A operand: row kt = (head, group); this lane supplies the k slots of
@@ -191,6 +226,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     const int m = kt;
     const int h = m / NG, g = m % NG;
     const bool row_ok = m < M;
+    const int hq = row_ok ? h : 0;  // padding rows read a real row, then drop it
     int Eh = 0;
 #pragma unroll
     for (int hh = 0; hh < G; ++hh)
@@ -206,8 +242,12 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
           constexpr int e = lo ? op.lo_e : op.hi_e;
           constexpr int o = lo ? op.lo_o : op.hi_o;
           if constexpr (e >= 0) {
+            // An unconditional read times 0 or 1 (a select would be turned
+            // back into a branch around the read): the reads issue back to
+            // back instead of one wait each.
             const int ch = kj * EK + e;
-            if (row_ok && ch / GS == g) val = __builtin_ldexpf(s_q[h][ch], Eh - o);
+            const float x = s_q[hq][ch];
+            val = __builtin_ldexpf(x, Eh - o) * ((row_ok && ch / GS == g) ? 1.0f : 0.0f);
           }
         }
         v[decltype(S)::value] = _Float16(val);
@@ -620,14 +660,24 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h][vcd.e] = fmaf(acc[h][vcd.e], unscale, bacc[h]);
   });
+  // The 8 token-pair groups (lanes vp = lane / 8) summed as a butterfly:
+  // lane ^ 8 by DPP row_ror:8 within each row of 16, lane ^ 16 and lane ^ 32
+  // by gfx950's v_permlane16_swap / v_permlane32_swap of a value with
+  // itself (the two halves they return are the lane's and its partner's).
+  auto xor_sum = [](float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, true));
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                      false, false);
+    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                      false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+  };
 #pragma unroll
-  for (int off = 8; off < kWave; off <<= 1) {
+  for (int h = 0; h < G; ++h) {
+    l[h] = xor_sum(l[h]);
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      l[h] += __shfl_xor(l[h], off, kWave);
-#pragma unroll
-      for (int e = 0; e < EV; ++e) acc[h][e] += __shfl_xor(acc[h][e], off, kWave);
-    }
+    for (int e = 0; e < EV; ++e) acc[h][e] = xor_sum(acc[h][e]);
   }
 
   __shared__ float s_m[kWaves][G], s_l[kWaves][G];
