@@ -184,10 +184,10 @@ def main():
     ms_per_step = total_ms / steps
     # HBM bytes per decode launch: the two counter passes recorded in
     # profiles/decode_affine_config2.md over the default command's 50 timed
-    # launches (FETCH_SIZE 922,851.2 KiB x 2.000 + WRITE_SIZE 336.0 KiB x
+    # launches (FETCH_SIZE 922,781.7 KiB x 2.000 + WRITE_SIZE 336.0 KiB x
     # 1.000, the factors a 1 GiB read and a 1 GiB write kernel of the same
-    # library give) = 1,890,343,227 B against 1,888,980,992 B algorithmic
-    # (the launch quantizing the new token): 1.000721 per algorithmic byte.
+    # library give) = 1,890,201,014 B against 1,888,980,992 B algorithmic
+    # (the launch quantizing the new token): 1.000646 per algorithmic byte.
     # Counters cannot be read inside this process; other step counts of the
     # same config scale by that ratio (the context differs by a few tokens),
     # other configs and the two-launch step report null.
@@ -195,7 +195,7 @@ def main():
     kernel = ("decode_mfma_kernel<256,3,3,2,4,8>" if kind == "mfma"
               else "decode_affine_kernel<256,3,3,2,32,8>")
     default_shape = (B, N) == (32, 32768)
-    traffic = (int(alg_bytes * 1.000721) if default_shape and kind == "mfma" and fused
+    traffic = (int(alg_bytes * 1.000646) if default_shape and kind == "mfma" and fused
                else None)
     tokens_per_s = B / (ms_per_step * 1e-3)
 
