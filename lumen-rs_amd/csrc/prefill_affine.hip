@@ -2,6 +2,8 @@
 // kernel choice and the launch. The kernel and its design notes are in
 // prefill_affine.hpp.
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 
 #include "prefill_affine.hpp"
 
@@ -21,6 +23,57 @@ KernelFn pick(int D, int bk, int bv, bool h16 = false) {
   }
   return nullptr;
 }
+
+// Dequantize-once: keys [0, total) of every (batch row, KV head), K into kd
+// and V into vd as bf16 rows [B * H_kv, total, D], with mlx::dequantize's
+// arithmetic (bf16(bf16(scale * code) + bias)). Grid: (row chunks, slab,
+// K or V); a thread writes 8 consecutive values of one row (one 16-byte
+// store). Keys [0, n0) come from segment 0, the rest from segment 1.
+template <int D>
+__global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int bk, int bv,
+                                                              uint16_t* kd, uint16_t* vd) {
+  constexpr int kPerRow = D / 8;
+  const uint32_t j = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t row = j / kPerRow;
+  if (row >= uint32_t(a.total)) return;
+  const int c8 = int(j % kPerRow), e0 = 8 * c8;
+  const int slab = int(blockIdx.y), bb = slab / a.H_kv, kv = slab % a.H_kv;
+  const bool isv = blockIdx.z != 0;
+  const bool first = row < uint32_t(a.n0);
+  const Seg& s = a.seg[first ? 0 : 1];
+  const int64_t src = int64_t(bb) * s.b_stride + int64_t(kv) * s.cap +
+                      (first ? row : row - uint32_t(a.n0));
+  const int bits = isv ? bv : bk;
+  const uint32_t* pw = (isv ? s.vw : s.kw) + src * (D * bits / 32);
+  const int groups = D / a.gs, g = e0 / a.gs;
+  const float sc = bf16_to_f32((isv ? s.vs : s.ks)[src * groups + g]);
+  const float bi = bf16_to_f32((isv ? s.vb : s.kb)[src * groups + g]);
+  // The 8 codes start on a byte (8 * bits bits from bit e0 * bits) and, at
+  // every width, end within the next 64 bits of the word holding their
+  // first bit: two loads, the second only when they run into it.
+  const int bit0 = e0 * bits, sh = bit0 % 32;
+  uint64_t win = pw[bit0 / 32];
+  if (sh + 8 * bits > 32) win |= uint64_t(pw[bit0 / 32 + 1]) << 32;
+  win >>= sh;
+  uint32_t out[4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t code = uint32_t(win >> (e * bits)) & ((1u << bits) - 1);
+    const float prod = bf16_to_f32(f32_to_bf16(sc * float(code)));
+    const uint32_t v = f32_to_bf16(prod + bi);
+    if (e % 2 == 0)
+      out[e / 2] = v;
+    else
+      out[e / 2] |= v << 16;
+  }
+  *reinterpret_cast<uint4*>((isv ? vd : kd) + (int64_t(slab) * a.total + row) * D + e0) =
+      uint4{out[0], out[1], out[2], out[3]};
+}
+
+// Row blocks sharing one (batch row, KV head) from which the keys are
+// dequantized once into scratch instead of in every block: the blocks would
+// otherwise repeat the same dequantization, the kernel's VALU-bound part.
+constexpr int64_t kOnceBlocks = 8;
 
 }  // namespace
 }  // namespace prefill
@@ -174,6 +227,45 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   if (grid > 0x7fffffff) return fail(TQKV_EINVAL_SHAPE, "grid too large");
   a.n_blocks = int(blocks);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // TQKV_PREFILL_DEQUANT_ONCE=0 / 1 forces the choice (tests compare them).
+  const char* once_env = getenv("TQKV_PREFILL_DEQUANT_ONCE");
+  const bool once = once_env ? strcmp(once_env, "0") != 0 : blocks >= kOnceBlocks;
+  if (once) {
+    const int64_t slabs = int64_t(B) * H_kv;
+    const size_t need = 2 * size_t(slabs) * size_t(a.total) * size_t(D) * 2;
+    void* ws = nullptr;
+    if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+    uint16_t* kd = static_cast<uint16_t*>(ws);
+    uint16_t* vd = kd + size_t(slabs) * size_t(a.total) * size_t(D);
+    if (slabs > 65535) return fail(TQKV_EINVAL_SHAPE, "B * H_kv = %lld slabs", (long long)slabs);
+    const dim3 dq_grid(unsigned((a.total * (D / 8) + 255) / 256), unsigned(slabs), 2);
+    switch (D) {
+      case 64:
+        hipLaunchKernelGGL(dequantize_rows_kernel<64>, dq_grid, dim3(256), 0, st, a, bits_k,
+                           bits_v, kd, vd);
+        break;
+      case 128:
+        hipLaunchKernelGGL(dequantize_rows_kernel<128>, dq_grid, dim3(256), 0, st, a, bits_k,
+                           bits_v, kd, vd);
+        break;
+      default:
+        hipLaunchKernelGGL(dequantize_rows_kernel<256>, dq_grid, dim3(256), 0, st, a, bits_k,
+                           bits_v, kd, vd);
+        break;
+    }
+    TQKV_LAUNCHED();
+    Args p = a;
+    const uint16_t* none = kd;  // scales and biases: never read at this width
+    p.seg[0] = Seg{reinterpret_cast<const uint32_t*>(kd), none, none,
+                   reinterpret_cast<const uint32_t*>(vd), none, none, a.total,
+                   int64_t(H_kv) * a.total};
+    p.seg[1] = p.seg[0];
+    p.n0 = a.total;
+    hipLaunchKernelGGL(pick(D, kPreBits, kPreBits), dim3(unsigned(grid)), dim3(threads), 0, st,
+                       p);
+    TQKV_LAUNCHED();
+    return ok();
+  }
   hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(threads), 0, st, a);
   TQKV_LAUNCHED();
   return ok();

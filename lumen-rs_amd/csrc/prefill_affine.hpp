@@ -221,21 +221,31 @@ __device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, cons
                   sc1 + r1 * groups,         bi0 + r0 * groups,         bi1 + r1 * groups};
 }
 
+// Width 16 stands for keys dequantized beforehand: rows of D bf16 values
+// (mlx::dequantize's bits, written once per (batch row, KV head) by
+// dequantize_rows_kernel), which the loaders copy into LDS as they are.
+constexpr int kPreBits = 16;
+
 // Loads run `run` of key kk (counted across both segments) of K or V.
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, const Args& a, int kk,
                                            int run) {
   st.ok = kk < a.total;
   if (!st.ok) return;
-  const bool first = kk < a.n0;
-  const uint32_t row = uint32_t(first ? kk : kk - int(a.n0));
-  const uint32_t g = row * uint32_t(D / a.gs) + uint32_t(run * 32) / uint32_t(a.gs);
-  const uint32_t* w = first ? p.w0 : p.w1;
-  const uint16_t* sc = first ? p.s0 : p.s1;
-  const uint16_t* bi = first ? p.b0 : p.b1;
-  load_words<BITS>(st.w, w + (row * (D * BITS / 32) + run * BITS));
-  st.s = sc[g];
-  st.b = bi[g];
+  if constexpr (BITS == kPreBits) {  // one segment of bf16 rows, no scales
+    load_words<BITS>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
+    st.s = st.b = 0u;
+  } else {
+    const bool first = kk < a.n0;
+    const uint32_t row = uint32_t(first ? kk : kk - int(a.n0));
+    const uint32_t g = row * uint32_t(D / a.gs) + uint32_t(run * 32) / uint32_t(a.gs);
+    const uint32_t* w = first ? p.w0 : p.w1;
+    const uint16_t* sc = first ? p.s0 : p.s1;
+    const uint16_t* bi = first ? p.b0 : p.b1;
+    load_words<BITS>(st.w, w + (row * (D * BITS / 32) + run * BITS));
+    st.s = sc[g];
+    st.b = bi[g];
+  }
 }
 
 // The 32 codes of a run as floats. 2-, 4- and 8-bit codes are split into
@@ -323,20 +333,25 @@ __device__ __forceinline__ void dequant_run_h16(const uint32_t* w, uint32_t sb, 
 
 template <int BITS, bool H16>
 __device__ __forceinline__ void dequant_run(const uint32_t* w, uint32_t sb, uint32_t* out) {
-  if constexpr (H16 && (BITS == 8 || BITS == 4)) {
-    dequant_run_h16<BITS>(w, sb, out);
-    return;
-  }
-  float f[32];
-  run_codes<BITS>(w, f);
-  const float s = __uint_as_float(sb << 16), bias = __uint_as_float(sb & 0xffff0000u);
+  if constexpr (BITS == kPreBits) {  // already bf16
+    static_assert(!H16, "dequantized rows are bf16");
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if constexpr (H16) {
-      out[i] = pack_h16(s * f[2 * i] + bias, s * f[2 * i + 1] + bias);
-    } else {
-      const uint32_t m = pack_bf16(s * f[2 * i], s * f[2 * i + 1]);
-      out[i] = pack_bf16(__uint_as_float(m << 16) + bias, __uint_as_float(m & 0xffff0000u) + bias);
+    for (int i = 0; i < 16; ++i) out[i] = w[i];
+  } else if constexpr (H16 && (BITS == 8 || BITS == 4)) {
+    dequant_run_h16<BITS>(w, sb, out);
+  } else {
+    float f[32];
+    run_codes<BITS>(w, f);
+    const float s = __uint_as_float(sb << 16), bias = __uint_as_float(sb & 0xffff0000u);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if constexpr (H16) {
+        out[i] = pack_h16(s * f[2 * i] + bias, s * f[2 * i + 1] + bias);
+      } else {
+        const uint32_t m = pack_bf16(s * f[2 * i], s * f[2 * i + 1]);
+        out[i] = pack_bf16(__uint_as_float(m << 16) + bias,
+                           __uint_as_float(m & 0xffff0000u) + bias);
+      }
     }
   }
 }
@@ -727,8 +742,9 @@ void prefill_affine_kernel(const Args a) {
 
 typedef void (*KernelFn)(Args);
 
-// The kernel for (D, bits_k, bits_v), bits in {2, 3, 4, 5, 6, 8}; null if
-// unsupported. h16: the f16-operand variant.
+// The kernel for (D, bits_k, bits_v), bits in {2, 3, 4, 5, 6, 8}, or both
+// kPreBits for keys dequantized beforehand; null if unsupported. h16: the
+// f16-operand variant.
 KernelFn pick_d64(int bk, int bv, bool h16);
 KernelFn pick_d128(int bk, int bv, bool h16);
 KernelFn pick_d256(int bk, int bv, bool h16);
@@ -748,6 +764,8 @@ KernelFn pick_bv(int bv) {
 
 template <int D, bool H16>
 KernelFn pick_for(int bk, int bv) {
+  if constexpr (!H16)
+    if (bk == kPreBits && bv == kPreBits) return prefill_affine_kernel<D, kPreBits, kPreBits, false>;
   switch (bk) {
     case 2: return pick_bv<D, 2, H16>(bv);
     case 3: return pick_bv<D, 3, H16>(bv);

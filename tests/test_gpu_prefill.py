@@ -10,6 +10,8 @@ mean-abs, as for decode. Cases cover the reference's prefill branches
 that do not divide the 128-row block (G = 3), rows that see no key, a shared
 prefix segment, every head dim the kernel takes and mixed K/V widths, and the
 cache-level entry on growing and rotating caches across chunk boundaries.
+The dequantize-once path (keys dequantized into scratch, then copied) must
+match the in-block path bit for bit.
 """
 import numpy as np
 import pytest
@@ -197,3 +199,57 @@ def test_cache_prefill_rejects(T):
     with pytest.raises(T.TqkvError) as e:
         c.prefill_attend(q.ptr, 4, 8, 1.0, out.ptr)  # 8 queries, 4 tokens appended
     assert e.value.status == T.EINVAL_SHAPE
+
+
+@pytest.mark.parametrize("case", [0, 1, 3, 4, 5, 7, 9])
+def test_prefill_dequantize_once_is_bit_identical(T, monkeypatch, case):
+    # Keys dequantized once into scratch (mlx::dequantize's bits) and then
+    # copied into LDS give the same bf16 operands as dequantizing them in
+    # every row block: the outputs must agree bit for bit, and with the
+    # oracle to the bar.
+    B, H, Hkv, D, L, N, bk, bv, gs, q_start, k_start, causal, window, scale = PREFILL_CASES[case]
+    seed = 4099 + case
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    q = kv_bf16((B, H, L, D), seed)
+    k = kv_bf16((B, Hkv, N, D), seed + 1, frac=0.01, mult=10.0)
+    v = kv_bf16((B, Hkv, N, D), seed + 2, frac=0.01, mult=10.0)
+    if scale == 1.0:
+        q = O.bf16_from_f32(O.bf16_to_f32(q) / np.sqrt(D))
+    (kh, kd), (vh, vd) = _cache(k, gs, bk, N + 5), _cache(v, gs, bv, N + 5)
+    got = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("TQKV_PREFILL_DEQUANT_ONCE", mode)
+        got[mode] = run(T, q, [(kd, vd, N + 5, N, False)], B, H, Hkv, L, D, gs, bk, bv, scale,
+                        q_start, k_start, causal, window)
+    assert np.array_equal(got["0"], got["1"])
+    want, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale, causal=causal, q_start=q_start,
+                                 first_held=k_start, window=window, dequant="bf16")
+    check(got["1"], want, f"once case {case}")
+
+
+def test_prefill_dequantize_once_two_segments_by_default(T, monkeypatch):
+    # 512 positions x 4 heads = 8 row blocks a KV head: the default picks the
+    # dequantize-once path; a shared prefix segment (batch stride 0) plus
+    # per-row suffixes, windowed, against the in-block path and the oracle.
+    monkeypatch.delenv("TQKV_PREFILL_DEQUANT_ONCE", raising=False)
+    B, H, Hkv, D, L, gs, bk, bv = 2, 16, 4, 128, 512, 64, 8, 4
+    P, S = 300, 600
+    q = kv_bf16((B, H, L, D), 21)
+    kp = kv_bf16((1, Hkv, P, D), 22, frac=0.01, mult=10.0)
+    vp = kv_bf16((1, Hkv, P, D), 23)
+    ks = kv_bf16((B, Hkv, S, D), 24, frac=0.01, mult=10.0)
+    vs = kv_bf16((B, Hkv, S, D), 25)
+    (kph, kpd), (vph, vpd) = _cache(kp, gs, bk), _cache(vp, gs, bv)
+    (ksh, ksd), (vsh, vsd) = _cache(ks, gs, bk, S + 3), _cache(vs, gs, bv, S + 3)
+    scale = 1.0 / np.sqrt(D)
+    segs = [(kpd, vpd, P, P, True), (ksd, vsd, S + 3, S, False)]
+    got = run(T, q, segs, B, H, Hkv, L, D, gs, bk, bv, scale, P + S - L, 0, True, 700)
+    monkeypatch.setenv("TQKV_PREFILL_DEQUANT_ONCE", "0")
+    ref = run(T, q, segs, B, H, Hkv, L, D, gs, bk, bv, scale, P + S - L, 0, True, 700)
+    assert np.array_equal(got, ref)
+    cat = lambda a, b: np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
+    kh = tuple(cat(a, b) for a, b in zip(kph, ksh))
+    vh = tuple(cat(a, b) for a, b in zip(vph, vsh))
+    want, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale, causal=True, q_start=P + S - L,
+                                 first_held=0, window=700, dequant="bf16")
+    check(got, want, "once, two segments")
