@@ -384,7 +384,8 @@ def prefill_main(T, hip, args):
         "roofline": {
             "bound": "mfma", "achieved": round(tf_g, 1), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tf_g / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "kernel": "prefill_affine_kernel<128,4,4>",
+            "kernel": "tqkv_prefill_attend_affine call: dequantize_rows_kernel<128> (the "
+                      "keys once, as bf16) + prefill_affine_kernel<128,16,16>",
             "alg_flops_per_launch": fl_g, "avg_launch_ms": round(ms_g, 5),
         },
         "sliding_layer_chunk": {
