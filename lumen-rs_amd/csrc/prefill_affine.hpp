@@ -423,6 +423,27 @@ __device__ __forceinline__ float sum2(uint32_t w, float acc) {
   }
 }
 
+// Lane l combined with lane l ^ 16 (l ^ 32): gfx950's v_permlane16_swap
+// (v_permlane32_swap) of a value with itself returns the lane's and its
+// partner's halves, with no LDS round trip (a ds_bpermute shuffle would sit
+// on the path from the scores to the softmax).
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Two wavefronts per SIMD (at most 256 registers a lane): one wavefront's
 // softmax and dequantization then overlap the other's matrix-core work.
 template <int D, int BK, int BV, bool H16>
@@ -639,8 +660,7 @@ void prefill_affine_kernel(const Args a) {
           for (int i = 0; i < 4; ++i)
   #pragma unroll
             for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[i][j][r]);
-          mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+          mx = xor32_max(xor16_max(mx));
           mx *= a.qscale;  // qscale > 0: the max of the scaled scores
           const bool up = mx > m[j] + kTau;
           if (__any(up)) {
@@ -713,8 +733,7 @@ void prefill_affine_kernel(const Args a) {
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     float tot = lsum[j];
-    tot += __shfl_xor(tot, 16, kWave);
-    tot += __shfl_xor(tot, 32, kWave);
+    tot = xor32_sum(xor16_sum(tot));
     if (!rvalid[j]) continue;
     if (a.part_o) {
       const int64_t r = row0 + wave * RW + 16 * j + lr;
