@@ -54,6 +54,77 @@ struct Buf {
   int64_t cap = 0;  // rows per slab
 };
 
+// The copies of one plan step over every slot, in one launch: job z copies
+// rows [src_row, src_row + n) of every slab of src (zeros when src is null)
+// into rows [dst_row, ...) of dst, slab strides src_cap / dst_cap rows of rb
+// bytes. (Per slot and piece, a step was up to a dozen launches of a few µs
+// each.)
+struct CopyJob {
+  uint8_t* dst;
+  const uint8_t* src;
+  int64_t dst_cap, dst_row, src_cap, src_row, n, rb;
+  int words;  // 4-byte units (everything 4-aligned)
+};
+constexpr int kMaxJobs = 24;
+struct CopyBatch {
+  CopyJob job[kMaxJobs];
+  int n_jobs;
+};
+
+__global__ void rows_copy_batch_kernel(const CopyBatch b) {
+  const CopyJob& j = b.job[blockIdx.z];
+  const int64_t slab = blockIdx.y;
+  const int64_t bytes = j.n * j.rb;
+  uint8_t* d = j.dst + (slab * j.dst_cap + j.dst_row) * j.rb;
+  const uint8_t* src = j.src ? j.src + (slab * j.src_cap + j.src_row) * j.rb : nullptr;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  if (j.words) {
+    uint32_t* dw = reinterpret_cast<uint32_t*>(d);
+    const uint32_t* sw = reinterpret_cast<const uint32_t*>(src);
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes / 4; i += stride)
+      dw[i] = sw ? sw[i] : 0u;
+  } else {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < bytes; i += stride)
+      d[i] = src ? src[i] : uint8_t(0);
+  }
+}
+
+class CopyBatcher {
+ public:
+  CopyBatcher(hipStream_t st, int64_t n_slabs) : st_(st), n_slabs_(n_slabs) { b_.n_jobs = 0; }
+  int32_t add(uint8_t* dst, int64_t dst_cap, int64_t dst_row, const uint8_t* src, int64_t src_cap,
+              int64_t src_row, int64_t n, int64_t rb) {
+    if (n <= 0 || n_slabs_ <= 0) return TQKV_OK;
+    if (b_.n_jobs == kMaxJobs)
+      if (int32_t rc = flush()) return rc;
+    const bool words = (rb % 4 == 0) && (reinterpret_cast<uintptr_t>(dst) % 4 == 0) &&
+                       (!src || reinterpret_cast<uintptr_t>(src) % 4 == 0);
+    b_.job[b_.n_jobs++] = CopyJob{dst, src, dst_cap, dst_row, src_cap, src_row, n, rb, words ? 1 : 0};
+    const int64_t units = words ? n * rb / 4 : n * rb;
+    const int64_t blocks = (units + 255) / 256;
+    if (blocks > blocks_) blocks_ = blocks > 1024 ? 1024 : blocks;
+    return TQKV_OK;
+  }
+  int32_t flush() {
+    if (b_.n_jobs == 0) return TQKV_OK;
+    if (n_slabs_ > 65535)
+      return fail(TQKV_EINVAL_SHAPE, "%lld slabs exceed one launch", (long long)n_slabs_);
+    hipLaunchKernelGGL(rows_copy_batch_kernel,
+                       dim3(unsigned(blocks_), unsigned(n_slabs_), unsigned(b_.n_jobs)), dim3(256),
+                       0, st_, b_);
+    TQKV_LAUNCHED();
+    b_.n_jobs = 0;
+    blocks_ = 0;
+    return TQKV_OK;
+  }
+
+ private:
+  hipStream_t st_;
+  int64_t n_slabs_;
+  CopyBatch b_{};
+  int64_t blocks_ = 0;
+};
+
 int32_t rows_copy(hipStream_t st, int64_t n_slabs, int64_t rb, uint8_t* dst, int64_t dst_cap,
                   int64_t dst_row, const uint8_t* src, int64_t src_cap, int64_t src_row,
                   int64_t n) {
@@ -136,40 +207,57 @@ int32_t execute(tqkv_cache* c, const cacheplan::Plan& p, int64_t old_len, hipStr
     }
   }
   (void)old_len;
+  // Every slot's copies go out in one batch; buffers they replace are freed
+  // once the stream has drained past them (one wait, not one per slot).
+  CopyBatcher cb(st, c->n_slabs);
+  Buf retired[kMaxSlots];
+  int n_retired = 0;
+  // Launches what was batched, then (after the stream has drained past the
+  // replaced buffers) frees them; on an error too, so nothing leaks.
+  auto finish = [&](int32_t rc) {
+    const int32_t frc = cb.flush();
+    if (n_retired > 0) {
+      const hipError_t e = hipStreamSynchronize(st);
+      for (int i = 0; i < n_retired; ++i) release(retired[i]);
+      if (rc == TQKV_OK && e != hipSuccess)
+        return fail(TQKV_EDEVICE, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    }
+    return rc != TQKV_OK ? rc : frc;
+  };
   for (int s = 0; s < c->n_slots; ++s) {
     Buf& cur = c->cur[s];
     const int64_t rb = c->rb[s];
     if (in_place) {
       if (cur.cap < p.len) {
         Buf nb;
-        if (int32_t rc = alloc(c, nb, capacity_for(c, p.len, cur.cap), s)) return rc;
-        if (int32_t rc = rows_copy(st, c->n_slabs, rb, nb.ptr, nb.cap, 0, cur.ptr, cur.cap, 0, a))
-          return rc;
-        if (cur.ptr) TQKV_HIP(hipStreamSynchronize(st));
-        release(cur);
+        if (int32_t rc = alloc(c, nb, capacity_for(c, p.len, cur.cap), s)) return finish(rc);
+        if (int32_t rc = cb.add(nb.ptr, nb.cap, 0, cur.ptr, cur.cap, 0, a, rb)) {
+          release(nb);
+          return finish(rc);
+        }
+        if (cur.ptr) retired[n_retired++] = cur;
         cur = nb;
       }
-      if (int32_t rc = rows_copy(st, c->n_slabs, rb, cur.ptr, cur.cap, a, nullptr, 0, 0, p.len - a))
-        return rc;
+      if (int32_t rc = cb.add(cur.ptr, cur.cap, a, nullptr, 0, 0, p.len - a, rb))
+        return finish(rc);
     } else {
       Buf& alt = c->alt[s];
       if (alt.cap < p.len) {
-        if (alt.ptr) TQKV_HIP(hipStreamSynchronize(st));
-        release(alt);
-        if (int32_t rc = alloc(c, alt, capacity_for(c, p.len, cur.cap), s)) return rc;
+        if (alt.ptr) retired[n_retired++] = alt;
+        alt = Buf{};
+        if (int32_t rc = alloc(c, alt, capacity_for(c, p.len, cur.cap), s)) return finish(rc);
       }
       int64_t at = 0;
       for (const cacheplan::Piece& q : p.pieces) {
-        if (int32_t rc = rows_copy(st, c->n_slabs, rb, alt.ptr, alt.cap, at,
-                                   q.src >= 0 ? cur.ptr : nullptr, cur.cap, q.src >= 0 ? q.src : 0,
-                                   q.n))
-          return rc;
+        if (int32_t rc = cb.add(alt.ptr, alt.cap, at, q.src >= 0 ? cur.ptr : nullptr, cur.cap,
+                                q.src >= 0 ? q.src : 0, q.n, rb))
+          return finish(rc);
         at += q.n;
       }
       std::swap(cur, alt);
     }
   }
-  return TQKV_OK;
+  return finish(TQKV_OK);
 }
 
 int32_t upload(void** dst, const void* src, size_t bytes) {
