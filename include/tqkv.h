@@ -287,8 +287,11 @@ int32_t tqkv_decode_attend_codebook_qjl(const uint16_t* q, int32_t B, int32_t H,
  * softmax(scale * Q K^T + mask) V for a chunk of L query rows per head.
  * Replaces dequantized_prefill_attention (gemma4_moe.rs:2382-2411): K and V
  * dequantize as mlx::dequantize does for bf16 (bf16(bf16(scale * code) +
- * bias)) in LDS, never in HBM, then attention runs with bf16 operands and f32
- * accumulation. The mask is build_causal_mask_abs (native_attention.rs:
+ * bias)), then attention runs with bf16 operands and f32 accumulation. When
+ * 8 or more 256-row blocks share a KV head, the keys are dequantized once
+ * into the library's per-device scratch (2 * B * H_kv * keys * D * 2 bytes,
+ * at most 4 GiB; larger contexts dequantize in every block instead, in LDS)
+ * and read from there; the two ways give the same bits. The mask is build_causal_mask_abs (native_attention.rs:
  * 545-622) in absolute positions: query row l sits at q_start + l and key k
  * (counted across both segments) at k_start + k; with causal != 0, key k is
  * visible iff k_abs <= q_abs and, when window > 0, q_abs < k_abs + window
@@ -300,7 +303,9 @@ int32_t tqkv_decode_attend_codebook_qjl(const uint16_t* q, int32_t B, int32_t H,
  * q: bf16 [B, H, L, D]; out: bf16 [B, H, L, D]; segs as for
  * tqkv_decode_attend_affine (1 or 2: a shared prefix, then a suffix).
  * D in {64, 128, 256}; bits_k, bits_v in {2, 3, 4, 5, 6, 8}; group_size in
- * {32, 64, 128}. Needs no workspace.
+ * {32, 64, 128}. Takes no workspace argument; calls that use the library's
+ * scratch (this one, and decodes given a null workspace) must not overlap in
+ * time on one device.
  */
 int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
                                    int32_t L, int32_t D, int32_t group_size, int32_t bits_k,

@@ -74,6 +74,9 @@ __global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int 
 // dequantized once into scratch instead of in every block: the blocks would
 // otherwise repeat the same dequantization, the kernel's VALU-bound part.
 constexpr int64_t kOnceBlocks = 8;
+// The scratch that path may take (bf16 K and V of every visible key); larger
+// contexts dequantize in every block instead.
+constexpr size_t kOnceMaxBytes = size_t(4) << 30;
 
 }  // namespace
 }  // namespace prefill
@@ -229,10 +232,11 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // TQKV_PREFILL_DEQUANT_ONCE=0 / 1 forces the choice (tests compare them).
   const char* once_env = getenv("TQKV_PREFILL_DEQUANT_ONCE");
-  const bool once = once_env ? strcmp(once_env, "0") != 0 : blocks >= kOnceBlocks;
+  const int64_t slabs = int64_t(B) * H_kv;
+  const size_t need = 2 * size_t(slabs) * size_t(a.total) * size_t(D) * 2;
+  const bool once = once_env ? strcmp(once_env, "0") != 0
+                             : blocks >= kOnceBlocks && need <= kOnceMaxBytes;
   if (once) {
-    const int64_t slabs = int64_t(B) * H_kv;
-    const size_t need = 2 * size_t(slabs) * size_t(a.total) * size_t(D) * 2;
     void* ws = nullptr;
     if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
     uint16_t* kd = static_cast<uint16_t*>(ws);
