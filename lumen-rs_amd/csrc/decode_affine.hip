@@ -84,6 +84,67 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   }
 }
 
+// The merge for at most NMAX splits (4, 8, 16 or 32), in one round of
+// loads: every thread loads all the splits' (m, l) (the same addresses
+// across the block, served by the caches) and its two channels' partial
+// outputs, then combines them in registers: no LDS, no barrier, no second
+// trip to memory.
+constexpr int kMergeSmall = 32;
+
+template <int NMAX>
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_small_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_m,
+    const float* __restrict__ part_l, int n_splits, int D, uint16_t* __restrict__ out) {
+  const int64_t bh = blockIdx.x;
+  const float* pm = part_m + bh * n_splits;
+  const float* pl = part_l + bh * n_splits;
+  const float* po = part_o + bh * n_splits * D;
+  const int d0 = threadIdx.x, d1 = threadIdx.x + kMergeThreads;
+  const bool has0 = d0 < D, has1 = d1 < D;
+  float m[NMAX], l[NMAX], o0[NMAX], o1[NMAX];
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    const bool live = s < n_splits;
+    m[s] = live ? pm[s] : -INFINITY;
+    l[s] = live ? pl[s] : 0.0f;
+    o0[s] = live && has0 ? po[int64_t(s) * D + d0] : 0.0f;
+    o1[s] = live && has1 ? po[int64_t(s) * D + d1] : 0.0f;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) mx = fmaxf(mx, m[s]);
+  float ls = 0.0f, os0 = 0.0f, os1 = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NMAX; ++s) {
+    const float w = m[s] == -INFINITY ? 0.0f : exp2f(m[s] - mx);
+    ls += w * l[s];
+    os0 += w * o0[s];
+    os1 += w * o1[s];
+  }
+  if (has0) out[bh * D + d0] = f32_to_bf16(ls > 0.0f ? os0 / ls : 0.0f);
+  if (has1) out[bh * D + d1] = f32_to_bf16(ls > 0.0f ? os1 / ls : 0.0f);
+}
+
+// The merge launch for n_splits partial slots of every (batch row, head).
+void launch_merge(const float* po, const float* pm, const float* pl, int n_splits, int D,
+                  int64_t rows, uint16_t* out, hipStream_t st) {
+  auto small = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(unsigned(rows)), dim3(kMergeThreads), 0, st, po, pm, pl,
+                       n_splits, D, out);
+  };
+  if (n_splits <= 4)
+    small(decode_merge_small_kernel<4>);
+  else if (n_splits <= 8)
+    small(decode_merge_small_kernel<8>);
+  else if (n_splits <= 16)
+    small(decode_merge_small_kernel<16>);
+  else if (n_splits <= kMergeSmall)
+    small(decode_merge_small_kernel<kMergeSmall>);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(rows)), dim3(kMergeThreads), 0, st, po,
+                       pm, pl, n_splits, D, out);
+}
+
 // Splits per (batch row, KV head). With at least ~2048 wavefronts of whole
 // (batch row, KV head) units the chip is full and each workgroup owns its
 // keys (one launch); otherwise the keys are split until the grid holds ~2048
@@ -349,8 +410,7 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
                          dim3(kWave * waves), 0, st, s);
       TQKV_LAUNCHED();
     }
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(kMergeThreads), 0, st,
-                       po, pm, pl, n_part, D, out);
+    launch_merge(po, pm, pl, n_part, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
     return ok();
   }
@@ -376,8 +436,7 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
                      dim3(kWave * waves), 0, st, a);
   TQKV_LAUNCHED();
   if (a.n_splits > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(kMergeThreads), 0, st,
-                       a.part_o, a.part_m, a.part_l, a.n_splits, D, out);
+    launch_merge(a.part_o, a.part_m, a.part_l, a.n_splits, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
   }
   return ok();
@@ -492,8 +551,7 @@ extern "C" int32_t tqkv_decode_attend_affine_pages(
                      dim3(kWave * waves), 0, st, a);
   TQKV_LAUNCHED();
   if (a.n_splits > 1) {
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(unsigned(B * H)), dim3(kMergeThreads), 0, st,
-                       a.part_o, a.part_m, a.part_l, a.n_splits, D, out);
+    launch_merge(a.part_o, a.part_m, a.part_l, a.n_splits, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
   }
   return ok();
