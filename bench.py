@@ -541,7 +541,8 @@ def append_main(T, hip, args):
          "turboquant_encode": {"ms": round(ms_t, 5), "tokens_per_s": round(S / (ms_t * 1e-3), 1),
                                "bytes": in_bytes + tq_bytes, "qjl_m": M,
                                "note": "compress_one restated bit-exactly: sequential f32 "
-                                       "sums, one wavefront per vector; latency-bound"}},
+                                       "sums, four lanes per vector, R and Phi from LDS; "
+                                       "VALU-bound (unfused mul + add)"}},
         settle)
     if not args.no_cpu_baseline:
         O, threads = _oracle()

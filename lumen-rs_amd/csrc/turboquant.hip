@@ -18,6 +18,8 @@
 // Rust's f32 `Sum` folds from -0.0, explicit accumulators from +0.0; the
 // kernels start each sum the way the corresponding Rust line does.
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 
 #include "common.hpp"
 
@@ -131,6 +133,285 @@ __global__ __launch_bounds__(kWave) void tq_encode_kernel(
       signs[dst * words + w0] = uint32_t(ball);
       if (w0 + 1 < words) signs[dst * words + w0 + 1] = uint32_t(ball >> 32);
     }
+  }
+}
+
+// The same encode for D <= 128 with SUB = 4 lanes per row. Each output is
+// still the sequential sum over j that compress_one forms, but the loops run
+// j outermost: a lane keeps the partial sums of its D / SUB outputs in
+// registers while the matrix entries of column (or row) j reach the lanes as
+// LDS reads shared by every row of the block: R transposed for y = R x and R
+// as stored for the reconstruction R^T (centroid * scale), each lane's
+// quarter of a matrix row padded by 4 floats so the four quarters sit in
+// different banks. The sums over all D outputs (sigma, the residual norm)
+// run quarter after quarter, the carry passed lane to lane. For the QJL
+// signs the residual goes through LDS so each lane holds all of it, and the
+// SUB lanes of a row take Phi rows in turn (Phi staged 32 rows at a time).
+// tq_encode_kernel spends a wavefront per row and reads R rows strided
+// across lanes; here 128 rows share one copy of R in LDS.
+constexpr int kLaneSub = 4;
+constexpr int kLaneBlock = 512;
+constexpr int kLaneRows = kLaneBlock / kLaneSub;
+
+__device__ __forceinline__ void load8(const void* __restrict__ xv, int x_bf16, int64_t off,
+                                      float (&o)[8]) {
+  if (x_bf16) {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(xv) + off);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      o[2 * k] = __uint_as_float(u[k] << 16);
+      o[2 * k + 1] = __uint_as_float(u[k] & 0xffff0000u);
+    }
+  } else {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(xv) + off);
+    const float4 a = p[0], b = p[1];
+    o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
+  }
+}
+
+template <int D>
+struct LaneLayout {
+  static constexpr int NI = D / kLaneSub;       // outputs a lane owns
+  static constexpr int SEG = NI + 4;            // padded quarter of a matrix row
+  static constexpr int PS = kLaneSub * SEG;     // padded matrix row stride
+  static constexpr int RS = D + 4;              // residual / Phi row stride
+  static constexpr int PHI_ROWS = 32;           // Phi rows staged at a time
+  static constexpr int RES = kLaneRows * RS;    // residual rows of the block
+  static constexpr int MAT = D * PS > RES + PHI_ROWS * RS ? D * PS : RES + PHI_ROWS * RS;
+};
+
+template <int D>
+__global__ __launch_bounds__(kLaneBlock) void tq_encode_lane_kernel(
+    const void* __restrict__ xv, int x_bf16, int64_t rows, int64_t s, const float* __restrict__ R,
+    const double* __restrict__ bnd, const float* __restrict__ cent_f32, int n_levels,
+    const float* __restrict__ phi, int m, uint8_t* __restrict__ codes, float* __restrict__ sigma,
+    uint32_t* __restrict__ signs, float* __restrict__ rnorm, int64_t dst_cap, int64_t dst_start) {
+  using L = LaneLayout<D>;
+  constexpr int NI = L::NI;
+  __shared__ __attribute__((aligned(16))) float mat[L::MAT];
+  __shared__ uint32_t code_words[(D / 4) * kLaneRows];
+  __shared__ float cent_s[256];
+  __shared__ double bnd_s[256];
+  const int tid = threadIdx.x;
+  const int vec = tid / kLaneSub, sub = tid % kLaneSub;
+  const int lane = tid % kWave;
+  const int first = lane & ~(kLaneSub - 1);  // lane of sub 0 of this row
+  const int64_t r_raw = int64_t(blockIdx.x) * kLaneRows + vec;
+  const bool valid = r_raw < rows;
+  const int64_t r = valid ? r_raw : rows - 1;  // idle rows recompute the last row, store nothing
+  const int64_t dst = (r / s) * dst_cap + dst_start + (r % s);
+  const int i0 = sub * NI;  // first output of this lane
+  for (int i = tid; i < n_levels; i += kLaneBlock) cent_s[i] = cent_f32[i], bnd_s[i] = bnd[i];
+  // mat[j * PS + quarter(i) * SEG + i % NI] = R[i][j]
+  for (int idx = tid; idx < D * D; idx += kLaneBlock) {
+    const int i = idx / D, j = idx % D;
+    mat[j * L::PS + (i / NI) * L::SEG + i % NI] = R[idx];
+  }
+  __syncthreads();
+
+  // y = R x: y[i] = sum_j R[i][j] x[j] from -0.0, j in order.
+  float acc[NI];
+#pragma unroll
+  for (int l = 0; l < NI; ++l) acc[l] = -0.0f;
+  for (int j0 = 0; j0 < D; j0 += 8) {
+    float x8[8];
+    load8(xv, x_bf16, r * D + j0, x8);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const float4* col = reinterpret_cast<const float4*>(mat + (j0 + jj) * L::PS + sub * L::SEG);
+#pragma unroll
+      for (int c = 0; c < NI / 4; ++c) {
+        const float4 w = col[c];
+        acc[4 * c + 0] = add(acc[4 * c + 0], mul(w.x, x8[jj]));
+        acc[4 * c + 1] = add(acc[4 * c + 1], mul(w.y, x8[jj]));
+        acc[4 * c + 2] = add(acc[4 * c + 2], mul(w.z, x8[jj]));
+        acc[4 * c + 3] = add(acc[4 * c + 3], mul(w.w, x8[jj]));
+      }
+    }
+  }
+  // sum_i y[i]^2 from -0.0, quarter after quarter.
+  float ss = -0.0f;
+#pragma unroll
+  for (int q = 0; q < kLaneSub; ++q) {
+    if (sub == q) {
+#pragma unroll
+      for (int l = 0; l < NI; ++l) ss = add(ss, mul(acc[l], acc[l]));
+    }
+    ss = __shfl(ss, first + q);
+  }
+  const float scale = sqrt_rn(div_rn(ss, float(D)));
+  const bool degenerate = scale < 1e-10f;
+  const float inv = degenerate ? 0.0f : div_rn(1.0f, scale);
+#pragma unroll
+  for (int q = 0; q < NI / 16; ++q) {
+    uint32_t w4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int l = 16 * q + 4 * k + b;
+        const uint32_t c = degenerate ? 0u : level_of(double(mul(acc[l], inv)), bnd_s, n_levels);
+        w |= c << (8 * b);
+      }
+      w4[k] = w;
+      code_words[((i0 + 16 * q + 4 * k) / 4) * kLaneRows + vec] = w;
+    }
+    if (valid)
+      reinterpret_cast<uint4*>(codes + dst * D + i0)[q] = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+  }
+  if (valid && sub == 0) sigma[dst] = scale;
+  if (m <= 0) return;  // uniform: the whole block leaves together
+
+  // Residual against R^T (centroid * scale): sum_j R[j][i] * cv[j] from +0.0.
+  __syncthreads();  // every lane is done with R^T; code_words are complete
+  for (int idx = tid; idx < D * D; idx += kLaneBlock) {
+    const int j = idx / D, i = idx % D;
+    mat[j * L::PS + (i / NI) * L::SEG + i % NI] = R[idx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int l = 0; l < NI; ++l) acc[l] = 0.0f;
+  for (int wid = 0; wid < D / 4; ++wid) {
+    const uint32_t w = code_words[wid * kLaneRows + vec];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float cv = mul(cent_s[(w >> (8 * b)) & 0xffu], scale);
+      const float4* row = reinterpret_cast<const float4*>(mat + (4 * wid + b) * L::PS + sub * L::SEG);
+#pragma unroll
+      for (int c = 0; c < NI / 4; ++c) {
+        const float4 e = row[c];
+        acc[4 * c + 0] = add(acc[4 * c + 0], mul(e.x, cv));
+        acc[4 * c + 1] = add(acc[4 * c + 1], mul(e.y, cv));
+        acc[4 * c + 2] = add(acc[4 * c + 2], mul(e.z, cv));
+        acc[4 * c + 3] = add(acc[4 * c + 3], mul(e.w, cv));
+      }
+    }
+  }
+#pragma unroll
+  for (int l0 = 0; l0 < NI; l0 += 8) {
+    float x8[8];
+    load8(xv, x_bf16, r * D + i0 + l0, x8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[l0 + e] = __fsub_rn(x8[e], acc[l0 + e]);
+  }
+  float rn = 0.0f;
+#pragma unroll
+  for (int q = 0; q < kLaneSub; ++q) {
+    if (sub == q) {
+#pragma unroll
+      for (int l = 0; l < NI; ++l) rn = add(rn, mul(acc[l], acc[l]));
+    }
+    rn = __shfl(rn, first + q);
+  }
+  if (valid && sub == 0) rnorm[dst] = sqrt_rn(rn);
+
+  // QJL signs: bit `row` = (Phi[row] . r >= 0) from -0.0, LSB-first u32
+  // words. The residual rows go to mat[0, RES) and Phi rows to the rest.
+  __syncthreads();  // every lane is done with R
+  float* res = mat;
+  float* phis = mat + L::RES;
+#pragma unroll
+  for (int c = 0; c < NI / 4; ++c)
+    reinterpret_cast<float4*>(res + vec * L::RS + i0)[c] =
+        make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
+  __syncthreads();
+  float rf[D];
+#pragma unroll
+  for (int c = 0; c < D / 4; ++c) {
+    const float4 e = reinterpret_cast<const float4*>(res + vec * L::RS)[c];
+    rf[4 * c] = e.x, rf[4 * c + 1] = e.y, rf[4 * c + 2] = e.z, rf[4 * c + 3] = e.w;
+  }
+  const int words = (m + 31) / 32;
+  for (int base = 0; base < m; base += L::PHI_ROWS) {
+    const int nr = m - base < L::PHI_ROWS ? m - base : L::PHI_ROWS;
+    __syncthreads();  // the previous rows are consumed
+    for (int idx = tid; idx < nr * D; idx += kLaneBlock)
+      phis[(idx / D) * L::RS + idx % D] = phi[int64_t(base) * D + idx];
+    __syncthreads();
+    uint32_t word = 0;
+    constexpr int T = L::PHI_ROWS / kLaneSub;
+    float a[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) a[t] = -0.0f;
+#pragma unroll
+    for (int c = 0; c < D / 4; ++c) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const int rr = kLaneSub * t + sub;
+        const float4 e = reinterpret_cast<const float4*>(phis + (rr < nr ? rr : 0) * L::RS)[c];
+        a[t] = add(a[t], mul(e.x, rf[4 * c + 0]));
+        a[t] = add(a[t], mul(e.y, rf[4 * c + 1]));
+        a[t] = add(a[t], mul(e.z, rf[4 * c + 2]));
+        a[t] = add(a[t], mul(e.w, rf[4 * c + 3]));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int rr = kLaneSub * t + sub;
+      if (rr < nr && a[t] >= 0.0f) word |= 1u << rr;
+    }
+    word |= __shfl_xor(word, 1);
+    word |= __shfl_xor(word, 2);
+    if (valid && sub == 0) signs[dst * words + base / 32] = word;
+  }
+}
+
+// y = x M with M = R (transpose = 0) or R^T, the same fmaf chain over j from
+// 0.0 as tq_rotate_rows_kernel, laid out as tq_encode_lane_kernel: SUB lanes
+// a row, each holding D / SUB outputs, M's row j read from LDS by every row
+// of the block (tq_rotate_rows_kernel reads all of R from L2 for each row).
+template <int D>
+__global__ __launch_bounds__(kLaneBlock) void tq_rotate_lane_kernel(const uint16_t* __restrict__ x,
+                                                                    int64_t rows,
+                                                                    const float* __restrict__ R,
+                                                                    int transpose,
+                                                                    uint16_t* __restrict__ y) {
+  using L = LaneLayout<D>;
+  constexpr int NI = L::NI;
+  __shared__ __attribute__((aligned(16))) float mat[D * L::PS];
+  const int tid = threadIdx.x;
+  const int vec = tid / kLaneSub, sub = tid % kLaneSub;
+  const int64_t r_raw = int64_t(blockIdx.x) * kLaneRows + vec;
+  const bool valid = r_raw < rows;
+  const int64_t r = valid ? r_raw : rows - 1;
+  const int i0 = sub * NI;
+  // mat[j * PS + quarter(i) * SEG + i % NI] = M[j][i]
+  for (int idx = tid; idx < D * D; idx += kLaneBlock) {
+    const int a = idx / D, b = idx % D;  // R[a][b]
+    const int j = transpose ? b : a, i = transpose ? a : b;
+    mat[j * L::PS + (i / NI) * L::SEG + i % NI] = R[idx];
+  }
+  __syncthreads();
+  float acc[NI];
+#pragma unroll
+  for (int l = 0; l < NI; ++l) acc[l] = 0.0f;
+  for (int j0 = 0; j0 < D; j0 += 8) {
+    float x8[8];
+    load8(x, 1, r * D + j0, x8);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const float4* row = reinterpret_cast<const float4*>(mat + (j0 + jj) * L::PS + sub * L::SEG);
+#pragma unroll
+      for (int c = 0; c < NI / 4; ++c) {
+        const float4 e = row[c];
+        acc[4 * c + 0] = fmaf(x8[jj], e.x, acc[4 * c + 0]);
+        acc[4 * c + 1] = fmaf(x8[jj], e.y, acc[4 * c + 1]);
+        acc[4 * c + 2] = fmaf(x8[jj], e.z, acc[4 * c + 2]);
+        acc[4 * c + 3] = fmaf(x8[jj], e.w, acc[4 * c + 3]);
+      }
+    }
+  }
+  if (!valid) return;
+#pragma unroll
+  for (int c = 0; c < NI / 8; ++c) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w[k] = uint32_t(f32_to_bf16(acc[8 * c + 2 * k])) |
+             (uint32_t(f32_to_bf16(acc[8 * c + 2 * k + 1])) << 16);
+    reinterpret_cast<uint4*>(y + r * D + i0)[c] = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -334,7 +615,25 @@ extern "C" int32_t tqkv_tq_encode(const void* x, int32_t x_is_bf16, int64_t n_sl
   if (rows > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "too many rows");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int n = 1 << bits;
-#define TQKV_ENC(DIM)                                                                        \
+  // The lane-per-row kernel loads x in 16-byte pieces and stores 16 code
+  // bytes at a time; other alignments take the wavefront-per-row kernel.
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(codes)) % 16 == 0;
+  // TQKV_TQ_ENCODE_LANE=0 keeps the wavefront-per-row kernel (tests compare both).
+  const char* lane_env = getenv("TQKV_TQ_ENCODE_LANE");
+  if ((dim == 64 || dim == 128) && aligned && !(lane_env && strcmp(lane_env, "0") == 0)) {
+    const unsigned blocks = unsigned((rows + kLaneRows - 1) / kLaneRows);
+    if (dim == 64)
+      hipLaunchKernelGGL(tq_encode_lane_kernel<64>, dim3(blocks), dim3(kLaneBlock), 0, st, x,
+                         x_is_bf16, rows, s, rotation, boundaries, centroids_f32, n, qjl, qjl_m,
+                         codes, sigma, signs, rnorm, dst_cap, dst_start);
+    else
+      hipLaunchKernelGGL(tq_encode_lane_kernel<128>, dim3(blocks), dim3(kLaneBlock), 0, st, x,
+                         x_is_bf16, rows, s, rotation, boundaries, centroids_f32, n, qjl, qjl_m,
+                         codes, sigma, signs, rnorm, dst_cap, dst_start);
+    TQKV_LAUNCHED();
+    return ok();
+  }
+#define TQKV_ENC(DIM)                                                                      \
   case DIM:                                                                                 \
     hipLaunchKernelGGL(tq_encode_kernel<DIM>, dim3(unsigned(rows)), dim3(kWave), 0, st, x,   \
                        x_is_bf16, s, rotation, boundaries, centroids_f32, n, qjl, qjl_m,     \
@@ -449,6 +748,22 @@ extern "C" int32_t tqkv_rotate_bf16(const uint16_t* x, int64_t rows, int32_t dim
   if (!x || !rotation || !y) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (dim <= 0 || dim > 4096 || rows < 0 || rows > 0x7fffffffLL)
     return fail(TQKV_EINVAL_SHAPE, "rows=%lld dim=%d", (long long)rows, dim);
+  // TQKV_TQ_ENCODE_LANE=0 also keeps the block-per-row rotation.
+  const char* lane_env = getenv("TQKV_TQ_ENCODE_LANE");
+  if ((dim == 64 || dim == 128) &&
+      (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % 16 == 0 &&
+      !(lane_env && strcmp(lane_env, "0") == 0)) {
+    const unsigned blocks = unsigned((rows + kLaneRows - 1) / kLaneRows);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (dim == 64)
+      hipLaunchKernelGGL(tq_rotate_lane_kernel<64>, dim3(blocks), dim3(kLaneBlock), 0, st, x, rows,
+                         rotation, transpose, y);
+    else
+      hipLaunchKernelGGL(tq_rotate_lane_kernel<128>, dim3(blocks), dim3(kLaneBlock), 0, st, x,
+                         rows, rotation, transpose, y);
+    TQKV_LAUNCHED();
+    return ok();
+  }
   hipLaunchKernelGGL(tq_rotate_rows_kernel, dim3(unsigned(rows)), dim3(dim < 256 ? dim : 256),
                      size_t(dim) * sizeof(float), reinterpret_cast<hipStream_t>(stream), x, rows,
                      dim, rotation, transpose, y);

@@ -102,6 +102,64 @@ def test_encode_writes_into_cache_rows(T):
     assert np.all(sigma.numpy()[:, :6] == -1.0)
 
 
+def _encode_rows(T, dim, bits, m, x_dev, bf16_in, slabs, s, cap, start, tabs, env):
+    import os
+    dR, dphi, db, dc = tabs
+    W = max((m + 31) // 32, 1)
+    codes = T.DeviceArray((slabs, cap, dim), np.uint8, np.full((slabs, cap, dim), 0xAB, np.uint8))
+    sigma = T.DeviceArray((slabs, cap), np.float32, np.full((slabs, cap), -1.0, np.float32))
+    signs = T.DeviceArray((slabs, cap, W), np.uint32, np.full((slabs, cap, W), 0xCDCDCDCD, np.uint32))
+    rnorm = T.DeviceArray((slabs, cap), np.float32, np.full((slabs, cap), -1.0, np.float32))
+    old = os.environ.get("TQKV_TQ_ENCODE_LANE")
+    os.environ["TQKV_TQ_ENCODE_LANE"] = env
+    try:
+        T.tq_encode(x_dev.ptr, bf16_in, slabs, s, dim, dR.ptr, db.ptr, dc.ptr, bits, dphi.ptr, m,
+                    codes.ptr, sigma.ptr, signs.ptr, rnorm.ptr, cap, start)
+        T.hip().sync()
+    finally:
+        if old is None:
+            del os.environ["TQKV_TQ_ENCODE_LANE"]
+        else:
+            os.environ["TQKV_TQ_ENCODE_LANE"] = old
+    return codes.numpy(), sigma.numpy(), signs.numpy(), rnorm.numpy()
+
+
+@pytest.mark.parametrize("dim,bits,m", [(64, 8, 200), (128, 3, 100), (128, 4, 64), (128, 8, 0),
+                                        (64, 2, 31)])
+def test_encode_lane_kernel_many_rows(T, dim, bits, m):
+    """The four-lanes-per-row kernel (D <= 128) over several 128-row blocks, a
+    ragged last block, slab-to-cache-row mapping, Phi longer than one LDS
+    chunk (m > D): bit-exact with the oracle and with the wavefront-per-row
+    kernel, rows outside [start, start + s) untouched."""
+    slabs, s, cap, start = 3, 211, 240, 17
+    print(f"[tq-encode-lane] dim={dim} bits={bits} m={m} rows={slabs * s}", flush=True)
+    R, phi, b, c = tables(T, dim, bits, m)
+    x = inputs_f32(slabs * s, dim, 1000 + dim + bits + m)
+    xb = O.bf16_from_f32(x)
+    x = O.bf16_to_f32(xb)
+    dx = T.DeviceArray.of(xb.reshape(slabs, s, dim))
+    tabs = tuple(T.DeviceArray.of(a) for a in (R, phi, b, c.astype(np.float32)))
+    lane = _encode_rows(T, dim, bits, m, dx, True, slabs, s, cap, start, tabs, "1")
+    wave = _encode_rows(T, dim, bits, m, dx, True, slabs, s, cap, start, tabs, "0")
+    for a, w in zip(lane, wave):
+        assert np.array_equal(a.view(np.uint8), w.view(np.uint8)), "lane vs wavefront kernel"
+    codes, sigma, signs, rnorm = lane
+    comp = O.Compressor(dim, bits, max(m, 1), R, phi[:max(m, 1)])
+    s1, s2, rn, sc = comp.compress(x)
+    rows = slice(start, start + s)
+    got = codes[:, rows].reshape(-1, dim)
+    packed = np.stack([O.pack_codes(got[i], bits) for i in range(slabs * s)])
+    assert np.array_equal(packed, s1), "codes"
+    assert np.array_equal(sigma[:, rows].reshape(-1).view(np.uint32), sc.view(np.uint32)), "scale"
+    if m > 0:
+        W = (m + 31) // 32
+        assert np.array_equal(rnorm[:, rows].reshape(-1).view(np.uint32), rn.view(np.uint32))
+        want = s2.view(np.uint32).reshape(slabs * s, -1)[:, :W]
+        assert np.array_equal(signs[:, rows].reshape(-1, W), want), "QJL signs"
+    assert np.all(codes[:, :start] == 0xAB) and np.all(codes[:, start + s:] == 0xAB)
+    assert np.all(sigma[:, :start] == -1.0) and np.all(sigma[:, start + s:] == -1.0)
+
+
 def test_kvcache_matches_simple_cache(T):
     dim, bits, m, layers, heads = 128, 3, 64, 2, 2
     kv = T.KVCache(dim, bits, m, 42, layers, heads)
@@ -160,3 +218,38 @@ def test_kvcache_from_given_tables(T):
     assert np.array_equal(np.stack([O.pack_codes(r, bits) for r in codes]), s1)
     assert np.array_equal(signs, s2.view(np.uint32).reshape(11, -1)[:, :1])
     assert np.array_equal(rnorm.view(np.uint32), rn.view(np.uint32))
+
+
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("transpose", [False, True])
+def test_rotate_bf16(T, dim, transpose):
+    """tqkv_rotate_bf16 (the GPU path's rotate_last_axis, turboquant.rs:258-267:
+    y = x R, or x R^T): the four-lanes-per-row kernel (D <= 128, several blocks and a
+    ragged last one) bit-identical to the block-per-row kernel, and both
+    within one bf16 rounding of the f64 product."""
+    import os
+    rows = 333
+    print(f"[rotate] dim={dim} transpose={transpose} rows={rows}", flush=True)
+    R = T.rotation_matrix(dim, 42)
+    xb = kv_bf16((rows, dim), 5, frac=0.02, mult=8.0)
+    dx, dR = T.DeviceArray.of(xb), T.DeviceArray.of(R)
+    outs = []
+    for env in ("1", "0"):
+        y = T.DeviceArray((rows, dim), np.uint16, np.zeros((rows, dim), np.uint16))
+        old = os.environ.get("TQKV_TQ_ENCODE_LANE")
+        os.environ["TQKV_TQ_ENCODE_LANE"] = env
+        try:
+            T.rotate_bf16(dx.ptr, rows, dim, dR.ptr, transpose, y.ptr)
+            T.hip().sync()
+        finally:
+            if old is None:
+                del os.environ["TQKV_TQ_ENCODE_LANE"]
+            else:
+                os.environ["TQKV_TQ_ENCODE_LANE"] = old
+        outs.append(y.numpy())
+    assert np.array_equal(outs[0], outs[1]), "lane vs block-per-row kernel"
+    x = O.bf16_to_f32(xb).astype(np.float64)
+    M = R.astype(np.float64)
+    want = x @ (M.T if transpose else M)
+    got = O.bf16_to_f32(outs[0]).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-5)
