@@ -23,6 +23,8 @@
 #include "lkv.hpp"
 
 namespace tqkv {
+size_t decode_need_bytes(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
+                         bool app);
 namespace {
 
 constexpr int kMaxSlots = 6;
@@ -886,6 +888,34 @@ int32_t tqkv_cache_append_decode(tqkv_cache* c, const uint16_t* k, const uint16_
   const bool has_prefix = c->prefix && c->base_offset > 0;
   const bool last = p.write_at == p.view - 1;
   if (p.write_at < 0 || p.write_at >= p.view || (!last && has_prefix)) return two_calls();
+  if (c->cur[0].cap != c->cur[3].cap)
+    return fail(TQKV_EINVAL_ARG, "K and V buffers of different capacity");
+  // The decode must not fail once the update is committed (its row is only
+  // written by the decode kernel): the workspace it will need is settled
+  // first, from the segment lengths it will attend.
+  {
+    tqkv_affine_seg vs[2]{};
+    int vn = 0;
+    if (has_prefix) {
+      vs[vn].n = c->base_offset;
+      vs[vn++].shared = 1;
+    }
+    if (last) {
+      vs[vn++].n = p.view - 1;
+    } else {
+      vs[vn++].n = p.write_at;
+      vs[vn++].n = p.view - p.write_at - 1;
+    }
+    const size_t need = decode_need_bytes(g.batch, H, g.kv_heads, g.k_dim, vs, vn, true);
+    if (need > 0) {
+      if (!workspace) {
+        void* ws = nullptr;
+        if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+      } else if (workspace_bytes < need) {
+        return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
+      }
+    }
+  }
   const int64_t old_len = c->st.has ? c->st.len : 0;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (int32_t rc = execute(c, p, old_len, st)) return rc;
@@ -912,8 +942,6 @@ int32_t tqkv_cache_append_decode(tqkv_cache* c, const uint16_t* k, const uint16_
     own.n = p.write_at;
     segs[n++] = hi;
   }
-  if (c->cur[0].cap != c->cur[3].cap)
-    return fail(TQKV_EINVAL_ARG, "K and V buffers of different capacity");
   return tqkv_decode_attend_affine_append(
       q, g.batch, H, g.kv_heads, g.k_dim, g.group_size, g.bits_k, g.bits_v, scale, segs, n, k, v,
       reinterpret_cast<uint32_t*>(c->cur[0].ptr), reinterpret_cast<uint16_t*>(c->cur[1].ptr),

@@ -287,6 +287,54 @@ struct AppendDst {
   int64_t cap, row;
 };
 
+// How a decode call splits its keys, and the workspace bytes that needs (0:
+// none). Only the segments' lengths and shared flags matter.
+struct DecodePlan {
+  bool shared_path = false;
+  // Shared prefix read once: prefix splits, then the suffix's.
+  int sp_p = 0, split_len_p = 0, sp_s = 0;
+  int64_t split_len_s = 0;
+  // Per-sequence: splits of the whole context.
+  int n_splits = 1;
+  int64_t split_len = 0;
+  int n_part = 1;
+  size_t need = 0;
+};
+
+DecodePlan plan_decode(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
+                       bool app) {
+  DecodePlan pl;
+  const int G = H / H_kv;
+  const int waves = waves_for_shape(G, D);
+  const int64_t total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
+  // A prefix shared by B >= 2 sequences: read it once per KV head for all of
+  // them (the prefill kernel with the sequences as query rows, split over
+  // the prefix, into partials), each sequence's own suffix with the decode
+  // kernel into further partial slots, then one merge. TQKV_SHARED_PREFIX=0
+  // reads the prefix per sequence instead (tests compare the two).
+  const char* sp_env = getenv("TQKV_SHARED_PREFIX");
+  pl.shared_path = n_segs == 2 && segs[0].shared && B >= 2 && segs[0].n > 0 &&
+                   (D == 64 || D == 128 || D == 256) && !(sp_env && strcmp(sp_env, "0") == 0);
+  const size_t row = size_t(D) + 2;
+  if (pl.shared_path) {
+    pl.sp_p = prefix_splits(H_kv, int64_t(B) * G, prefill::shared_prefix_block_rows(D),
+                            segs[0].n, &pl.split_len_p);
+    const int64_t S = segs[1].n;
+    if (S > 0) plan_splits(B, H_kv, waves, S, &pl.sp_s, &pl.split_len_s);
+    if (app && pl.sp_s == 0) {  // the new row needs a suffix launch
+      pl.sp_s = 1;
+      pl.split_len_s = 64;
+    }
+    pl.n_part = pl.sp_p + pl.sp_s;
+    pl.need = size_t(B) * H * pl.n_part * row * sizeof(float);
+    return pl;
+  }
+  plan_splits(B, H_kv, waves, total, &pl.n_splits, &pl.split_len);
+  pl.n_part = pl.n_splits;
+  pl.need = pl.n_splits > 1 ? size_t(B) * H * pl.n_splits * row * sizeof(float) : 0;
+  return pl;
+}
+
 int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D,
                       int32_t group_size, int32_t bits_k, int32_t bits_v, float scale,
                       const tqkv_affine_seg* segs, int32_t n_segs, const AppendDst* app,
@@ -357,81 +405,56 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
 
   const int waves = waves_for_shape(G, D);
   a.out = out;
+  const DecodePlan pl = plan_decode(B, H, H_kv, D, segs, n_segs, app != nullptr);
+  void* ws = workspace;
+  if (pl.need > 0) {
+    if (!ws) {
+      if (int32_t rc = scratch_for_current_device(pl.need, &ws)) return rc;
+    } else if (workspace_bytes < pl.need) {
+      return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, pl.need);
+    }
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 
-  // A prefix shared by B >= 2 sequences: read it once per KV head for all of
-  // them (the prefill kernel with the sequences as query rows, split over
-  // the prefix, into partials), each sequence's own suffix with the decode
-  // kernel into further partial slots, then one merge. TQKV_SHARED_PREFIX=0
-  // reads the prefix per sequence instead (tests compare the two).
-  const char* sp_env = getenv("TQKV_SHARED_PREFIX");
-  const bool shared_path = n_segs == 2 && segs[0].shared && B >= 2 && segs[0].n > 0 &&
-                           (D == 64 || D == 128 || D == 256) &&
-                           !(sp_env && strcmp(sp_env, "0") == 0);
-  if (shared_path) {
-    int split_len_p = 0;
-    const int sp_p = prefix_splits(H_kv, int64_t(B) * G, prefill::shared_prefix_block_rows(D),
-                                   segs[0].n, &split_len_p);
-    const int64_t S = segs[1].n;
+  if (pl.shared_path) {
     Args s = a;
     s.seg[0] = a.seg[1];
-    s.n0 = S;
-    s.total = S;
-    int sp_s = 0;
-    if (S > 0) plan_splits(B, H_kv, waves, S, &sp_s, &s.split_len);
-    if (app && sp_s == 0) {  // the new row needs a suffix launch
-      sp_s = 1;
-      s.split_len = 64;
-    }
-    const int n_part = sp_p + sp_s;
-    const size_t need = size_t(B) * H * n_part * (size_t(D) + 2) * sizeof(float);
-    void* ws = workspace;
-    if (!ws) {
-      if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
-    } else if (workspace_bytes < need) {
-      return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
-    }
+    s.n0 = segs[1].n;
+    s.total = segs[1].n;
+    s.split_len = pl.split_len_s;
     float* po = static_cast<float*>(ws);
-    float* pm = po + size_t(B) * H * n_part * D;
-    float* pl = pm + size_t(B) * H * n_part;
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    float* pm = po + size_t(B) * H * pl.n_part * D;
+    float* pl_ = pm + size_t(B) * H * pl.n_part;
     if (int32_t rc = prefill::shared_prefix_partials(q, B, H, H_kv, D, group_size, bits_k, bits_v,
-                                                     scale, segs[0], sp_p, split_len_p, n_part,
-                                                     po, pm, pl, st))
+                                                     scale, segs[0], pl.sp_p, pl.split_len_p,
+                                                     pl.n_part, po, pm, pl_, st))
       return rc;
-    if (sp_s > 0) {
-      KernelFn sfn = app ? fn : pick(D, bits_k, bits_v, G, group_size, S);
-      s.n_splits = sp_s;
-      s.split_base = sp_p;
-      s.n_part = n_part;
+    if (pl.sp_s > 0) {
+      KernelFn sfn = app ? fn : pick(D, bits_k, bits_v, G, group_size, segs[1].n);
+      s.n_splits = pl.sp_s;
+      s.split_base = pl.sp_p;
+      s.n_part = pl.n_part;
       s.part_o = po;
       s.part_m = pm;
-      s.part_l = pl;
-      hipLaunchKernelGGL(sfn, dim3(unsigned(sp_s), unsigned(H_kv), unsigned(B)),
+      s.part_l = pl_;
+      hipLaunchKernelGGL(sfn, dim3(unsigned(pl.sp_s), unsigned(H_kv), unsigned(B)),
                          dim3(kWave * waves), 0, st, s);
       TQKV_LAUNCHED();
     }
-    launch_merge(po, pm, pl, n_part, D, int64_t(B) * H, out, st);
+    launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
     return ok();
   }
 
-  plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
+  a.n_splits = pl.n_splits;
+  a.split_len = pl.split_len;
   a.split_base = 0;
   a.n_part = a.n_splits;
   if (a.n_splits > 1) {
-    const size_t need = size_t(B) * H * a.n_splits * (size_t(D) + 2) * sizeof(float);
-    void* ws = workspace;
-    if (!ws) {
-      if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
-    } else if (workspace_bytes < need) {
-      return fail(TQKV_EINVAL_ARG, "workspace of %zu bytes, need %zu", workspace_bytes, need);
-    }
     a.part_o = static_cast<float*>(ws);
     a.part_m = a.part_o + size_t(B) * H * a.n_splits * D;
     a.part_l = a.part_m + size_t(B) * H * a.n_splits;
   }
-
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
                      dim3(kWave * waves), 0, st, a);
   TQKV_LAUNCHED();
@@ -470,6 +493,17 @@ extern "C" int32_t tqkv_decode_attend_affine_append(
   return decode_affine(q, B, H, H_kv, D, group_size, bits_k, bits_v, scale, segs, n_segs, &app,
                        out, workspace, workspace_bytes, stream);
 }
+
+namespace tqkv {
+// The workspace bytes a decode over segments of these lengths needs (0: it
+// writes no split partials). tqkv_cache_append_decode checks it before it
+// commits a cache update.
+size_t decode_need_bytes(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
+                         bool app) {
+  if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n_segs < 1 || n_segs > 2) return 0;
+  return plan_decode(B, H, H_kv, D, segs, n_segs, app).need;
+}
+}  // namespace tqkv
 
 // Decode over chosen 64-row pages of one cache segment plus its undigested
 // tail (the attention half of sdpa_page_sparse, native_attention.rs:272-291):

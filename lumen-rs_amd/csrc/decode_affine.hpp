@@ -14,9 +14,10 @@
 //   Keys: pairs of channels of one token against f16 query pairs pre-scaled by
 //   2^(E - o); the score is scale * sum(q * c) + bias * sum(q) per group (the
 //   affine terms factor out), summed over the lane group by a butterfly.
-//   Values: one channel of the token pair against the two tokens' f32 weights
-//   p * scale split into f16 hi + lo parts (~22 significant bits); the bias
-//   term p * bias accumulates apart in f32.
+//   Values: one channel of the token pair against the two tokens' weights
+//   p * scale rounded to f16; the bias term p * bias accumulates apart in
+//   f32. A wave-uniform power of two per head (folded into the softmax
+//   reference) keeps the f16 weights finite whatever the value scales.
 // The online softmax keeps its running maximum up to kTau (log2 units) behind
 // the true one, so accumulators are rescaled only when it moves by more.
 // Lane groups, then wavefronts (through LDS), merge their (max, sum, acc)
@@ -218,10 +219,24 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Max over the whole wavefront, every lane getting it.
+__device__ __forceinline__ float wave_max_all(float v) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
 // Running maxima may lag the true maximum by up to kTau (log2 units) before
 // the accumulators are rescaled: weights stay <= 2^kTau, and rescales become
 // rare after the first keys.
 constexpr float kTau = 8.0f;
+
+// Value weights p * scale travel as f16 (finite below 65,504). With p <=
+// 2^kTau, scales up to kScaleSafe keep every weight <= kWeightMax; a step
+// with a larger scale checks its products and, where one passes kWeightMax,
+// moves the head's softmax reference up by a power of two.
+constexpr float kScaleSafe = 128.0f;  // 2^(15 - kTau)
+constexpr float kWeightMax = 32768.0f;
 
 template <int D, int BK, int BV, int G, int EPL, int kWaves>
 __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
@@ -282,11 +297,16 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
   const int64_t w_begin = t_begin + wave * chunk;
   const int64_t w_end = w_begin + chunk < t_end ? w_begin + chunk : t_end;
 
-  float m[G], l[G], bacc[G];
+  // m: the lane group's running maximum; ev: a wave-uniform exponent raised
+  // only when an f16 value weight would overflow; mr = m + ev, the reference
+  // the weights 2^(s - mr), l and acc are taken against.
+  float m[G], mr[G], ev[G], l[G], bacc[G];
   float acc[G][EPL];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     m[h] = -INFINITY;
+    mr[h] = -INFINITY;
+    ev[h] = 0.0f;
     l[h] = 0.0f;
     bacc[h] = 0.0f;
 #pragma unroll
@@ -332,6 +352,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
     uint32_t wp[G];
     const float vs0 = bf16_to_f32(f.vs[0]), vs1 = bf16_to_f32(f.vs[1]);
     const float vb0 = bf16_to_f32(f.vb[0]), vb1 = bf16_to_f32(f.vb[1]);
+    const bool big = __builtin_expect(__any(fmaxf(fabsf(vs0), fabsf(vs1)) > kScaleSafe), 0);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       // Online softmax with a lazily moved maximum.
@@ -345,9 +366,27 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[h][e] *= fct;
         m[h] = mnew;
+        mr[h] = mnew + ev[h];
       }
-      const float p0 = (kMasked && sc[0][h] == -INFINITY) ? 0.0f : ex2(sc[0][h] - m[h]);
-      const float p1 = (kMasked && sc[1][h] == -INFINITY) ? 0.0f : ex2(sc[1][h] - m[h]);
+      float p0 = (kMasked && sc[0][h] == -INFINITY) ? 0.0f : ex2(sc[0][h] - mr[h]);
+      float p1 = (kMasked && sc[1][h] == -INFINITY) ? 0.0f : ex2(sc[1][h] - mr[h]);
+      if (big) {
+        // p <= 2^kTau and a scale past kScaleSafe: check the products.
+        const float pm = wave_max_all(fmaxf(fabsf(p0 * vs0), fabsf(p1 * vs1)));
+        if (pm > kWeightMax) {
+          int e = 0;
+          frexpf(pm * (1.0f / kWeightMax), &e);  // pm * 2^-e < kWeightMax
+          const float fct = __builtin_ldexpf(1.0f, -e);
+          ev[h] += float(e);
+          mr[h] = m[h] + ev[h];
+          l[h] *= fct;
+          bacc[h] *= fct;
+#pragma unroll
+          for (int e2 = 0; e2 < EPL; ++e2) acc[h][e2] *= fct;
+          p0 *= fct;
+          p1 *= fct;
+        }
+      }
       l[h] += p0 + p1;
       bacc[h] = fmaf(p0, vb0, fmaf(p1, vb1, bacc[h]));
       wp[h] = h2_bits(h2_t{_Float16(p0 * vs0), _Float16(p1 * vs1)});
@@ -406,6 +445,9 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h][vc.e] = fmaf(acc[h][vc.e], unscale, bacc[h]);
   });
+  // From here m is the reference of l and acc (the running maximum + ev).
+#pragma unroll
+  for (int h = 0; h < G; ++h) m[h] = mr[h];
 #pragma unroll
   for (int off = LPT; off < kWave; off <<= 1) {
 #pragma unroll

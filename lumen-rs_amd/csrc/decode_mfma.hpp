@@ -333,10 +333,14 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   const int64_t w_begin = t_begin + wave * chunk;
   const int64_t w_end = w_begin + chunk < t_end ? w_begin + chunk : t_end;
 
-  float m[G], l[G], bacc[G], mlane[HPL];
+  // ev[h]: a wave-uniform exponent folded into head h's softmax reference
+  // (weights are 2^(s - m - ev)), raised only when a value weight p * scale
+  // would leave the f16 range (see values()).
+  float m[G], l[G], bacc[G], mlane[HPL], ev[G];
   float acc[G][EV];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
+    ev[h] = 0.0f;
     m[h] = -INFINITY;
     l[h] = 0.0f;
     bacc[h] = 0.0f;
@@ -504,7 +508,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 #pragma unroll
         for (int h = 0; h < G; ++h)
           if (hl[hh] == h) {
-            mlane[hh] = m[h];
+            mlane[hh] = m[h] + ev[h];
             mtau[hh] = m[h] + kTau;
           }
       }
@@ -520,10 +524,40 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       out.p1[h] = __shfl(p[reg], grp_lane + vp + 8, kWave);
     });
   };
-  // Values of a scored step.
-  auto values = [&](const VBuf& f, const Pend& w) {
+  // Values of a scored step; `nxt` holds the next step's weights, already
+  // scored against the same reference.
+  // The f16 weight p * scale must stay finite: p <= 2^kTau, so a step whose
+  // |scales| are all <= 2^(15 - kTau) is safe as it stands (the common case:
+  // one max and one compare). Otherwise the products are checked, and a head
+  // where one passes 2^15 moves its reference up by a power of two: every
+  // accumulator and pending weight of that head is scaled down by it, exactly
+  // as when the running maximum moves.
+  auto values = [&](const VBuf& f, Pend& w, Pend& nxt) {
     const float vs0 = bf16_to_f32(f.vs[0]), vs1 = bf16_to_f32(f.vs[1]);
     const float vb0 = bf16_to_f32(f.vb[0]), vb1 = bf16_to_f32(f.vb[1]);
+    if (__builtin_expect(__any(fmaxf(fabsf(vs0), fabsf(vs1)) > kScaleSafe), 0)) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float pm = wave_max(fmaxf(fabsf(w.p0[h] * vs0), fabsf(w.p1[h] * vs1)));
+        if (pm > kWeightMax) {
+          int e = 0;
+          frexpf(pm * (1.0f / kWeightMax), &e);  // pm * 2^-e < kWeightMax
+          const float fct = __builtin_ldexpf(1.0f, -e);
+          ev[h] += float(e);
+          l[h] *= fct;
+          bacc[h] *= fct;
+#pragma unroll
+          for (int c = 0; c < EV; ++c) acc[h][c] *= fct;
+          w.p0[h] *= fct;
+          w.p1[h] *= fct;
+          nxt.p0[h] *= fct;
+          nxt.p1[h] *= fct;
+#pragma unroll
+          for (int hh = 0; hh < HPL; ++hh)
+            if (hl[hh] == h) mlane[hh] = m[h] + ev[h];
+        }
+      }
+    }
     uint32_t wp[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -590,19 +624,19 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
         load_k(k0, r, cl(i + 2), kt);
         load_v(v1, r, cl(i + 1), vp, vp + 8);
         score(k1, true, full, p0, p1);
-        values(v0, p0);
+        values(v0, p0, p1);
         load_k(k1, r, cl(i + 3), kt);
         load_v(v0, r, cl(i + 2), vp, vp + 8);
         score(k0, true, full, p1, p0);
-        values(v1, p1);
+        values(v1, p1, p0);
       }
       if (i + 1 < n) {
         load_v(v1, r, cl(i + 1), vp, vp + 8);
         score(k1, true, full, p0, p1);
-        values(v0, p0);
-        values(v1, p1);
+        values(v0, p0, p1);
+        values(v1, p1, p0);
       } else {
-        values(v0, p0);
+        values(v0, p0, p1);
       }
     }
     const uint32_t left = nrows - n * kStep;
@@ -618,7 +652,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       load_k(kf_, r, 0, kt < left ? kt : lst);
       load_v(vf_, r, 0, vp < left ? vp : lst, vp + 8 < left ? vp + 8 : lst);
       score(kf_, kt < left, masked, pz, pt);
-      values(vf_, pt);
+      values(vf_, pt, pz);
     }
   }
   if (app) {
@@ -649,7 +683,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
     vf_.vs[0] = vf_.vs[1] = s_avs[vgrp];
     vf_.vb[0] = vf_.vb[1] = s_avb[vgrp];
     score(kf_, kt == 0, std::integral_constant<bool, true>{}, pz, pt);
-    values(vf_, pt);
+    values(vf_, pt, pz);
   }
 
   // ---- merge: undo the code scale, add the bias term, sum the token pairs
@@ -686,7 +720,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       if (vc == 0) {
-        s_m[wave][h] = m[h];
+        s_m[wave][h] = m[h] + ev[h];  // the reference of l and acc
         s_l[wave][h] = l[h];
       }
 #pragma unroll

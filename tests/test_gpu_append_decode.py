@@ -248,3 +248,59 @@ def test_kernel_entry_row_mid_buffer(T):
     want = want_of(q, np.concatenate([K0, k], axis=2), np.concatenate([V0, v], axis=2),
                    64, bk, bv, 0.0625)
     check_close(out.numpy(), want)
+
+
+def test_single_split_with_append(T, monkeypatch):
+    # One split a unit (the headline's launch shape: no partials, the output
+    # normalized in the kernel) with the new token quantized in the kernel,
+    # across a growth step, against the two calls and the oracle.
+    monkeypatch.setenv("TQKV_DECODE_SPLITS", "1")
+    B, Hq, Hkv, D, bits = 2, 16, 8, 256, 3
+    tw = Twin(T, B, Hkv, D, bits, bits, prealloc=True)
+    k0 = kv_bf16((B, Hkv, 509, D), 41, frac=0.01, mult=10.0)
+    v0 = kv_bf16((B, Hkv, 509, D), 42, frac=0.01, mult=10.0)
+    tw.append(k0, v0)
+    ks, vs = [k0], [v0]
+    for i in range(4):  # rows 509-512: the last crosses the 512-row buffer
+        k = kv_bf16((B, Hkv, 1, D), 43 + i, frac=0.01, mult=10.0)
+        v = kv_bf16((B, Hkv, 1, D), 53 + i, frac=0.01, mult=10.0)
+        q = kv_bf16((B, Hq, 1, D), 63 + i)
+        ks.append(k)
+        vs.append(v)
+        got, ref = tw.step(k, v, q, Hq, D ** -0.5)
+        K, V = np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
+        print(f"[append-decode 1split] step={i} keys={K.shape[2]}", flush=True)
+        want = want_of(q, K, V, 64, bits, bits, D ** -0.5)
+        check_close(got, want)
+        check_close(ref, want)
+
+
+def test_failed_decode_leaves_cache_unchanged(T):
+    # A decode step whose workspace is too small for its split partials must
+    # fail before the cache counts the token: state and bytes as before, and
+    # the same step then succeeds with room (tqkv_cache_append_decode).
+    B, Hq, Hkv, D, bits = 1, 32, 8, 128, 4
+    tw = Twin(T, B, Hkv, D, bits, bits, prealloc=True)
+    k0 = kv_bf16((B, Hkv, 3000, D), 71)
+    v0 = kv_bf16((B, Hkv, 3000, D), 72)
+    tw.append(k0, v0)
+    before = tw.fused.state()
+    bytes_before = slots_of(tw.fused, B, Hkv, D, 64, bits, bits)
+    k, v, q = kv_bf16((B, Hkv, 1, D), 73), kv_bf16((B, Hkv, 1, D), 74), kv_bf16((B, Hq, 1, D), 75)
+    dk, dv, dq = T.DeviceArray.of(k), T.DeviceArray.of(v), T.DeviceArray.of(q)
+    out = T.DeviceArray(q.shape, np.uint16)
+    small = T.DeviceArray((16,), np.uint8)
+    with pytest.raises(T.TqkvError) as e:
+        tw.fused.append_decode(dk.ptr, dv.ptr, dq.ptr, Hq, D ** -0.5, out.ptr, small.ptr, 16)
+    assert e.value.status == T.EINVAL_ARG
+    T.hip().sync()
+    after = tw.fused.state()
+    assert (after.offset, after.idx, after.cached_len, after.view) == \
+        (before.offset, before.idx, before.cached_len, before.view)
+    for i, (x, y) in enumerate(zip(bytes_before, slots_of(tw.fused, B, Hkv, D, 64, bits, bits))):
+        assert np.array_equal(x, y), f"slot {i} changed"
+    got, ref = tw.step(k, v, q, Hq, D ** -0.5)
+    want = want_of(q, np.concatenate([k0, k], axis=2), np.concatenate([v0, v], axis=2),
+                   64, bits, bits, D ** -0.5)
+    check_close(got, want)
+    check_close(ref, want)
