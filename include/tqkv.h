@@ -144,6 +144,26 @@ int32_t tqkv_decode_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32
                                   size_t workspace_bytes, tqkv_stream stream);
 
 /*
+ * tqkv_decode_attend_affine without any allocation: no counterpart in the
+ * reference. For callers that cannot call hipMalloc (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid it). Same arguments
+ * and results (bit-identical: the same kernels and split plan) as
+ * tqkv_decode_attend_affine without a workspace: the split partials live in
+ * a static device array of TQKV_NOALLOC_SCRATCH_BYTES that every device
+ * running the library holds until the process ends. The first call on a
+ * device looks up that device's copy (make it outside any graph capture);
+ * later calls allocate nothing. A call needing more partial bytes than the
+ * array holds returns TQKV_EINVAL_SHAPE. All calls on one device share the
+ * array: calls that overlap in time on one device race.
+ */
+#define TQKV_NOALLOC_SCRATCH_BYTES 33554432 /* 32 MiB */
+int32_t tqkv_decode_attend_affine_noalloc(const uint16_t* q, int32_t B, int32_t H,
+                                          int32_t H_kv, int32_t D, int32_t group_size,
+                                          int32_t bits_k, int32_t bits_v, float scale,
+                                          const tqkv_affine_seg* segs, int32_t n_segs,
+                                          uint16_t* out, tqkv_stream stream);
+
+/*
  * A decode step's append and attention in one kernel: the reference's
  * update_and_fetch of one token followed by quantized_decode_attention over
  * the fetched view (gemma4_moe.rs:4081, 4125). Same result as

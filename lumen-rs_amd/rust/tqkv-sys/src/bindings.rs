@@ -14,6 +14,7 @@ pub const TQKV_EDEVICE: i32 = 4;
 pub const TQKV_ENOMEM: i32 = 5;
 pub const TQKV_EINVAL_ARG: i32 = 6;
 pub const TQKV_ECORRUPT: i32 = 7;
+pub const TQKV_NOALLOC_SCRATCH_BYTES: i32 = 33554432;
 pub const TQKV_CACHE_BF16: i32 = 0;
 pub const TQKV_CACHE_AFFINE: i32 = 1;
 pub const TQKV_CACHE_CODEBOOK: i32 = 2;
@@ -115,6 +116,7 @@ extern "C" {
     pub fn tqkv_affine_quantize_kv(k: *const u16, v: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits_k: i32, bits_v: i32, k_packed: *mut u32, k_scales: *mut u16, k_biases: *mut u16, v_packed: *mut u32, v_scales: *mut u16, v_biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_dequantize(packed: *const u32, scales: *const u16, biases: *const u16, rows: i64, dim: i32, group_size: i32, bits: i32, out: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_decode_attend_affine(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
+    pub fn tqkv_decode_attend_affine_noalloc(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, out: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_decode_attend_affine_append(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, k: *const u16, v: *const u16, k_packed: *mut u32, k_scales: *mut u16, k_biases: *mut u16, v_packed: *mut u32, v_scales: *mut u16, v_biases: *mut u16, dst_cap: i64, dst_row: i64, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
     pub fn tqkv_page_digest_affine(k_packed: *const u32, k_scales: *const u16, k_biases: *const u16, n_slabs: i64, cap: i64, dim: i32, group_size: i32, bits: i32, page_from: i64, page_to: i64, key_min: *mut u16, key_max: *mut u16, max_pages: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_sparse_keep_pages(pages: i64) -> i64;

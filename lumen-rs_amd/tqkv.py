@@ -86,6 +86,8 @@ _SIGS = {
     "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
+    "tqkv_decode_attend_affine_noalloc": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
+                                                ctypes.POINTER(AffineSeg), I32, P, P]),
     "tqkv_decode_attend_affine_append": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                                ctypes.POINTER(AffineSeg), I32, P, P, P, P, P,
                                                P, P, P, I64, I64, P, P, SZ, P]),
@@ -351,6 +353,15 @@ def decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, out,
     arr = (AffineSeg * len(segs))(*segs)
     check(lib().tqkv_decode_attend_affine(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, arr,
                                           len(segs), out, workspace, workspace_bytes, stream))
+
+
+def decode_attend_affine_noalloc(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, out,
+                                 stream=None):
+    """tqkv_decode_attend_affine with its split partials in the library's
+    static device scratch (no allocation)."""
+    arr = (AffineSeg * len(segs))(*segs)
+    check(lib().tqkv_decode_attend_affine_noalloc(q, B, H, H_kv, D, gs, bits_k, bits_v, scale,
+                                                  arr, len(segs), out, stream))
 
 
 def decode_attend_affine_append(q, B, H, H_kv, D, gs, bits_k, bits_v, scale, segs, k, v, dst,
