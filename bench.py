@@ -217,7 +217,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16 in/out, f16 operands, f32 accumulate",
         "data": "synthetic",
         "config": {
             "workload": "BASELINE config 2: batched decode over a 3-bit affine cache "
@@ -236,6 +236,10 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": ("profile-derived, not counted in this run: the FETCH_SIZE x 2.000 + "
+                               "WRITE_SIZE counter passes of profiles/decode_affine_config2.md "
+                               "give 1.000646 HBM bytes per algorithmic byte, applied to this "
+                               "run's algorithmic bytes" if traffic is not None else None),
             "kernel": kernel,
             "alg_bytes_per_launch": int(alg_bytes),
             "avg_launch_ms": round(dec_avg_ms, 5),
@@ -252,37 +256,70 @@ def main():
 
 
 def cpu_baseline(T, cache, q, out, B, H, HKV, D, N, GS, BITS, scale, cap, budget_s):
-    """The oracle's dequantize-then-attend (the reference's CPU semantics,
-    restated in C++, OpenMP over heads) on a bounded sample: whole sequences
-    of the same cache, as many as fit the time budget."""
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import oracle_lib as O
-
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    """The reference's decode semantics as an f32 CPU port (dequantize
+    exactly, f32 scores / softmax / weighted sum, bf16 out; OpenMP over
+    (sequence, KV head)) on whole sequences of the same cache: sequence 0 at
+    one thread, and enough sequences for every thread at the box's thread
+    count."""
+    O, threads = _oracle()
+    n_seq = max(1, min(B, -(-2 * threads // HKV)))
     qh = q.numpy()
-    triples = {}
-    for name in ("k", "v"):
-        triples[name] = [a.numpy().reshape(B, HKV, cap, -1) for a in cache[name]]
+    kt = tuple(T.hip().download(a.ptr, (n_seq, HKV, cap, a.shape[-1]), a.dtype)
+               for a in cache["k"])
+    vt = tuple(T.hip().download(a.ptr, (n_seq, HKV, cap, a.shape[-1]), a.dtype)
+               for a in cache["v"])
 
-    def one(b):
-        kt = tuple(np.ascontiguousarray(a[b:b + 1, :, :N]) for a in triples["k"])
-        vt = tuple(np.ascontiguousarray(a[b:b + 1, :, :N]) for a in triples["v"])
+    def run(n, th):
+        return lambda: O.attend_affine_f32(qh[:n], tuple(a[:n] for a in kt),
+                                           tuple(a[:n] for a in vt), N, GS, BITS, BITS, scale,
+                                           threads=th)
+
+    return _port_baseline(run(1, 1), 1, run(n_seq, threads), n_seq, threads, budget_s,
+                          f"decode steps over the benchmark's own cache, {HKV} KV heads x {N} "
+                          f"tokens a sequence: sequence 0 at 1 thread, sequences 0-{n_seq - 1} "
+                          f"at {threads} threads")
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _port_baseline(fn1, tok1, fnn, tokn, threads, budget_s, sample):
+    """Median time of fn1 (1 thread, tok1 tokens a call) and fnn (`threads`
+    threads, tokn tokens a call) after one warm-up call each, as many timed
+    calls (3 to 10) as fit about half the budget each; value = tokens/s at
+    `threads` threads, single_thread beside it."""
+    def med(fn):
         t = time.perf_counter()
-        O.attend_affine(qh[b:b + 1], kt, vt, GS, BITS, BITS, scale)
-        return time.perf_counter() - t
+        fn()
+        first = time.perf_counter() - t
+        reps = int(max(3, min(10, 0.5 * budget_s / max(first, 1e-3))))
+        times = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t)
+        return float(np.median(times)), reps
 
-    first = one(0)
-    n_seq = max(1, min(B, int(budget_s / max(first, 1e-3))))
-    times = [first] + [one(b) for b in range(1, n_seq)]
-    per_seq = float(np.median(times))
+    t1, r1 = med(fn1)
+    tn, rn = med(fnn)
     return {
-        "value": round(1.0 / per_seq, 3),
-        "unit": "tokens/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"{n_seq} of {B} sequences of the same cache, {HKV} KV heads x {N} tokens each "
-                  f"(median {per_seq:.3f} s per sequence-step); C++ restatement of "
-                  "dequantize-then-attend, OpenMP over heads",
+        "value": round(tokn / tn, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+        "sample": sample + f"; f32 dequantize-then-attend (the oracle library's CPU port of "
+                           f"the reference's semantics), median of {r1} / {rn} calls after a "
+                           f"warm-up",
+        "single_thread": {"value": round(tok1 / t1, 3), "unit": "tokens/s", "cores": 1,
+                          "s_per_call": round(t1, 4)},
+        "s_per_call": round(tn, 4),
+        "cpu_model": _cpu_model(),
+        "cpus_visible": os.cpu_count(),
     }
 
 
@@ -400,25 +437,24 @@ def prefill_main(T, hip, args):
 
 
 def prefill_cpu_baseline(T, cg, q, B, H, HKV, D, L, N, GS, BITS, q_start):
-    """The oracle's dequantize(bf16)-then-attend on the last 32 query rows of
-    batch row 0 (all heads, all 16,384 keys): tokens/s = rows / time."""
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    import oracle_lib as O
-
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    """The f32 CPU port of dequantize(bf16)-then-attend on the chunk's last
+    32 query rows (all heads, all keys): batch row 0 at one thread, every
+    batch row at the box's thread count; tokens/s = rows / time."""
+    O, threads = _oracle()
     rows = 32
-    qh = q.numpy()[0:1, :, L - rows:]
-    kt = tuple(np.ascontiguousarray(a.numpy().reshape(B, HKV, N, -1)[0:1]) for a in cg["k"])
-    vt = tuple(np.ascontiguousarray(a.numpy().reshape(B, HKV, N, -1)[0:1]) for a in cg["v"])
-    t = time.perf_counter()
-    O.attend_affine(np.ascontiguousarray(qh), kt, vt, GS, BITS, BITS, 1.0, causal=True,
-                    q_start=q_start + L - rows, first_held=0, dequant="bf16")
-    dt = time.perf_counter() - t
-    return {
-        "value": round(rows / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-        "sample": f"last {rows} query rows of batch row 0, {H} heads x {N} keys "
-                  f"({dt:.2f} s); C++ restatement of dequantize(bf16)-then-attend",
-    }
+    qh = np.ascontiguousarray(q.numpy()[:, :, L - rows:])
+    kt = tuple(np.ascontiguousarray(a.numpy().reshape(B, HKV, N, -1)) for a in cg["k"])
+    vt = tuple(np.ascontiguousarray(a.numpy().reshape(B, HKV, N, -1)) for a in cg["v"])
+
+    def run(n, th):
+        return lambda: O.attend_affine_f32(qh[:n], tuple(a[:n] for a in kt),
+                                           tuple(a[:n] for a in vt), N, GS, BITS, BITS, 1.0,
+                                           threads=th, causal=True, q_start=q_start + L - rows,
+                                           first_held=0, dequant="bf16")
+
+    return _port_baseline(run(1, 1), rows, run(B, threads), B * rows, threads, 12.0,
+                          f"the last {rows} query rows of the chunk, {H} heads x {N} keys: batch "
+                          f"row 0 at 1 thread, all {B} batch rows at {threads} threads")
 
 
 # ------------------------------------------------------------ other configs
@@ -641,7 +677,7 @@ def decode1_main(T, hip, args):
     alg = 2 * slabs * ctx * row + 2 * B * H * D * 2
     result = _line(
         "single-sequence quantized-KV decode tokens/s", 1.0 / (step_ms * 1e-3), "tokens/s", step_ms,
-        args, "f32",
+        args, "bf16 in/out, f16 operands, f32 accumulate",
         {"workload": "BASELINE config 1: 1 sequence, 32/8 heads, D=128, 4-bit gs64, 8,192 "
                      "context, 256 steps each appending one token",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N, "steps": steps,
@@ -654,13 +690,15 @@ def decode1_main(T, hip, args):
         O, threads = _oracle()
         kt = tuple(a.numpy()[:, :pos[0]].reshape(B, HKV, pos[0], -1) for a in kc)
         vt = tuple(a.numpy()[:, :pos[0]].reshape(B, HKV, pos[0], -1) for a in vc)
-        t = time.perf_counter()
-        O.attend_affine(q.numpy(), kt, vt, GS, BITS, BITS, D ** -0.5)
-        dt = time.perf_counter() - t
-        result["cpu_baseline"] = {"value": round(1.0 / dt, 2), "unit": "tokens/s", "cores": threads,
-                                  "kind": "port",
-                                  "sample": f"oracle dequantize-then-attend of one decode step "
-                                            f"({pos[0]} keys, {dt:.3f} s)"}
+        qh = q.numpy()
+
+        def run(th):
+            return lambda: O.attend_affine_f32(qh, kt, vt, pos[0], GS, BITS, BITS, D ** -0.5,
+                                               threads=th)
+
+        result["cpu_baseline"] = _port_baseline(
+            run(1), 1, run(threads), 1, threads, 12.0,
+            f"one decode step of the sequence ({pos[0]} keys, {HKV} KV heads)")
     print(json.dumps(result))
 
 
@@ -744,7 +782,7 @@ def prefix_main(T, hip, args):
     naive = B * HKV * (P + ctx) * row + 2 * B * H * D * 2
     result = _line(
         "prefix-shared quantized-KV decode tokens/s", B / (total / steps * 1e-3), "tokens/s",
-        total / steps, args, "f32",
+        total / steps, args, "bf16 in/out, f16 operands, f32 accumulate",
         {"workload": "BASELINE config 4: 8 sequences sharing a 65,536-token prefix plus 4,096 "
                      "own tokens, 32/8 heads, D=128, K 8-bit / V 4-bit gs64, 128 decode steps",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "prefix": P, "suffix": S0,
@@ -757,17 +795,25 @@ def prefix_main(T, hip, args):
          "per_sequence_path_ms_per_step": round(per_seq_ms, 5)}, settle, steps)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
-        cat = lambda a, b: np.concatenate([a.numpy()[:, :P].reshape(1, HKV, P, -1),
-                                           b.numpy()[:HKV, :pos[0]].reshape(1, HKV, pos[0], -1)], axis=2)
-        kt = tuple(cat(a, b) for a, b in zip(pk, sk))
-        vt = tuple(cat(a, b) for a, b in zip(pv, sv))
-        t = time.perf_counter()
-        O.attend_affine(q.numpy()[:1], kt, vt, GS, BK, BV, D ** -0.5)
-        dt = time.perf_counter() - t
-        result["cpu_baseline"] = {"value": round(1.0 / dt, 3), "unit": "tokens/s", "cores": threads,
-                                  "kind": "port",
-                                  "sample": f"oracle dequantize-then-attend of sequence 0 over "
-                                            f"prefix + suffix ({P + pos[0]} keys, {dt:.2f} s)"}
+        n_seq = max(1, min(B, -(-2 * threads // HKV)))
+        pre = [a.numpy()[:, :P] for a in (*pk, *pv)]
+        suf = [a.numpy()[:n_seq * HKV, :pos[0]] for a in (*sk, *sv)]
+        cat = lambda p_, s_: np.concatenate(
+            [np.broadcast_to(p_.reshape(1, HKV, P, -1), (n_seq, HKV, P, p_.shape[-1])),
+             s_.reshape(n_seq, HKV, pos[0], -1)], axis=2)
+        full = [cat(p_, s_) for p_, s_ in zip(pre, suf)]
+        kt, vt = tuple(full[:3]), tuple(full[3:])
+        qh = q.numpy()
+
+        def run(n, th):
+            return lambda: O.attend_affine_f32(qh[:n], tuple(a[:n] for a in kt),
+                                               tuple(a[:n] for a in vt), P + pos[0], GS, BK, BV,
+                                               D ** -0.5, threads=th)
+
+        result["cpu_baseline"] = _port_baseline(
+            run(1, 1), 1, run(n_seq, threads), n_seq, threads, 12.0,
+            f"decode steps over prefix + suffix ({P + pos[0]} keys, the prefix read per "
+            f"sequence): sequence 0 at 1 thread, sequences 0-{n_seq - 1} at {threads} threads")
     print(json.dumps(result))
 
 
@@ -853,7 +899,7 @@ def sparse_main(T, hip, args):
     dense_b = 2 * slabs * (ctx0 + steps / 2.0) * row + 2 * B * H * D * 2
     result = _line(
         "page-sparse quantized-KV decode tokens/s @ B=32, 32K ctx", B / (step_ms * 1e-3),
-        "tokens/s", step_ms, args, "f32",
+        "tokens/s", step_ms, args, "bf16 in/out, f16 operands, f32 accumulate",
         {"workload": "config 2's shape (B=32, 16/8 heads, D=256, 32K context, 3-bit gs64) with "
                      "page-sparse decode: keep max(pages/8, 64) pages + sink + 4 recent + tail",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N,
@@ -933,7 +979,7 @@ def layers_main(T, hip, args):
     alg = sum(2 * slabs * v * row for v in avg_view) + n_layers * 2 * B * H * D * 2
     result = _line(
         "30-layer rotating-window decode tokens/s", B / (step_ms * 1e-3), "tokens/s", step_ms, args,
-        "f32",
+        "bf16 in/out, f16 operands, f32 accumulate",
         {"workload": "BASELINE config 3: 30 layers (5 global, 25 sliding ring 1024), B=4, "
                      "32/8 heads, D=128, 4-bit gs64; 16,384-token prefill in 2,048 chunks "
                      "(MFMA chunk attention), then decode steps over all layers",
@@ -945,6 +991,49 @@ def layers_main(T, hip, args):
          "prefill_tokens_per_s": round(B * L / (prefill_ms * 1e-3), 1),
          "decode_bytes_per_step": int(alg),
          "views_at_end": {"global": int(views1[5]), "sliding": int(views1[0])}}, settle, steps)
+    if not args.no_cpu_baseline:
+        # A step of batch row 0 = 25 sliding-layer decodes + 5 global ones;
+        # one of each is timed over that layer's cache view (its own keys),
+        # and the step time is 25 x sliding + 5 x global.
+        O, threads = _oracle()
+        spec = [(np.uint32, D * BITS // 32), (np.uint16, D // GS), (np.uint16, D // GS)]
+        qh = q.numpy()
+
+        def layer_fn(c, n_b, th):
+            v = c.buffers()
+            t3 = [T.view_slot(v, i, slabs, dt, w).reshape(B, HKV, v.n, w)[:n_b]
+                  for i, (dt, w) in enumerate(spec * 2)]
+            return lambda: O.attend_affine_f32(qh[:n_b], tuple(t3[:3]), tuple(t3[3:]), v.n, GS,
+                                               BITS, BITS, 1.0, threads=th)
+
+        def step_fn(n_b, th):
+            fs, fg = layer_fn(caches[0], n_b, th), layer_fn(caches[5], n_b, th)
+
+            def run():
+                t = time.perf_counter()
+                fs()
+                ts = time.perf_counter() - t
+                t = time.perf_counter()
+                fg()
+                tg = time.perf_counter() - t
+                return ts, tg
+            return run
+
+        def timed(run):
+            run()
+            ts, tg = zip(*[run() for _ in range(3)])
+            return 25 * float(np.median(ts)) + 5 * float(np.median(tg))
+
+        t1, tn = timed(step_fn(1, 1)), timed(step_fn(B, threads))
+        result["cpu_baseline"] = {
+            "value": round(B / tn, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one sliding layer ({int(views1[0])} keys) and one global layer "
+                      f"({int(views1[5])} keys) decoded, a step priced as 25 + 5 of them; f32 "
+                      f"dequantize-then-attend, median of 3 after a warm-up: batch row 0 at 1 "
+                      f"thread, all {B} rows at {threads} threads",
+            "single_thread": {"value": round(1.0 / t1, 3), "unit": "tokens/s", "cores": 1,
+                              "s_per_step": round(t1, 4)},
+            "s_per_step": round(tn, 4), "cpu_model": _cpu_model(), "cpus_visible": os.cpu_count()}
     print(json.dumps(result))
 
 

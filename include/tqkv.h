@@ -128,9 +128,10 @@ typedef struct tqkv_affine_seg {
  * 174-208): the keys of both segments enter one softmax.
  *
  * q: bf16 [B, H, 1, D]; out: bf16 [B, H, 1, D]. Query head h reads KV head
- * h / (H / H_kv). bits_k, bits_v in {3, 4, 8}; group_size in {32, 64, 128};
- * D in {64, 128, 256, 512}; H / H_kv in {1, 2, 3, 4, 6, 8} (at most 4 when
- * either width is 3 bits). n_segs in {1, 2}.
+ * h / (H / H_kv). (bits_k, bits_v): 3, 4 or 8 bits each in any pair, or 2,
+ * 5 or 6 bits for both; group_size in {32, 64, 128}; D in {64, 128, 256,
+ * 512}; H / H_kv in {1, 2, 3, 4, 6, 8} (6 or 8 heads of a 2/3/5/6-bit cache
+ * are served as two launches of half the heads). n_segs in {1, 2}.
  * workspace: device scratch of tqkv_decode_workspace_size() bytes for the
  * split partials, or NULL to use a buffer the library keeps per device (grown
  * on demand); calls that share a workspace must not overlap in time. One
@@ -322,7 +323,7 @@ int32_t tqkv_decode_attend_codebook_qjl(const uint16_t* q, int32_t B, int32_t H,
  *
  * q: bf16 [B, H, L, D]; out: bf16 [B, H, L, D]; segs as for
  * tqkv_decode_attend_affine (1 or 2: a shared prefix, then a suffix).
- * D in {64, 128, 256}; bits_k, bits_v in {2, 3, 4, 5, 6, 8}; group_size in
+ * D in {64, 128, 256, 512}; bits_k, bits_v in {2, 3, 4, 5, 6, 8}; group_size in
  * {32, 64, 128}. Takes no workspace argument; calls that use the library's
  * scratch (this one, and decodes given a null workspace) must not overlap in
  * time on one device.
@@ -383,6 +384,10 @@ typedef struct tqkv_cache_config {
   int64_t max_size;
   int64_t keep;
   uint64_t seed;      /* codebook: rotation seed (QJL at seed + 1); the reference uses 42 */
+  int32_t encode;     /* codebook: 0 = compress_one (tqkv_tq_encode: codes of R x), 1 = the
+                         reference GPU cache's chain (tqkv_tq_encode_gpu_path mode 1 on keys
+                         and values: codes of x R; QJL signs of the rotated residual) */
+  int32_t reserved;
 } tqkv_cache_config;
 
 /*
@@ -511,7 +516,13 @@ int32_t tqkv_cache_append_decode(tqkv_cache* cache, const uint16_t* k, const uin
  * queries at absolute positions [offset - L, offset) and the view's keys
  * ending at offset, causal, with the given sliding window (< 0: none). The
  * reference derives the same positions (cache_first_held_pos = kv_offset +
- * L - kv_actual, gemma4_moe.rs:2228). Affine kind with k_dim == v_dim.
+ * L - kv_actual, gemma4_moe.rs:2228). k_dim == v_dim. Affine caches read
+ * their packed rows directly. Codebook caches follow the reference's
+ * TurboQuant branch (gemma4_moe.rs:4546-4600): K and V dequantized to
+ * bf16(centroid * sigma) (lloyd_max_dequantize_scaled), keys with QJL signs
+ * corrected to K_eff, queries rotated by R and the output rotated back (the
+ * cache holds rotated rows); this uses library scratch. bf16 caches attend
+ * their rows as they are. An attached prefix is read for affine caches only.
  * q: bf16 [B, H, L, D]; out: bf16 [B, H, L, D].
  */
 int32_t tqkv_cache_prefill_attend(const tqkv_cache* cache, const uint16_t* q, int32_t H,
@@ -632,6 +643,27 @@ int32_t tqkv_tq_encode(const void* x, int32_t x_is_bf16, int64_t n_slabs, int64_
                        uint8_t* codes, float* sigma, uint32_t* signs, float* rnorm,
                        int64_t dst_cap, int64_t dst_start, tqkv_stream stream);
 /* rq = R q (RotationMatrix::apply, rotation.rs:91-99), f32 [dim], device. */
+/*
+ * The reference GPU cache's TurboQuant encode (the codes its TurboQuant
+ * caches hold, turboquant.rs:398-423, 708-745; called at gemma4_moe.rs:
+ * 4396-4430): y = x (mode 0, lloyd_max_quantize_stage1{,_fused}), y =
+ * bf16(x M) (mode 1, rotate_last_axis then the encode: the reference's
+ * default for K and V), or y = x M in f32 (mode 2,
+ * rotate_and_lloyd_max_quantize_stage1_fused), M = rotation (transpose = 0)
+ * or its transpose; sigma = sqrt(sum y^2 / dim) (f32), codes = the number
+ * of boundaries_inner (f32 [2^bits - 1], lloyd_max_boundaries_inner,
+ * ascending) at or below bf16(y / sigma) (IEEE divide). compress_one's
+ * codes (tqkv_tq_encode) differ from these by the bf16 rounding of y /
+ * sigma, the f32 boundaries and the rotation convention (R x there, x R
+ * here). x: bf16 [n_slabs, s, dim]; row j of slab i writes row (i * dst_cap
+ * + dst_start + j) of codes u8 [., dim] and sigma f32 [.]. dim in {64, 128,
+ * 256, 512}. Device.
+ */
+int32_t tqkv_tq_encode_gpu_path(const uint16_t* x, int64_t n_slabs, int64_t s, int32_t dim,
+                                const float* rotation, int32_t mode, int32_t transpose,
+                                const float* boundaries_inner, int32_t bits, uint8_t* codes,
+                                float* sigma, int64_t dst_cap, int64_t dst_start,
+                                tqkv_stream stream);
 int32_t tqkv_tq_rotate_query(const float* rotation, const float* q, int32_t dim, float* rq,
                              tqkv_stream stream);
 /* estimate_inner_products_stage1 (compressor.rs:165-184) for n stored keys:
@@ -664,6 +696,13 @@ int32_t tqkv_qjl_encode_stage2(const uint16_t* k_rot, const uint16_t* k_dq, cons
 int32_t tqkv_qjl_apply_correction(const uint16_t* k_dq, const uint32_t* signs,
                                   const float* rnorm, const float* qjl, int64_t rows, int32_t dim,
                                   int32_t m, uint16_t* k_eff, tqkv_stream stream);
+/* lloyd_max_dequantize_scaled (turboquant.rs:428-439): out = bf16(centroids[c]
+ * * sigma) for codes u8 [rows, dim] and sigma f32 [rows] (the TurboQuant
+ * cache's codes and scales), centroids f32 [2^bits]. codes and out 16-byte
+ * aligned; dim a multiple of 8. Device. */
+int32_t tqkv_codebook_dequantize(const uint8_t* codes, const float* sigma,
+                                 const float* centroids, int32_t bits, int64_t rows, int32_t dim,
+                                 uint16_t* out, tqkv_stream stream);
 /* SimpleCache::attend_values (simple.rs:40-62, 105-118): out = sum_t w_t *
  * R^T(centroid[c_t] * sigma_t), tokens with |w_t| < 1e-10 skipped, in the
  * reference's accumulation order. Device. */

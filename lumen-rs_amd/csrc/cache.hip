@@ -23,8 +23,22 @@
 #include "lkv.hpp"
 
 namespace tqkv {
-size_t decode_need_bytes(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
-                         bool app);
+size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits_k, int bits_v,
+                         const tqkv_affine_seg* segs, int n_segs, bool app);
+int32_t prefill_bf16_rows(const uint16_t* q, int B, int H, int H_kv, int L, int D,
+                          const uint16_t* k, const uint16_t* v, int64_t cap, int64_t n,
+                          int64_t q_start, int64_t k_start, int64_t window, float scale,
+                          uint16_t* out, hipStream_t stream);
+int32_t codebook_dequantize_slabs(const uint8_t* codes, const float* sigma, const float* cent,
+                                  int bits, int64_t slabs, int64_t cap, int64_t rows, int D,
+                                  uint16_t* out, hipStream_t st);
+int32_t decode_codebook_qjl_rotated(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,
+    const float* rotation, const float* centroids_k, int32_t bits_k, const float* centroids_v,
+    int32_t bits_v, const uint8_t* k_codes, const float* k_sigma, const uint32_t* k_signs,
+    const float* k_rnorm, const float* qjl, int32_t qjl_m, const uint8_t* v_codes,
+    const float* v_sigma, int64_t cap, int64_t n, uint16_t* out, void* workspace,
+    size_t workspace_bytes, tqkv_stream stream);
 namespace {
 
 constexpr int kMaxSlots = 6;
@@ -167,6 +181,8 @@ struct tqkv_cache {
   double* bnd_v = nullptr;
   float* cent_k = nullptr;     // [2^bits_k], the f64 centroids rounded
   float* cent_v = nullptr;
+  float* inner_k = nullptr;    // [2^bits_k - 1] inner boundaries as f32 (GPU-path encode)
+  float* inner_v = nullptr;
 };
 
 namespace {
@@ -283,12 +299,22 @@ int32_t codebook_tables(tqkv_cache* c, const float* R_host, const float* phi_hos
     std::vector<double> b(size_t(n) + 1), ce(static_cast<size_t>(n));
     if (int32_t rc = tqkv_lloyd_max(uint32_t(bits), 1000, b.data(), ce.data())) return rc;
     std::vector<float> cf(ce.begin(), ce.end());
+    std::vector<float> inner(b.begin() + 1, b.end() - 1);  // lloyd_max_boundaries_inner
     if (int32_t rc = upload(reinterpret_cast<void**>(kv ? &c->bnd_v : &c->bnd_k), b.data(), b.size() * 8)) return rc;
     if (int32_t rc = upload(reinterpret_cast<void**>(kv ? &c->cent_v : &c->cent_k), cf.data(), cf.size() * 4)) return rc;
+    if (int32_t rc = upload(reinterpret_cast<void**>(kv ? &c->inner_v : &c->inner_k), inner.data(), inner.size() * 4)) return rc;
   }
   std::vector<float> R(size_t(D) * D);
   if (R_host) std::memcpy(R.data(), R_host, R.size() * 4);
   else if (int32_t rc = tqkv_rotation_matrix(D, g.seed, R.data())) return rc;
+  if (g.encode == 1) {
+    // The GPU path stores x R = R^T x: the cache's rotation (the one its
+    // decode and prefill apply to queries, R_eff x) is R^T.
+    std::vector<float> Rt(R.size());
+    for (int i = 0; i < D; ++i)
+      for (int j = 0; j < D; ++j) Rt[size_t(i) * D + j] = R[size_t(j) * D + i];
+    R.swap(Rt);
+  }
   if (int32_t rc = upload(reinterpret_cast<void**>(&c->R), R.data(), R.size() * 4)) return rc;
   if (m > 0) {
     std::vector<float> P(size_t(m) * D);
@@ -368,6 +394,10 @@ lkv::Opt some(uint64_t v) { return lkv::Opt{true, v}; }
 // (kv_disk.rs:2005-2025). `first` is the index of its first record.
 int32_t plan_layer(const tqkv_cache* c, int64_t first, LayerPlan* out) {
   const tqkv_cache_config& g = c->cfg;
+  // A snapshot layer records no encode chain, and import rebuilds a
+  // compress_one cache: GPU-path rows would come back in the wrong basis.
+  if (g.encode != 0)
+    return fail(TQKV_EUNSUPPORTED, "snapshots of GPU-path (encode = 1) codebook caches");
   LayerPlan L;
   const bool ring = g.max_size > 0;
   const int64_t B = g.batch, H = g.kv_heads;
@@ -500,6 +530,144 @@ int32_t write_record(tqkv_cache* c, const RecSpec& r, const uint8_t* src) {
 
 }  // namespace
 
+namespace {
+
+// The reference GPU cache's append of s rows a slab at row `row` (gemma4_moe.rs:
+// 4384-4430 with its defaults): keys and values rotated by rotate_last_axis
+// (x R, bf16) and encoded by lloyd_max_quantize_stage1 (tqkv_tq_encode_gpu_path
+// mode 1; the cache keeps R^T, so x R = x R_eff^T); with QJL, the keys' signs
+// and residual norms from the rotated keys against their dequantized codes
+// (qjl_encode_stage2_packed).
+int32_t append_gpu_path(tqkv_cache* c, const uint16_t* k, const uint16_t* v, int64_t s,
+                        int64_t row, hipStream_t st) {
+  const tqkv_cache_config& g = c->cfg;
+  const int D = g.k_dim;
+  const bool qjl = g.qjl_words > 0;
+  const int vi = qjl ? 4 : 2;
+  const int64_t rows = c->n_slabs * s, cap = c->cur[0].cap;
+  const tqkv_stream ts = reinterpret_cast<tqkv_stream>(st);
+  if (!qjl) {
+    if (int32_t rc = tqkv_tq_encode_gpu_path(k, c->n_slabs, s, D, c->R, 1, 1, c->inner_k, g.bits_k,
+                                             c->cur[0].ptr, reinterpret_cast<float*>(c->cur[1].ptr),
+                                             cap, row, ts))
+      return rc;
+  } else {
+    const int words = g.qjl_words, m = 32 * words;
+    const size_t need = size_t(rows) * D * 2 * 2 + size_t(rows) * (words * 4 + 4) + 64;
+    void* ws = nullptr;
+    if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+    uint16_t* k_rot = static_cast<uint16_t*>(ws);
+    uint16_t* k_dq = k_rot + size_t(rows) * D;
+    uint32_t* sg = reinterpret_cast<uint32_t*>(k_dq + size_t(rows) * D);
+    float* rn = reinterpret_cast<float*>(sg + size_t(rows) * words);
+    if (int32_t rc = tqkv_rotate_bf16(k, rows, D, c->R, 1, k_rot, ts)) return rc;
+    if (int32_t rc = tqkv_tq_encode_gpu_path(k_rot, c->n_slabs, s, D, nullptr, 0, 0, c->inner_k,
+                                             g.bits_k, c->cur[0].ptr,
+                                             reinterpret_cast<float*>(c->cur[1].ptr), cap, row, ts))
+      return rc;
+    if (int32_t rc = codebook_dequantize_slabs(c->cur[0].ptr + row * D,
+                                               reinterpret_cast<const float*>(c->cur[1].ptr) + row,
+                                               c->cent_k, g.bits_k, c->n_slabs, cap, s, D, k_dq, st))
+      return rc;
+    if (int32_t rc = tqkv_qjl_encode_stage2(k_rot, k_dq, c->phi, rows, D, m, sg, rn, ts))
+      return rc;
+    // Into rows [row, row + s) of every slab of the signs and norms slots.
+    const size_t sw = size_t(words) * 4;
+    TQKV_HIP(hipMemcpy2DAsync(c->cur[2].ptr + row * sw, size_t(cap) * sw, sg, size_t(s) * sw,
+                              size_t(s) * sw, size_t(c->n_slabs), hipMemcpyDeviceToDevice, st));
+    TQKV_HIP(hipMemcpy2DAsync(c->cur[3].ptr + row * 4, size_t(cap) * 4, rn, size_t(s) * 4,
+                              size_t(s) * 4, size_t(c->n_slabs), hipMemcpyDeviceToDevice, st));
+  }
+  return tqkv_tq_encode_gpu_path(v, c->n_slabs, s, D, c->R, 1, 1, c->inner_v, g.bits_v,
+                                 c->cur[vi].ptr, reinterpret_cast<float*>(c->cur[vi + 1].ptr),
+                                 c->cur[vi].cap, row, ts);
+}
+
+// Prefill over a codebook (TurboQuant) cache, as the reference's TurboQuant
+// branch does (gemma4_moe.rs:4546-4600): K and V of the view dequantized to
+// bf16(centroid * sigma) (lloyd_max_dequantize_scaled), keys with QJL signs
+// corrected to K_eff (qjl_apply_correction_packed), V rotated back to the
+// original basis (its unrotate_v_dq), then the chunk's attention. The cache
+// holds rotated rows (R x), so the queries are rotated by R (bf16, as
+// rotate_last_axis returns them) to meet the keys. bf16 caches take the
+// attention step directly over their buffers.
+int32_t prefill_rows(const tqkv_cache* c, const uint16_t* q, int32_t H, int32_t L, float scale,
+                     int64_t window, uint16_t* out, hipStream_t st) {
+  const tqkv_cache_config& g = c->cfg;
+  const int D = g.k_dim;
+  if (g.k_dim != g.v_dim) return fail(TQKV_EUNSUPPORTED, "prefill attention needs k_dim == v_dim");
+  if (c->prefix && c->base_offset > 0)
+    return fail(TQKV_EUNSUPPORTED, "prefill over an attached prefix of this cache kind");
+  const int64_t offset = c->base_offset + c->st.offset;
+  if (H <= 0 || H % g.kv_heads != 0 || L <= 0 || L > offset)
+    return fail(TQKV_EINVAL_SHAPE, "H=%d L=%d queries but %lld tokens appended", H, L,
+                (long long)offset);
+  const int64_t n = c->view_n;
+  if (n <= 0) return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
+  const int64_t cap = c->cur[0].cap;
+  const int64_t q_start = offset - L, k_start = offset - n;
+  if (g.kind == TQKV_CACHE_BF16)
+    return prefill_bf16_rows(q, g.batch, H, g.kv_heads, L, D,
+                             reinterpret_cast<const uint16_t*>(c->cur[0].ptr),
+                             reinterpret_cast<const uint16_t*>(c->cur[1].ptr), cap, n, q_start,
+                             k_start, window, scale, out, st);
+  if (!c->R) return fail(TQKV_EINVAL_ARG, "codebook cache has no tables yet (append first)");
+  // compress_one's QJL signs are of the original-basis residual; the
+  // reference's prefill correction (qjl_apply_correction_packed) adds
+  // Phi^T signs in the rotated basis, which holds only for the rotated
+  // residual signs its GPU cache stores.
+  if (g.qjl_words > 0 && g.encode == 0)
+    return fail(TQKV_EUNSUPPORTED, "prefill over compress_one codes with QJL signs (the "
+                "reference prefills QJL only over its GPU-path cache)");
+  const int64_t slabs = int64_t(g.batch) * g.kv_heads;
+  const size_t qe = size_t(g.batch) * H * L * D;  // query / output elements
+  const size_t ke = size_t(slabs) * n * D;        // dequantized K or V elements
+  const bool qjl = g.qjl_words > 0;
+  const size_t need = (qe + 3 * ke + (qjl ? size_t(n) * D : 0)) * sizeof(uint16_t) + 64;
+  void* ws = nullptr;
+  if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+  uint16_t* qr = static_cast<uint16_t*>(ws);
+  uint16_t* kd = qr + qe;
+  uint16_t* vd = kd + ke;   // V_dq in the rotated basis
+  uint16_t* vo = vd + ke;   // V_dq rotated back
+  uint16_t* tmp = vo + ke;  // one slab's K_dq before the QJL correction
+  const int vi = qjl ? 4 : 2;
+  if (int32_t rc = tqkv_rotate_bf16(q, int64_t(g.batch) * H * L, D, c->R, 1, qr,
+                                    reinterpret_cast<tqkv_stream>(st)))
+    return rc;
+  if (!qjl) {
+    if (int32_t rc = codebook_dequantize_slabs(c->cur[0].ptr,
+                                               reinterpret_cast<const float*>(c->cur[1].ptr),
+                                               c->cent_k, g.bits_k, slabs, cap, n, D, kd, st))
+      return rc;
+  } else {
+    const int words = g.qjl_words;
+    for (int64_t sl = 0; sl < slabs; ++sl) {
+      if (int32_t rc = codebook_dequantize_slabs(
+              c->cur[0].ptr + sl * cap * D, reinterpret_cast<const float*>(c->cur[1].ptr) + sl * cap,
+              c->cent_k, g.bits_k, 1, cap, n, D, tmp, st))
+        return rc;
+      if (int32_t rc = tqkv_qjl_apply_correction(
+              tmp, reinterpret_cast<const uint32_t*>(c->cur[2].ptr) + sl * cap * words,
+              reinterpret_cast<const float*>(c->cur[3].ptr) + sl * cap, c->phi, n, D,
+              32 * words, kd + sl * n * D, reinterpret_cast<tqkv_stream>(st)))
+        return rc;
+    }
+  }
+  if (int32_t rc = codebook_dequantize_slabs(c->cur[vi].ptr,
+                                             reinterpret_cast<const float*>(c->cur[vi + 1].ptr),
+                                             c->cent_v, g.bits_v, slabs, cap, n, D, vd, st))
+    return rc;
+  // A row y = R v goes back as y R (= (R^T y)^T).
+  if (int32_t rc = tqkv_rotate_bf16(vd, slabs * n, D, c->R, 0, vo,
+                                    reinterpret_cast<tqkv_stream>(st)))
+    return rc;
+  return prefill_bf16_rows(qr, g.batch, H, g.kv_heads, L, D, kd, vo, n, n, q_start, k_start,
+                           window, scale, out, st);
+}
+
+}  // namespace
+
 extern "C" {
 
 int32_t tqkv_cache_create(const tqkv_cache_config* cfg, tqkv_cache** out) {
@@ -512,6 +680,8 @@ int32_t tqkv_cache_create(const tqkv_cache_config* cfg, tqkv_cache** out) {
   if (k.max_size < 0 || k.keep < 0 || (k.max_size > 0 && k.keep >= k.max_size))
     return fail(TQKV_EINVAL_ARG, "max_size=%lld keep=%lld", (long long)k.max_size,
                 (long long)k.keep);
+  if (k.encode < 0 || k.encode > 1 || (k.encode != 0 && k.kind != TQKV_CACHE_CODEBOOK))
+    return fail(TQKV_EINVAL_ARG, "encode=%d (0 or 1, and 1 for codebook caches only)", k.encode);
   tqkv_cache* c = new (std::nothrow) tqkv_cache();
   if (!c) return fail(TQKV_ENOMEM, "cache object");
   c->cfg = k;
@@ -612,6 +782,8 @@ int32_t tqkv_cache_clone(const tqkv_cache* src, tqkv_cache** out, tqkv_stream st
     if (rc == TQKV_OK) rc = table(&c->bnd_v, src->bnd_v, (nv + 1) * sizeof(double));
     if (rc == TQKV_OK) rc = table(&c->cent_k, src->cent_k, nk * sizeof(float));
     if (rc == TQKV_OK) rc = table(&c->cent_v, src->cent_v, nv * sizeof(float));
+    if (rc == TQKV_OK) rc = table(&c->inner_k, src->inner_k, (nk - 1) * sizeof(float));
+    if (rc == TQKV_OK) rc = table(&c->inner_v, src->inner_v, (nv - 1) * sizeof(float));
   }
   if (rc != TQKV_OK) {
     tqkv_cache_destroy(c);
@@ -633,7 +805,8 @@ int32_t tqkv_cache_destroy(tqkv_cache* c) {
     release(c->alt[s]);
   }
   for (void* p : {static_cast<void*>(c->R), static_cast<void*>(c->phi), static_cast<void*>(c->bnd_k),
-                  static_cast<void*>(c->bnd_v), static_cast<void*>(c->cent_k), static_cast<void*>(c->cent_v)})
+                  static_cast<void*>(c->bnd_v), static_cast<void*>(c->cent_k), static_cast<void*>(c->cent_v),
+                  static_cast<void*>(c->inner_k), static_cast<void*>(c->inner_v)})
     if (p) (void)hipFree(p);
   delete c;
   return ok();
@@ -681,6 +854,13 @@ int32_t tqkv_cache_append(tqkv_cache* c, const uint16_t* k, const uint16_t* v, i
     const tqkv_cache_config& g = c->cfg;
     const bool qjl = g.qjl_words > 0;
     const int vi = qjl ? 4 : 2;
+    if (g.encode == 1) {
+      if (int32_t rc = append_gpu_path(c, k, v, s, p.write_at, st)) return rc;
+      c->st = next;
+      c->view_n = p.view;
+      if (fetched) fill_view(c, p.view, fetched);
+      return ok();
+    }
     if (int32_t rc = tqkv_tq_encode(
             k, 1, c->n_slabs, s, g.k_dim, c->R, c->bnd_k, c->cent_k, g.bits_k, c->phi,
             32 * g.qjl_words, c->cur[0].ptr, reinterpret_cast<float*>(c->cur[1].ptr),
@@ -836,7 +1016,7 @@ int32_t tqkv_cache_decode_attend(const tqkv_cache* c, const uint16_t* q, int32_t
     const tqkv_cache_config& g = c->cfg;
     const int vi = g.qjl_words > 0 ? 4 : 2;
     if (g.qjl_words > 0)  // keys' QJL residual signs correct the scores
-      return tqkv_decode_attend_codebook_qjl(
+      return (g.encode == 1 ? decode_codebook_qjl_rotated : tqkv_decode_attend_codebook_qjl)(
           q, g.batch, H, g.kv_heads, g.k_dim, scale, c->R, c->cent_k, g.bits_k, c->cent_v,
           g.bits_v, c->cur[0].ptr, reinterpret_cast<const float*>(c->cur[1].ptr),
           reinterpret_cast<const uint32_t*>(c->cur[2].ptr),
@@ -906,7 +1086,8 @@ int32_t tqkv_cache_append_decode(tqkv_cache* c, const uint16_t* k, const uint16_
       vs[vn++].n = p.write_at;
       vs[vn++].n = p.view - p.write_at - 1;
     }
-    const size_t need = decode_need_bytes(g.batch, H, g.kv_heads, g.k_dim, vs, vn, true);
+    const size_t need = decode_need_bytes(g.batch, H, g.kv_heads, g.k_dim, g.group_size,
+                                          g.bits_k, g.bits_v, vs, vn, true);
     if (need > 0) {
       if (!workspace) {
         void* ws = nullptr;
@@ -954,6 +1135,8 @@ int32_t tqkv_cache_prefill_attend(const tqkv_cache* c, const uint16_t* q, int32_
                                   float scale, int64_t window, uint16_t* out,
                                   tqkv_stream stream) {
   if (!c || !q || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (c->cfg.kind == TQKV_CACHE_CODEBOOK || c->cfg.kind == TQKV_CACHE_BF16)
+    return prefill_rows(c, q, H, L, scale, window, out, reinterpret_cast<hipStream_t>(stream));
   if (c->cfg.kind != TQKV_CACHE_AFFINE)
     return fail(TQKV_EUNSUPPORTED, "prefill attention over this cache kind");
   if (c->cfg.k_dim != c->cfg.v_dim)

@@ -239,6 +239,24 @@ KernelFn pick(int D, int bk, int bv, int G, int gs, int64_t max_rows = 0) {
   return nullptr;
 }
 
+// The MFMA kernel for a layout (nullptr where none applies).
+KernelFn pick_mfma_only(int D, int bk, int bv, int G, int gs) {
+  switch (D) {
+    case 64: return pick_mfma_d64(bk, bv, G, gs);
+    case 128: return pick_mfma_d128(bk, bv, G, gs);
+    case 256: return pick_mfma_d256(bk, bv, G, gs);
+  }
+  return nullptr;
+}
+
+// Query heads one launch serves: the group's G, or G / 2 where the dot2
+// kernel takes the group in two launches (split_heads).
+int kernel_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows) {
+  KernelFn fn = pick(D, bk, bv, G, gs, max_rows);
+  if (!fn || fn == pick_mfma_only(D, bk, bv, G, gs)) return G;
+  return split_heads_rt(bk, bv, G) ? G / 2 : G;
+}
+
 }  // namespace
 }  // namespace decode
 }  // namespace tqkv
@@ -301,11 +319,12 @@ struct DecodePlan {
   size_t need = 0;
 };
 
-DecodePlan plan_decode(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
-                       bool app) {
+// Gk: the query heads one decode launch serves (kernel_heads).
+DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, const tqkv_affine_seg* segs,
+                       int n_segs, bool app) {
   DecodePlan pl;
   const int G = H / H_kv;
-  const int waves = waves_for_shape(G, D);
+  const int waves = waves_for_shape(Gk, D);
   const int64_t total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
   // A prefix shared by B >= 2 sequences: read it once per KV head for all of
   // them (the prefill kernel with the sequences as query rows, split over
@@ -353,13 +372,20 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
   if (!fn)
     return fail(TQKV_EUNSUPPORTED, "decode layout D=%d bits_k=%d bits_v=%d gqa=%d", D, bits_k,
                 bits_v, G);
-  const int epl = (bits_k == 3 || bits_v == 3) ? 32 : (G >= 6 ? 8 : 16);
-  if (group_size < epl) return fail(TQKV_EUNSUPPORTED, "group_size=%d below %d", group_size, epl);
+  const bool mfma = fn == pick_mfma_only(D, bits_k, bits_v, G, group_size);
+  const int epl = epl_rt(bits_k, bits_v, G);
+  if (!mfma && group_size < epl)
+    return fail(TQKV_EUNSUPPORTED, "group_size=%d below %d", group_size, epl);
+  // The dot2 kernel takes 6 or 8 heads of 2/3/5/6-bit caches as two
+  // launches of half the heads each (both read the keys).
+  const int Gk = kernel_heads(D, bits_k, bits_v, G, group_size, max_rows);
 
   Args a{};
   a.q = q;
   a.H = H;
   a.H_kv = H_kv;
+  a.Gt = G;
+  a.h_off = 0;
   a.gs = group_size;
   a.qscale = scale * kLog2e;
   for (int i = 0; i < n_segs; ++i) {
@@ -377,13 +403,7 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
   a.total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
   if (app) {
     // Only the MFMA kernels quantize in place.
-    KernelFn mf = nullptr;
-    switch (D) {
-      case 64: mf = pick_mfma_d64(bits_k, bits_v, G, group_size); break;
-      case 128: mf = pick_mfma_d128(bits_k, bits_v, G, group_size); break;
-      case 256: mf = pick_mfma_d256(bits_k, bits_v, G, group_size); break;
-    }
-    if (fn != mf)
+    if (!mfma)
       return fail(TQKV_EUNSUPPORTED, "fused append needs the MFMA decode kernel (D=%d bits %d/%d "
                   "gqa=%d gs=%d)", D, bits_k, bits_v, G, group_size);
     if (app->row < 0 || app->row >= app->cap)
@@ -403,9 +423,9 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
   }
 
-  const int waves = waves_for_shape(G, D);
+  const int waves = waves_for_shape(Gk, D);
   a.out = out;
-  const DecodePlan pl = plan_decode(B, H, H_kv, D, segs, n_segs, app != nullptr);
+  const DecodePlan pl = plan_decode(B, H, H_kv, D, Gk, segs, n_segs, app != nullptr);
   void* ws = workspace;
   if (pl.need > 0) {
     if (!ws) {
@@ -430,16 +450,19 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
                                                      pl.n_part, po, pm, pl_, st))
       return rc;
     if (pl.sp_s > 0) {
-      KernelFn sfn = app ? fn : pick(D, bits_k, bits_v, G, group_size, segs[1].n);
+      // The suffix kernel is the one the whole call picked (its longest
+      // segment decides between the MFMA and dot2 kernels).
       s.n_splits = pl.sp_s;
       s.split_base = pl.sp_p;
       s.n_part = pl.n_part;
       s.part_o = po;
       s.part_m = pm;
       s.part_l = pl_;
-      hipLaunchKernelGGL(sfn, dim3(unsigned(pl.sp_s), unsigned(H_kv), unsigned(B)),
-                         dim3(kWave * waves), 0, st, s);
-      TQKV_LAUNCHED();
+      for (s.h_off = 0; s.h_off < G; s.h_off += Gk) {
+        hipLaunchKernelGGL(fn, dim3(unsigned(pl.sp_s), unsigned(H_kv), unsigned(B)),
+                           dim3(kWave * waves), 0, st, s);
+        TQKV_LAUNCHED();
+      }
     }
     launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
@@ -455,9 +478,11 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     a.part_m = a.part_o + size_t(B) * H * a.n_splits * D;
     a.part_l = a.part_m + size_t(B) * H * a.n_splits;
   }
-  hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
-                     dim3(kWave * waves), 0, st, a);
-  TQKV_LAUNCHED();
+  for (a.h_off = 0; a.h_off < G; a.h_off += Gk) {
+    hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
+                       dim3(kWave * waves), 0, st, a);
+    TQKV_LAUNCHED();
+  }
   if (a.n_splits > 1) {
     launch_merge(a.part_o, a.part_m, a.part_l, a.n_splits, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
@@ -498,10 +523,13 @@ namespace tqkv {
 // The workspace bytes a decode over segments of these lengths needs (0: it
 // writes no split partials). tqkv_cache_append_decode checks it before it
 // commits a cache update.
-size_t decode_need_bytes(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
-                         bool app) {
+size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits_k, int bits_v,
+                         const tqkv_affine_seg* segs, int n_segs, bool app) {
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n_segs < 1 || n_segs > 2) return 0;
-  return plan_decode(B, H, H_kv, D, segs, n_segs, app).need;
+  int64_t max_rows = 0;
+  for (int i = 0; i < n_segs; ++i) max_rows = segs[i].n > max_rows ? segs[i].n : max_rows;
+  const int Gk = kernel_heads(D, bits_k, bits_v, H / H_kv, group_size, max_rows);
+  return plan_decode(B, H, H_kv, D, Gk, segs, n_segs, app).need;
 }
 }  // namespace tqkv
 
@@ -542,6 +570,8 @@ extern "C" int32_t tqkv_decode_attend_affine_pages(
   a.q = q;
   a.H = H;
   a.H_kv = H_kv;
+  a.Gt = G;
+  a.h_off = 0;
   a.gs = group_size;
   a.qscale = scale * kLog2e;
   const int64_t tail0 = pages * kPageRows;

@@ -61,6 +61,10 @@ struct Seg {
 struct Args {
   const uint16_t* q;
   int H, H_kv, gs;
+  // Query heads of a KV head: the kernel serves G of the group's Gt heads,
+  // from h_off on (Gt = G, h_off = 0 unless the group is split over
+  // launches; the dot2 kernels only).
+  int Gt, h_off;
   float qscale;  // softmax scale * log2(e)
   Seg seg[2];
   int64_t n0, total;
@@ -110,31 +114,35 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// The 32 bits starting at byte BYTE of a lane's chunk of NW words (bytes past
-// the chunk read as zero).
-template <int NW, int BYTE>
+// The 32 bits starting at bit BIT of a lane's chunk of NW words (bits past
+// the chunk read as zero): a word, or one funnel shift of two.
+template <int NW, int BIT>
 __device__ __forceinline__ uint32_t window(const uint32_t* w) {
-  constexpr int k = BYTE / 4, r = BYTE % 4;
+  constexpr int k = BIT / 32, r = BIT % 32;
   const uint32_t lo = k < NW ? w[k] : 0u;
   if constexpr (r == 0) {
     return lo;
   } else {
     const uint32_t hi = k + 1 < NW ? w[k + 1] : 0u;
-    return __builtin_amdgcn_alignbyte(hi, lo, r);
+    if constexpr (r % 8 == 0)
+      return __builtin_amdgcn_alignbyte(hi, lo, r / 8);
+    else
+      return __builtin_amdgcn_alignbit(hi, lo, r);
   }
 }
 
-// Bytes BYTE and BYTE+1 of token 0's chunk in the low half, the same bytes
-// of token 1's chunk in the high half.
-template <int NW, int BYTE>
+// Bits [BIT, BIT + 16) of token 0's chunk in the low half, the same bits of
+// token 1's chunk in the high half: one byte permute when BIT is a byte
+// inside a word's first three, else the two windows then the permute.
+template <int NW, int BIT>
 __device__ __forceinline__ uint32_t merge_pair(const uint32_t* w0, const uint32_t* w1) {
-  constexpr int k = BYTE / 4, r = BYTE % 4;
-  if constexpr (r < 3) {
+  constexpr int k = BIT / 32, r = (BIT % 32) / 8;
+  if constexpr (BIT % 8 == 0 && r < 3) {
     constexpr uint32_t sel = uint32_t(r) | uint32_t(r + 1) << 8 | uint32_t(4 + r) << 16 |
                              uint32_t(5 + r) << 24;
     return __builtin_amdgcn_perm(w1[k], w0[k], sel);
   } else {
-    return __builtin_amdgcn_perm(window<NW, BYTE>(w1), window<NW, BYTE>(w0), 0x05040100u);
+    return __builtin_amdgcn_perm(window<NW, BIT>(w1), window<NW, BIT>(w0), 0x05040100u);
   }
 }
 
@@ -173,7 +181,7 @@ __device__ __forceinline__ float k_dot(const uint32_t* w, const uint32_t* qp) {
   float acc = 0.0f;
   static_for<KP::kN>([&](auto J) {
     constexpr KOp op = KP::k[J];
-    const uint32_t c = window<KW, op.byte>(w) & op.mask;
+    const uint32_t c = window<KW, op.bit>(w) & op.mask;
     acc = __builtin_amdgcn_fdot2(as_h2(c), as_h2(qp[J]), acc, false);
   });
   return acc;
@@ -187,7 +195,7 @@ __device__ __forceinline__ void v_accumulate(const uint32_t* w0, const uint32_t*
   using VP = Plan<BV, EPL>;
   static_for<VP::vN>([&](auto I) {
     constexpr VWin win = VP::vw[I];
-    const uint32_t m = merge_pair<VW, win.byte>(w0, w1);
+    const uint32_t m = merge_pair<VW, win.bit>(w0, w1);
     static_for<win.count>([&](auto C) {
       constexpr VCode vc = VP::vc[win.first + C];
       const uint32_t codes = m & vc.mask;
@@ -265,7 +273,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
   float kfac[G], qbias[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const uint16_t* qrow = a.q + (int64_t(b) * a.H + kvh * G + h) * D + e0;
+    const uint16_t* qrow = a.q + (int64_t(b) * a.H + kvh * a.Gt + a.h_off + h) * D + e0;
     float qr[EPL];
     float qsum = 0.0f, qmax = 0.0f;
 #pragma unroll
@@ -494,7 +502,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       ls += s_l[w][h] * f;
       os += s_acc[w][h][d] * f;
     }
-    const int64_t bh = int64_t(b) * a.H + kvh * G + h;
+    const int64_t bh = int64_t(b) * a.H + kvh * a.Gt + a.h_off + h;
     if (a.n_part == 1) {
       a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
     } else {
@@ -517,38 +525,78 @@ constexpr int waves_for() {
   return G * D <= 1024 ? 8 : 4;
 }
 
+// Channels a lane holds: a width every plan of both widths has (3 and 5
+// bits pack whole words only from 32 codes, 2 and 6 bits from 16), 8 for
+// 4/8-bit caches of 6+ heads a KV head, else 16.
+template <int BK, int BV, int G>
+constexpr int epl_for() {
+  if constexpr (BK == 3 || BV == 3 || BK == 5 || BV == 5) return 32;
+  else if constexpr (BK == 2 || BV == 2 || BK == 6 || BV == 6) return 16;
+  else return G >= 6 ? 8 : 16;
+}
+
+// The dot2 kernel serves 6 or 8 heads a KV head in one launch only with 8
+// channels a lane (registers); wider lanes take the group in two launches of
+// half the heads each (split_heads).
+template <int BK, int BV>
+constexpr bool split_heads(int G) {
+  return G >= 6 && epl_for<BK, BV, 8>() > 8;
+}
+
 template <int D, int BK, int BV, int G>
 KernelFn pick_kernel() {
-  constexpr int EPL = (BK == 3 || BV == 3) ? 32 : (G >= 6 ? 8 : 16);
+  constexpr int EPL = epl_for<BK, BV, G>();
   return decode_affine_kernel<D, BK, BV, G, EPL, waves_for<G, D>()>;
 }
 
+// G heads in one launch, or (split_heads) the G / 2 kernel for each half.
 template <int D, int BK, int BV>
 KernelFn pick_g(int G) {
+  if (split_heads<BK, BV>(G)) G /= 2;
   switch (G) {
     case 1: return pick_kernel<D, BK, BV, 1>();
     case 2: return pick_kernel<D, BK, BV, 2>();
     case 3: return pick_kernel<D, BK, BV, 3>();
     case 4: return pick_kernel<D, BK, BV, 4>();
     case 6:
-      if constexpr (BK == 3 || BV == 3) return nullptr;
+      if constexpr (split_heads<BK, BV>(6)) return nullptr;
       else return pick_kernel<D, BK, BV, 6>();
     case 8:
-      if constexpr (BK == 3 || BV == 3) return nullptr;
+      if constexpr (split_heads<BK, BV>(8)) return nullptr;
       else return pick_kernel<D, BK, BV, 8>();
   }
   return nullptr;
 }
 
+// The (K, V) widths the decode kernels take: 3, 4 and 8 bits in any pair,
+// and 2, 5 and 6 bits with the same width for keys and values.
+#define TQKV_DECODE_PAIRS(X)                                                         \
+  X(3, 3) X(4, 4) X(8, 8) X(3, 4) X(4, 3) X(3, 8) X(8, 3) X(4, 8) X(8, 4) X(2, 2) \
+  X(5, 5) X(6, 6)
+
 template <int D>
 KernelFn pick_bits(int bk, int bv, int G) {
 #define TQKV_PAIR(K, V) \
   if (bk == K && bv == V) return pick_g<D, K, V>(G);
-  TQKV_PAIR(3, 3) TQKV_PAIR(4, 4) TQKV_PAIR(8, 8)
-  TQKV_PAIR(3, 4) TQKV_PAIR(4, 3) TQKV_PAIR(3, 8)
-  TQKV_PAIR(8, 3) TQKV_PAIR(4, 8) TQKV_PAIR(8, 4)
+  TQKV_DECODE_PAIRS(TQKV_PAIR)
 #undef TQKV_PAIR
   return nullptr;
+}
+
+// Whether the dot2 kernel takes this (K, V, G) in two launches of G / 2.
+inline bool split_heads_rt(int bk, int bv, int G) {
+#define TQKV_PAIR(K, V) \
+  if (bk == K && bv == V) return split_heads<K, V>(G);
+  TQKV_DECODE_PAIRS(TQKV_PAIR)
+#undef TQKV_PAIR
+  return false;
+}
+
+// Channels a lane holds in the dot2 kernel for these widths and heads.
+inline int epl_rt(int bk, int bv, int G) {
+  if (bk == 3 || bv == 3 || bk == 5 || bv == 5) return 32;
+  if (bk == 2 || bv == 2 || bk == 6 || bv == 6) return 16;
+  return G >= 6 ? 8 : 16;
 }
 
 // One translation unit per head_dim instantiates its kernels.

@@ -42,9 +42,11 @@ namespace decode {
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
+// The lane widths gen_pair_plans.py writes plans for.
 template <int BITS, int EPL>
 constexpr bool has_plan() {
-  return (BITS == 3 && (EPL == 32 || EPL == 64)) ||
+  return ((BITS == 3 || BITS == 5) && (EPL == 32 || EPL == 64)) ||
+         ((BITS == 2 || BITS == 6) && (EPL == 16 || EPL == 32 || EPL == 64)) ||
          ((BITS == 4 || BITS == 8) && (EPL == 8 || EPL == 16 || EPL == 32 || EPL == 64));
 }
 
@@ -446,7 +448,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
         constexpr int J = 4 * decltype(I)::value + decltype(S)::value;
         if constexpr (J < KP::kN) {
           constexpr KOp op = KP::k[J];
-          bw[decltype(S)::value] = window<KW, op.byte>(f.kw) & op.mask;
+          bw[decltype(S)::value] = window<KW, op.bit>(f.kw) & op.mask;
         } else {
           bw[decltype(S)::value] = 0u;
         }
@@ -781,9 +783,7 @@ KernelFn pick_mfma(int bk, int bv, int G, int gs) {
   if (gs != 64) return nullptr;
 #define TQKV_PAIR(K, V) \
   if (bk == K && bv == V) return pick_mfma_bits_g<D, K, V, PAGED>(G);
-  TQKV_PAIR(3, 3) TQKV_PAIR(4, 4) TQKV_PAIR(8, 8)
-  TQKV_PAIR(3, 4) TQKV_PAIR(4, 3) TQKV_PAIR(3, 8)
-  TQKV_PAIR(8, 3) TQKV_PAIR(4, 8) TQKV_PAIR(8, 4)
+  TQKV_DECODE_PAIRS(TQKV_PAIR)
 #undef TQKV_PAIR
   return nullptr;
 }

@@ -21,8 +21,8 @@
 #include "common.hpp"
 
 namespace tqkv {
-size_t decode_need_bytes(int B, int H, int H_kv, int D, const tqkv_affine_seg* segs, int n_segs,
-                         bool app);
+size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits_k, int bits_v,
+                         const tqkv_affine_seg* segs, int n_segs, bool app);
 }  // namespace tqkv
 
 namespace {
@@ -70,7 +70,8 @@ extern "C" int32_t tqkv_decode_attend_affine_noalloc(const uint16_t* q, int32_t 
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0)
     return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d", B, H, H_kv);
   if (n_segs < 1 || n_segs > 2) return fail(TQKV_EINVAL_ARG, "n_segs=%d", n_segs);
-  const size_t need = tqkv::decode_need_bytes(B, H, H_kv, D, segs, n_segs, false);
+  const size_t need =
+      tqkv::decode_need_bytes(B, H, H_kv, D, group_size, bits_k, bits_v, segs, n_segs, false);
   if (need > kScratchBytes)
     return fail(TQKV_EINVAL_SHAPE,
                 "this decode needs %zu bytes of split partials; the no-allocation entry's "

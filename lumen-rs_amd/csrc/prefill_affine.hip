@@ -20,6 +20,7 @@ KernelFn pick(int D, int bk, int bv, bool h16 = false) {
     case 64: return pick_d64(bk, bv, h16);
     case 128: return pick_d128(bk, bv, h16);
     case 256: return pick_d256(bk, bv, h16);
+    case 512: return pick_d512(bk, bv, h16);
   }
   return nullptr;
 }
@@ -153,24 +154,31 @@ int32_t shared_prefix_partials(const uint16_t* q, int B, int H, int H_kv, int D,
 }  // namespace prefill
 }  // namespace tqkv
 
-extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H,
-                                              int32_t H_kv, int32_t L, int32_t D,
-                                              int32_t group_size, int32_t bits_k, int32_t bits_v,
-                                              float scale, const tqkv_affine_seg* segs,
-                                              int32_t n_segs, int64_t q_start, int64_t k_start,
-                                              int32_t causal, int64_t window, uint16_t* out,
-                                              tqkv_stream stream) {
+namespace {
+
+// The prefill launch over affine segments, or (bf16_rows) over one segment
+// whose "packed" arrays are bf16 rows of D values (K and V already
+// dequantized or stored in bf16; scales and biases unused).
+int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t L,
+                       int32_t D, int32_t group_size, int32_t bits_k, int32_t bits_v, float scale,
+                       const tqkv_affine_seg* segs, int32_t n_segs, int64_t q_start,
+                       int64_t k_start, int32_t causal, int64_t window, uint16_t* out,
+                       tqkv_stream stream, bool bf16_rows) {
   if (!q || !out || !segs) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || L <= 0)
     return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
-  if (n_segs < 1 || n_segs > 2) return fail(TQKV_EINVAL_ARG, "n_segs=%d", n_segs);
-  if (!valid_bits(bits_k) || !valid_bits(bits_v))
+  if (n_segs < 1 || n_segs > 2 || (bf16_rows && n_segs != 1))
+    return fail(TQKV_EINVAL_ARG, "n_segs=%d", n_segs);
+  if (bf16_rows) {
+    bits_k = bits_v = kPreBits;
+  } else if (!valid_bits(bits_k) || !valid_bits(bits_v)) {
     return fail(TQKV_EUNSUPPORTED, "affine bits_k=%d bits_v=%d not in {2,3,4,5,6,8}", bits_k,
                 bits_v);
+  }
   if (!(group_size == 32 || group_size == 64 || group_size == 128) || D % group_size != 0)
     return fail(TQKV_EUNSUPPORTED, "group_size=%d with D=%d", group_size, D);
   KernelFn fn = pick(D, bits_k, bits_v);
-  if (!fn) return fail(TQKV_EUNSUPPORTED, "prefill head dim D=%d (64, 128 or 256)", D);
+  if (!fn) return fail(TQKV_EUNSUPPORTED, "prefill head dim D=%d (64, 128, 256 or 512)", D);
   if (causal && window == 0) return fail(TQKV_EINVAL_ARG, "window=0 hides every key");
   if (!(scale > 0.0f) || !std::isfinite(scale))
     return fail(TQKV_EINVAL_ARG, "softmax scale %g must be positive and finite", double(scale));
@@ -223,7 +231,8 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   switch (D) {
     case 64: rows_per_block = Shape<64, false>::kRows, threads = Shape<64, false>::kThreads; break;
     case 128: rows_per_block = Shape<128, false>::kRows, threads = Shape<128, false>::kThreads; break;
-    default: rows_per_block = Shape<256, false>::kRows, threads = Shape<256, false>::kThreads; break;
+    case 256: rows_per_block = Shape<256, false>::kRows, threads = Shape<256, false>::kThreads; break;
+    default: rows_per_block = Shape<512, false>::kRows, threads = Shape<512, false>::kThreads; break;
   }
   const int64_t blocks = (int64_t(L) * a.G + rows_per_block - 1) / rows_per_block;
   const int64_t grid = blocks * a.n_splits * H_kv * B;
@@ -234,8 +243,8 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   const char* once_env = getenv("TQKV_PREFILL_DEQUANT_ONCE");
   const int64_t slabs = int64_t(B) * H_kv;
   const size_t need = 2 * size_t(slabs) * size_t(a.total) * size_t(D) * 2;
-  const bool once = once_env ? strcmp(once_env, "0") != 0
-                             : blocks >= kOnceBlocks && need <= kOnceMaxBytes;
+  const bool once = !bf16_rows && (once_env ? strcmp(once_env, "0") != 0
+                                             : blocks >= kOnceBlocks && need <= kOnceMaxBytes);
   if (once) {
     void* ws = nullptr;
     if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
@@ -252,8 +261,12 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
         hipLaunchKernelGGL(dequantize_rows_kernel<128>, dq_grid, dim3(256), 0, st, a, bits_k,
                            bits_v, kd, vd);
         break;
-      default:
+      case 256:
         hipLaunchKernelGGL(dequantize_rows_kernel<256>, dq_grid, dim3(256), 0, st, a, bits_k,
+                           bits_v, kd, vd);
+        break;
+      default:
+        hipLaunchKernelGGL(dequantize_rows_kernel<512>, dq_grid, dim3(256), 0, st, a, bits_k,
                            bits_v, kd, vd);
         break;
     }
@@ -274,3 +287,36 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
   TQKV_LAUNCHED();
   return ok();
 }
+
+}  // namespace
+
+extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H,
+                                              int32_t H_kv, int32_t L, int32_t D,
+                                              int32_t group_size, int32_t bits_k, int32_t bits_v,
+                                              float scale, const tqkv_affine_seg* segs,
+                                              int32_t n_segs, int64_t q_start, int64_t k_start,
+                                              int32_t causal, int64_t window, uint16_t* out,
+                                              tqkv_stream stream) {
+  return prefill_launch(q, B, H, H_kv, L, D, group_size, bits_k, bits_v, scale, segs, n_segs,
+                        q_start, k_start, causal, window, out, stream, false);
+}
+
+namespace tqkv {
+// Prefill-chunk attention over bf16 K and V rows ([B, H_kv, cap, D], keys
+// [0, n) of each slab): the same MFMA kernel with the dequantization left
+// out (codebook caches after tqkv_codebook_dequantize, bf16 caches).
+int32_t prefill_bf16_rows(const uint16_t* q, int B, int H, int H_kv, int L, int D,
+                          const uint16_t* k, const uint16_t* v, int64_t cap, int64_t n,
+                          int64_t q_start, int64_t k_start, int64_t window, float scale,
+                          uint16_t* out, hipStream_t stream) {
+  tqkv_affine_seg s{};
+  s.k_packed = reinterpret_cast<const uint32_t*>(k);
+  s.v_packed = reinterpret_cast<const uint32_t*>(v);
+  s.k_scales = s.k_biases = k;  // never read at this width
+  s.v_scales = s.v_biases = v;
+  s.cap = cap;
+  s.n = n;
+  return prefill_launch(q, B, H, H_kv, L, D, 64, 0, 0, scale, &s, 1, q_start, k_start, 1, window,
+                        out, reinterpret_cast<tqkv_stream>(stream), true);
+}
+}  // namespace tqkv

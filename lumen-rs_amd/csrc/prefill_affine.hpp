@@ -109,10 +109,14 @@ struct Args {
 // The f16 variant serves decode over a shared prefix, where a block holds
 // only the B x G query rows of a KV head: 16 rows a wavefront there spread
 // those rows' products over more SIMDs.
+// D = 512 (Gemma 4's global layers): one LDS tile buffer (two would pass
+// the 160 KB of LDS), so a tile costs two barriers, and four wavefronts, one
+// a SIMD, so each holds its 512 O accumulators a row in the whole register
+// file.
 template <int D, bool H16>
 struct Shape {
-  static constexpr int kWaves = D == 64 ? 4 : 8;
-  static constexpr int kRW = (D == 256 || H16) ? 16 : 32;
+  static constexpr int kWaves = (D == 64 || D == 512) ? 4 : 8;
+  static constexpr int kRW = (D >= 256 || H16) ? 16 : 32;
   static constexpr int kRows = kWaves * kRW;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kPer = 4 * D / kThreads;
@@ -120,6 +124,8 @@ struct Shape {
   // computed. The f16 (decode) variant serves few query rows, so a tile's
   // compute is short and the loads must run further ahead to keep HBM busy.
   static constexpr int kSets = H16 ? 2 : 1;
+  static constexpr int kBufs = D == 512 ? 1 : 2;      // LDS tile buffers
+  static constexpr int kWavesPerEu = D == 512 ? 1 : 2;
   static_assert(kPer * kThreads == 4 * D, "whole loader tasks per thread");
 };
 
@@ -445,18 +451,22 @@ __device__ __forceinline__ float xor32_sum(float v) {
 }
 
 // Two wavefronts per SIMD (at most 256 registers a lane): one wavefront's
-// softmax and dequantization then overlap the other's matrix-core work.
+// softmax and dequantization then overlap the other's matrix-core work
+// (D = 512: one, with the whole register file).
 template <int D, int BK, int BV, bool H16>
-__global__ __launch_bounds__((Shape<D, H16>::kThreads)) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__((Shape<D, H16>::kThreads))
+__attribute__((amdgpu_waves_per_eu(Shape<D, H16>::kWavesPerEu)))
 void prefill_affine_kernel(const Args a) {
   constexpr int kWaves = Shape<D, H16>::kWaves, RW = Shape<D, H16>::kRW, kRows = Shape<D, H16>::kRows;
   constexpr int NR = RW / 16, ND = D / 32, NT = D / 16;
   constexpr int KSTR = kKStride<D>, VSTR = kVStride;
   constexpr int kPer = Shape<D, H16>::kPer, kThreads = Shape<D, H16>::kThreads;
+  constexpr int kBufs = Shape<D, H16>::kBufs;
   // Two tile buffers: tile t is read from one while tile t + 1 is written
-  // into the other, so a tile costs one barrier.
-  __shared__ __attribute__((aligned(16))) uint16_t Ks2[2][kTile * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt2[2][D * VSTR];
+  // into the other, so a tile costs one barrier. One buffer (D = 512): tile
+  // t + 1 is written after every wavefront has read tile t.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks2[kBufs][kTile * KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt2[kBufs][D * VSTR];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -598,7 +608,7 @@ void prefill_affine_kernel(const Args a) {
     // it); S then fetches tile t + 1 + NS.
     auto tile = [&](int t, int cur, auto set) __attribute__((always_inline)) {
       constexpr int S = decltype(set)::value;
-      if (dequant_first && t < t_hi) {
+      if (kBufs == 2 && dequant_first && t < t_hi) {
         TQKV_STORE_TILE(S, cur ^ 1)
         if (t + NS < t_hi + 1) {
           TQKV_LOAD_TILE(S, t + 1 + NS)
@@ -707,10 +717,20 @@ void prefill_affine_kernel(const Args a) {
           }
         }
       }
-      if (!dequant_first && t < t_hi) {
-        TQKV_STORE_TILE(S, cur ^ 1)
-        if (t + NS < t_hi + 1) {
-          TQKV_LOAD_TILE(S, t + 1 + NS)
+      if constexpr (kBufs == 2) {
+        if (!dequant_first && t < t_hi) {
+          TQKV_STORE_TILE(S, cur ^ 1)
+          if (t + NS < t_hi + 1) {
+            TQKV_LOAD_TILE(S, t + 1 + NS)
+          }
+        }
+      } else {
+        __syncthreads();  // every wavefront is done with this tile's LDS
+        if (t < t_hi) {
+          TQKV_STORE_TILE(S, 0)
+          if (t + NS < t_hi + 1) {
+            TQKV_LOAD_TILE(S, t + 1 + NS)
+          }
         }
       }
       __syncthreads();
@@ -722,7 +742,7 @@ void prefill_affine_kernel(const Args a) {
         if (t <= int(t_hi)) {
           tile(t, cur, std::integral_constant<int, (k.value + 1) % NS>{});
           ++t;
-          cur ^= 1;
+          cur ^= kBufs - 1;
         }
       });
     }
@@ -767,6 +787,7 @@ typedef void (*KernelFn)(Args);
 KernelFn pick_d64(int bk, int bv, bool h16);
 KernelFn pick_d128(int bk, int bv, bool h16);
 KernelFn pick_d256(int bk, int bv, bool h16);
+KernelFn pick_d512(int bk, int bv, bool h16);
 
 template <int D, int BK, bool H16>
 KernelFn pick_bv(int bv) {

@@ -570,6 +570,67 @@ __global__ void tq_values_kernel(const float* __restrict__ R, const uint8_t* __r
   out[i] = acc;
 }
 
+// The reference GPU cache's encode chain: lloyd_max_quantize_stage1
+// (turboquant.rs:398-423) over y = x (mode 0), over y = bf16(x M) (mode 1:
+// rotate_last_axis, then the encode) or over y = x M kept in f32 (mode 2:
+// rotate_and_lloyd_max_quantize_stage1_fused, :720-745), M = R or R^T
+// (transpose). sigma = sqrt(sum y^2 / D); code = the number of inner
+// boundaries b (ascending, f32) with b <= bf16(y / sigma) (the level scan of
+// lloyd_max_boundaries_inner, :310-331). One wavefront per row, lane l
+// holding channels l + 64 k: the rotation is tq_rotate_rows_kernel's fmaf
+// chain over j from 0.0; the sum of squares runs over k in each lane, then
+// over the lanes by an xor butterfly 32, 16, ..., 1 (MLX's own reduction
+// order is not in the reference; this one is fixed, and the oracle
+// restates it).
+template <int D>
+__global__ __launch_bounds__(kWave) void tq_encode_gpu_kernel(
+    const uint16_t* __restrict__ x, int64_t s, const float* __restrict__ R, int mode,
+    int transpose, const float* __restrict__ inner, int n_inner, uint8_t* __restrict__ codes,
+    float* __restrict__ sigma, int64_t dst_cap, int64_t dst_start) {
+  constexpr int PER = D / kWave;
+  __shared__ float xs[D];
+  __shared__ float bnd[256];
+  const int64_t r = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int i = lane; i < D; i += kWave) xs[i] = bf16_to_f32(x[r * D + i]);
+  for (int i = lane; i < n_inner; i += kWave) bnd[i] = inner[i];
+  __syncthreads();
+  float y[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int i = lane + k * kWave;
+    if (mode == 0) {
+      y[k] = xs[i];
+    } else {
+      float acc = 0.0f;
+      for (int j = 0; j < D; ++j)
+        acc = fmaf(xs[j], transpose ? R[int64_t(i) * D + j] : R[int64_t(j) * D + i], acc);
+      y[k] = mode == 1 ? bf16_to_f32(f32_to_bf16(acc)) : acc;
+    }
+  }
+  float p = 0.0f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) p = add(p, mul(y[k], y[k]));
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off >>= 1) p = add(p, __shfl_xor(p, off, kWave));
+  const float sg = sqrt_rn(div_rn(p, float(D)));
+  const int64_t dst = (r / s) * dst_cap + dst_start + r % s;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const float xn = bf16_to_f32(f32_to_bf16(div_rn(y[k], sg)));
+    int lo = 0, hi = n_inner;
+    while (lo < hi) {
+      const int mid = (lo + hi) / 2;
+      if (bnd[mid] <= xn)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    codes[dst * D + lane + k * kWave] = uint8_t(lo);
+  }
+  if (lane == 0) sigma[dst] = sg;
+}
+
 // y = x R (x bf16 [rows, D] -> bf16): the GPU path's rotate_last_axis
 // (turboquant.rs:258-267), f32 accumulation. transpose = 1 applies R^T.
 __global__ void tq_rotate_rows_kernel(const uint16_t* __restrict__ x, int64_t rows, int D,
@@ -638,6 +699,40 @@ extern "C" int32_t tqkv_tq_encode(const void* x, int32_t x_is_bf16, int64_t n_sl
     hipLaunchKernelGGL(tq_encode_kernel<DIM>, dim3(unsigned(rows)), dim3(kWave), 0, st, x,   \
                        x_is_bf16, s, rotation, boundaries, centroids_f32, n, qjl, qjl_m,     \
                        codes, sigma, signs, rnorm, dst_cap, dst_start);                      \
+    break;
+  switch (dim) {
+    TQKV_ENC(64) TQKV_ENC(128) TQKV_ENC(256) TQKV_ENC(512)
+  }
+#undef TQKV_ENC
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_encode_gpu_path(const uint16_t* x, int64_t n_slabs, int64_t s,
+                                           int32_t dim, const float* rotation, int32_t mode,
+                                           int32_t transpose, const float* boundaries_inner,
+                                           int32_t bits, uint8_t* codes, float* sigma,
+                                           int64_t dst_cap, int64_t dst_start,
+                                           tqkv_stream stream) {
+  if (bits < 1 || bits > 8) return fail(TQKV_EUNSUPPORTED, "codebook bits=%d", bits);
+  if (!(dim == 64 || dim == 128 || dim == 256 || dim == 512))
+    return fail(TQKV_EUNSUPPORTED, "encode dim=%d not in {64,128,256,512}", dim);
+  if (mode < 0 || mode > 2) return fail(TQKV_EINVAL_ARG, "mode=%d not in {0, 1, 2}", mode);
+  if (n_slabs < 0 || s < 0 || dst_start < 0 || dst_start + s > dst_cap)
+    return fail(TQKV_EINVAL_SHAPE, "rows [%lld, %lld) do not fit a buffer of %lld",
+                (long long)dst_start, (long long)(dst_start + s), (long long)dst_cap);
+  if (n_slabs == 0 || s == 0) return ok();
+  if (!x || !boundaries_inner || !codes || !sigma || (mode != 0 && !rotation))
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  const int64_t rows = n_slabs * s;
+  if (rows > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "too many rows");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int n_inner = (1 << bits) - 1;
+#define TQKV_ENC(DIM)                                                                       \
+  case DIM:                                                                                  \
+    hipLaunchKernelGGL(tq_encode_gpu_kernel<DIM>, dim3(unsigned(rows)), dim3(kWave), 0, st, x, \
+                       s, rotation, mode, transpose ? 1 : 0, boundaries_inner, n_inner, codes,  \
+                       sigma, dst_cap, dst_start);                                            \
     break;
   switch (dim) {
     TQKV_ENC(64) TQKV_ENC(128) TQKV_ENC(256) TQKV_ENC(512)
@@ -802,6 +897,18 @@ __global__ void cb_project_q_kernel(const uint16_t* __restrict__ q, const float*
   for (int row = threadIdx.x; row < m; row += blockDim.x) {
     float acc = 0.0f;
     for (int j = 0; j < D; ++j) acc = fmaf(phi[int64_t(row) * D + j], bf16_to_f32(q[bh * D + j]), acc);
+    pq[bh * m + row] = acc;
+  }
+}
+
+// pq = Phi (R_eff q) from the rotated f32 query: the QJL projection of a
+// cache whose signs are of the rotated-basis residual (the GPU-path encode).
+__global__ void cb_project_qr_kernel(const float* __restrict__ qr, const float* __restrict__ phi,
+                                     int D, int m, float* __restrict__ pq) {
+  const int64_t bh = blockIdx.x;
+  for (int row = threadIdx.x; row < m; row += blockDim.x) {
+    float acc = 0.0f;
+    for (int j = 0; j < D; ++j) acc = fmaf(phi[int64_t(row) * D + j], qr[bh * D + j], acc);
     pq[bh * m + row] = acc;
   }
 }
@@ -1005,6 +1112,77 @@ int32_t launch_cb(int G, dim3 grid, hipStream_t st, const float* qr, int H, cons
 }  // namespace tq
 }  // namespace tqkv
 
+namespace tqkv {
+namespace tq {
+namespace {
+// lloyd_max_dequantize_scaled (turboquant.rs:428-439): bf16(centroid[c] *
+// sigma) for rows [0, rows) of each slab of codes [slabs, cap, D] and sigma
+// [slabs, cap], into out [slabs, rows, D]. A thread writes 8 values (one
+// 16-byte store) from 8 codes (one 8-byte load); the centroids sit in LDS.
+__global__ __launch_bounds__(256) void cb_dequant_kernel(const uint8_t* __restrict__ codes,
+                                                         const float* __restrict__ sigma,
+                                                         const float* __restrict__ cent,
+                                                         int n_cent, int64_t rows, int64_t cap,
+                                                         int D, int64_t slabs,
+                                                         uint16_t* __restrict__ out) {
+  __shared__ float s_c[256];
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) s_c[i] = i < n_cent ? cent[i] : 0.0f;
+  __syncthreads();
+  const int per_row = D / 8;
+  const int64_t total = slabs * rows * per_row;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; j < total; j += stride) {
+    const int64_t r = j / per_row, slab = r / rows, t = r % rows;
+    const int e0 = int(j % per_row) * 8;
+    const int64_t src = slab * cap + t;
+    const uint2 c8 = *reinterpret_cast<const uint2*>(codes + src * D + e0);
+    const float sg = sigma[src];
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t word = k < 2 ? c8.x : c8.y;
+      const int sh = 16 * (k % 2);
+      const uint32_t lo = f32_to_bf16(s_c[(word >> sh) & 0xffu] * sg);
+      const uint32_t hi = f32_to_bf16(s_c[(word >> (sh + 8)) & 0xffu] * sg);
+      w[k] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(out + (slab * rows + t) * D + e0) = uint4{w[0], w[1], w[2], w[3]};
+  }
+}
+}  // namespace
+}  // namespace tq
+
+// Codes rows [0, rows) of each slab of a [slabs, cap, D] codebook slot,
+// dequantized to bf16 into out [slabs, rows, D].
+int32_t codebook_dequantize_slabs(const uint8_t* codes, const float* sigma, const float* cent,
+                                  int bits, int64_t slabs, int64_t cap, int64_t rows, int D,
+                                  uint16_t* out, hipStream_t st) {
+  if (rows == 0 || slabs == 0) return TQKV_OK;
+  if (!codes || !sigma || !cent || !out) return fail(TQKV_EINVAL_ARG, "null pointer");
+  if (bits < 1 || bits > 8 || D <= 0 || D % 8 != 0 || slabs < 0 || rows < 0 || rows > cap)
+    return fail(TQKV_EINVAL_SHAPE, "bits=%d D=%d slabs=%lld rows=%lld cap=%lld", bits, D,
+                (long long)slabs, (long long)rows, (long long)cap);
+  if ((reinterpret_cast<uintptr_t>(codes) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
+    return fail(TQKV_EINVAL_ARG, "codes and output must be 16-byte aligned");
+  int64_t blocks = (slabs * rows * (D / 8) + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(tq::cb_dequant_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, codes,
+                     sigma, cent, 1 << bits, rows, cap, D, slabs, out);
+  TQKV_LAUNCHED();
+  return TQKV_OK;
+}
+}  // namespace tqkv
+
+extern "C" int32_t tqkv_codebook_dequantize(const uint8_t* codes, const float* sigma,
+                                            const float* centroids, int32_t bits, int64_t rows,
+                                            int32_t dim, uint16_t* out, tqkv_stream stream) {
+  if (rows < 0) return fail(TQKV_EINVAL_SHAPE, "rows=%lld", (long long)rows);
+  if (int32_t rc = tqkv::codebook_dequantize_slabs(codes, sigma, centroids, bits, 1, rows, rows,
+                                                   dim, out, reinterpret_cast<hipStream_t>(stream)))
+    return rc;
+  return ok();
+}
+
 extern "C" size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int32_t D,
                                                        int64_t total_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || total_tokens <= 0) return 0;
@@ -1021,7 +1199,7 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
                         const float* k_rnorm, const float* qjl, int32_t qjl_m,
                         const uint8_t* v_codes, const float* v_sigma, int64_t cap, int64_t n,
                         uint16_t* out, void* workspace, size_t workspace_bytes,
-                        tqkv_stream stream) {
+                        tqkv_stream stream, bool qjl_rotated = false) {
   if (!q || !rotation || !centroids_k || !centroids_v || !k_codes || !k_sigma || !v_codes ||
       !v_sigma || !out)
     return fail(TQKV_EINVAL_ARG, "null pointer");
@@ -1054,8 +1232,12 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
                      st, q, rotation, D, qr);
   TQKV_LAUNCHED();
   if (qjl_m > 0) {
-    hipLaunchKernelGGL(tq::cb_project_q_kernel, dim3(unsigned(B * H)), dim3(256), 0, st, q, qjl,
-                       D, qjl_m, pq);
+    if (qjl_rotated)
+      hipLaunchKernelGGL(tq::cb_project_qr_kernel, dim3(unsigned(B * H)), dim3(256), 0, st, qr,
+                         qjl, D, qjl_m, pq);
+    else
+      hipLaunchKernelGGL(tq::cb_project_q_kernel, dim3(unsigned(B * H)), dim3(256), 0, st, q,
+                         qjl, D, qjl_m, pq);
     TQKV_LAUNCHED();
   }
   const uint32_t* sg = qjl_m > 0 ? k_signs : nullptr;
@@ -1086,6 +1268,23 @@ extern "C" int32_t tqkv_decode_attend_codebook(
                          bits_v, k_codes, k_sigma, nullptr, nullptr, nullptr, 0, v_codes, v_sigma,
                          cap, n, out, workspace, workspace_bytes, stream);
 }
+
+namespace tqkv {
+// Codebook decode with QJL signs of the rotated-basis residual (a GPU-path
+// cache): the score correction projects the rotated query.
+int32_t decode_codebook_qjl_rotated(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,
+    const float* rotation, const float* centroids_k, int32_t bits_k, const float* centroids_v,
+    int32_t bits_v, const uint8_t* k_codes, const float* k_sigma, const uint32_t* k_signs,
+    const float* k_rnorm, const float* qjl, int32_t qjl_m, const uint8_t* v_codes,
+    const float* v_sigma, int64_t cap, int64_t n, uint16_t* out, void* workspace,
+    size_t workspace_bytes, tqkv_stream stream) {
+  if (qjl_m <= 0) return fail(TQKV_EINVAL_ARG, "qjl_m=%d", qjl_m);
+  return decode_codebook(q, B, H, H_kv, D, scale, rotation, centroids_k, bits_k, centroids_v,
+                         bits_v, k_codes, k_sigma, k_signs, k_rnorm, qjl, qjl_m, v_codes, v_sigma,
+                         cap, n, out, workspace, workspace_bytes, stream, true);
+}
+}  // namespace tqkv
 
 extern "C" int32_t tqkv_decode_attend_codebook_qjl(
     const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t D, float scale,

@@ -60,6 +60,8 @@ pub struct tqkv_cache_config {
     pub max_size: i64,
     pub keep: i64,
     pub seed: u64,
+    pub encode: i32,
+    pub reserved: i32,
 }
 
 #[repr(C)]
@@ -156,12 +158,14 @@ extern "C" {
     pub fn tqkv_rotation_matrix(dim: i32, seed: u64, out: *mut f32) -> i32;
     pub fn tqkv_qjl_matrix(dim: i32, m: i32, seed: u64, out: *mut f32) -> i32;
     pub fn tqkv_tq_encode(x: *const c_void, x_is_bf16: i32, n_slabs: i64, s: i64, dim: i32, rotation: *const f32, boundaries: *const f64, centroids_f32: *const f32, bits: i32, qjl: *const f32, qjl_m: i32, codes: *mut u8, sigma: *mut f32, signs: *mut u32, rnorm: *mut f32, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
+    pub fn tqkv_tq_encode_gpu_path(x: *const u16, n_slabs: i64, s: i64, dim: i32, rotation: *const f32, mode: i32, transpose: i32, boundaries_inner: *const f32, bits: i32, codes: *mut u8, sigma: *mut f32, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_tq_rotate_query(rotation: *const f32, q: *const f32, dim: i32, rq: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_tq_scores(rq: *const f32, codes: *const u8, sigma: *const f32, centroids_f32: *const f32, dim: i32, n: i64, scores: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_qjl_project_query(qjl: *const f32, m: i32, dim: i32, q: *const f32, pq: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_tq_scores_two_stage(rq: *const f32, pq: *const f32, codes: *const u8, sigma: *const f32, centroids_f32: *const f32, signs: *const u32, rnorm: *const f32, dim: i32, m: i32, n: i64, scores: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_qjl_encode_stage2(k_rot: *const u16, k_dq: *const u16, qjl: *const f32, rows: i64, dim: i32, m: i32, signs: *mut u32, rnorm: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_qjl_apply_correction(k_dq: *const u16, signs: *const u32, rnorm: *const f32, qjl: *const f32, rows: i64, dim: i32, m: i32, k_eff: *mut u16, stream: tqkv_stream) -> i32;
+    pub fn tqkv_codebook_dequantize(codes: *const u8, sigma: *const f32, centroids: *const f32, bits: i32, rows: i64, dim: i32, out: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_tq_values(rotation: *const f32, codes: *const u8, sigma: *const f32, centroids_f32: *const f32, weights: *const f32, dim: i32, n: i64, out: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_rotate_bf16(x: *const u16, rows: i64, dim: i32, rotation: *const f32, transpose: i32, y: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_kvcache_create(cfg: *const tqkv_tq_config, rotation: *const f32, qjl: *const f32, n_layers: i32, n_kv_heads: i32, out: *mut *mut tqkv_kvcache) -> i32;

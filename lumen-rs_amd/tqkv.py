@@ -53,7 +53,7 @@ class CacheConfig(ctypes.Structure):
     _fields_ = [("kind", I32), ("batch", I32), ("kv_heads", I32), ("k_dim", I32),
                 ("v_dim", I32), ("group_size", I32), ("bits_k", I32), ("bits_v", I32),
                 ("qjl_words", I32), ("prealloc", I32), ("max_size", I64), ("keep", I64),
-                ("seed", ctypes.c_uint64)]
+                ("seed", ctypes.c_uint64), ("encode", I32), ("reserved", I32)]
 
 
 class CacheView(ctypes.Structure):
@@ -112,6 +112,7 @@ _SIGS = {
     "tqkv_tq_encode": (I32, [P, I32, I64, I64, I32, P, P, P, I32, P, I32, P, P, P, P, I64, I64,
                              P]),
     "tqkv_tq_rotate_query": (I32, [P, P, I32, P, P]),
+    "tqkv_tq_encode_gpu_path": (I32, [P, I64, I64, I32, P, I32, I32, P, I32, P, P, I64, I64, P]),
     "tqkv_tq_scores": (I32, [P, P, P, P, I32, I64, P, P]),
     "tqkv_qjl_project_query": (I32, [P, I32, I32, P, P, P]),
     "tqkv_tq_scores_two_stage": (I32, [P, P, P, P, P, P, P, I32, I32, I64, P, P]),
@@ -120,6 +121,7 @@ _SIGS = {
     "tqkv_decode_attend_codebook_qjl": (I32, [P, I32, I32, I32, I32, F32, P, P, I32, P, I32, P, P,
                                               P, P, P, I32, P, P, I64, I64, P, P, SZ, P]),
     "tqkv_tq_values": (I32, [P, P, P, P, P, I32, I64, P, P]),
+    "tqkv_codebook_dequantize": (I32, [P, P, P, I32, I64, I32, P, P]),
     "tqkv_rotate_bf16": (I32, [P, I64, I32, P, I32, P, P]),
     "tqkv_kvcache_create": (I32, [ctypes.POINTER(TqConfig), P, P, I32, I32, ctypes.POINTER(P)]),
     "tqkv_kvcache_destroy": (I32, [P]),
@@ -495,9 +497,9 @@ class Cache:
     bf16 / affine / codebook slots."""
 
     def __init__(self, kind, batch, kv_heads, k_dim, v_dim, group_size=64, bits_k=4, bits_v=4,
-                 qjl_words=0, prealloc=True, max_size=0, keep=0, seed=42):
+                 qjl_words=0, prealloc=True, max_size=0, keep=0, seed=42, encode=0):
         self.cfg = CacheConfig(kind, batch, kv_heads, k_dim, v_dim, group_size, bits_k, bits_v,
-                               qjl_words, int(prealloc), max_size, keep, seed)
+                               qjl_words, int(prealloc), max_size, keep, seed, encode, 0)
         h = P()
         check(lib().tqkv_cache_create(ctypes.byref(self.cfg), ctypes.byref(h)))
         self.h = h.value
@@ -630,6 +632,19 @@ def tq_encode(x, x_is_bf16, n_slabs, s, dim, R, bnd, cent, bits, phi, m, codes, 
     check(lib().tqkv_tq_encode(x, int(x_is_bf16), n_slabs, s, dim, R, bnd, cent, bits, phi, m,
                                codes, sigma, signs, rnorm, s if dst_cap is None else dst_cap,
                                dst_start, stream))
+
+
+def codebook_dequantize(codes, sigma, centroids, bits, rows, dim, out, stream=None):
+    """bf16(centroids[c] * sigma) of codebook rows; device pointers."""
+    check(lib().tqkv_codebook_dequantize(codes, sigma, centroids, bits, rows, dim, out, stream))
+
+
+def tq_encode_gpu_path(x, n_slabs, s, dim, R, mode, transpose, inner, bits, codes, sigma,
+                       dst_cap=None, dst_start=0, stream=None):
+    """The reference GPU cache's TurboQuant encode; device pointers."""
+    check(lib().tqkv_tq_encode_gpu_path(x, n_slabs, s, dim, R, mode, int(transpose), inner, bits,
+                                        codes, sigma, s if dst_cap is None else dst_cap, dst_start,
+                                        stream))
 
 
 def rotate_bf16(x, rows, dim, R, transpose, y, stream=None):

@@ -33,7 +33,7 @@ uint32_t read_code(const uint32_t* words, size_t i, int bits) {
   return uint32_t(v & ((1u << bits) - 1));
 }
 
-static void write_code(uint32_t* words, size_t i, int bits, uint32_t code) {
+void write_code(uint32_t* words, size_t i, int bits, uint32_t code) {
   size_t bit = i * size_t(bits);
   size_t w = bit / 32, off = bit % 32;
   words[w] |= code << off;
@@ -86,10 +86,12 @@ void affine_quantize_rows(const uint16_t* w, size_t rows, int dim, int gs, int b
 }
 
 // mlx dequantize for bf16 scales: out = scale * code + bias in bf16
-// arithmetic (each operation rounds to bf16).
+// arithmetic (each operation rounds to bf16); one_rounding: the product and
+// sum in f32 (the product is exact: 8 by at most 8 significant bits), then
+// one rounding to bf16.
 void affine_dequantize_rows(const uint32_t* packed, const uint16_t* scales,
                             const uint16_t* biases, size_t rows, int dim, int gs,
-                            int bits, uint16_t* out) {
+                            int bits, uint16_t* out, bool one_rounding) {
   const int groups = dim / gs;
   const size_t words_per_row = size_t(dim) * bits / 32;
   for (size_t r = 0; r < rows; ++r) {
@@ -98,6 +100,10 @@ void affine_dequantize_rows(const uint32_t* packed, const uint16_t* scales,
       float s = bf16_to_f32(scales[r * groups + i / gs]);
       float b = bf16_to_f32(biases[r * groups + i / gs]);
       float c = float(read_code(pw, size_t(i), bits));
+      if (one_rounding) {
+        out[r * dim + i] = f32_to_bf16(s * c + b);
+        continue;
+      }
       float sc = bf16_to_f32(f32_to_bf16(s * c));
       out[r * dim + i] = f32_to_bf16(sc + b);
     }

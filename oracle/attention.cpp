@@ -116,8 +116,9 @@ void oracle_attend_bf16(const uint16_t* q, const uint16_t* K, const uint16_t* V,
 
 // Affine-quantized K/V triples [B, H_kv, N, .] dequantized, then attended.
 // dequant_f32 = 0: mlx::dequantize to bf16 (the reference's prefill path,
-// gemma4_moe.rs:2394-2399); 1: exact f32 scale * code + bias (its decode
-// paths). K and V may use different bit widths.
+// gemma4_moe.rs:2394-2399) with two bf16 roundings; 1: exact f32
+// scale * code + bias (its decode paths); 2: mlx::dequantize read as one
+// rounding of the f32 result. K and V may use different bit widths.
 void oracle_attend_affine(const uint16_t* q, const uint32_t* kw, const uint16_t* ks,
                           const uint16_t* kb, const uint32_t* vw, const uint16_t* vs,
                           const uint16_t* vb, int B, int H, int H_kv, int L, size_t N, int D,
@@ -134,8 +135,8 @@ void oracle_attend_affine(const uint16_t* q, const uint32_t* kw, const uint16_t*
     return;
   }
   std::vector<uint16_t> K(rows * D), V(rows * D);
-  affine_dequantize_rows(kw, ks, kb, rows, D, gs, bits_k, K.data());
-  affine_dequantize_rows(vw, vs, vb, rows, D, gs, bits_v, V.data());
+  affine_dequantize_rows(kw, ks, kb, rows, D, gs, bits_k, K.data(), dequant_f32 == 2);
+  affine_dequantize_rows(vw, vs, vb, rows, D, gs, bits_v, V.data(), dequant_f32 == 2);
   attend(q, K.data(), V.data(), B, H, H_kv, L, N, D, scale, causal, q_start, first_held, window,
          out_f32, out_bf16, lse);
 }
@@ -161,3 +162,93 @@ void oracle_attend_codebook(const uint16_t* q, const uint8_t* kc, const float* k
 }
 
 }  // extern "C"
+
+// ---- CPU baseline: the reference's attention semantics in f32 (bench only)
+//
+// Attention over an affine cache the way a CPU port of the reference would
+// compute it, not the f64 oracle above: K/V dequantized exactly in f32
+// (scale * code + bias, the decode paths, native_quant_attention.rs:131-166)
+// or as mlx::dequantize's bf16 (dequant_bf16 = 1, the prefill path,
+// gemma4_moe.rs:2394-2399); f32 scores, softmax (expf) and weighted sum;
+// bf16 out. Each key and value row is dequantized once per (batch row, KV
+// head) and shared by the group's query heads and rows. OpenMP over (batch
+// row, KV head) with `threads` threads. q [B, H, L, D]; triples
+// [B, H_kv, cap, .] holding n rows; causal: the absolute-position mask with
+// query row l at q_start + l and key t at first_held + t (window < 0: none);
+// out bf16 [B, H, L, D].
+extern "C" void oracle_attend_affine_f32(const uint16_t* q, const uint32_t* kw,
+                                         const uint16_t* ks, const uint16_t* kb,
+                                         const uint32_t* vw, const uint16_t* vs,
+                                         const uint16_t* vb, int B, int H, int H_kv, int L,
+                                         size_t cap, size_t n, int D, int gs, int bits_k,
+                                         int bits_v, float scale, int causal, size_t q_start,
+                                         size_t first_held, long window, int dequant_bf16,
+                                         int threads, uint16_t* out) {
+  const int G = H / H_kv;
+  const int groups = D / gs;
+  const size_t rows_q = size_t(G) * L;
+  const size_t kwords = size_t(D) * bits_k / 32, vwords = size_t(D) * bits_v / 32;
+  auto deq = [&](const uint32_t* w, const uint16_t* sc, const uint16_t* bi, size_t r,
+                 size_t words, int bits, float* row) {
+    if (dequant_bf16) {
+      uint16_t tmp[1024];
+      affine_dequantize_rows(w + r * words, sc + r * groups, bi + r * groups, 1, D, gs, bits,
+                             tmp);
+      for (int i = 0; i < D; ++i) row[i] = bf16_to_f32(tmp[i]);
+      return;
+    }
+    for (int i = 0; i < D; ++i)
+      row[i] = bf16_to_f32(sc[r * groups + i / gs]) * float(read_code(w + r * words, size_t(i), bits)) +
+               bf16_to_f32(bi[r * groups + i / gs]);
+  };
+#pragma omp parallel for collapse(2) schedule(dynamic) num_threads(threads)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H_kv; ++h) {
+      const size_t slab = (size_t(b) * H_kv + h) * cap;
+      // Query rows j = g * L + l of the group.
+      std::vector<float> qf(rows_q * D), row(D), s(rows_q * n), o(rows_q * D, 0.0f);
+      for (int g = 0; g < G; ++g)
+        for (int l = 0; l < L; ++l)
+          for (int i = 0; i < D; ++i)
+            qf[(size_t(g) * L + l) * D + i] =
+                bf16_to_f32(q[((size_t(b) * H + h * G + g) * L + l) * D + i]);
+      std::vector<float> mx(rows_q, -INFINITY), lsum(rows_q, 0.0f);
+      for (size_t t = 0; t < n; ++t) {
+        deq(kw, ks, kb, slab + t, kwords, bits_k, row.data());
+        for (size_t j = 0; j < rows_q; ++j) {
+          const int l = int(j % size_t(L));
+          if (causal && !mask_allowed(q_start + size_t(l), first_held + t, window)) {
+            s[j * n + t] = -INFINITY;
+            continue;
+          }
+          float acc = 0.0f;
+          for (int i = 0; i < D; ++i) acc += qf[j * D + i] * row[i];
+          const float sc = acc * scale;
+          s[j * n + t] = sc;
+          if (sc > mx[j]) mx[j] = sc;
+        }
+      }
+      for (size_t j = 0; j < rows_q; ++j)
+        for (size_t t = 0; t < n; ++t) {
+          const float x = s[j * n + t];
+          const float p = x == -INFINITY ? 0.0f : std::exp(x - mx[j]);
+          s[j * n + t] = p;
+          lsum[j] += p;
+        }
+      for (size_t t = 0; t < n; ++t) {
+        deq(vw, vs, vb, slab + t, vwords, bits_v, row.data());
+        for (size_t j = 0; j < rows_q; ++j) {
+          const float p = s[j * n + t];
+          if (p == 0.0f) continue;
+          for (int i = 0; i < D; ++i) o[j * D + i] += p * row[i];
+        }
+      }
+      for (int g = 0; g < G; ++g)
+        for (int l = 0; l < L; ++l) {
+          const size_t j = size_t(g) * L + l;
+          for (int i = 0; i < D; ++i)
+            out[((size_t(b) * H + h * G + g) * L + l) * D + i] =
+                f32_to_bf16(lsum[j] > 0.0f ? o[j * D + i] / lsum[j] : 0.0f);
+        }
+    }
+}

@@ -197,6 +197,17 @@ void oracle_affine_dequantize(const uint32_t* packed, const uint16_t* scales,
                               uint16_t* out) {
   affine_dequantize_rows(packed, scales, biases, rows, dim, gs, bits, out);
 }
+void oracle_affine_dequantize_one_rounding(const uint32_t* packed, const uint16_t* scales,
+                                           const uint16_t* biases, size_t rows, int dim, int gs,
+                                           int bits, uint16_t* out) {
+  affine_dequantize_rows(packed, scales, biases, rows, dim, gs, bits, out, true);
+}
+void oracle_write_code(uint32_t* words, size_t i, int bits, uint32_t code) {
+  write_code(words, i, bits, code);
+}
+uint32_t oracle_read_code(const uint32_t* words, size_t i, int bits) {
+  return read_code(words, i, bits);
+}
 
 // ---- masks
 int oracle_mask_allowed(size_t q_abs, size_t k_abs, long window) {

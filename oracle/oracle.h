@@ -138,11 +138,16 @@ struct AffineOpts {
 void affine_quantize_rows(const uint16_t* w, size_t rows, int dim, int gs, int bits,
                           uint32_t* packed, uint16_t* scales, uint16_t* biases,
                           const AffineOpts& o = AffineOpts());
-// MLX dequantize: bf16(bf16(scale * code) + bias), two bf16 roundings.
+// MLX dequantize: bf16(bf16(scale * code) + bias), two bf16 roundings (the
+// restatement), or with one_rounding bf16(scale * code + bias) from f32
+// arithmetic, the other reading of MLX's kernel. Nothing in the reference
+// records either, so tests that depend on this rounding check both.
 void affine_dequantize_rows(const uint32_t* packed, const uint16_t* scales,
                             const uint16_t* biases, size_t rows, int dim, int gs,
-                            int bits, uint16_t* out);
+                            int bits, uint16_t* out, bool one_rounding = false);
 uint32_t read_code(const uint32_t* words, size_t i, int bits);
+// Code i of an LSB-first u32 stream (offload/lowbit.rs:220-240 write_code).
+void write_code(uint32_t* words, size_t i, int bits, uint32_t code);
 
 // ---------------------------------------------------------------- caches
 // Every cache kind of native_cache.rs restated over Arr buffers, replaying the

@@ -124,3 +124,54 @@ void oracle_attend_codebook_qjl(const uint16_t* q, const uint8_t* kc, const floa
 }
 
 }  // extern "C"
+
+// The GPU TurboQuant encode (lloyd_max_quantize_stage1, turboquant.rs:
+// 398-423, and its rotate variants :720-745; test infrastructure only): y =
+// x (mode 0), bf16(x M) (mode 1) or x M in f32 (mode 2), M = R or R^T;
+// y_i = fma chain over j from 0.0; sigma = sqrt(sum y^2 / D) with the sum
+// over channels l + 64 k first along k (per lane l), then across the 64
+// lane partials by an xor butterfly of offsets 32, 16, ..., 1 (the order the
+// device kernel fixes; MLX's reduction order is not in the reference);
+// code = the number of inner boundaries b with b <= bf16(y / sigma).
+extern "C" void oracle_tq_encode_gpu_path(const uint16_t* x, size_t rows, int D, const float* R,
+                                          int mode, int transpose, const float* inner,
+                                          int n_inner, uint8_t* codes, float* sigma) {
+  const int lanes = 64, per = D / lanes;
+  std::vector<float> xs(static_cast<size_t>(D)), y(static_cast<size_t>(D));
+  for (size_t r = 0; r < rows; ++r) {
+    for (int i = 0; i < D; ++i) xs[i] = bf16_to_f32(x[r * D + i]);
+    for (int i = 0; i < D; ++i) {
+      if (mode == 0) {
+        y[i] = xs[i];
+        continue;
+      }
+      float acc = 0.0f;
+      for (int j = 0; j < D; ++j)
+        acc = std::fma(xs[j], transpose ? R[size_t(i) * D + j] : R[size_t(j) * D + i], acc);
+      y[i] = mode == 1 ? bf16_to_f32(f32_to_bf16(acc)) : acc;
+    }
+    float p[64];
+    for (int l = 0; l < lanes; ++l) {
+      float a = 0.0f;
+      for (int k = 0; k < per; ++k) {
+        const float v = y[l + k * lanes];
+        const float sq = v * v;
+        a = a + sq;
+      }
+      p[l] = a;
+    }
+    for (int off = lanes / 2; off >= 1; off >>= 1) {
+      float q[64];
+      for (int l = 0; l < lanes; ++l) q[l] = p[l] + p[l ^ off];
+      for (int l = 0; l < lanes; ++l) p[l] = q[l];
+    }
+    const float sg = std::sqrt(p[0] / float(D));
+    sigma[r] = sg;
+    for (int i = 0; i < D; ++i) {
+      const float xn = bf16_to_f32(f32_to_bf16(y[i] / sg));
+      int c = 0;
+      while (c < n_inner && inner[c] <= xn) ++c;
+      codes[r * D + i] = uint8_t(c);
+    }
+  }
+}

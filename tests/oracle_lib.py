@@ -53,10 +53,16 @@ def lib():
             "oracle_attend_values": (None, [P, P, SZ, P, P, P, P, P]),
             "oracle_affine_quantize": (None, [P, SZ, I, I, I, P, P, P, I, I, I]),
             "oracle_affine_dequantize": (None, [P, P, P, SZ, I, I, I, P]),
+            "oracle_affine_dequantize_one_rounding": (None, [P, P, P, SZ, I, I, I, P]),
+            "oracle_write_code": (None, [P, SZ, I, U32]),
+            "oracle_read_code": (U32, [P, SZ, I]),
             "oracle_mask_allowed": (I, [SZ, SZ, L]),
             "oracle_attend_bf16": (None, [P, P, P, I, I, I, I, SZ, I, F, I, SZ, SZ, L, P, P, P]),
             "oracle_attend_affine": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, I, I, I, F, I,
                                             SZ, SZ, L, P, P, P, I]),
+            "oracle_tq_encode_gpu_path": (None, [P, SZ, I, P, I, I, P, I, P, P]),
+            "oracle_attend_affine_f32": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, SZ, I, I,
+                                                I, I, F, I, SZ, SZ, L, I, I, P]),
             "oracle_attend_codebook": (None, [P, P, P, P, P, P, P, I, I, I, I, SZ, I, F, I, SZ,
                                               SZ, L, P, P, P]),
             "oracle_golden_tape": (ctypes.c_int64, [ctypes.c_char_p, ctypes.c_char_p, P,
@@ -173,13 +179,27 @@ def affine_quantize(w_bf16, gs, bits, round_mode=0, wmax0=1, clip_low=0):
     return packed, scales, biases
 
 
-def affine_dequantize(packed, scales, biases, gs, bits):
+def affine_dequantize(packed, scales, biases, gs, bits, one_rounding=False):
+    """mlx::dequantize to bf16: two bf16 roundings (the restatement), or
+    one_rounding=True, the other reading (f32 arithmetic, one rounding)."""
     d = packed.shape[-1] * 32 // bits
     rows = packed.size // packed.shape[-1]
     out = np.empty(packed.shape[:-1] + (d,), np.uint16)
-    lib().oracle_affine_dequantize(ptr(np.ascontiguousarray(packed)), ptr(np.ascontiguousarray(scales)),
-                                   ptr(np.ascontiguousarray(biases)), rows, d, gs, bits, ptr(out))
+    fn = lib().oracle_affine_dequantize_one_rounding if one_rounding \
+        else lib().oracle_affine_dequantize
+    fn(ptr(np.ascontiguousarray(packed)), ptr(np.ascontiguousarray(scales)),
+       ptr(np.ascontiguousarray(biases)), rows, d, gs, bits, ptr(out))
     return out
+
+
+def write_code(words, i, bits, code):
+    """offload/lowbit.rs write_code into a u32 array, in place."""
+    assert words.dtype == np.uint32 and words.flags.c_contiguous
+    lib().oracle_write_code(ptr(words), i, bits, code)
+
+
+def read_code(words, i, bits):
+    return int(lib().oracle_read_code(ptr(np.ascontiguousarray(words, np.uint32)), i, bits))
 
 
 class Compressor:
@@ -241,7 +261,8 @@ def attend_bf16(q, K, V, scale, causal=False, q_start=0, first_held=0, window=-1
 def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0, first_held=0,
                   window=-1, dequant="f32"):
     """dequant="f32": exact scale * code + bias (the reference's decode paths);
-    "bf16": mlx::dequantize to bf16 first (its prefill path)."""
+    "bf16": mlx::dequantize to bf16 first (its prefill path), two roundings;
+    "bf16_1r": the same read as one rounding of the f32 result."""
     B, H, Lq, D = q.shape
     Hkv, N = kt[0].shape[1], kt[0].shape[2]
     of = np.empty((B, H, Lq, D), np.float32)
@@ -250,8 +271,24 @@ def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0,
     c = [np.ascontiguousarray(a) for a in (*kt, *vt)]
     lib().oracle_attend_affine(ptr(np.ascontiguousarray(q)), *[ptr(a) for a in c], B, H, Hkv, Lq,
                                N, D, gs, bits_k, bits_v, scale, int(causal), q_start, first_held,
-                               window, ptr(of), ptr(ob), ptr(lse), int(dequant == "f32"))
+                               window, ptr(of), ptr(ob), ptr(lse),
+                               {"bf16": 0, "f32": 1, "bf16_1r": 2}[dequant])
     return of, ob, lse
+
+
+def attend_affine_f32(q, kt, vt, n, gs, bits_k, bits_v, scale, threads=1, causal=False,
+                      q_start=0, first_held=0, window=-1, dequant="f32"):
+    """The CPU baseline (f32 dequantize-then-attend, bf16 out) over rows
+    [0, n) of [B, H_kv, cap, .] triples; dequant "f32" (exact, the decode
+    paths) or "bf16" (mlx::dequantize, the prefill path)."""
+    B, H, Lq, D = q.shape
+    Hkv, cap = kt[0].shape[1], kt[0].shape[2]
+    out = np.empty((B, H, Lq, D), np.uint16)
+    c = [np.ascontiguousarray(a) for a in (*kt, *vt)]
+    lib().oracle_attend_affine_f32(ptr(np.ascontiguousarray(q)), *[ptr(a) for a in c], B, H, Hkv,
+                                   Lq, cap, n, D, gs, bits_k, bits_v, scale, int(causal), q_start,
+                                   first_held, window, int(dequant == "bf16"), threads, ptr(out))
+    return out
 
 
 # ------------------------------------------------------------- page-sparse
@@ -321,6 +358,26 @@ def attend_affine_pages(q, kt, vt, chosen, pages, n, gs, bits_k, bits_v, scale):
 
 
 # ------------------------------------------------------- QJL (GPU path)
+def tq_encode_gpu_path(x_bf16, inner, R=None, mode=0, transpose=False):
+    """The GPU TurboQuant encode restated: (codes u8 [rows, D], sigma f32)."""
+    x = np.ascontiguousarray(x_bf16, np.uint16)
+    D = x.shape[-1]
+    rows = x.size // D
+    codes = np.zeros((rows, D), np.uint8)
+    sigma = np.zeros(rows, np.float32)
+    Rm = np.ascontiguousarray(R if R is not None else np.zeros((1,)), np.float32)
+    inner = np.ascontiguousarray(inner, np.float32)
+    lib().oracle_tq_encode_gpu_path(ptr(x), rows, D, ptr(Rm), mode, int(transpose), ptr(inner),
+                                    inner.size, ptr(codes), ptr(sigma))
+    return codes, sigma
+
+
+def boundaries_inner(bits):
+    """lloyd_max_boundaries_inner (turboquant.rs:310-331): the f64 inner
+    boundaries of the codebook as f32."""
+    b = codebook(bits)[0]
+    return np.asarray(b[1:-1], np.float64).astype(np.float32)
+
 def qjl_encode_stage2(k_rot, k_dq, phi, m):
     """turboquant.rs:592-622 restated: (signs u32 [rows, ceil(m/32)], r_norm)."""
     k_rot = np.ascontiguousarray(k_rot, np.uint16)

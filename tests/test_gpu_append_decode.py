@@ -97,6 +97,8 @@ def want_of(q, K, V, gs, bk, bv, scale):
     (2, 16, 8, 256, 3, 3, 254, 4, False),   # config 2's layout, across 256 (growth copy)
     (2, 32, 8, 128, 8, 4, 500, 2, True),    # config 4's widths
     (3, 8, 4, 64, 4, 8, 63, 3, True),       # D = 64, mixed widths
+    (1, 32, 8, 128, 6, 6, 100, 2, True),    # 6-bit (MFMA kernel at D = 128)
+    (2, 16, 8, 128, 2, 2, 30, 2, False),    # 2-bit
 ])
 def test_growing(T, B, Hq, Hkv, D, bk, bv, prefill, steps, prealloc):
     assert T.decode_kernel_name(Hq, Hkv, D, 64, bk, bv) == "mfma"

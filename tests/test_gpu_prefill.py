@@ -33,14 +33,37 @@ def T():
     return tqkv
 
 
-def check(got_bf16, want_f32, tag):
+def want_mlx(q, kh, vh, gs, bk, bv, scale, **kw):
+    """The oracle under both readings of mlx::dequantize's bf16 rounding
+    (two roundings, or one of the f32 result): nothing in the reference
+    records which one MLX performs, so the kernel must meet the bar against
+    either."""
+    return tuple(O.attend_affine(q, kh, vh, gs, bk, bv, scale, dequant=d, **kw)[0]
+                 for d in ("bf16", "bf16_1r"))
+
+
+def check(got_bf16, wants, tag):
+    """The bar (max-abs beyond half a bf16 step of the expected value, and
+    mean-abs; the raw max-abs is printed: the bf16 softmax weights of the
+    product, the reference SDPA's own operand type, move an output by up to
+    2^-8 of its value range, which on x10 outlier channels passes 2e-2 raw)
+    against the restatement's two-rounding dequantization; against
+    the other reading, the bar beyond the two readings' own difference,
+    which on a sharp softmax (a few keys carrying all the weight) exceeds
+    the bar by itself: there parity depends on which rounding MLX performs,
+    which nothing in the reference records."""
     got = O.bf16_to_f32(got_bf16).astype(np.float64)
-    raw = np.abs(got - want_f32)
-    err = np.maximum(raw - 0.5 * bf16_ulp(want_f32), 0.0)
-    print(f"[prefill] {tag} max_abs={raw.max():.3e} beyond_half_ulp={err.max():.3e} "
-          f"mean_abs={raw.mean():.3e}", flush=True)
     assert np.all(np.isfinite(got))
-    assert err.max() <= MAX_ABS and raw.mean() <= MEAN_ABS
+    wants = wants if isinstance(wants, tuple) else (wants,)
+    for i, want_f32 in enumerate(wants):
+        raw = np.abs(got - want_f32)
+        gap = np.abs(np.asarray(want_f32, np.float64) - wants[0]) if i else np.zeros_like(raw)
+        big = np.ones(np.shape(want_f32), bool)
+        err = np.where(big, np.maximum(raw - 0.5 * bf16_ulp(want_f32), 0.0), raw) - gap
+        print(f"[prefill] {tag} candidate {i}: max_abs={raw.max():.3e} "
+              f"bar_err={err.max():.3e} mean_abs={raw.mean():.3e} "
+              f"candidate_gap_max={gap.max():.3e}", flush=True)
+        assert err.max() <= MAX_ABS and raw.mean() <= MEAN_ABS + gap.mean()
 
 
 def run(T, q, segs_host, B, H, Hkv, L, D, gs, bk, bv, scale, q_start, k_start, causal, window):
@@ -66,6 +89,9 @@ PREFILL_CASES = [
     (1, 8, 8, 256, 1, 333, 6, 2, 64, 332, 0, True, -1, 1.0),         # one query row
     (1, 8, 2, 128, 96, 160, 4, 4, 64, 0, 50, True, -1, None),        # rows before any key
     (1, 4, 1, 64, 300, 64, 4, 8, 64, 0, 0, True, 1, None),           # window 1: self only
+    (1, 16, 2, 512, 40, 600, 4, 4, 64, 560, 0, True, -1, None),      # D = 512 (Gemma 4 global)
+    (2, 8, 4, 512, 70, 300, 8, 6, 128, 230, 0, True, 100, 1.0),      # D = 512, window, 8/6-bit
+    (1, 16, 2, 512, 96, 450, 3, 5, 32, 354, 0, True, -1, None),      # D = 512, 12 row blocks
 ]
 
 
@@ -85,8 +111,8 @@ def test_prefill_matches_dequantize_then_attend(T, B, H, Hkv, D, L, N, bk, bv, g
     (kh, kd), (vh, vd) = _cache(k, gs, bk, N + 5), _cache(v, gs, bv, N + 5)
     got = run(T, q, [(kd, vd, N + 5, N, False)], B, H, Hkv, L, D, gs, bk, bv, scale, q_start,
               k_start, causal, window)
-    want, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale, causal=causal, q_start=q_start,
-                                 first_held=k_start, window=window, dequant="bf16")
+    want = want_mlx(q, kh, vh, gs, bk, bv, scale, causal=causal, q_start=q_start,
+                    first_held=k_start, window=window)
     check(got, want, "chunk")
     if causal and k_start > q_start:
         # Query rows before the first key see nothing and return zeros.
@@ -112,8 +138,8 @@ def test_prefill_two_segments(T):
     cat = lambda a, b: np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
     kh = tuple(cat(a, b) for a, b in zip(kph, ksh))
     vh = tuple(cat(a, b) for a, b in zip(vph, vsh))
-    want, _, _ = O.attend_affine(q, kh, vh, gs, bits, bits, scale, causal=True,
-                                 q_start=P + S - L, first_held=0, window=300, dequant="bf16")
+    want = want_mlx(q, kh, vh, gs, bits, bits, scale, causal=True, q_start=P + S - L,
+                    first_held=0, window=300)
     check(got, want, "two segments")
 
 
@@ -127,15 +153,15 @@ def test_prefill_sharp_softmax(T):
     (kh, kd), (vh, vd) = _cache(k, gs, bits), _cache(v, gs, bits)
     got = run(T, q, [(kd, vd, N, N, False)], B, H, Hkv, L, D, gs, bits, bits, 1.0, N - L, 0,
               True, -1)
-    want, _, _ = O.attend_affine(q, kh, vh, gs, bits, bits, 1.0, causal=True, q_start=N - L,
-                                 first_held=0, dequant="bf16")
+    want = want_mlx(q, kh, vh, gs, bits, bits, 1.0, causal=True, q_start=N - L, first_held=0)
     check(got, want, "sharp")
 
 
 def test_prefill_rejects_bad_arguments(T):
     seg = T.affine_seg((1, 1, 1), (1, 1, 1), 8, 8)
     cases = [
-        (dict(D=512), T.EUNSUPPORTED),
+        (dict(D=1024), T.EUNSUPPORTED),
+        (dict(D=96), T.EUNSUPPORTED),
         (dict(bk=7), T.EUNSUPPORTED),
         (dict(gs=16), T.EUNSUPPORTED),
         (dict(window=0), T.EINVAL_ARG),
@@ -184,9 +210,8 @@ def test_cache_prefill_chunks(T, max_size, window):
         first = pos - n
         kh = O.affine_quantize(np.ascontiguousarray(k_all[:, :, first:pos]), gs, bits)
         vh = O.affine_quantize(np.ascontiguousarray(v_all[:, :, first:pos]), gs, bits)
-        want, _, _ = O.attend_affine(q, kh, vh, gs, bits, bits, 1.0 / np.sqrt(D), causal=True,
-                                     q_start=pos - L, first_held=first, window=window,
-                                     dequant="bf16")
+        want = want_mlx(q, kh, vh, gs, bits, bits, 1.0 / np.sqrt(D), causal=True,
+                        q_start=pos - L, first_held=first, window=window)
         check(out.numpy(), want, f"cache chunk L={L} view={n}")
 
 
@@ -201,7 +226,7 @@ def test_cache_prefill_rejects(T):
     assert e.value.status == T.EINVAL_SHAPE
 
 
-@pytest.mark.parametrize("case", [0, 1, 3, 4, 5, 7, 9])
+@pytest.mark.parametrize("case", [0, 1, 3, 4, 5, 7, 9, 10, 12])
 def test_prefill_dequantize_once_is_bit_identical(T, monkeypatch, case):
     # Keys dequantized once into scratch (mlx::dequantize's bits) and then
     # copied into LDS give the same bf16 operands as dequantizing them in
@@ -222,8 +247,8 @@ def test_prefill_dequantize_once_is_bit_identical(T, monkeypatch, case):
         got[mode] = run(T, q, [(kd, vd, N + 5, N, False)], B, H, Hkv, L, D, gs, bk, bv, scale,
                         q_start, k_start, causal, window)
     assert np.array_equal(got["0"], got["1"])
-    want, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale, causal=causal, q_start=q_start,
-                                 first_held=k_start, window=window, dequant="bf16")
+    want = want_mlx(q, kh, vh, gs, bk, bv, scale, causal=causal, q_start=q_start,
+                    first_held=k_start, window=window)
     check(got["1"], want, f"once case {case}")
 
 
@@ -250,6 +275,6 @@ def test_prefill_dequantize_once_two_segments_by_default(T, monkeypatch):
     cat = lambda a, b: np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
     kh = tuple(cat(a, b) for a, b in zip(kph, ksh))
     vh = tuple(cat(a, b) for a, b in zip(vph, vsh))
-    want, _, _ = O.attend_affine(q, kh, vh, gs, bk, bv, scale, causal=True, q_start=P + S - L,
-                                 first_held=0, window=700, dequant="bf16")
+    want = want_mlx(q, kh, vh, gs, bk, bv, scale, causal=True, q_start=P + S - L,
+                    first_held=0, window=700)
     check(got, want, "once, two segments")

@@ -253,3 +253,59 @@ def test_rotate_bf16(T, dim, transpose):
     want = x @ (M.T if transpose else M)
     got = O.bf16_to_f32(outs[0]).astype(np.float64)
     assert np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-5)
+
+
+# ------------------------------------------------- the GPU cache's encode
+@pytest.mark.parametrize("mode,transpose", [(0, False), (1, False), (2, False), (2, True)])
+@pytest.mark.parametrize("bits,D", [(4, 128), (3, 256), (8, 64), (2, 512), (6, 128)])
+def test_gpu_path_encode_bit_exact(T, mode, transpose, bits, D):
+    # tqkv_tq_encode_gpu_path against the oracle's restatement, rows written
+    # into the middle of a larger buffer.
+    slabs, s, cap, start = 3, 37, 50, 6
+    print(f"[tq-gpu-path] mode={mode} transpose={transpose} bits={bits} D={D}", flush=True)
+    x = O.bf16_from_f32(np.random.default_rng(D + bits + mode).standard_normal(
+        (slabs, s, D)).astype(np.float32) * 3)
+    R = T.rotation_matrix(D, 42)
+    b, _ = T.lloyd_max(bits)
+    inner = np.asarray(b[1:-1]).astype(np.float32)
+    dx, dR, di = T.DeviceArray.of(x), T.DeviceArray.of(R), T.DeviceArray.of(inner)
+    codes = T.DeviceArray((slabs, cap, D), np.uint8, np.full((slabs, cap, D), 0xAB, np.uint8))
+    sigma = T.DeviceArray((slabs, cap), np.float32, np.full((slabs, cap), -7.0, np.float32))
+    T.tq_encode_gpu_path(dx.ptr, slabs, s, D, dR.ptr, mode, transpose, di.ptr, bits, codes.ptr,
+                         sigma.ptr, cap, start)
+    T.hip().sync()
+    wc, ws = O.tq_encode_gpu_path(x.reshape(-1, D), inner, R, mode=mode, transpose=transpose)
+    gc, gs = codes.numpy(), sigma.numpy()
+    assert np.array_equal(gc[:, start:start + s].reshape(-1, D), wc)
+    assert np.array_equal(gs[:, start:start + s].reshape(-1).view(np.uint32), ws.view(np.uint32))
+    assert np.all(gc[:, :start] == 0xAB) and np.all(gc[:, start + s:] == 0xAB)
+    assert np.all(gs[:, :start] == -7.0) and np.all(gs[:, start + s:] == -7.0)
+
+
+def test_gpu_path_fused_matches_rotate_then_encode(T):
+    # The reference's own test of its rotate+encode kernel
+    # (turboquant.rs:1385-1456), on the device outputs: [1, 8, 64, 256] bf16
+    # N(0,1), 4 bits, seed-42 rotation; mode 2 against mode 1.
+    D, bits, rows = 256, 4, 8 * 64
+    x = O.bf16_from_f32(np.random.default_rng(0xABCDEF01).standard_normal((rows, D)).astype(
+        np.float32))
+    R = T.rotation_matrix(D, 42)
+    b, cent = T.lloyd_max(bits)
+    inner = np.asarray(b[1:-1]).astype(np.float32)
+    dx, dR, di = T.DeviceArray.of(x), T.DeviceArray.of(R), T.DeviceArray.of(inner)
+    out = {}
+    for mode in (1, 2):
+        c = T.DeviceArray((rows, D), np.uint8)
+        s = T.DeviceArray((rows,), np.float32)
+        T.tq_encode_gpu_path(dx.ptr, 1, rows, D, dR.ptr, mode, False, di.ptr, bits, c.ptr, s.ptr)
+        T.hip().sync()
+        out[mode] = (c.numpy(), s.numpy())
+    (c1, s1), (c2, s2) = out[1], out[2]
+    cf = cent.astype(np.float32)
+    dq = lambda c, s: O.bf16_to_f32(O.bf16_from_f32(cf[c] * s[:, None]))
+    sig_mse = float(np.mean((s1 - s2) ** 2))
+    agree = float(np.mean(c1 == c2))
+    dq_mse = float(np.mean((dq(c1, s1) - dq(c2, s2)) ** 2))
+    print(f"[tq-gpu-path] sigma MSE {sig_mse:.3e}, agreement {agree:.4f}, V_dq MSE {dq_mse:.3e}",
+          flush=True)
+    assert sig_mse < 1e-3 and agree > 0.99 and dq_mse < 1e-2

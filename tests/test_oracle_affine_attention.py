@@ -27,19 +27,81 @@ def _codes(packed, bits, d):
 
 
 def test_lowbit_packing_known_answers():
-    # offload/lowbit.rs:612-623: two 4-bit codes share a word from the bottom
-    # up; the eleventh 3-bit code starts at bit 30 and runs into the next word.
-    w = np.zeros((1, 64), np.uint16)
-    p, s, b = O.affine_quantize(w, 64, 4)
-    assert p.shape == (1, 8)
+    # offload/lowbit.rs:612-623, word for word: two 4-bit codes share a word
+    # from the bottom up; the eleventh 3-bit code starts at bit 30 and runs
+    # into the next word.
+    w = np.zeros(1, np.uint32)
+    O.write_code(w, 0, 4, 0xA)
+    O.write_code(w, 1, 4, 0x5)
+    assert w[0] == 0x5A
+    w = np.zeros(2, np.uint32)
+    O.write_code(w, 10, 3, 0b101)
+    assert list(w) == [0b01 << 30, 0b1]
+    assert O.read_code(w, 10, 3) == 0b101
+    # lowbit.rs:626-640: every code of every width reads back, with the
+    # same multiplicative-hash codes as the reference's test.
+    for bits in (2, 3, 4, 5, 6, 8):
+        n = 32 * 8
+        w = np.zeros(n * bits // 32, np.uint32)
+        codes = [((i * 2654435761) & 0xFFFFFFFF) >> (32 - bits) for i in range(n)]
+        for i, c in enumerate(codes):
+            O.write_code(w, i, bits, c)
+        assert [O.read_code(w, i, bits) for i in range(n)] == codes
+    # The quantizer packs with the same writer: a row alternating 0 and 7 has
+    # scale -1 and bias 7 (the larger-magnitude edge), so its codes alternate
+    # 7 and 0 and pack to the reference's word pattern.
     x = np.zeros((1, 64), np.float32)
-    x[0, 0], x[0, 1] = 0.0, 1.0
-    x[0, 2:] = 0.5
-    p, s, b = O.affine_quantize(O.bf16_from_f32(x), 64, 3)
-    c = _codes(p, 3, 64)[0]
-    deq = O.bf16_to_f32(O.affine_dequantize(p, s, b, 64, 3))[0]
-    assert np.allclose(deq, x[0], atol=O.bf16_to_f32(s)[0, 0].__abs__() / 2 + 1e-6)
-    assert c[1] in (0, 7) and c[0] in (0, 7) and c[0] != c[1]
+    x[0, 1::2] = 7.0
+    p, _, _ = O.affine_quantize(O.bf16_from_f32(x), 64, 3)
+    want = np.zeros(6, np.uint32)
+    for i in range(64):
+        O.write_code(want, i, 3, 0 if i % 2 else 7)
+    assert np.array_equal(p[0], want)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_half_way_ties_round_away_from_zero(bits):
+    # A group spanning exactly [0, n_bins] has scale -1 and bias n_bins (the
+    # larger-magnitude edge), so the code of w is round(n_bins - w). Values
+    # k + 0.5 put every code on a tie: MLX's Metal kernel rounds half away
+    # from zero (the 4-bit golden digests fix that; the kernel is one
+    # template over the width), so the code is n_bins - k, where half-to-even
+    # would give n_bins - k - 1 for half of them.
+    top = (1 << bits) - 1
+    x = np.zeros((1, 64), np.float32)
+    x[0, 0], x[0, 1] = 0.0, float(top)
+    ks = np.arange(62) % top
+    x[0, 2:] = ks + 0.5
+    p, s, b = O.affine_quantize(O.bf16_from_f32(x), 64, bits)
+    assert O.bf16_to_f32(s)[0, 0] == -1.0 and O.bf16_to_f32(b)[0, 0] == float(top)
+    c = _codes(p, bits, 64)[0]
+    assert c[0] == top and c[1] == 0
+    assert np.array_equal(c[2:], top - ks)
+    even = np.rint(top - (ks + 0.5)).astype(np.int64)
+    assert np.any(even != top - ks)
+    p2, _, _ = O.affine_quantize(O.bf16_from_f32(x), 64, bits, round_mode=1)
+    assert not np.array_equal(p2, p)
+
+
+def test_dequantize_candidates_differ():
+    # The two readings of mlx::dequantize (two bf16 roundings, or one of the
+    # f32 result) must disagree on ordinary inputs, or checking prefill and
+    # the page digest against both would test nothing; where they agree with
+    # each other they agree with the exact value rounded once.
+    w = _bf16_normal((256, 256), 5, std=3.0)
+    for bits in (3, 4, 8):
+        p, s, b = O.affine_quantize(w, 64, bits)
+        two = O.affine_dequantize(p, s, b, 64, bits)
+        one = O.affine_dequantize(p, s, b, 64, bits, one_rounding=True)
+        assert np.mean(two != one) > 0.01
+        c = _codes(p, bits, 256).reshape(256, 4, 64).astype(np.float64)
+        prod = (O.bf16_to_f32(s)[..., None] * c).reshape(256, 256)
+        exact = prod + np.repeat(O.bf16_to_f32(b), 64, axis=-1)
+        assert np.array_equal(one, O.bf16_from_f32(exact.astype(np.float32)))
+        # Two roundings: half a bf16 step of the product, then of the sum.
+        ulp = lambda v: 2.0 ** (np.floor(np.log2(np.maximum(np.abs(v), 2.0 ** -126))) - 7)
+        bound = 0.5 * ulp(prod) + 0.5 * ulp(np.abs(exact) + 0.5 * ulp(prod))
+        assert np.all(np.abs(O.bf16_to_f32(two) - exact) <= bound)
 
 
 @pytest.mark.parametrize("bits", [3, 4, 8])
@@ -178,3 +240,23 @@ def test_attend_affine_is_dequantize_then_attend():
         ref[0, h] = e @ Ve[0, h // 2] / e.sum()
     assert np.abs(of32 - ref).max() < 1e-5
     assert np.abs(of32 - of).max() > 0  # the two dequantizations differ
+
+
+@pytest.mark.parametrize("L,causal,window,dequant", [(1, False, -1, "f32"), (7, True, 40, "bf16"),
+                                                      (5, True, -1, "f32")])
+def test_cpu_baseline_port_agrees_with_the_oracle(L, causal, window, dequant):
+    # The bench's CPU baseline (an f32 port of dequantize-then-attend) must
+    # compute what the oracle computes: within the decode bar of the f64
+    # oracle on the same cache (GQA 4, a row past the window, 3-bit keys and
+    # 8-bit values), and the same bits at any thread count.
+    B, H, Hkv, D, N, gs = 2, 8, 2, 128, 300, 64
+    q = _bf16_normal((B, H, L, D), 71)
+    kt = O.affine_quantize(_bf16_normal((B, Hkv, N, D), 72), gs, 3)
+    vt = O.affine_quantize(_bf16_normal((B, Hkv, N, D), 73), gs, 8)
+    kw = dict(causal=causal, q_start=N - L, first_held=0, window=window)
+    got = O.attend_affine_f32(q, kt, vt, N, gs, 3, 8, D ** -0.5, threads=1, dequant=dequant, **kw)
+    want, _, _ = O.attend_affine(q, kt, vt, gs, 3, 8, D ** -0.5, dequant=dequant, **kw)
+    err = np.abs(O.bf16_to_f32(got).astype(np.float64) - want)
+    assert err.max() <= 2e-2 and err.mean() <= 1e-3
+    assert np.array_equal(got, O.attend_affine_f32(q, kt, vt, N, gs, 3, 8, D ** -0.5, threads=4,
+                                                   dequant=dequant, **kw))
