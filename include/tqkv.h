@@ -709,6 +709,32 @@ int32_t tqkv_codebook_dequantize(const uint8_t* codes, const float* sigma,
 int32_t tqkv_tq_values(const float* rotation, const uint8_t* codes, const float* sigma,
                        const float* centroids_f32, const float* weights, int32_t dim, int64_t n,
                        float* out, tqkv_stream stream);
+/* bitpack::packed_words (bitpack.rs:9-14): u64 words a vector of `dim`
+ * codes at `bits` (1..8) takes, 64 / bits codes a word; -1 for bits or dim
+ * out of range. Host only. */
+int64_t tqkv_packed_words(int32_t dim, int32_t bits);
+/* bitpack::pack_codes (bitpack.rs:17-33) over n vectors: codes u8 [n, dim]
+ * -> words u64 [n, tqkv_packed_words(dim, bits)], code j of a vector at
+ * bits (j % (64 / bits)) * bits of word j / (64 / bits), unused high bits
+ * zero. Device. */
+int32_t tqkv_pack_codes(const uint8_t* codes, int64_t n, int32_t dim, int32_t bits,
+                        uint64_t* words, tqkv_stream stream);
+/* bitpack::unpack_codes (bitpack.rs:36-49), the inverse over n vectors.
+ * Device. */
+int32_t tqkv_unpack_codes(const uint64_t* words, int64_t n, int32_t dim, int32_t bits,
+                          uint8_t* codes, tqkv_stream stream);
+/* tqkv_tq_scores over codes in the packed layout, as
+ * estimate_inner_products_stage1 reads CompressedVector::stage1_packed
+ * (compressor.rs:165-184, simple.rs:50-56). Bit-identical to
+ * tqkv_tq_scores on the unpacked codes. Device. */
+int32_t tqkv_tq_scores_packed(const float* rq, const uint64_t* words, const float* sigma,
+                              const float* centroids_f32, int32_t bits, int32_t dim, int64_t n,
+                              float* scores, tqkv_stream stream);
+/* tqkv_tq_values over codes in the packed layout (simple.rs:40-62).
+ * Bit-identical to tqkv_tq_values on the unpacked codes. Device. */
+int32_t tqkv_tq_values_packed(const float* rotation, const uint64_t* words, const float* sigma,
+                              const float* centroids_f32, const float* weights, int32_t bits,
+                              int32_t dim, int64_t n, float* out, tqkv_stream stream);
 /* rotate_last_axis (turboquant.rs:258-267): y = x R (transpose = 0) or
  * y = x R^T (transpose = 1), bf16 rows [rows, dim] in and out, f32
  * accumulation. The affine+rotation cache mode (gemma4_moe.rs:4154-4173)
@@ -737,7 +763,9 @@ typedef struct tqkv_kvcache tqkv_kvcache;
  * (compressor.rs:20-32), or ::from_files (:35-58) when `rotation` (host
  * [head_dim, head_dim] row-major) and `qjl` (host [qjl_m, head_dim]) are
  * given; NULL draws them from the seed (R at seed, Phi at seed + 1).
- * head_dim in {64, 128, 256, 512}. Compressed vectors live on the device.
+ * head_dim in {64, 128, 256, 512}. Compressed vectors live on the device,
+ * their codes packed as CompressedVector::stage1_packed packs them
+ * (tqkv_pack_codes), with scale, QJL sign words and residual norm.
  */
 int32_t tqkv_kvcache_create(const tqkv_tq_config* cfg, const float* rotation, const float* qjl,
                             int32_t n_layers, int32_t n_kv_heads, tqkv_kvcache** out);
@@ -762,8 +790,18 @@ int32_t tqkv_kvcache_clear(tqkv_kvcache* cache);
 /* KVCache::truncate: keep the first n_keep tokens of every head of a layer
  * (no-op where fewer are held). */
 int32_t tqkv_kvcache_truncate(tqkv_kvcache* cache, int32_t layer, int64_t n_keep);
-/* SimpleCache::memory_bytes (CompressedVector::size_bytes, config.rs:50-55). */
+/* SimpleCache::memory_bytes (simple.rs:65-80): the sum of
+ * CompressedVector::size_bytes (config.rs:50-55) over the stored vectors,
+ * the reference's own accounting (its dim and bits fields and u64 sign
+ * words included). tqkv_kvcache_device_bytes reports what the device
+ * holds. */
 int64_t tqkv_kvcache_memory_bytes(const tqkv_kvcache* cache);
+/* Device bytes of the cache (no counterpart in the reference): *held = the
+ * stored vectors' packed codes, scales, and with QJL their u32 sign words
+ * and residual norms; *reserved = all device memory the cache owns (array
+ * capacity, the R / Phi / codebook tables and its staging buffer). Either
+ * pointer may be NULL. */
+int32_t tqkv_kvcache_device_bytes(const tqkv_kvcache* cache, int64_t* held, int64_t* reserved);
 /* The stored CompressedVector fields of vectors [first, first + n) of a
  * (layer, head) (which_values = 0 keys, 1 values), to host: codes u8 [n,
  * head_dim], scale [n], QJL sign words u32 [n, ceil(qjl_m / 32)] and

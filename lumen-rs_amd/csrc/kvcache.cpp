@@ -3,9 +3,12 @@
 // (simple.rs:13-149), with the compressed vectors kept on the device and the
 // compression and estimators run by the kernels of turboquant.hip. Host
 // pointers in and out, synchronous, like the trait's borrowed slices and
-// owned Vecs. Storage per (layer, head), keys and values alike: codes u8
-// [D], scale f32, QJL signs u32 [ceil(m/32)], residual norm f32 per token,
-// in arrays that double when full.
+// owned Vecs. Storage per (layer, head), keys and values alike: the codes in
+// CompressedVector::stage1_packed's layout (u64 words, 64 / bits codes a
+// word, LSB first, none straddling: bitpack.rs:11-52), scale f32, QJL signs
+// u32 [ceil(m/32)] and residual norm f32 per token, in arrays that double
+// when full. The encode writes one byte per code into staging and packs it
+// on the device; the estimators read the packed words directly.
 #include <cstring>
 #include <new>
 #include <vector>
@@ -23,12 +26,17 @@ int32_t tqkv_tq_encode(const void* x, int32_t x_is_bf16, int64_t n_slabs, int64_
                        tqkv_stream stream);
 int32_t tqkv_tq_rotate_query(const float* rotation, const float* q, int32_t dim, float* rq,
                              tqkv_stream stream);
-int32_t tqkv_tq_scores(const float* rq, const uint8_t* codes, const float* sigma,
-                       const float* centroids_f32, int32_t dim, int64_t n, float* scores,
-                       tqkv_stream stream);
-int32_t tqkv_tq_values(const float* rotation, const uint8_t* codes, const float* sigma,
-                       const float* centroids_f32, const float* weights, int32_t dim, int64_t n,
-                       float* out, tqkv_stream stream);
+int64_t tqkv_packed_words(int32_t dim, int32_t bits);
+int32_t tqkv_pack_codes(const uint8_t* codes, int64_t n, int32_t dim, int32_t bits,
+                        uint64_t* words, tqkv_stream stream);
+int32_t tqkv_unpack_codes(const uint64_t* words, int64_t n, int32_t dim, int32_t bits,
+                          uint8_t* codes, tqkv_stream stream);
+int32_t tqkv_tq_scores_packed(const float* rq, const uint64_t* words, const float* sigma,
+                              const float* centroids_f32, int32_t bits, int32_t dim, int64_t n,
+                              float* scores, tqkv_stream stream);
+int32_t tqkv_tq_values_packed(const float* rotation, const uint64_t* words, const float* sigma,
+                              const float* centroids_f32, const float* weights, int32_t bits,
+                              int32_t dim, int64_t n, float* out, tqkv_stream stream);
 }
 
 namespace tqkv {
@@ -45,7 +53,7 @@ int32_t dalloc(T** p, size_t n) {
 
 // The compressed vectors of one (layer, head, keys|values) on the device.
 struct Stream {
-  uint8_t* codes = nullptr;
+  uint64_t* words = nullptr;  // packed codes [cap, words a vector]
   float* sigma = nullptr;
   uint32_t* signs = nullptr;
   float* rnorm = nullptr;
@@ -61,6 +69,7 @@ struct tqkv_kvcache {
   tqkv_tq_config cfg{};
   int n_layers = 0, n_heads = 0;
   int words = 0;  // QJL u32 words per vector
+  int pw = 0;     // packed code u64 words per vector
   float* R = nullptr;
   float* phi = nullptr;
   double* bnd = nullptr;
@@ -73,7 +82,7 @@ struct tqkv_kvcache {
 namespace {
 
 void free_stream(Stream& s) {
-  (void)hipFree(s.codes);
+  (void)hipFree(s.words);
   (void)hipFree(s.sigma);
   (void)hipFree(s.signs);
   (void)hipFree(s.rnorm);
@@ -84,16 +93,20 @@ int32_t reserve(const tqkv_kvcache* c, Stream& s, int64_t need) {
   if (need <= s.cap) return TQKV_OK;
   int64_t cap = s.cap ? s.cap : 64;
   while (cap < need) cap *= 2;
-  const int D = c->cfg.head_dim, W = c->words;
+  const int PW = c->pw, W = c->words;
   Stream ns;
   ns.n = s.n;
   ns.cap = cap;
-  if (int32_t rc = dalloc(&ns.codes, size_t(cap) * D)) return rc;
-  if (int32_t rc = dalloc(&ns.sigma, size_t(cap))) return rc;
-  if (int32_t rc = dalloc(&ns.signs, size_t(cap) * (W ? W : 1))) return rc;
-  if (int32_t rc = dalloc(&ns.rnorm, size_t(cap))) return rc;
+  int32_t rc = dalloc(&ns.words, size_t(cap) * PW);
+  if (!rc) rc = dalloc(&ns.sigma, size_t(cap));
+  if (!rc) rc = dalloc(&ns.signs, size_t(cap) * (W ? W : 1));
+  if (!rc) rc = dalloc(&ns.rnorm, size_t(cap));
+  if (rc) {
+    free_stream(ns);
+    return rc;
+  }
   if (s.n > 0) {
-    TQKV_HIP(hipMemcpy(ns.codes, s.codes, size_t(s.n) * D, hipMemcpyDeviceToDevice));
+    TQKV_HIP(hipMemcpy(ns.words, s.words, size_t(s.n) * PW * 8, hipMemcpyDeviceToDevice));
     TQKV_HIP(hipMemcpy(ns.sigma, s.sigma, size_t(s.n) * 4, hipMemcpyDeviceToDevice));
     if (W) TQKV_HIP(hipMemcpy(ns.signs, s.signs, size_t(s.n) * W * 4, hipMemcpyDeviceToDevice));
     TQKV_HIP(hipMemcpy(ns.rnorm, s.rnorm, size_t(s.n) * 4, hipMemcpyDeviceToDevice));
@@ -124,15 +137,33 @@ int32_t check_lh(const tqkv_kvcache* c, int32_t layer, int32_t head) {
 }
 
 int32_t encode_into(tqkv_kvcache* c, Stream& s, const float* host, int64_t n) {
-  const int D = c->cfg.head_dim;
+  const int D = c->cfg.head_dim, W = c->words;
   if (int32_t rc = reserve(c, s, s.n + n)) return rc;
+  // Staging: x f32 [n, D], sigma [n], residual norms [n], signs u32
+  // [n, max(W, 1)], then the encode's codes u8 [n, D]. The encode writes
+  // them all at rows [0, n); the codes are packed into the stream and the
+  // rest copied to rows [s.n, s.n + n) of it.
+  // (codes start on a 16-byte boundary, as the encode's 16-byte stores want).
+  const size_t nd = size_t(n) * D, ws = size_t(W ? W : 1);
+  const size_t codes_at = (nd + 2 * size_t(n) + size_t(n) * ws + 3) / 4 * 4;
   float* x = nullptr;
-  if (int32_t rc = staging(c, size_t(n) * D, &x)) return rc;
-  TQKV_HIP(hipMemcpy(x, host, size_t(n) * D * 4, hipMemcpyHostToDevice));
+  if (int32_t rc = staging(c, codes_at + (nd + 3) / 4, &x)) return rc;
+  float* sigma = x + nd;
+  float* rnorm = sigma + n;
+  uint32_t* signs = reinterpret_cast<uint32_t*>(rnorm + n);
+  uint8_t* codes = reinterpret_cast<uint8_t*>(x + codes_at);
+  TQKV_HIP(hipMemcpy(x, host, nd * 4, hipMemcpyHostToDevice));
   if (int32_t rc = tqkv_tq_encode(x, 0, 1, n, D, c->R, c->bnd, c->cent, c->cfg.bits, c->phi,
-                                  c->cfg.qjl_m, s.codes, s.sigma, s.signs, s.rnorm, s.cap, s.n,
-                                  nullptr))
+                                  c->cfg.qjl_m, codes, sigma, signs, rnorm, n, 0, nullptr))
     return rc;
+  const int64_t at = s.n;
+  if (int32_t rc = tqkv_pack_codes(codes, n, D, c->cfg.bits, s.words + at * c->pw, nullptr))
+    return rc;
+  TQKV_HIP(hipMemcpy(s.sigma + at, sigma, size_t(n) * 4, hipMemcpyDeviceToDevice));
+  if (W) {
+    TQKV_HIP(hipMemcpy(s.signs + at * W, signs, size_t(n) * W * 4, hipMemcpyDeviceToDevice));
+    TQKV_HIP(hipMemcpy(s.rnorm + at, rnorm, size_t(n) * 4, hipMemcpyDeviceToDevice));
+  }
   TQKV_HIP(hipDeviceSynchronize());
   s.n += n;
   return TQKV_OK;
@@ -157,6 +188,7 @@ int32_t tqkv_kvcache_create(const tqkv_tq_config* cfg, const float* rotation, co
   c->n_layers = n_layers;
   c->n_heads = n_kv_heads;
   c->words = (m + 31) / 32;
+  c->pw = int(tqkv_packed_words(D, cfg->bits));
   c->keys.resize(size_t(n_layers) * n_kv_heads);
   c->values.resize(size_t(n_layers) * n_kv_heads);
   const int n = 1 << cfg->bits;
@@ -235,7 +267,9 @@ int32_t tqkv_kvcache_attend_keys(tqkv_kvcache* c, int32_t layer, int32_t head,
   float *q = buf, *rq = buf + D, *out = buf + 2 * D;
   TQKV_HIP(hipMemcpy(q, query, size_t(D) * 4, hipMemcpyHostToDevice));
   if (int32_t rc = tqkv_tq_rotate_query(c->R, q, D, rq, nullptr)) return rc;
-  if (int32_t rc = tqkv_tq_scores(rq, s.codes, s.sigma, c->cent, D, s.n, out, nullptr)) return rc;
+  if (int32_t rc = tqkv_tq_scores_packed(rq, s.words, s.sigma, c->cent, c->cfg.bits, D, s.n, out,
+                                         nullptr))
+    return rc;
   TQKV_HIP(hipMemcpy(scores, out, size_t(s.n) * 4, hipMemcpyDeviceToHost));
   return ok();
 }
@@ -251,7 +285,9 @@ int32_t tqkv_kvcache_attend_values(tqkv_kvcache* c, int32_t layer, int32_t head,
   if (int32_t rc = staging(c, size_t(s.n) + size_t(D), &buf)) return rc;
   float *w = buf, *o = buf + s.n;
   if (s.n > 0) TQKV_HIP(hipMemcpy(w, weights, size_t(s.n) * 4, hipMemcpyHostToDevice));
-  if (int32_t rc = tqkv_tq_values(c->R, s.codes, s.sigma, c->cent, w, D, s.n, o, nullptr)) return rc;
+  if (int32_t rc = tqkv_tq_values_packed(c->R, s.words, s.sigma, c->cent, w, c->cfg.bits, D, s.n,
+                                         o, nullptr))
+    return rc;
   TQKV_HIP(hipMemcpy(out, o, size_t(D) * 4, hipMemcpyDeviceToHost));
   return ok();
 }
@@ -277,13 +313,35 @@ int32_t tqkv_kvcache_truncate(tqkv_kvcache* c, int32_t layer, int64_t n_keep) {
 
 int64_t tqkv_kvcache_memory_bytes(const tqkv_kvcache* c) {
   if (!c) return 0;
-  // CompressedVector::size_bytes (config.rs:50-55) per stored vector.
-  const int64_t D = c->cfg.head_dim, bits = c->cfg.bits, m = c->cfg.qjl_m;
-  const int64_t per = ((D + (64 / bits) - 1) / (64 / bits)) * 8 + ((m + 63) / 64) * 8 + 4 + 4 + 8 + 4;
+  // CompressedVector::size_bytes (config.rs:50-55) per stored vector: packed
+  // codes, QJL bits in u64 words, residual norm and scale, dim and bits.
+  const int64_t m = c->cfg.qjl_m;
+  const int64_t per = int64_t(c->pw) * 8 + ((m + 63) / 64) * 8 + 4 + 4 + 8 + 4;
   int64_t n = 0;
   for (const Stream& s : c->keys) n += s.n;
   for (const Stream& s : c->values) n += s.n;
   return n * per;
+}
+
+int32_t tqkv_kvcache_device_bytes(const tqkv_kvcache* c, int64_t* held, int64_t* reserved) {
+  if (!c) return fail(TQKV_EINVAL_ARG, "null cache");
+  const int64_t D = c->cfg.head_dim, W = c->words, PW = c->pw;
+  // Per stored vector: packed codes, scale, and with QJL its sign words and
+  // residual norm.
+  const int64_t per_held = PW * 8 + 4 + (W ? W * 4 + 4 : 0);
+  const int64_t per_slot = PW * 8 + 4 + (W ? W : 1) * 4 + 4;
+  int64_t n = 0, slots = 0;
+  for (const std::vector<Stream>* v : {&c->keys, &c->values})
+    for (const Stream& s : *v) {
+      n += s.n;
+      slots += s.cap;
+    }
+  const int64_t n_levels = int64_t(1) << c->cfg.bits;
+  const int64_t tables = D * D * 4 + (W ? int64_t(c->cfg.qjl_m) : 1) * D * 4 +
+                         (n_levels + 1) * 8 + n_levels * 4;
+  if (held) *held = n * per_held;
+  if (reserved) *reserved = slots * per_slot + tables + int64_t(c->scratch_floats) * 4;
+  return ok();
 }
 
 int32_t tqkv_kvcache_read(tqkv_kvcache* c, int32_t layer, int32_t head, int32_t which_values,
@@ -296,7 +354,14 @@ int32_t tqkv_kvcache_read(tqkv_kvcache* c, int32_t layer, int32_t head, int32_t 
                 (long long)(first + n), (long long)s.n);
   if (n == 0) return ok();
   const int D = c->cfg.head_dim, W = c->words;
-  if (codes) TQKV_HIP(hipMemcpy(codes, s.codes + first * D, size_t(n) * D, hipMemcpyDeviceToHost));
+  if (codes) {
+    float* buf = nullptr;
+    if (int32_t rc = staging(c, (size_t(n) * D + 3) / 4, &buf)) return rc;
+    uint8_t* u8 = reinterpret_cast<uint8_t*>(buf);
+    if (int32_t rc = tqkv_unpack_codes(s.words + first * c->pw, n, D, c->cfg.bits, u8, nullptr))
+      return rc;
+    TQKV_HIP(hipMemcpy(codes, u8, size_t(n) * D, hipMemcpyDeviceToHost));
+  }
   if (scale) TQKV_HIP(hipMemcpy(scale, s.sigma + first, size_t(n) * 4, hipMemcpyDeviceToHost));
   if (signs && W)
     TQKV_HIP(hipMemcpy(signs, s.signs + first * W, size_t(n) * W * 4, hipMemcpyDeviceToHost));

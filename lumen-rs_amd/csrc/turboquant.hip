@@ -426,18 +426,64 @@ __global__ __launch_bounds__(kWave) void tq_rotate_query_kernel(const float* __r
   }
 }
 
+// Code j of vector t, stored one byte per code ([n, D] u8) ...
+struct CodesU8 {
+  const uint8_t* __restrict__ p;
+  int D;
+  __device__ __forceinline__ int operator()(int64_t t, int j) const { return p[t * D + j]; }
+};
+// ... or in CompressedVector::stage1_packed's layout (bitpack.rs:11-52):
+// `per` = 64 / bits codes to a u64 word, code j of a vector at bits
+// (j % per) * bits of word j / per, none straddling two words; `words` =
+// ceil(D / per) words a vector.
+struct CodesPacked {
+  const uint64_t* __restrict__ p;
+  int words, bits, per;
+  __device__ __forceinline__ int operator()(int64_t t, int j) const {
+    const uint64_t w = p[t * words + j / per];
+    return int(w >> ((j % per) * bits)) & ((1 << bits) - 1);
+  }
+};
+
 // Stage-1 scores: one thread per token, sum over channels from -0.0, times
 // the token's scale (compressor.rs:165-184).
-__global__ void tq_scores_kernel(const float* __restrict__ rq, const uint8_t* __restrict__ codes,
+template <class Codes>
+__global__ void tq_scores_kernel(const float* __restrict__ rq, Codes code,
                                  const float* __restrict__ sigma,
                                  const float* __restrict__ cent_f32, int D, int64_t n,
                                  float* __restrict__ scores) {
   const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t >= n) return;
-  const uint8_t* c = codes + t * D;
   float acc = -0.0f;
-  for (int i = 0; i < D; ++i) acc = add(acc, mul(rq[i], cent_f32[c[i]]));
+  for (int i = 0; i < D; ++i) acc = add(acc, mul(rq[i], cent_f32[code(t, i)]));
   scores[t] = mul(acc, sigma[t]);
+}
+
+// pack_codes (bitpack.rs:17-33) over n vectors of D u8 codes: one thread per
+// output word.
+__global__ void pack_codes_kernel(const uint8_t* __restrict__ codes, int64_t n, int D, int bits,
+                                  int words, uint64_t* __restrict__ out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n * words) return;
+  const int64_t t = i / words;
+  const int w = int(i - t * words), per = 64 / bits;
+  const uint8_t* c = codes + t * D;
+  uint64_t acc = 0;
+  for (int k = 0; k < per; ++k) {
+    const int j = w * per + k;
+    if (j < D) acc |= uint64_t(c[j]) << (k * bits);
+  }
+  out[i] = acc;
+}
+
+// unpack_codes (bitpack.rs:36-49): one thread per code.
+__global__ void unpack_codes_kernel(const uint64_t* __restrict__ words_in, int64_t n, int D,
+                                    int bits, int words, uint8_t* __restrict__ codes) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n * D) return;
+  const int64_t t = i / D;
+  const CodesPacked code{words_in, words, bits, 64 / bits};
+  codes[i] = uint8_t(code(t, int(i - t * D)));
 }
 
 // QJLProjector::project_query (qjl.rs:76-84): pq[row] = sum_j Phi[row][j] *
@@ -553,7 +599,8 @@ __global__ void qjl_apply_correction_kernel(const uint16_t* __restrict__ k_dq,
 // attend_values: output channel i sums, token by token in order and channel
 // j by channel j, R[j][i] * (centroid * (scale * w)); tokens with |w| < 1e-10
 // are skipped (simple.rs:40-62, 105-118).
-__global__ void tq_values_kernel(const float* __restrict__ R, const uint8_t* __restrict__ codes,
+template <class Codes>
+__global__ void tq_values_kernel(const float* __restrict__ R, Codes code,
                                  const float* __restrict__ sigma,
                                  const float* __restrict__ cent_f32, const float* __restrict__ w,
                                  int D, int64_t n, float* __restrict__ out) {
@@ -564,8 +611,8 @@ __global__ void tq_values_kernel(const float* __restrict__ R, const uint8_t* __r
     const float wt = w[t];
     if (fabsf(wt) < 1e-10f) continue;
     const float sc = mul(sigma[t], wt);
-    const uint8_t* c = codes + t * D;
-    for (int j = 0; j < D; ++j) acc = add(acc, mul(R[int64_t(j) * D + i], mul(cent_f32[c[j]], sc)));
+    for (int j = 0; j < D; ++j)
+      acc = add(acc, mul(R[int64_t(j) * D + i], mul(cent_f32[code(t, j)], sc)));
   }
   out[i] = acc;
 }
@@ -816,9 +863,10 @@ extern "C" int32_t tqkv_tq_scores(const float* rq, const uint8_t* codes, const f
   if (n == 0) return ok();
   if (!rq || !codes || !sigma || !centroids_f32 || !scores) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (dim <= 0 || n < 0) return fail(TQKV_EINVAL_SHAPE, "dim=%d n=%lld", dim, (long long)n);
-  hipLaunchKernelGGL(tq_scores_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), rq, codes, sigma, centroids_f32, dim,
-                     n, scores);
+  if ((n + 255) / 256 > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "n=%lld", (long long)n);
+  hipLaunchKernelGGL(tq_scores_kernel<CodesU8>, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), rq, CodesU8{codes, dim}, sigma,
+                     centroids_f32, dim, n, scores);
   TQKV_LAUNCHED();
   return ok();
 }
@@ -829,8 +877,91 @@ extern "C" int32_t tqkv_tq_values(const float* rotation, const uint8_t* codes, c
   if (!rotation || !centroids_f32 || !out || (n > 0 && (!codes || !sigma || !weights)))
     return fail(TQKV_EINVAL_ARG, "null pointer");
   if (dim <= 0 || n < 0) return fail(TQKV_EINVAL_SHAPE, "dim=%d n=%lld", dim, (long long)n);
-  hipLaunchKernelGGL(tq_values_kernel, dim3(unsigned((dim + 63) / 64)), dim3(64), 0,
-                     reinterpret_cast<hipStream_t>(stream), rotation, codes, sigma, centroids_f32,
+  hipLaunchKernelGGL(tq_values_kernel<CodesU8>, dim3(unsigned((dim + 63) / 64)), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), rotation, CodesU8{codes, dim}, sigma,
+                     centroids_f32, weights, dim, n, out);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+namespace {
+
+// The packed layout's shape for (dim, bits), or an error status.
+int32_t packed_shape(int32_t dim, int32_t bits, int64_t n, CodesPacked* out) {
+  if (bits < 1 || bits > 8) return fail(TQKV_EUNSUPPORTED, "bits=%d not in 1..8", bits);
+  if (dim <= 0 || dim > 65536 || n < 0)
+    return fail(TQKV_EINVAL_SHAPE, "dim=%d n=%lld", dim, (long long)n);
+  const int per = 64 / bits;
+  *out = CodesPacked{nullptr, (dim + per - 1) / per, bits, per};
+  return ok();
+}
+
+}  // namespace
+
+extern "C" int64_t tqkv_packed_words(int32_t dim, int32_t bits) {
+  CodesPacked c{};
+  if (bits < 1 || bits > 8 || dim <= 0) return -1;
+  if (packed_shape(dim, bits, 0, &c)) return -1;
+  return c.words;
+}
+
+extern "C" int32_t tqkv_pack_codes(const uint8_t* codes, int64_t n, int32_t dim, int32_t bits,
+                                   uint64_t* words, tqkv_stream stream) {
+  CodesPacked c{};
+  if (int32_t rc = packed_shape(dim, bits, n, &c)) return rc;
+  if (n == 0) return ok();
+  if (!codes || !words) return fail(TQKV_EINVAL_ARG, "null pointer");
+  const int64_t blocks = (n * c.words + 255) / 256;
+  if (blocks > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "n=%lld", (long long)n);
+  hipLaunchKernelGGL(pack_codes_kernel, dim3(unsigned(blocks)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), codes, n, dim, bits, c.words, words);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_unpack_codes(const uint64_t* words, int64_t n, int32_t dim, int32_t bits,
+                                     uint8_t* codes, tqkv_stream stream) {
+  CodesPacked c{};
+  if (int32_t rc = packed_shape(dim, bits, n, &c)) return rc;
+  if (n == 0) return ok();
+  if (!codes || !words) return fail(TQKV_EINVAL_ARG, "null pointer");
+  const int64_t blocks = (n * dim + 255) / 256;
+  if (blocks > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "n=%lld", (long long)n);
+  hipLaunchKernelGGL(unpack_codes_kernel, dim3(unsigned(blocks)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), words, n, dim, bits, c.words, codes);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_scores_packed(const float* rq, const uint64_t* words,
+                                         const float* sigma, const float* centroids_f32,
+                                         int32_t bits, int32_t dim, int64_t n, float* scores,
+                                         tqkv_stream stream) {
+  CodesPacked c{};
+  if (int32_t rc = packed_shape(dim, bits, n, &c)) return rc;
+  if (n == 0) return ok();
+  if (!rq || !words || !sigma || !centroids_f32 || !scores)
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  if ((n + 255) / 256 > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "n=%lld", (long long)n);
+  c.p = words;
+  hipLaunchKernelGGL(tq_scores_kernel<CodesPacked>, dim3(unsigned((n + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), rq, c, sigma, centroids_f32, dim, n,
+                     scores);
+  TQKV_LAUNCHED();
+  return ok();
+}
+
+extern "C" int32_t tqkv_tq_values_packed(const float* rotation, const uint64_t* words,
+                                         const float* sigma, const float* centroids_f32,
+                                         const float* weights, int32_t bits, int32_t dim,
+                                         int64_t n, float* out, tqkv_stream stream) {
+  CodesPacked c{};
+  if (int32_t rc = packed_shape(dim, bits, n, &c)) return rc;
+  if (!rotation || !centroids_f32 || !out || (n > 0 && (!words || !sigma || !weights)))
+    return fail(TQKV_EINVAL_ARG, "null pointer");
+  c.p = words;
+  hipLaunchKernelGGL(tq_values_kernel<CodesPacked>, dim3(unsigned((dim + 63) / 64)), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), rotation, c, sigma, centroids_f32,
                      weights, dim, n, out);
   TQKV_LAUNCHED();
   return ok();

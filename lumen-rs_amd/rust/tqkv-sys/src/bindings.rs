@@ -167,6 +167,11 @@ extern "C" {
     pub fn tqkv_qjl_apply_correction(k_dq: *const u16, signs: *const u32, rnorm: *const f32, qjl: *const f32, rows: i64, dim: i32, m: i32, k_eff: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_codebook_dequantize(codes: *const u8, sigma: *const f32, centroids: *const f32, bits: i32, rows: i64, dim: i32, out: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_tq_values(rotation: *const f32, codes: *const u8, sigma: *const f32, centroids_f32: *const f32, weights: *const f32, dim: i32, n: i64, out: *mut f32, stream: tqkv_stream) -> i32;
+    pub fn tqkv_packed_words(dim: i32, bits: i32) -> i64;
+    pub fn tqkv_pack_codes(codes: *const u8, n: i64, dim: i32, bits: i32, words: *mut u64, stream: tqkv_stream) -> i32;
+    pub fn tqkv_unpack_codes(words: *const u64, n: i64, dim: i32, bits: i32, codes: *mut u8, stream: tqkv_stream) -> i32;
+    pub fn tqkv_tq_scores_packed(rq: *const f32, words: *const u64, sigma: *const f32, centroids_f32: *const f32, bits: i32, dim: i32, n: i64, scores: *mut f32, stream: tqkv_stream) -> i32;
+    pub fn tqkv_tq_values_packed(rotation: *const f32, words: *const u64, sigma: *const f32, centroids_f32: *const f32, weights: *const f32, bits: i32, dim: i32, n: i64, out: *mut f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_rotate_bf16(x: *const u16, rows: i64, dim: i32, rotation: *const f32, transpose: i32, y: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_kvcache_create(cfg: *const tqkv_tq_config, rotation: *const f32, qjl: *const f32, n_layers: i32, n_kv_heads: i32, out: *mut *mut tqkv_kvcache) -> i32;
     pub fn tqkv_kvcache_destroy(cache: *mut tqkv_kvcache) -> i32;
@@ -177,6 +182,7 @@ extern "C" {
     pub fn tqkv_kvcache_clear(cache: *mut tqkv_kvcache) -> i32;
     pub fn tqkv_kvcache_truncate(cache: *mut tqkv_kvcache, layer: i32, n_keep: i64) -> i32;
     pub fn tqkv_kvcache_memory_bytes(cache: *const tqkv_kvcache) -> i64;
+    pub fn tqkv_kvcache_device_bytes(cache: *const tqkv_kvcache, held: *mut i64, reserved: *mut i64) -> i32;
     pub fn tqkv_kvcache_read(cache: *mut tqkv_kvcache, layer: i32, head: i32, which_values: i32, first: i64, n: i64, codes: *mut u8, scale: *mut f32, signs: *mut u32, residual_norm: *mut f32) -> i32;
     pub fn tqkv_synth_bf16(out: *mut u16, rows: i64, dim: i32, seed: u64, outlier_frac: f32, outlier_mult: f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_read_probe(data: *const f32, bytes: usize, scratch: *mut f32, scratch_bytes: usize, out: *mut f32, stream: tqkv_stream) -> i32;

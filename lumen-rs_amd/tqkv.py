@@ -121,6 +121,11 @@ _SIGS = {
     "tqkv_decode_attend_codebook_qjl": (I32, [P, I32, I32, I32, I32, F32, P, P, I32, P, I32, P, P,
                                               P, P, P, I32, P, P, I64, I64, P, P, SZ, P]),
     "tqkv_tq_values": (I32, [P, P, P, P, P, I32, I64, P, P]),
+    "tqkv_packed_words": (I64, [I32, I32]),
+    "tqkv_pack_codes": (I32, [P, I64, I32, I32, P, P]),
+    "tqkv_unpack_codes": (I32, [P, I64, I32, I32, P, P]),
+    "tqkv_tq_scores_packed": (I32, [P, P, P, P, I32, I32, I64, P, P]),
+    "tqkv_tq_values_packed": (I32, [P, P, P, P, P, I32, I32, I64, P, P]),
     "tqkv_codebook_dequantize": (I32, [P, P, P, I32, I64, I32, P, P]),
     "tqkv_rotate_bf16": (I32, [P, I64, I32, P, I32, P, P]),
     "tqkv_kvcache_create": (I32, [ctypes.POINTER(TqConfig), P, P, I32, I32, ctypes.POINTER(P)]),
@@ -132,6 +137,7 @@ _SIGS = {
     "tqkv_kvcache_clear": (I32, [P]),
     "tqkv_kvcache_truncate": (I32, [P, I32, I64]),
     "tqkv_kvcache_memory_bytes": (I64, [P]),
+    "tqkv_kvcache_device_bytes": (I32, [P, ctypes.POINTER(I64), ctypes.POINTER(I64)]),
     "tqkv_kvcache_read": (I32, [P, I32, I32, I32, I64, I64, P, P, P, P]),
     "tqkv_cache_create": (I32, [ctypes.POINTER(CacheConfig), ctypes.POINTER(P)]),
     "tqkv_cache_destroy": (I32, [P]),
@@ -651,6 +657,30 @@ def rotate_bf16(x, rows, dim, R, transpose, y, stream=None):
     check(lib().tqkv_rotate_bf16(x, rows, dim, R, int(transpose), y, stream))
 
 
+def packed_words(dim, bits):
+    """u64 words one vector of `dim` codes at `bits` packs into (-1 if out
+    of range)."""
+    return lib().tqkv_packed_words(dim, bits)
+
+
+def pack_codes(codes, n, dim, bits, words, stream=None):
+    """u8 codes [n, dim] -> u64 words in the stage1_packed layout; device."""
+    check(lib().tqkv_pack_codes(codes, n, dim, bits, words, stream))
+
+
+def unpack_codes(words, n, dim, bits, codes, stream=None):
+    check(lib().tqkv_unpack_codes(words, n, dim, bits, codes, stream))
+
+
+def tq_scores_packed(rq, words, sigma, centroids, bits, dim, n, scores, stream=None):
+    check(lib().tqkv_tq_scores_packed(rq, words, sigma, centroids, bits, dim, n, scores, stream))
+
+
+def tq_values_packed(R, words, sigma, centroids, weights, bits, dim, n, out, stream=None):
+    check(lib().tqkv_tq_values_packed(R, words, sigma, centroids, weights, bits, dim, n, out,
+                                      stream))
+
+
 class KVCache:
     """turboquant_cache::KVCache (SimpleCache semantics) on the device."""
 
@@ -707,6 +737,13 @@ class KVCache:
 
     def memory_bytes(self):
         return lib().tqkv_kvcache_memory_bytes(self.h)
+
+    def device_bytes(self):
+        """(held, reserved): bytes of the stored vectors on the device, and
+        all device memory the cache owns."""
+        held, reserved = I64(), I64()
+        check(lib().tqkv_kvcache_device_bytes(self.h, ctypes.byref(held), ctypes.byref(reserved)))
+        return held.value, reserved.value
 
     def read(self, layer, head, values=False, first=0, n=None):
         if n is None:

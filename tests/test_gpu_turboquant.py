@@ -191,13 +191,21 @@ def test_kvcache_matches_simple_cache(T):
     cos = rec @ V[7] / (np.linalg.norm(rec) * np.linalg.norm(V[7]))
     assert cos > 0.95
     assert 2 * 40 * dim * 4 / kv.memory_bytes() > 2.0
+    # memory_bytes is CompressedVector::size_bytes summed (config.rs:50-55):
+    # 128 3-bit codes at 21 a word take 7 words (56 bytes), one u64 of QJL
+    # bits, 20 bytes of fields, 80 vectors. The device holds the packed
+    # words, the scale, two u32 sign words and the residual norm of each.
+    assert kv.memory_bytes() == 80 * (56 + 8 + 20)
+    held, reserved = kv.device_bytes()
+    assert held == 80 * (56 + 4 + 8 + 4), held
+    assert 2 * 40 * dim * 4 / held > 2.0 and reserved > held
     # truncate keeps the first n_keep of every head of the layer; clear empties.
     kv.store(1, 1, K[:10], V[:10])
     kv.truncate(1, 12)
     assert (kv.seq_len(1, 0), kv.seq_len(1, 1)) == (12, 10)
     assert np.array_equal(kv.attend_keys(1, 0, q).view(np.uint32), s[:12].view(np.uint32))
     kv.clear()
-    assert kv.seq_len(1, 0) == 0 and kv.memory_bytes() == 0
+    assert kv.seq_len(1, 0) == 0 and kv.memory_bytes() == 0 and kv.device_bytes()[0] == 0
     with pytest.raises(T.TqkvError) as e:
         kv.store(2, 0, K[:1], V[:1])
     assert e.value.status == T.EINVAL_ARG
@@ -309,3 +317,87 @@ def test_gpu_path_fused_matches_rotate_then_encode(T):
     print(f"[tq-gpu-path] sigma MSE {sig_mse:.3e}, agreement {agree:.4f}, V_dq MSE {dq_mse:.3e}",
           flush=True)
     assert sig_mse < 1e-3 and agree > 0.99 and dq_mse < 1e-2
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("dim", [1, 21, 64, 100, 128, 512])
+def test_pack_codes_matches_bitpack(T, bits, dim):
+    """tqkv_pack_codes / tqkv_unpack_codes against the oracle's restatement
+    of bitpack::pack_codes / unpack_codes (bitpack.rs:11-52), itself pinned
+    to the reference's round-trip and size tests: word for word, unused high
+    bits zero, and back to the same codes."""
+    n = 37
+    print(f"[pack] bits={bits} dim={dim} n={n}", flush=True)
+    codes = np.random.default_rng(bits * 1000 + dim).integers(0, 1 << bits, (n, dim),
+                                                               dtype=np.uint8)
+    pw = T.packed_words(dim, bits)
+    assert pw == O.lib().oracle_packed_words(dim, bits) == -(-dim // (64 // bits))
+    want = np.stack([O.pack_codes(r, bits) for r in codes])
+    dc = T.DeviceArray.of(codes)
+    dw = T.DeviceArray((n, pw), np.uint64, np.full((n, pw), 0xA5A5A5A5A5A5A5A5, np.uint64))
+    T.pack_codes(dc.ptr, n, dim, bits, dw.ptr)
+    T.hip().sync()
+    assert np.array_equal(dw.numpy(), want)
+    back = T.DeviceArray((n, dim), np.uint8, np.full((n, dim), 0xEE, np.uint8))
+    T.unpack_codes(dw.ptr, n, dim, bits, back.ptr)
+    T.hip().sync()
+    assert np.array_equal(back.numpy(), codes)
+
+
+def test_pack_codes_rejects_bad_shapes(T):
+    assert T.packed_words(64, 0) == -1 and T.packed_words(64, 9) == -1
+    assert T.packed_words(0, 3) == -1
+    for bits, dim, status in [(0, 64, T.EUNSUPPORTED), (9, 64, T.EUNSUPPORTED),
+                              (3, 0, T.EINVAL_SHAPE)]:
+        with pytest.raises(T.TqkvError) as e:
+            T.pack_codes(None, 1, dim, bits, None)
+        assert e.value.status == status
+    with pytest.raises(T.TqkvError) as e:
+        T.pack_codes(None, 4, 64, 3, None)
+    assert e.value.status == T.EINVAL_ARG
+    T.pack_codes(None, 0, 64, 3, None)  # nothing to pack
+
+
+@pytest.mark.parametrize("dim,bits", [(64, 2), (128, 3), (128, 4), (256, 5), (64, 8), (128, 1)])
+def test_packed_estimators_match_unpacked(T, dim, bits):
+    """tqkv_tq_scores_packed / tqkv_tq_values_packed read the packed words
+    and give the u8-code kernels' results bit for bit (same sums, same
+    order), and those equal the oracle's SimpleCache estimators."""
+    n, m = 53, 0
+    print(f"[packed-est] dim={dim} bits={bits} n={n}", flush=True)
+    R, phi, b, c = tables(T, dim, bits, m)
+    comp = O.Compressor(dim, bits, 1, R, phi[:1])
+    x = inputs_f32(n, dim, 77 + bits)
+    ck = comp.compress(x)
+    codes = np.stack([O.unpack_codes(w, dim, bits) for w in ck[0]])
+    sigma = ck[3].astype(np.float32)
+    cent = c.astype(np.float32)
+    dR, dcent = T.DeviceArray.of(R), T.DeviceArray.of(cent)
+    dcodes, dsig = T.DeviceArray.of(codes), T.DeviceArray.of(sigma)
+    dw = T.DeviceArray.of(np.ascontiguousarray(ck[0]))
+    rng = np.random.default_rng(dim + bits)
+    q = rng.standard_normal(dim).astype(np.float32)
+    dq = T.DeviceArray.of(q)
+    rq = T.DeviceArray((dim,), np.float32)
+    T.tq_rotate_query(dR.ptr, dq.ptr, dim, rq.ptr)
+    s_u8 = T.DeviceArray((n,), np.float32)
+    s_pk = T.DeviceArray((n,), np.float32)
+    T.check(T.lib().tqkv_tq_scores(rq.ptr, dcodes.ptr, dsig.ptr, dcent.ptr, dim, n, s_u8.ptr,
+                                   None))
+    T.tq_scores_packed(rq.ptr, dw.ptr, dsig.ptr, dcent.ptr, bits, dim, n, s_pk.ptr)
+    T.hip().sync()
+    a, p = s_u8.numpy(), s_pk.numpy()
+    assert np.array_equal(a.view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(p.view(np.uint32), comp.scores(q, ck).view(np.uint32))
+    w = rng.random(n).astype(np.float32)
+    w[5] = 0.0
+    dwt = T.DeviceArray.of(w)
+    o_u8 = T.DeviceArray((dim,), np.float32)
+    o_pk = T.DeviceArray((dim,), np.float32)
+    T.check(T.lib().tqkv_tq_values(dR.ptr, dcodes.ptr, dsig.ptr, dcent.ptr, dwt.ptr, dim, n,
+                                   o_u8.ptr, None))
+    T.tq_values_packed(dR.ptr, dw.ptr, dsig.ptr, dcent.ptr, dwt.ptr, bits, dim, n, o_pk.ptr)
+    T.hip().sync()
+    a, p = o_u8.numpy(), o_pk.numpy()
+    assert np.array_equal(a.view(np.uint32), p.view(np.uint32))
+    assert np.array_equal(p.view(np.uint32), comp.attend_values(w, ck).view(np.uint32))
