@@ -502,8 +502,8 @@ def append_main(T, hip, args):
     """one layer's append-quantize round trip, B=1, 8 KV
     heads, D=128, 4,096 tokens, bf16 N(0,1) with 2% of channels x8, 4-bit
     gs64, seed-42 rotation. Timed: quantize K and V (mlx affine), the
-    dequantize back, the affine+rotation mode (rotate, then quantize;
-    gemma4_moe.rs:4162-4173) and the TurboQuant codebook encode
+    dequantize back, the affine+rotation mode (K rotated by R, then K and V
+    quantized, one launch; gemma4_moe.rs:4154-4173) and the TurboQuant codebook encode
     (compress_one, QJL m=64). value = tokens/s of the affine K+V quantize."""
     B, HKV, D, S, GS, BITS, M = 1, 8, 128, 4096, 64, 4, 64
     stream = hip.stream()
@@ -533,10 +533,18 @@ def append_main(T, hip, args):
         for n in ("k", "v"):
             T.affine_dequantize(*(a.ptr for a in q3[n]), slabs * S, D, GS, BITS, deq[n].ptr, stream)
 
-    def rotq():
-        for n in ("k", "v"):
-            T.rotate_bf16(x[n].ptr, slabs * S, D, R.ptr, False, rot[n].ptr, stream)
-        T.affine_quantize_kv(rot["k"].ptr, rot["v"].ptr, slabs, S, D, GS, BITS, BITS,
+    def rotq():  # the affine + rotation mode: K rotated and quantized, V quantized, one launch
+        T.affine_quantize_kv_rotated(x["k"].ptr, x["v"].ptr, slabs, S, D, GS, BITS, BITS, R.ptr,
+                                     tuple(a.ptr for a in q3["k"]), tuple(a.ptr for a in q3["v"]),
+                                     stream=stream)
+
+    def rotq_k():  # the rotate-and-quantize of K alone (the rotation's FLOPs)
+        T.affine_quantize_rotated(x["k"].ptr, slabs, S, D, GS, BITS, R.ptr,
+                                  *(a.ptr for a in q3["k"]), stream=stream)
+
+    def rotq_two():  # the same with the VALU rotation kernel, then the K+V quantize
+        T.rotate_bf16(x["k"].ptr, slabs * S, D, R.ptr, False, rot["k"].ptr, stream)
+        T.affine_quantize_kv(rot["k"].ptr, x["v"].ptr, slabs, S, D, GS, BITS, BITS,
                              tuple(a.ptr for a in q3["k"]), tuple(a.ptr for a in q3["v"]),
                              stream=stream)
 
@@ -547,12 +555,15 @@ def append_main(T, hip, args):
 
     settle = 16 if args.settle is None else max(0, args.settle)
     for _ in range(settle + args.warmup):
-        quant(), dequant(), rotq(), tq()
+        quant(), dequant(), rotq(), rotq_k(), rotq_two(), tq()
     hip.sync()
     n = args.steps
     ms_q = _loop_ms(hip, stream, quant, n)
     ms_d = _loop_ms(hip, stream, dequant, n)
     ms_r = _loop_ms(hip, stream, rotq, n)
+    ms_rk = _loop_ms(hip, stream, rotq_k, n)
+    ms_r2 = _loop_ms(hip, stream, rotq_two, n)
+    rot_flop = 2 * slabs * S * D * D  # K only: V is not rotated (gemma4_moe.rs:4154-4173)
     ms_t = _loop_ms(hip, stream, tq, max(3, n // 5))
     in_bytes = 2 * slabs * S * D * 2
     q_bytes = 2 * slabs * S * (words * 4 + 2 * groups * 2)
@@ -573,7 +584,19 @@ def append_main(T, hip, args):
         {"dequantize": {"ms": round(ms_d, 5), "gbps": round((q_bytes + in_bytes) / (ms_d * 1e-3) / 1e9, 1)},
          "affine_rotation": {"ms": round(ms_r, 5),
                              "tokens_per_s": round(S / (ms_r * 1e-3), 1),
-                             "rotation_flop": 2 * 2 * slabs * S * D * D},
+                             "kernel": "affine_quantize_rot_kernel<128>: K = bf16(x R) "
+                                       "(R split exactly into three bf16 parts, "
+                                       "v_mfma_f32_16x16x32_bf16, f32 accumulation), "
+                                       "quantized in registers; then V quantized; one launch",
+                             "rotation_flop": rot_flop,
+                             "k_only_ms": round(ms_rk, 5),
+                             "k_only_tflops": round(rot_flop / (ms_rk * 1e-3) / 1e12, 1),
+                             "k_only_frac_fp32_peak": round(rot_flop / (ms_rk * 1e-3) / 157.3e12, 4),
+                             "bytes": in_bytes + q_bytes,
+                             "gbps": round((in_bytes + q_bytes) / (ms_r * 1e-3) / 1e9, 1),
+                             "two_launch_ms": round(ms_r2, 5),
+                             "two_launch": "tqkv_rotate_bf16 (VALU f32, R in LDS) of K, then "
+                                           "the K+V quantize"},
          "turboquant_encode": {"ms": round(ms_t, 5), "tokens_per_s": round(S / (ms_t * 1e-3), 1),
                                "bytes": in_bytes + tq_bytes, "qjl_m": M,
                                "note": "compress_one restated bit-exactly: sequential f32 "

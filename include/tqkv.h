@@ -88,6 +88,38 @@ int32_t tqkv_affine_quantize_kv(const uint16_t* k, const uint16_t* v, int64_t n_
                                 int64_t dst_cap, int64_t dst_start, tqkv_stream stream);
 
 /*
+ * The affine + rotation cache mode (gemma4_moe.rs:4154-4173): k_to_cache =
+ * rotate_last_axis(k, R) (turboquant.rs:258-267: bf16(f32(x) @ R)), then the
+ * cache's mlx::quantize, in one pass with no rotated copy in HBM. The product
+ * runs on the matrix cores in f32 (MLX's summation order is its own; each
+ * rotated element is within an f32 sum's error bound plus half a bf16 step
+ * of the exact product), the quantize is tqkv_affine_quantize's bit for bit
+ * on the rotated bf16 rows.
+ * rotation: device f32 [dim, dim] row-major (y = x R). dim in {128, 256}
+ * (TQKV_EUNSUPPORTED otherwise: use tqkv_rotate_bf16, then
+ * tqkv_affine_quantize), group_size <= 128; x and rotation 16-byte aligned.
+ * `rotated` (optional, NULL for none): bf16 [n_slabs * s, dim] receives the
+ * rotated rows. Device.
+ */
+int32_t tqkv_affine_quantize_rotated(const uint16_t* x, int64_t n_slabs, int64_t s, int32_t dim,
+                                     int32_t group_size, int32_t bits, const float* rotation,
+                                     uint32_t* packed, uint16_t* scales, uint16_t* biases,
+                                     int64_t dst_cap, int64_t dst_start, uint16_t* rotated,
+                                     tqkv_stream stream);
+/*
+ * A cache append of that mode in one launch: K rotated by R and quantized
+ * (as tqkv_affine_quantize_rotated), V quantized as it is (the reference does
+ * not rotate V). Arguments as tqkv_affine_quantize_kv plus `rotation`.
+ */
+int32_t tqkv_affine_quantize_kv_rotated(const uint16_t* k, const uint16_t* v, int64_t n_slabs,
+                                        int64_t s, int32_t dim, int32_t group_size,
+                                        int32_t bits_k, int32_t bits_v, const float* rotation,
+                                        uint32_t* k_packed, uint16_t* k_scales,
+                                        uint16_t* k_biases, uint32_t* v_packed,
+                                        uint16_t* v_scales, uint16_t* v_biases, int64_t dst_cap,
+                                        int64_t dst_start, tqkv_stream stream);
+
+/*
  * mlx::dequantize(packed, scales, biases, group_size, bits) to bf16, as the
  * reference's prefill fallback uses it (gemma4_moe.rs:2394-2399):
  * out = bf16(bf16(scale * code) + bias). rows = number of [dim] rows.

@@ -39,19 +39,30 @@ __device__ __forceinline__ void load_lane(const uint16_t* p, float (&v)[kLaneEle
   }
 }
 
-// Quantizes the lane's elements; a group is gs / 16 adjacent lanes (a power
-// of two), whose min and max meet in a butterfly. Every lane of the
-// wavefront must call it (the butterfly exchanges across lanes).
-__device__ __forceinline__ LaneCodes quantize_lane(const float (&v)[kLaneElems], int gs, int bits) {
+// Quantizes N (a multiple of 8) consecutive elements of a row held by each
+// lane; a group is `lpg` adjacent lanes (a power of two), whose min and max
+// meet in a butterfly. Writes the group's f32 scale and bias and the lane's
+// codes as N / 8 chunks of 8. Every lane of the wavefront must call it (the
+// butterfly exchanges across lanes).
+//
+// kFastQuotient: the code of an element is roundf(RN((v - bias) / scale))
+// clamped; instead of the correctly rounded division it multiplies by
+// RN(1 / scale), whose product is within 3 ulp of the rounded quotient, and
+// takes the exact division only where the product lies within 2^-20 of
+// its value from a rounding boundary k + 1/2 (where the two could round to
+// different integers). The codes are the same bits either way.
+template <int N, bool kFastQuotient = false>
+__device__ __forceinline__ void quantize_elems(const float (&v)[N], int lpg, int bits,
+                                               float& scale_out, float& bias_out,
+                                               uint64_t (&chunk)[N / 8]) {
   // The Metal kernel starts w_min at the dtype's max and w_max at 0.
   float w_min = __uint_as_float(0x7f7f0000u);
   float w_max = 0.0f;
 #pragma unroll
-  for (int e = 0; e < kLaneElems; ++e) {
+  for (int e = 0; e < N; ++e) {
     w_min = fminf(w_min, v[e]);
     w_max = fmaxf(w_max, v[e]);
   }
-  const int lpg = gs / kLaneElems;
   for (int off = 1; off < lpg; off <<= 1) {
     w_min = fminf(w_min, __shfl_xor(w_min, off, 64));
     w_max = fmaxf(w_max, __shfl_xor(w_max, off, 64));
@@ -67,20 +78,47 @@ __device__ __forceinline__ LaneCodes quantize_lane(const float (&v)[kLaneElems],
   scale = at_zero ? scale : edge / q0;
   const float bias = at_zero ? 0.0f : edge;
 
-  LaneCodes r;
-  r.scale = scale;
-  r.bias = bias;
+  scale_out = scale;
+  bias_out = bias;
+  if constexpr (kFastQuotient) {
+    const float inv = 1.0f / scale;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint64_t c = 0;
+    for (int h = 0; h < N / 8; ++h) {
+      uint64_t c = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float q = fminf(roundf((v[8 * h + e] - bias) / scale), n_bins);
-      const uint32_t code = q <= 0.0f ? 0u : uint32_t(q);
-      c |= uint64_t(code) << (bits * e);
+      for (int e = 0; e < 8; ++e) {
+        const float num = v[8 * h + e] - bias;
+        const float qa = num * inv;
+        const float fl = floorf(qa);
+        const float fr = qa - fl;  // exact (Sterbenz, or fl = qa)
+        float r = fr >= 0.5f ? fl + 1.0f : fl;
+        if (__builtin_expect(fabsf(fr - 0.5f) <= fabsf(qa) * 0x1p-20f, 0))
+          r = roundf(num / scale);
+        const float q = fminf(r, n_bins);
+        const uint32_t code = q <= 0.0f ? 0u : uint32_t(q);
+        c |= uint64_t(code) << (bits * e);
+      }
+      chunk[h] = c;
     }
-    r.chunk[h] = c;
+  } else {
+#pragma unroll
+    for (int h = 0; h < N / 8; ++h) {
+      uint64_t c = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = fminf(roundf((v[8 * h + e] - bias) / scale), n_bins);
+        const uint32_t code = q <= 0.0f ? 0u : uint32_t(q);
+        c |= uint64_t(code) << (bits * e);
+      }
+      chunk[h] = c;
+    }
   }
+}
+
+// Quantizes the lane's 16 elements; a group is gs / 16 adjacent lanes.
+__device__ __forceinline__ LaneCodes quantize_lane(const float (&v)[kLaneElems], int gs, int bits) {
+  LaneCodes r;
+  quantize_elems<kLaneElems>(v, gs / kLaneElems, bits, r.scale, r.bias, r.chunk);
   return r;
 }
 

@@ -116,6 +116,8 @@ extern "C" {
     pub fn tqkv_version() -> i32;
     pub fn tqkv_affine_quantize(x: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits: i32, packed: *mut u32, scales: *mut u16, biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_quantize_kv(k: *const u16, v: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits_k: i32, bits_v: i32, k_packed: *mut u32, k_scales: *mut u16, k_biases: *mut u16, v_packed: *mut u32, v_scales: *mut u16, v_biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
+    pub fn tqkv_affine_quantize_rotated(x: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits: i32, rotation: *const f32, packed: *mut u32, scales: *mut u16, biases: *mut u16, dst_cap: i64, dst_start: i64, rotated: *mut u16, stream: tqkv_stream) -> i32;
+    pub fn tqkv_affine_quantize_kv_rotated(k: *const u16, v: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits_k: i32, bits_v: i32, rotation: *const f32, k_packed: *mut u32, k_scales: *mut u16, k_biases: *mut u16, v_packed: *mut u32, v_scales: *mut u16, v_biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_dequantize(packed: *const u32, scales: *const u16, biases: *const u16, rows: i64, dim: i32, group_size: i32, bits: i32, out: *mut u16, stream: tqkv_stream) -> i32;
     pub fn tqkv_decode_attend_affine(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
     pub fn tqkv_decode_attend_affine_noalloc(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, out: *mut u16, stream: tqkv_stream) -> i32;

@@ -83,6 +83,10 @@ _SIGS = {
     "tqkv_affine_quantize": (I32, [P, I64, I64, I32, I32, I32, P, P, P, I64, I64, P]),
     "tqkv_affine_quantize_kv": (I32, [P, P, I64, I64, I32, I32, I32, I32, P, P, P, P, P, P, I64,
                                       I64, P]),
+    "tqkv_affine_quantize_rotated": (I32, [P, I64, I64, I32, I32, I32, P, P, P, P, I64, I64, P,
+                                           P]),
+    "tqkv_affine_quantize_kv_rotated": (I32, [P, P, I64, I64, I32, I32, I32, I32, P, P, P, P, P,
+                                              P, P, I64, I64, P]),
     "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
@@ -344,6 +348,23 @@ def affine_quantize_kv(k, v, n_slabs, s, dim, gs, bits_k, bits_v, kt, vt, dst_ca
     pointers of each."""
     check(lib().tqkv_affine_quantize_kv(k, v, n_slabs, s, dim, gs, bits_k, bits_v, *kt, *vt,
                                         s if dst_cap is None else dst_cap, dst_start, stream))
+
+
+def affine_quantize_rotated(x, n_slabs, s, dim, gs, bits, R, packed, scales, biases,
+                            dst_cap=None, dst_start=0, rotated=None, stream=None):
+    """bf16(x R) quantized in one pass; `rotated` (optional) receives the
+    rotated bf16 rows. Device pointers."""
+    check(lib().tqkv_affine_quantize_rotated(x, n_slabs, s, dim, gs, bits, R, packed, scales,
+                                             biases, s if dst_cap is None else dst_cap,
+                                             dst_start, rotated, stream))
+
+
+def affine_quantize_kv_rotated(k, v, n_slabs, s, dim, gs, bits_k, bits_v, R, kt, vt,
+                               dst_cap=None, dst_start=0, stream=None):
+    """K rotated by R and quantized, V quantized as it is, in one launch."""
+    check(lib().tqkv_affine_quantize_kv_rotated(k, v, n_slabs, s, dim, gs, bits_k, bits_v, R,
+                                                *kt, *vt, s if dst_cap is None else dst_cap,
+                                                dst_start, stream))
 
 
 def affine_dequantize(packed, scales, biases, rows, dim, gs, bits, out, stream=None):

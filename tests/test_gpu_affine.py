@@ -98,6 +98,105 @@ def test_quantize_kv_one_launch_matches_two(T, dim, gs, bk, bv, slabs, s):
             assert np.all(g[:, :start] == fill) and np.all(g[:, start + s:] == fill)
 
 
+@pytest.mark.parametrize("dim,gs,bk,bv,slabs,s", [
+    (128, 64, 4, 4, 8, 4096),   # config 0's append (K rotated, V as is)
+    (128, 32, 3, 8, 3, 37), (128, 128, 8, 2, 2, 15), (256, 64, 4, 3, 2, 29),
+    (256, 128, 5, 4, 1, 1), (256, 32, 6, 6, 3, 50),
+])
+def test_quantize_rotated(T, dim, gs, bk, bv, slabs, s):
+    """tqkv_affine_quantize_rotated / _kv_rotated: the affine + rotation mode
+    (gemma4_moe.rs:4154-4173) in one pass. rotate_last_axis is an f32 x f32
+    matmul cast to bf16 whose summation order is MLX's (open): every rotated
+    element must be within the error bound of an f32 sum in any order plus
+    half a bf16 step of the f64 product (a dropped term or a transposed R is
+    far outside it), over 99% equal to the f64 product's bf16 rounding, and
+    the codes, scales and biases
+    bit-exact with the oracle's quantizer on the kernel's own rotated rows;
+    V (not rotated, as the reference leaves it) bit-exact with the oracle;
+    rows outside [start, start + s) untouched."""
+    start, cap = 5, s + 9
+    print(f"[quantize-rot] dim={dim} gs={gs} bits={bk}/{bv} slabs={slabs} s={s}", flush=True)
+    k = kv_bf16((slabs, s, dim), 500 + dim + bk, frac=0.02, mult=8.0)
+    v = kv_bf16((slabs, s, dim), 600 + dim + bv, frac=0.02, mult=8.0)
+    R = O.rotation(dim, 42)
+    dk, dv, dR = T.DeviceArray.of(k), T.DeviceArray.of(v), T.DeviceArray.of(R)
+    rot = T.DeviceArray((slabs, s, dim), np.uint16, np.zeros((slabs, s, dim), np.uint16))
+    kt1 = device_triple(T, slabs, cap, dim, gs, bk)
+    T.affine_quantize_rotated(dk.ptr, slabs, s, dim, gs, bk, dR.ptr, *(a.ptr for a in kt1), cap,
+                              start, rot.ptr)
+    kt, vt = device_triple(T, slabs, cap, dim, gs, bk), device_triple(T, slabs, cap, dim, gs, bv)
+    T.affine_quantize_kv_rotated(dk.ptr, dv.ptr, slabs, s, dim, gs, bk, bv, dR.ptr,
+                                 tuple(a.ptr for a in kt), tuple(a.ptr for a in vt), cap, start)
+    T.hip().sync()
+    y = rot.numpy()
+    xf = O.bf16_to_f32(k).astype(np.float64)
+    exact = xf @ R.astype(np.float64)
+    got = O.bf16_to_f32(y).astype(np.float64)
+    # Any f32 summation order of D products is within D * 2^-24 * sum |x_k R_kc|
+    # of the exact sum; the bf16 cast adds half a bf16 step of the result.
+    acc_err = dim * 2.0 ** -24 * (np.abs(xf) @ np.abs(R.astype(np.float64)))
+    mag = np.maximum(np.abs(exact) + acc_err, 2.0 ** -126)
+    bound = acc_err + 0.5 * 2.0 ** (np.floor(np.log2(mag)) - 7)
+    ratio = np.abs(got - exact) / bound
+    same = np.mean(y == O.bf16_from_f32(exact.astype(np.float32)))
+    print(f"[quantize-rot] rotated: max {ratio.max():.3f} of the f32-sum + bf16-cast bound, "
+          f"{100 * same:.2f}% equal to the f64 product's rounding", flush=True)
+    assert ratio.max() <= 1.0 and same > 0.99
+    want_k = O.affine_quantize(y, gs, bk)
+    want_v = O.affine_quantize(v, gs, bv)
+    for trip, want in ((kt1, want_k), (kt, want_k), (vt, want_v)):
+        for a, w, fill in zip(trip, want, (0xDEADBEEF, 0x7777, 0x7777)):
+            g = a.numpy()
+            assert np.array_equal(g[:, start:start + s], w)
+            assert np.all(g[:, :start] == fill) and np.all(g[:, start + s:] == fill)
+
+
+@pytest.mark.parametrize("dim", [128, 256])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 8])
+def test_quantize_rotated_ties_and_grid(T, dim, bits):
+    """With R = I the rotated rows are the input exactly (x * 1 plus exact
+    zeros), so the rotate path's quantizer (which multiplies by 1 / scale
+    and takes the exact division only near a rounding boundary) is checked
+    against the oracle on inputs built to land on boundaries: groups
+    spanning [0, n_bins] with every other value at k + 1/2 (every code a
+    tie), and the golden tests' 2^-22 grid, rich in exact ties."""
+    print(f"[quantize-rot-ties] dim={dim} bits={bits}", flush=True)
+    top = (1 << bits) - 1
+    rows = 40
+    x = np.zeros((rows, dim), np.float32)
+    for g in range(dim // 64):
+        x[:, 64 * g] = 0.0
+        x[:, 64 * g + 1] = float(top)
+        x[:, 64 * g + 2:64 * (g + 1)] = (np.arange(62) % top) + 0.5
+    x[::2] *= -1.0  # the other sign of every tie on half the rows
+    xb = np.concatenate([O.bf16_from_f32(x), grid_bf16((rows, dim), 70 + bits)])[None]
+    eye = np.eye(dim, dtype=np.float32)
+    dx, dR = T.DeviceArray.of(xb), T.DeviceArray.of(eye)
+    n = xb.shape[1]
+    rot = T.DeviceArray((1, n, dim), np.uint16, np.zeros((1, n, dim), np.uint16))
+    t = device_triple(T, 1, n, dim, 64, bits)
+    T.affine_quantize_rotated(dx.ptr, 1, n, dim, 64, bits, dR.ptr, *(a.ptr for a in t), n, 0,
+                              rot.ptr)
+    T.hip().sync()
+    y = rot.numpy()
+    # x * 1 plus zeros: the input, except that -0 sums to +0.
+    assert np.array_equal(y, np.where(xb == 0x8000, 0, xb).astype(np.uint16))
+    for a, w in zip(t, O.affine_quantize(y, 64, bits)):
+        assert np.array_equal(a.numpy(), w)
+
+
+def test_quantize_rotated_refuses_other_dims(T):
+    with pytest.raises(T.TqkvError) as e:
+        T.affine_quantize_rotated(0, 1, 1, 64, 64, 4, 0, 0, 0, 0)
+    assert e.value.status == T.EINVAL_ARG  # null pointers come first
+    R = T.DeviceArray.of(O.rotation(64, 42))
+    x = T.DeviceArray((1, 1, 64), np.uint16, np.zeros((1, 1, 64), np.uint16))
+    t = device_triple(T, 1, 1, 64, 64, 4)
+    with pytest.raises(T.TqkvError) as e:
+        T.affine_quantize_rotated(x.ptr, 1, 1, 64, 64, 4, R.ptr, *(a.ptr for a in t))
+    assert e.value.status == T.EUNSUPPORTED
+
+
 def test_quantize_kv_rejects_either_bad_width(T):
     for bk, bv in ((7, 4), (4, 7)):
         with pytest.raises(T.TqkvError) as e:
