@@ -52,6 +52,13 @@ const char* tqkv_status_string(int32_t status);
 const char* tqkv_last_error(void);
 /* ABI version, major * 10000 + minor * 100 + patch. */
 int32_t tqkv_version(void);
+/* Frees the scratch the library keeps per device for calls given no
+ * workspace (no counterpart in the reference). The scratch grows by at
+ * least doubling and keeps outgrown buffers until this call (so a growing
+ * call never waits for queued work); this waits for every device that holds
+ * scratch to finish its work, then frees it all. The next call that needs
+ * scratch allocates again. */
+int32_t tqkv_scratch_release(void);
 
 /* ======================================================================
  * Stateless kernels
@@ -356,9 +363,10 @@ int32_t tqkv_decode_attend_codebook_qjl(const uint16_t* q, int32_t B, int32_t H,
  * q: bf16 [B, H, L, D]; out: bf16 [B, H, L, D]; segs as for
  * tqkv_decode_attend_affine (1 or 2: a shared prefix, then a suffix).
  * D in {64, 128, 256, 512}; bits_k, bits_v in {2, 3, 4, 5, 6, 8}; group_size in
- * {32, 64, 128}. Takes no workspace argument; calls that use the library's
- * scratch (this one, and decodes given a null workspace) must not overlap in
- * time on one device.
+ * {32, 64, 128}. Uses the library's scratch for the dequantize-once rows:
+ * calls that use it (this one, and decodes given a null workspace) must not
+ * overlap in time on one device; tqkv_prefill_attend_affine_ws takes a
+ * workspace instead.
  */
 int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
                                    int32_t L, int32_t D, int32_t group_size, int32_t bits_k,
@@ -366,6 +374,22 @@ int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int32_t H, int3
                                    int32_t n_segs, int64_t q_start, int64_t k_start,
                                    int32_t causal, int64_t window, uint16_t* out,
                                    tqkv_stream stream);
+/* tqkv_prefill_attend_affine with the caller's workspace (no counterpart in
+ * the reference, whose prefill dequantizes into a fresh MLX array): the
+ * dequantize-once rows go into `workspace` when it holds
+ * tqkv_prefill_workspace_size(B, H_kv, D, keys of both segments) bytes;
+ * with less (or NULL) every block dequantizes its own tiles in LDS. Either
+ * way the same bits, no library allocation, and calls with different
+ * workspaces may run concurrently. */
+int32_t tqkv_prefill_attend_affine_ws(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
+                                      int32_t L, int32_t D, int32_t group_size, int32_t bits_k,
+                                      int32_t bits_v, float scale, const tqkv_affine_seg* segs,
+                                      int32_t n_segs, int64_t q_start, int64_t k_start,
+                                      int32_t causal, int64_t window, uint16_t* out,
+                                      void* workspace, size_t workspace_bytes,
+                                      tqkv_stream stream);
+/* Bytes of the prefill's dequantize-once rows: 2 * B * H_kv * keys * D * 2. */
+size_t tqkv_prefill_workspace_size(int32_t B, int32_t H_kv, int32_t D, int64_t total_keys);
 
 /* Bytes of workspace tqkv_decode_attend_affine needs for this shape. */
 size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,

@@ -33,8 +33,10 @@ int32_t ok();
   } while (0)
 
 // A device scratch buffer the library keeps per device for callers that pass
-// no workspace. Grown on demand; never shrinks.
+// no workspace. Grown on demand (at least doubling, without waiting for
+// queued work: outgrown buffers are kept); freed by tqkv_scratch_release.
 int32_t scratch_for_current_device(size_t bytes, void** out);
+int32_t scratch_release_all();
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(uint32_t(b) << 16);

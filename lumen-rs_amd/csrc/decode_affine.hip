@@ -1,7 +1,9 @@
 // Host side of the fused affine decode: split planning, workspace, dispatch.
 // The kernel itself (and its design notes) is in decode_affine.hpp.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "decode_mfma.hpp"
 
@@ -316,8 +318,54 @@ struct DecodePlan {
   int n_splits = 1;
   int64_t split_len = 0;
   int n_part = 1;
+  // The last workgroup of each unit merges (no merge launch): n_part slots
+  // of at most kInlineMergeMax, behind a launch that writes slots.
+  bool inline_merge = false;
   size_t need = 0;
 };
+
+// TQKV_INLINE_MERGE=1 merges in-kernel. Off by default: on MI355X the last
+// workgroup's counter round trip and its reads of the partials past the
+// L2 cost as much as the merge launch they replace (config 1: 17.0 against
+// 16.5 us a step; config 3: 0.517 against 0.506 ms).
+bool inline_merge_enabled() {
+  const char* e = getenv("TQKV_INLINE_MERGE");
+  return e && strcmp(e, "1") == 0;
+}
+
+// Unit counters of the in-kernel merge: a file-scope device array (zero at
+// load; every merge sets its counter back to zero), handed out in chunks of
+// kRingChunk counters, one chunk a launch, round robin over kRingChunks, so
+// launches in flight on different streams count in different chunks (a
+// chunk comes round again only after kRingChunks - 1 later launches).
+constexpr int kRingChunk = 4096;   // most units (batch rows x KV heads) a launch
+constexpr int kRingChunks = 256;
+static __device__ __attribute__((used)) uint32_t merge_ring[kRingChunk * kRingChunks];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_ring_mu;
+uint32_t* g_ring[kMaxDevices] = {};
+std::atomic<uint32_t> g_ring_next{0};
+
+// A chunk of the current device's counters, or null (the merge launch then
+// runs instead).
+uint32_t* merge_counters(int64_t units) {
+  if (units > kRingChunk) return nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  uint32_t* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_ring_mu);
+    if (!g_ring[dev]) {
+      void* p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(merge_ring)) != hipSuccess || !p) return nullptr;
+      g_ring[dev] = static_cast<uint32_t*>(p);
+    }
+    base = g_ring[dev];
+  }
+  const uint32_t c = g_ring_next.fetch_add(1, std::memory_order_relaxed) % kRingChunks;
+  return base + size_t(c) * kRingChunk;
+}
 
 // Gk: the query heads one decode launch serves (kernel_heads).
 DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, const tqkv_affine_seg* segs,
@@ -345,11 +393,13 @@ DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, const tqkv_affine_
       pl.split_len_s = 64;
     }
     pl.n_part = pl.sp_p + pl.sp_s;
+    pl.inline_merge = pl.sp_s > 0 && pl.n_part <= kInlineMergeMax && inline_merge_enabled();
     pl.need = size_t(B) * H * pl.n_part * row * sizeof(float);
     return pl;
   }
   plan_splits(B, H_kv, waves, total, &pl.n_splits, &pl.split_len);
   pl.n_part = pl.n_splits;
+  pl.inline_merge = pl.n_splits > 1 && pl.n_part <= kInlineMergeMax && inline_merge_enabled();
   pl.need = pl.n_splits > 1 ? size_t(B) * H * pl.n_splits * row * sizeof(float) : 0;
   return pl;
 }
@@ -435,7 +485,10 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     }
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // Each launch that merges in-kernel counts in a chunk of its own.
+  auto counters = [&]() { return pl.inline_merge ? merge_counters(int64_t(B) * H_kv) : nullptr; };
 
+  bool merged = false;  // the decode launches merged in-kernel
   if (pl.shared_path) {
     Args s = a;
     s.seg[0] = a.seg[1];
@@ -459,13 +512,17 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
       s.part_m = pm;
       s.part_l = pl_;
       for (s.h_off = 0; s.h_off < G; s.h_off += Gk) {
+        s.merge_cnt = counters();
+        merged = s.merge_cnt != nullptr;
         hipLaunchKernelGGL(fn, dim3(unsigned(pl.sp_s), unsigned(H_kv), unsigned(B)),
                            dim3(kWave * waves), 0, st, s);
         TQKV_LAUNCHED();
       }
     }
-    launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
-    TQKV_LAUNCHED();
+    if (!merged) {
+      launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
+      TQKV_LAUNCHED();
+    }
     return ok();
   }
 
@@ -479,11 +536,13 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     a.part_l = a.part_m + size_t(B) * H * a.n_splits;
   }
   for (a.h_off = 0; a.h_off < G; a.h_off += Gk) {
+    a.merge_cnt = a.n_splits > 1 ? counters() : nullptr;
+    merged = a.merge_cnt != nullptr;
     hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
                        dim3(kWave * waves), 0, st, a);
     TQKV_LAUNCHED();
   }
-  if (a.n_splits > 1) {
+  if (a.n_splits > 1 && !merged) {
     launch_merge(a.part_o, a.part_m, a.part_l, a.n_splits, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
   }

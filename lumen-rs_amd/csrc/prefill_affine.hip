@@ -163,7 +163,8 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
                        int32_t D, int32_t group_size, int32_t bits_k, int32_t bits_v, float scale,
                        const tqkv_affine_seg* segs, int32_t n_segs, int64_t q_start,
                        int64_t k_start, int32_t causal, int64_t window, uint16_t* out,
-                       tqkv_stream stream, bool bf16_rows) {
+                       tqkv_stream stream, bool bf16_rows, bool library_scratch = true,
+                       void* workspace = nullptr, size_t workspace_bytes = 0) {
   if (!q || !out || !segs) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || L <= 0)
     return fail(TQKV_EINVAL_SHAPE, "B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
@@ -243,11 +244,16 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
   const char* once_env = getenv("TQKV_PREFILL_DEQUANT_ONCE");
   const int64_t slabs = int64_t(B) * H_kv;
   const size_t need = 2 * size_t(slabs) * size_t(a.total) * size_t(D) * 2;
-  const bool once = !bf16_rows && (once_env ? strcmp(once_env, "0") != 0
-                                             : blocks >= kOnceBlocks && need <= kOnceMaxBytes);
+  // With a caller workspace (the _ws entry) the dequantized rows go there
+  // when it holds them, else every block dequantizes for itself.
+  const bool fits = library_scratch || (workspace && workspace_bytes >= need);
+  const bool once = !bf16_rows && fits &&
+                    (once_env ? strcmp(once_env, "0") != 0
+                              : blocks >= kOnceBlocks && need <= kOnceMaxBytes);
   if (once) {
-    void* ws = nullptr;
-    if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
+    void* ws = workspace;
+    if (library_scratch)
+      if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
     uint16_t* kd = static_cast<uint16_t*>(ws);
     uint16_t* vd = kd + size_t(slabs) * size_t(a.total) * size_t(D);
     if (slabs > 65535) return fail(TQKV_EINVAL_SHAPE, "B * H_kv = %lld slabs", (long long)slabs);
@@ -299,6 +305,22 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
                                               tqkv_stream stream) {
   return prefill_launch(q, B, H, H_kv, L, D, group_size, bits_k, bits_v, scale, segs, n_segs,
                         q_start, k_start, causal, window, out, stream, false);
+}
+
+extern "C" size_t tqkv_prefill_workspace_size(int32_t B, int32_t H_kv, int32_t D,
+                                              int64_t total_keys) {
+  if (B <= 0 || H_kv <= 0 || D <= 0 || total_keys <= 0) return 0;
+  return 2 * size_t(B) * size_t(H_kv) * size_t(total_keys) * size_t(D) * 2;
+}
+
+extern "C" int32_t tqkv_prefill_attend_affine_ws(
+    const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int32_t L, int32_t D,
+    int32_t group_size, int32_t bits_k, int32_t bits_v, float scale, const tqkv_affine_seg* segs,
+    int32_t n_segs, int64_t q_start, int64_t k_start, int32_t causal, int64_t window,
+    uint16_t* out, void* workspace, size_t workspace_bytes, tqkv_stream stream) {
+  return prefill_launch(q, B, H, H_kv, L, D, group_size, bits_k, bits_v, scale, segs, n_segs,
+                        q_start, k_start, causal, window, out, stream, false, false, workspace,
+                        workspace_bytes);
 }
 
 namespace tqkv {

@@ -27,6 +27,7 @@ namespace {
 struct Scratch {
   void* ptr = nullptr;
   size_t bytes = 0;
+  std::vector<void*> retired;  // outgrown buffers, freed by tqkv_scratch_release
 };
 std::mutex g_scratch_mu;
 std::vector<Scratch> g_scratch;
@@ -39,21 +40,45 @@ int32_t scratch_for_current_device(size_t bytes, void** out) {
   if (g_scratch.size() <= size_t(dev)) g_scratch.resize(size_t(dev) + 1);
   Scratch& s = g_scratch[size_t(dev)];
   if (s.bytes < bytes) {
-    // Growing frees the old buffer: wait for work that may still use it.
-    if (s.ptr) {
-      TQKV_HIP(hipDeviceSynchronize());
-      TQKV_HIP(hipFree(s.ptr));
-      s.ptr = nullptr;
-      s.bytes = 0;
-    }
+    // Work already queued may still use the outgrown buffer, and nothing
+    // here waits for it (the calls are asynchronous): it is kept until
+    // tqkv_scratch_release. Growth at least doubles, so what is kept stays
+    // below the current size.
     size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-    if (hipMalloc(&s.ptr, want) != hipSuccess) {
-      s.ptr = nullptr;
-      return fail(TQKV_ENOMEM, "scratch hipMalloc of %zu bytes failed", want);
+    if (want < 2 * s.bytes) want = 2 * s.bytes;
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+      // Doubling may ask for too much: the exact size, before giving up.
+      if (want > bytes && hipMalloc(&p, bytes) == hipSuccess) {
+        want = bytes;
+      } else {
+        return fail(TQKV_ENOMEM, "scratch hipMalloc of %zu bytes failed", bytes);
+      }
     }
+    if (s.ptr) s.retired.push_back(s.ptr);
+    s.ptr = p;
     s.bytes = want;
   }
   *out = s.ptr;
+  return TQKV_OK;
+}
+
+int32_t scratch_release_all() {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  int dev = 0;
+  TQKV_HIP(hipGetDevice(&dev));
+  for (size_t d = 0; d < g_scratch.size(); ++d) {
+    Scratch& s = g_scratch[d];
+    if (!s.ptr && s.retired.empty()) continue;
+    TQKV_HIP(hipSetDevice(int(d)));
+    TQKV_HIP(hipDeviceSynchronize());
+    for (void* p : s.retired) (void)hipFree(p);
+    s.retired.clear();
+    (void)hipFree(s.ptr);
+    s.ptr = nullptr;
+    s.bytes = 0;
+  }
+  TQKV_HIP(hipSetDevice(dev));
   return TQKV_OK;
 }
 
@@ -76,6 +101,11 @@ const char* tqkv_status_string(int32_t status) {
 }
 
 const char* tqkv_last_error(void) { return tqkv::g_last_error; }
+
+int32_t tqkv_scratch_release(void) {
+  if (int32_t rc = tqkv::scratch_release_all()) return rc;
+  return tqkv::ok();
+}
 
 int32_t tqkv_version(void) { return 100; }
 

@@ -114,6 +114,7 @@ extern "C" {
     pub fn tqkv_status_string(status: i32) -> *const c_char;
     pub fn tqkv_last_error() -> *const c_char;
     pub fn tqkv_version() -> i32;
+    pub fn tqkv_scratch_release() -> i32;
     pub fn tqkv_affine_quantize(x: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits: i32, packed: *mut u32, scales: *mut u16, biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_quantize_kv(k: *const u16, v: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits_k: i32, bits_v: i32, k_packed: *mut u32, k_scales: *mut u16, k_biases: *mut u16, v_packed: *mut u32, v_scales: *mut u16, v_biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_quantize_rotated(x: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits: i32, rotation: *const f32, packed: *mut u32, scales: *mut u16, biases: *mut u16, dst_cap: i64, dst_start: i64, rotated: *mut u16, stream: tqkv_stream) -> i32;
@@ -134,6 +135,8 @@ extern "C" {
     pub fn tqkv_decode_codebook_workspace_size(B: i32, H: i32, D: i32, total_tokens: i64) -> usize;
     pub fn tqkv_decode_attend_codebook_qjl(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, scale: f32, rotation: *const f32, centroids_k: *const f32, bits_k: i32, centroids_v: *const f32, bits_v: i32, k_codes: *const u8, k_sigma: *const f32, k_signs: *const u32, k_rnorm: *const f32, qjl: *const f32, qjl_m: i32, v_codes: *const u8, v_sigma: *const f32, cap: i64, n: i64, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
     pub fn tqkv_prefill_attend_affine(q: *const u16, B: i32, H: i32, H_kv: i32, L: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, q_start: i64, k_start: i64, causal: i32, window: i64, out: *mut u16, stream: tqkv_stream) -> i32;
+    pub fn tqkv_prefill_attend_affine_ws(q: *const u16, B: i32, H: i32, H_kv: i32, L: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, segs: *const tqkv_affine_seg, n_segs: i32, q_start: i64, k_start: i64, causal: i32, window: i64, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
+    pub fn tqkv_prefill_workspace_size(B: i32, H_kv: i32, D: i32, total_keys: i64) -> usize;
     pub fn tqkv_decode_workspace_size(B: i32, H: i32, H_kv: i32, D: i32, total_tokens: i64) -> usize;
     pub fn tqkv_cache_create(cfg: *const tqkv_cache_config, out: *mut *mut tqkv_cache) -> i32;
     pub fn tqkv_cache_destroy(cache: *mut tqkv_cache) -> i32;

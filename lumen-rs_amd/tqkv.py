@@ -88,6 +88,10 @@ _SIGS = {
     "tqkv_affine_quantize_kv_rotated": (I32, [P, P, I64, I64, I32, I32, I32, I32, P, P, P, P, P,
                                               P, P, I64, I64, P]),
     "tqkv_affine_dequantize": (I32, [P, P, P, I64, I32, I32, I32, P, P]),
+    "tqkv_prefill_attend_affine_ws": (I32, [P, I32, I32, I32, I32, I32, I32, I32, I32, F32, P, I32,
+                                            I64, I64, I32, I64, P, P, SZ, P]),
+    "tqkv_prefill_workspace_size": (SZ, [I32, I32, I32, I64]),
+    "tqkv_scratch_release": (I32, []),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
     "tqkv_decode_attend_affine_noalloc": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
@@ -412,6 +416,25 @@ def prefill_attend_affine(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, segs, 
     check(lib().tqkv_prefill_attend_affine(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, arr,
                                            len(segs), q_start, k_start, int(causal), window, out,
                                            stream))
+
+
+def prefill_attend_affine_ws(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, segs, out,
+                             workspace, workspace_bytes, q_start=0, k_start=0, causal=True,
+                             window=-1, stream=None):
+    """prefill_attend_affine with a caller workspace (None: dequantize in
+    every block)."""
+    arr = (AffineSeg * len(segs))(*segs)
+    check(lib().tqkv_prefill_attend_affine_ws(q, B, H, H_kv, L, D, gs, bits_k, bits_v, scale, arr,
+                                              len(segs), q_start, k_start, int(causal), window,
+                                              out, workspace, workspace_bytes, stream))
+
+
+def prefill_workspace_size(B, H_kv, D, total_keys):
+    return lib().tqkv_prefill_workspace_size(B, H_kv, D, total_keys)
+
+
+def scratch_release():
+    check(lib().tqkv_scratch_release())
 
 
 def decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v):

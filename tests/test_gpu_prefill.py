@@ -278,3 +278,32 @@ def test_prefill_dequantize_once_two_segments_by_default(T, monkeypatch):
     want = want_mlx(q, kh, vh, gs, bk, bv, scale, causal=True, q_start=P + S - L,
                     first_held=0, window=700)
     check(got, want, "once, two segments")
+
+
+def test_prefill_with_caller_workspace(T, monkeypatch):
+    """tqkv_prefill_attend_affine_ws: with a workspace that holds the
+    dequantized rows, without one (every block dequantizes), and after the
+    library's scratch is released: the same bits as the library-scratch
+    entry."""
+    monkeypatch.delenv("TQKV_PREFILL_DEQUANT_ONCE", raising=False)
+    B, H, Hkv, D, L, N, gs, bk, bv = 1, 32, 8, 128, 256, 1024, 64, 4, 4
+    q = kv_bf16((B, H, L, D), 31)
+    k = kv_bf16((B, Hkv, N, D), 32, frac=0.01, mult=10.0)
+    v = kv_bf16((B, Hkv, N, D), 33, frac=0.01, mult=10.0)
+    (_, kd), (_, vd) = _cache(k, gs, bk, N), _cache(v, gs, bv, N)
+    segs_host = [(kd, vd, N, N, False)]
+    scale = D ** -0.5
+    want = run(T, q, segs_host, B, H, Hkv, L, D, gs, bk, bv, scale, N - L, 0, True, -1)
+    T.scratch_release()
+    need = T.prefill_workspace_size(B, Hkv, D, N)
+    assert need == 2 * B * Hkv * N * D * 2
+    dq = T.DeviceArray.of(q)
+    segs = [T.affine_seg(tuple(a.ptr for a in kk), tuple(a.ptr for a in vv), c, n, sh)
+            for (kk, vv, c, n, sh) in segs_host]
+    for ws_bytes in (need, need - 1, 0):
+        ws = T.DeviceArray((max(ws_bytes, 1),), np.uint8) if ws_bytes else None
+        out = T.DeviceArray((B, H, L, D), np.uint16, np.full((B, H, L, D), 0x7FC0, np.uint16))
+        T.prefill_attend_affine_ws(dq.ptr, B, H, Hkv, L, D, gs, bk, bv, scale, segs, out.ptr,
+                                   None if ws is None else ws.ptr, ws_bytes, N - L, 0, True, -1)
+        T.hip().sync()
+        assert np.array_equal(out.numpy(), want), f"workspace of {ws_bytes} bytes"
