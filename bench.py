@@ -471,6 +471,15 @@ def _loop_ms(hip, stream, fn, n):
     return hip.elapsed_ms(t0, t1) / n
 
 
+def _launch_floor_us(T, hip, stream, n=400):
+    """Microseconds per launch of n back-to-back empty kernels of 256
+    workgroups on `stream`: the floor every launch of a latency-bound step
+    pays whatever it does."""
+    T.empty_launch(256, stream)
+    hip.sync()
+    return round(_loop_ms(hip, stream, lambda: T.empty_launch(256, stream), n) * 1e3, 3)
+
+
 def _line(metric, value, unit, ms, args, dtype, config, roofline, extra=None, settle=0,
           steps=None):
     """One result line; `steps` is the count actually timed (the workloads
@@ -708,7 +717,8 @@ def decode1_main(T, hip, args):
         _hbm(alg / (dec_ms * 1e-3) / 1e9, T.decode_kernel_name(H, HKV, D, GS, BITS, BITS) +
              (" split (quantizing the new token) + merge" if fused else " split + merge"),
              alg, dec_ms),
-        {"decode_us": round(dec_ms * 1e3, 2), "step_us": round(step_ms * 1e3, 2)}, settle, steps)
+        {"decode_us": round(dec_ms * 1e3, 2), "step_us": round(step_ms * 1e3, 2),
+         "launch_floor_us": _launch_floor_us(T, hip, stream)}, settle, steps)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
         kt = tuple(a.numpy()[:, :pos[0]].reshape(B, HKV, pos[0], -1) for a in kc)
@@ -815,7 +825,8 @@ def prefix_main(T, hip, args):
              "decode (" + T.decode_kernel_name(H, HKV, D, GS, BK, BV) + ") + merge", unique, dec_ms),
         {"naive_bytes_per_step": int(naive),
          "naive_gbps": round(naive / (dec_ms * 1e-3) / 1e9, 1),
-         "per_sequence_path_ms_per_step": round(per_seq_ms, 5)}, settle, steps)
+         "per_sequence_path_ms_per_step": round(per_seq_ms, 5),
+         "launch_floor_us": _launch_floor_us(T, hip, stream)}, settle, steps)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
         n_seq = max(1, min(B, -(-2 * threads // HKV)))
@@ -1013,7 +1024,8 @@ def layers_main(T, hip, args):
         {"prefill_ms": round(prefill_ms, 2),
          "prefill_tokens_per_s": round(B * L / (prefill_ms * 1e-3), 1),
          "decode_bytes_per_step": int(alg),
-         "views_at_end": {"global": int(views1[5]), "sliding": int(views1[0])}}, settle, steps)
+         "views_at_end": {"global": int(views1[5]), "sliding": int(views1[0])},
+         "launch_floor_us": _launch_floor_us(T, hip, stream)}, settle, steps)
     if not args.no_cpu_baseline:
         # A step of batch row 0 = 25 sliding-layer decodes + 5 global ones;
         # one of each is timed over that layer's cache view (its own keys),

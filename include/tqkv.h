@@ -889,6 +889,13 @@ int32_t tqkv_synth_bf16(uint16_t* out, int64_t rows, int32_t dim, uint64_t seed,
 int32_t tqkv_read_probe(const float* data, size_t bytes, float* scratch, size_t scratch_bytes,
                         float* out, tqkv_stream stream);
 
+/*
+ * An empty kernel of `workgroups` x 256 work-items: timed back to back, the
+ * floor a launch costs on this GPU, which latency-bound steps (a decode of
+ * a short context, one per layer) are measured beside.
+ */
+int32_t tqkv_empty_launch(int32_t workgroups, tqkv_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

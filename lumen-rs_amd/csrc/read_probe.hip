@@ -79,3 +79,19 @@ extern "C" int32_t tqkv_read_probe(const float* data, size_t bytes, float* scrat
   TQKV_LAUNCHED();
   return ok();
 }
+
+namespace tqkv {
+namespace {
+// Does nothing: the cost of a launch itself.
+__global__ void empty_kernel() {}
+}  // namespace
+}  // namespace tqkv
+
+extern "C" int32_t tqkv_empty_launch(int32_t workgroups, tqkv_stream stream) {
+  using namespace tqkv;
+  if (workgroups < 1) return fail(TQKV_EINVAL_ARG, "workgroups=%d", workgroups);
+  hipLaunchKernelGGL(empty_kernel, dim3(unsigned(workgroups)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream));
+  TQKV_LAUNCHED();
+  return ok();
+}

@@ -191,4 +191,5 @@ extern "C" {
     pub fn tqkv_kvcache_read(cache: *mut tqkv_kvcache, layer: i32, head: i32, which_values: i32, first: i64, n: i64, codes: *mut u8, scale: *mut f32, signs: *mut u32, residual_norm: *mut f32) -> i32;
     pub fn tqkv_synth_bf16(out: *mut u16, rows: i64, dim: i32, seed: u64, outlier_frac: f32, outlier_mult: f32, stream: tqkv_stream) -> i32;
     pub fn tqkv_read_probe(data: *const f32, bytes: usize, scratch: *mut f32, scratch_bytes: usize, out: *mut f32, stream: tqkv_stream) -> i32;
+    pub fn tqkv_empty_launch(workgroups: i32, stream: tqkv_stream) -> i32;
 }

@@ -92,6 +92,7 @@ _SIGS = {
                                             I64, I64, I32, I64, P, P, SZ, P]),
     "tqkv_prefill_workspace_size": (SZ, [I32, I32, I32, I64]),
     "tqkv_scratch_release": (I32, []),
+    "tqkv_empty_launch": (I32, [I32, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
     "tqkv_decode_attend_affine_noalloc": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
@@ -435,6 +436,10 @@ def prefill_workspace_size(B, H_kv, D, total_keys):
 
 def scratch_release():
     check(lib().tqkv_scratch_release())
+
+
+def empty_launch(workgroups=256, stream=None):
+    check(lib().tqkv_empty_launch(workgroups, stream))
 
 
 def decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v):

@@ -29,6 +29,12 @@ def test_status_strings_without_a_gpu():
     assert tqkv.lib().tqkv_version() >= 100
 
 
+def test_argument_checks_come_before_any_launch():
+    import tqkv
+    assert tqkv.lib().tqkv_empty_launch(0, None) == tqkv.EINVAL_ARG
+    assert tqkv.lib().tqkv_read_probe(None, 16, None, 0, None, None) == tqkv.EINVAL_ARG
+
+
 def test_workspace_size_is_host_arithmetic():
     import tqkv
     n = tqkv.decode_workspace_size(32, 16, 8, 256, 32768)
