@@ -186,7 +186,6 @@ int max_splits(int B, int H_kv, int64_t total) {
   return want < 1 ? 1 : int(want);
 }
 
-int waves_for_shape(int G, int D) { return G * D <= 1024 ? 8 : 4; }
 
 // Workgroups of the shared-prefix pass: one per CU of an MI355X (256). The
 // pass holds one workgroup per CU, and each workgroup's fixed costs (query
@@ -368,11 +367,11 @@ uint32_t* merge_counters(int64_t units) {
 }
 
 // Gk: the query heads one decode launch serves (kernel_heads).
-DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, const tqkv_affine_seg* segs,
-                       int n_segs, bool app) {
+// waves: the launch's wavefronts a workgroup (decode_waves).
+DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, int waves,
+                       const tqkv_affine_seg* segs, int n_segs, bool app) {
   DecodePlan pl;
   const int G = H / H_kv;
-  const int waves = waves_for_shape(Gk, D);
   const int64_t total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
   // A prefix shared by B >= 2 sequences: read it once per KV head for all of
   // them (the prefill kernel with the sequences as query rows, split over
@@ -473,9 +472,9 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
   }
 
-  const int waves = waves_for_shape(Gk, D);
+  const int waves = decode_waves(D, bits_k, bits_v, Gk, mfma);
   a.out = out;
-  const DecodePlan pl = plan_decode(B, H, H_kv, D, Gk, segs, n_segs, app != nullptr);
+  const DecodePlan pl = plan_decode(B, H, H_kv, D, Gk, waves, segs, n_segs, app != nullptr);
   void* ws = workspace;
   if (pl.need > 0) {
     if (!ws) {
@@ -587,8 +586,12 @@ size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n_segs < 1 || n_segs > 2) return 0;
   int64_t max_rows = 0;
   for (int i = 0; i < n_segs; ++i) max_rows = segs[i].n > max_rows ? segs[i].n : max_rows;
-  const int Gk = kernel_heads(D, bits_k, bits_v, H / H_kv, group_size, max_rows);
-  return plan_decode(B, H, H_kv, D, Gk, segs, n_segs, app).need;
+  const int G = H / H_kv;
+  const int Gk = kernel_heads(D, bits_k, bits_v, G, group_size, max_rows);
+  KernelFn fn = pick(D, bits_k, bits_v, G, group_size, max_rows);
+  const bool mfma = fn && fn == pick_mfma_only(D, bits_k, bits_v, G, group_size);
+  return plan_decode(B, H, H_kv, D, Gk, decode_waves(D, bits_k, bits_v, Gk, mfma), segs, n_segs,
+                     app).need;
 }
 }  // namespace tqkv
 
@@ -646,7 +649,7 @@ extern "C" int32_t tqkv_decode_attend_affine_pages(
   a.pages = chosen;
   a.n_pages = keep;
   a.out = out;
-  const int waves = waves_for_shape(G, D);
+  const int waves = decode_waves(D, bits_k, bits_v, G, true);
   plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
   // A wavefront holds its page numbers one a lane: at most kMaxWavePages
   // pages a wavefront, so a split spans at most waves * kMaxWavePages.

@@ -631,21 +631,33 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
 
 using KernelFn = void (*)(Args);
 
-// Wavefronts per workgroup: 8, unless the cross-wave merge buffer
-// (waves x G x D floats) would pass 32 KB of LDS.
-template <int G, int D>
-constexpr int waves_for() {
-  return G * D <= 1024 ? 8 : 4;
+// Channels a lane holds in the dot2 kernel: a width every plan of both
+// widths has (3 and 5 bits pack whole words only from 32 codes, 2 and 6
+// bits from 16), 8 for 4/8-bit caches of 6+ heads a KV head, else 16.
+constexpr int epl_of(int bk, int bv, int G) {
+  return (bk == 3 || bv == 3 || bk == 5 || bv == 5)   ? 32
+         : (bk == 2 || bv == 2 || bk == 6 || bv == 6) ? 16
+         : G >= 6                                     ? 8
+                                                      : 16;
 }
-
-// Channels a lane holds: a width every plan of both widths has (3 and 5
-// bits pack whole words only from 32 codes, 2 and 6 bits from 16), 8 for
-// 4/8-bit caches of 6+ heads a KV head, else 16.
 template <int BK, int BV, int G>
 constexpr int epl_for() {
-  if constexpr (BK == 3 || BV == 3 || BK == 5 || BV == 5) return 32;
-  else if constexpr (BK == 2 || BV == 2 || BK == 6 || BV == 6) return 16;
-  else return G >= 6 ? 8 : 16;
+  return epl_of(BK, BV, G);
+}
+
+// Wavefronts per workgroup of a decode kernel (the host launches with the
+// same function): 8, two a SIMD with at most 256 registers each, or 4 (one
+// a SIMD, up to 512) where the cross-wave merge buffer (waves x G x D
+// floats) would pass 32 KB of LDS, or where a wavefront's accumulators
+// outgrow 256 registers by far: the MFMA kernel's G x D/64 = 16 A rows
+// (600 registers spilled at 8 wavefronts; 4 measured 1.2-1.5x faster) and
+// the dot2 kernel's G heads x EPL channels above 64 (200-700 spilled; 4
+// measured 2.7-3.2x faster). At G x EPL = 64 the few spills of 8
+// wavefronts cost less than the lost occupancy (8 measured 10-25% faster).
+constexpr int decode_waves(int D, int bk, int bv, int G, bool mfma) {
+  return G * D > 1024 ? 4
+         : mfma       ? (G * (D / 64) >= 16 ? 4 : 8)
+                      : (G * epl_of(bk, bv, G) > 64 ? 4 : 8);
 }
 
 // The dot2 kernel serves 6 or 8 heads a KV head in one launch only with 8
@@ -659,7 +671,7 @@ constexpr bool split_heads(int G) {
 template <int D, int BK, int BV, int G>
 KernelFn pick_kernel() {
   constexpr int EPL = epl_for<BK, BV, G>();
-  return decode_affine_kernel<D, BK, BV, G, EPL, waves_for<G, D>()>;
+  return decode_affine_kernel<D, BK, BV, G, EPL, decode_waves(D, BK, BV, G, false)>;
 }
 
 // G heads in one launch, or (split_heads) the G / 2 kernel for each half.

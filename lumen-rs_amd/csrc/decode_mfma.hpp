@@ -771,7 +771,7 @@ template <int D, int BK, int BV, int G, bool PAGED>
 KernelFn pick_mfma_g() {
   constexpr int NG = D / 64;
   if constexpr (NG >= 1 && mfma_layout_ok<D, BK, BV, G, NG>())
-    return decode_mfma_kernel<D, BK, BV, G, NG, waves_for<G, D>(), PAGED>;
+    return decode_mfma_kernel<D, BK, BV, G, NG, decode_waves(D, BK, BV, G, true), PAGED>;
   else
     return nullptr;
 }
