@@ -472,7 +472,7 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     return fail(TQKV_EINVAL_SHAPE, "no keys to attend");
   }
 
-  const int waves = decode_waves(D, bits_k, bits_v, Gk, mfma);
+  const int waves = decode_waves(D, bits_k, bits_v, Gk, group_size, mfma);
   a.out = out;
   const DecodePlan pl = plan_decode(B, H, H_kv, D, Gk, waves, segs, n_segs, app != nullptr);
   void* ws = workspace;
@@ -590,8 +590,8 @@ size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits
   const int Gk = kernel_heads(D, bits_k, bits_v, G, group_size, max_rows);
   KernelFn fn = pick(D, bits_k, bits_v, G, group_size, max_rows);
   const bool mfma = fn && fn == pick_mfma_only(D, bits_k, bits_v, G, group_size);
-  return plan_decode(B, H, H_kv, D, Gk, decode_waves(D, bits_k, bits_v, Gk, mfma), segs, n_segs,
-                     app).need;
+  return plan_decode(B, H, H_kv, D, Gk, decode_waves(D, bits_k, bits_v, Gk, group_size, mfma),
+                     segs, n_segs, app).need;
 }
 }  // namespace tqkv
 
@@ -649,7 +649,7 @@ extern "C" int32_t tqkv_decode_attend_affine_pages(
   a.pages = chosen;
   a.n_pages = keep;
   a.out = out;
-  const int waves = decode_waves(D, bits_k, bits_v, G, true);
+  const int waves = decode_waves(D, bits_k, bits_v, G, group_size, true);
   plan_splits(B, H_kv, waves, a.total, &a.n_splits, &a.split_len);
   // A wavefront holds its page numbers one a lane: at most kMaxWavePages
   // pages a wavefront, so a split spans at most waves * kMaxWavePages.

@@ -183,12 +183,14 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   const int ve0 = vc * EV;
   const int vgrp = ve0 / GS;
 
-  // ---- queries: f32 in LDS, then per-head exponents and group sums. A
-  // group is 64 channels, so lane l reads channel l of every group, and the
-  // G * (NG + 1) reductions run side by side (DPP within rows of 16 lanes,
-  // then one readlane a row): their results are wave-uniform and no
-  // reduction waits on another.
-  static_assert(GS == kWave, "a lane a channel of each group");
+  // ---- queries: f32 in LDS, then per-head exponents and group sums. Lane
+  // l reads channel l of every 64-channel chunk, and the G * (D/64 + 1)
+  // reductions run side by side (DPP within rows of 16 lanes, then one
+  // readlane a row): their results are wave-uniform and no reduction waits
+  // on another. A group of 64 channels is a chunk's four rows; of 32, two
+  // rows; of 128, two chunks.
+  static_assert(GS == 32 || GS == 64 || GS == 128, "group size");
+  constexpr int NCH = D / kWave;
   __shared__ float s_q[G][D];
   for (int i = threadIdx.x; i < G * D; i += kWave * kWaves) {
     const int h = i / D, d = i % D;
@@ -198,15 +200,15 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   int E[G];
   float qsum[G][NG];
   {
-    float mx[G];
+    float mx[G], rs[G][NCH];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       mx[h] = 0.0f;
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const float x = s_q[h][g * kWave + lane];
+      for (int c = 0; c < NCH; ++c) {
+        const float x = s_q[h][c * kWave + lane];
         mx[h] = fmaxf(mx[h], fabsf(x));
-        qsum[h][g] = row_sum16(x);
+        rs[h][c] = row_sum16(x);
       }
       mx[h] = row_max16(mx[h]);
     }
@@ -217,7 +219,19 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       if (m > 0.0f) frexpf(m, &ex);
       E[h] = 15 - ex;
 #pragma unroll
-      for (int g = 0; g < NG; ++g) qsum[h][g] = rows_sum(qsum[h][g]);
+      for (int c = 0; c < NCH; ++c) {
+        if constexpr (GS == 64) {
+          qsum[h][c] = rows_sum(rs[h][c]);
+        } else if constexpr (GS == 32) {
+          qsum[h][2 * c] = rl(rs[h][c], 0) + rl(rs[h][c], 16);
+          qsum[h][2 * c + 1] = rl(rs[h][c], 32) + rl(rs[h][c], 48);
+        } else {
+          if (c % 2 == 0)
+            qsum[h][c / 2] = rows_sum(rs[h][c]);
+          else
+            qsum[h][c / 2] += rows_sum(rs[h][c]);
+        }
+      }
     }
   }
 
@@ -766,34 +780,51 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 }
 
 // The MFMA kernel for a layout, or nullptr where it does not apply (the dot2
-// kernel serves those). Instantiated for group size 64 only.
-template <int D, int BK, int BV, int G, bool PAGED>
+// kernel serves those). Group sizes 64 (here), 32 and 128 (decode_affine_gs_d*,
+// not for page segments).
+template <int D, int GS, int BK, int BV, int G, bool PAGED>
 KernelFn pick_mfma_g() {
-  constexpr int NG = D / 64;
-  if constexpr (NG >= 1 && mfma_layout_ok<D, BK, BV, G, NG>())
-    return decode_mfma_kernel<D, BK, BV, G, NG, decode_waves(D, BK, BV, G, true), PAGED>;
+  constexpr int NG = D / GS;
+  if constexpr (NG >= 1 && D % GS == 0 && mfma_layout_ok<D, BK, BV, G, NG>())
+    return decode_mfma_kernel<D, BK, BV, G, NG, decode_waves(D, BK, BV, G, GS, true), PAGED>;
   else
     return nullptr;
 }
 
-template <int D, int BK, int BV, bool PAGED>
+template <int D, int GS, int BK, int BV, bool PAGED>
 KernelFn pick_mfma_bits_g(int G) {
   switch (G) {
-    case 1: return pick_mfma_g<D, BK, BV, 1, PAGED>();
-    case 2: return pick_mfma_g<D, BK, BV, 2, PAGED>();
-    case 4: return pick_mfma_g<D, BK, BV, 4, PAGED>();
-    case 8: return pick_mfma_g<D, BK, BV, 8, PAGED>();
+    case 1: return pick_mfma_g<D, GS, BK, BV, 1, PAGED>();
+    case 2: return pick_mfma_g<D, GS, BK, BV, 2, PAGED>();
+    case 4: return pick_mfma_g<D, GS, BK, BV, 4, PAGED>();
+    case 8: return pick_mfma_g<D, GS, BK, BV, 8, PAGED>();
   }
   return nullptr;
 }
 
-template <int D, bool PAGED = false>
-KernelFn pick_mfma(int bk, int bv, int G, int gs) {
-  if (gs != 64) return nullptr;
+template <int D, int GS, bool PAGED = false>
+KernelFn pick_mfma_gs(int bk, int bv, int G) {
 #define TQKV_PAIR(K, V) \
-  if (bk == K && bv == V) return pick_mfma_bits_g<D, K, V, PAGED>(G);
+  if (bk == K && bv == V) return pick_mfma_bits_g<D, GS, K, V, PAGED>(G);
   TQKV_DECODE_PAIRS(TQKV_PAIR)
 #undef TQKV_PAIR
+  return nullptr;
+}
+
+// Group sizes 32 and 128 (instantiated in their own units).
+KernelFn pick_mfma_gs_d64(int bk, int bv, int G, int gs);
+KernelFn pick_mfma_gs_d128(int bk, int bv, int G, int gs);
+KernelFn pick_mfma_gs_d256(int bk, int bv, int G, int gs);
+
+template <int D, bool PAGED = false>
+KernelFn pick_mfma(int bk, int bv, int G, int gs) {
+  if (gs == 64) return pick_mfma_gs<D, 64, PAGED>(bk, bv, G);
+  if constexpr (PAGED) return nullptr;
+  switch (D) {
+    case 64: return pick_mfma_gs_d64(bk, bv, G, gs);
+    case 128: return pick_mfma_gs_d128(bk, bv, G, gs);
+    case 256: return pick_mfma_gs_d256(bk, bv, G, gs);
+  }
   return nullptr;
 }
 

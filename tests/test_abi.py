@@ -52,6 +52,10 @@ def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 5, 5) == "mfma"  # bit-anchored windows
     assert tqkv.decode_kernel_name(32, 8, 128, 64, 6, 6) == "mfma"  # Gemma's 6-bit cache
     assert tqkv.decode_kernel_name(32, 4, 128, 64, 3, 3) == "dot2"  # 8 heads: two launches
+    assert tqkv.decode_kernel_name(16, 8, 256, 32, 4, 4) == "mfma"  # gs32 (16 A rows)
+    assert tqkv.decode_kernel_name(32, 8, 128, 32, 6, 6) == "mfma"
+    assert tqkv.decode_kernel_name(16, 8, 128, 128, 8, 4) == "mfma"
+    assert tqkv.decode_kernel_name(32, 8, 256, 32, 4, 4) == "dot2"  # 32 A rows
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 7, 7) == ""
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 5, 4) == ""
     assert tqkv.decode_kernel_name(20, 4, 128, 64, 4, 4) == ""  # 5 heads a KV head

@@ -314,6 +314,11 @@ DECODE_CASES = [
     (2, 24, 4, 256, 1000, 3, 3, 64, 5),      # 3-bit, 6 heads a KV head
     (1, 64, 8, 128, 1500, 6, 6, 64, 0),      # 6-bit, 8 heads a KV head
     (3, 48, 8, 64, 700, 5, 5, 32, 0),        # 5-bit, 6 heads a KV head, D = 64
+    (2, 16, 8, 256, 3000, 4, 4, 32, 0),      # group size 32 at D = 256 (16 A rows)
+    (1, 32, 8, 128, 2000, 4, 4, 32, 0),      # group size 32, 4 heads a KV head
+    (1, 16, 8, 128, 1500, 8, 4, 128, 0),     # group size 128
+    (2, 16, 4, 256, 999, 6, 6, 128, 3),      # group size 128 at D = 256
+    (2, 8, 1, 64, 600, 4, 4, 32, 0),         # group size 32 at D = 64, 8 heads
 ]
 
 

@@ -92,17 +92,20 @@ def want_of(q, K, V, gs, bk, bv, scale):
     return want
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,D,bk,bv,prefill,steps,prealloc", [
-    (1, 32, 8, 128, 4, 4, 0, 3, True),      # config 1's layout, from empty
-    (2, 16, 8, 256, 3, 3, 254, 4, False),   # config 2's layout, across 256 (growth copy)
-    (2, 32, 8, 128, 8, 4, 500, 2, True),    # config 4's widths
-    (3, 8, 4, 64, 4, 8, 63, 3, True),       # D = 64, mixed widths
-    (1, 32, 8, 128, 6, 6, 100, 2, True),    # 6-bit (MFMA kernel at D = 128)
-    (2, 16, 8, 128, 2, 2, 30, 2, False),    # 2-bit
+@pytest.mark.parametrize("B,Hq,Hkv,D,bk,bv,prefill,steps,prealloc,gs", [
+    (1, 32, 8, 128, 4, 4, 0, 3, True, 64),      # config 1's layout, from empty
+    (2, 16, 8, 256, 3, 3, 254, 4, False, 64),   # config 2's layout, across 256 (growth copy)
+    (2, 32, 8, 128, 8, 4, 500, 2, True, 64),    # config 4's widths
+    (3, 8, 4, 64, 4, 8, 63, 3, True, 64),       # D = 64, mixed widths
+    (1, 32, 8, 128, 6, 6, 100, 2, True, 64),    # 6-bit (MFMA kernel at D = 128)
+    (2, 16, 8, 128, 2, 2, 30, 2, False, 64),    # 2-bit
+    (1, 16, 8, 256, 4, 4, 100, 3, True, 32),    # group size 32 (16 A rows)
+    (2, 32, 8, 128, 6, 6, 40, 2, True, 32),     # group size 32, 4 heads a KV head
+    (1, 16, 8, 128, 8, 4, 70, 2, True, 128),    # group size 128
 ])
-def test_growing(T, B, Hq, Hkv, D, bk, bv, prefill, steps, prealloc):
-    assert T.decode_kernel_name(Hq, Hkv, D, 64, bk, bv) == "mfma"
-    tw = Twin(T, B, Hkv, D, bk, bv, prealloc=prealloc)
+def test_growing(T, B, Hq, Hkv, D, bk, bv, prefill, steps, prealloc, gs):
+    assert T.decode_kernel_name(Hq, Hkv, D, gs, bk, bv) == "mfma"
+    tw = Twin(T, B, Hkv, D, bk, bv, gs=gs, prealloc=prealloc)
     ks, vs = [], []
     if prefill:
         k = kv_bf16((B, Hkv, prefill, D), 1, frac=0.02, mult=8.0)
@@ -119,8 +122,9 @@ def test_growing(T, B, Hq, Hkv, D, bk, bv, prefill, steps, prealloc):
         vs.append(v)
         got, ref = tw.step(k, v, q, Hq, scale)
         K, V = np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
-        want = want_of(q, K, V, 64, bk, bv, scale)
-        print(f"[append-decode] B={B} D={D} bits={bk}/{bv} step={i} keys={K.shape[2]}", flush=True)
+        want = want_of(q, K, V, gs, bk, bv, scale)
+        print(f"[append-decode] B={B} D={D} bits={bk}/{bv} gs={gs} step={i} keys={K.shape[2]}",
+              flush=True)
         check_close(got, want)
         check_close(ref, want)
 
