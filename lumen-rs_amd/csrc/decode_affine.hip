@@ -252,6 +252,19 @@ KernelFn pick_mfma_only(int D, int bk, int bv, int G, int gs) {
 
 // Query heads one launch serves: the group's G, or G / 2 where the dot2
 // kernel takes the group in two launches (split_heads).
+// The heads a KV head that one kernel instantiation is picked for: G where
+// a kernel takes G heads, else (G up to 32, the reference's limit,
+// native_quant_attention.rs:253) the largest divisor of G a kernel takes,
+// run as G / divisor launches that each read the keys once (Gemma 4's
+// full-attention layers: 16 heads a KV head). 0 when none applies.
+int group_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows = 0) {
+  if (pick(D, bk, bv, G, gs, max_rows)) return G;
+  if (G > 32) return 0;
+  for (int d : {8, 6, 4, 3, 2, 1})
+    if (d < G && G % d == 0 && pick(D, bk, bv, d, gs, max_rows)) return d;
+  return 0;
+}
+
 int kernel_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows) {
   KernelFn fn = pick(D, bk, bv, G, gs, max_rows);
   if (!fn || fn == pick_mfma_only(D, bk, bv, G, gs)) return G;
@@ -269,16 +282,10 @@ extern "C" const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t 
                                                int32_t group_size, int32_t bits_k,
                                                int32_t bits_v) {
   if (H <= 0 || H_kv <= 0 || H % H_kv != 0) return "";
-  const int G = H / H_kv;
-  KernelFn fn = pick(D, bits_k, bits_v, G, group_size);
-  if (!fn) return "";
-  KernelFn mf = nullptr;
-  switch (D) {
-    case 64: mf = pick_mfma_d64(bits_k, bits_v, G, group_size); break;
-    case 128: mf = pick_mfma_d128(bits_k, bits_v, G, group_size); break;
-    case 256: mf = pick_mfma_d256(bits_k, bits_v, G, group_size); break;
-  }
-  return fn == mf ? "mfma" : "dot2";
+  const int Gp = group_heads(D, bits_k, bits_v, H / H_kv, group_size);
+  if (!Gp) return "";
+  KernelFn fn = pick(D, bits_k, bits_v, Gp, group_size);
+  return fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size) ? "mfma" : "dot2";
 }
 
 extern "C" size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
@@ -417,17 +424,20 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
   const int G = H / H_kv;
   int64_t max_rows = 0;
   for (int i = 0; i < n_segs; ++i) max_rows = segs[i].n > max_rows ? segs[i].n : max_rows;
-  KernelFn fn = pick(D, bits_k, bits_v, G, group_size, max_rows);
+  // Gp: the heads the kernel is picked for (G, or a divisor of G whose
+  // launches cover the group).
+  const int Gp = group_heads(D, bits_k, bits_v, G, group_size, max_rows);
+  KernelFn fn = Gp ? pick(D, bits_k, bits_v, Gp, group_size, max_rows) : nullptr;
   if (!fn)
     return fail(TQKV_EUNSUPPORTED, "decode layout D=%d bits_k=%d bits_v=%d gqa=%d", D, bits_k,
                 bits_v, G);
-  const bool mfma = fn == pick_mfma_only(D, bits_k, bits_v, G, group_size);
-  const int epl = epl_rt(bits_k, bits_v, G);
+  const bool mfma = fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size);
+  const int epl = epl_rt(bits_k, bits_v, Gp);
   if (!mfma && group_size < epl)
     return fail(TQKV_EUNSUPPORTED, "group_size=%d below %d", group_size, epl);
-  // The dot2 kernel takes 6 or 8 heads of 2/3/5/6-bit caches as two
-  // launches of half the heads each (both read the keys).
-  const int Gk = kernel_heads(D, bits_k, bits_v, G, group_size, max_rows);
+  // Heads a launch: Gp, or half of it where the dot2 kernel takes 6 or 8
+  // heads of 2/3/5/6-bit caches as two launches (each launch reads the keys).
+  const int Gk = kernel_heads(D, bits_k, bits_v, Gp, group_size, max_rows);
 
   Args a{};
   a.q = q;
@@ -586,10 +596,11 @@ size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n_segs < 1 || n_segs > 2) return 0;
   int64_t max_rows = 0;
   for (int i = 0; i < n_segs; ++i) max_rows = segs[i].n > max_rows ? segs[i].n : max_rows;
-  const int G = H / H_kv;
-  const int Gk = kernel_heads(D, bits_k, bits_v, G, group_size, max_rows);
-  KernelFn fn = pick(D, bits_k, bits_v, G, group_size, max_rows);
-  const bool mfma = fn && fn == pick_mfma_only(D, bits_k, bits_v, G, group_size);
+  const int Gp = group_heads(D, bits_k, bits_v, H / H_kv, group_size, max_rows);
+  if (!Gp) return 0;
+  const int Gk = kernel_heads(D, bits_k, bits_v, Gp, group_size, max_rows);
+  KernelFn fn = pick(D, bits_k, bits_v, Gp, group_size, max_rows);
+  const bool mfma = fn && fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size);
   return plan_decode(B, H, H_kv, D, Gk, decode_waves(D, bits_k, bits_v, Gk, group_size, mfma),
                      segs, n_segs, app).need;
 }

@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
   __shared__ float s_q[G][D];
   for (int i = threadIdx.x; i < G * D; i += kWave * kWaves) {
     const int h = i / D, d = i % D;
-    s_q[h][d] = bf16_to_f32(a.q[(int64_t(b) * a.H + kvh * G + h) * D + d]);
+    s_q[h][d] = bf16_to_f32(a.q[(int64_t(b) * a.H + kvh * a.Gt + a.h_off + h) * D + d]);
   }
   __syncthreads();
   int E[G];
@@ -756,7 +756,7 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       ls += s_l[w][h] * f;
       os += s_acc[w][h][d] * f;
     }
-    const int64_t bh = int64_t(b) * a.H + kvh * G + h;
+    const int64_t bh = int64_t(b) * a.H + kvh * a.Gt + a.h_off + h;
     if (a.n_part == 1) {
       a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
     } else {

@@ -319,6 +319,10 @@ DECODE_CASES = [
     (1, 16, 8, 128, 1500, 8, 4, 128, 0),     # group size 128
     (2, 16, 4, 256, 999, 6, 6, 128, 3),      # group size 128 at D = 256
     (2, 8, 1, 64, 600, 4, 4, 32, 0),         # group size 32 at D = 64, 8 heads
+    (1, 32, 2, 512, 3000, 4, 4, 64, 0),      # Gemma 4 full attention: 16 heads a KV head, D = 512
+    (2, 32, 2, 128, 1500, 4, 4, 64, 0),      # 16 heads a KV head: two launches of 8
+    (1, 20, 4, 128, 700, 8, 8, 64, 0),       # 5 heads a KV head: five launches of 1
+    (1, 32, 1, 256, 900, 3, 3, 64, 0),       # 32 heads on one KV head
 ]
 
 
@@ -402,6 +406,7 @@ def test_decode_shared_prefix_plus_suffix(T, kernel):
     (2, 16, 8, 256, 1000, 0, 3, 3, 64),     # prefix only
     (4, 8, 8, 64, 777, 65, 4, 4, 32),
     (5, 12, 4, 128, 2049, 1, 4, 8, 128),    # odd batch, G = 3
+    (4, 32, 2, 128, 1000, 50, 4, 4, 64),    # 16 heads a KV head (suffix in two launches)
 ])
 def test_decode_shared_prefix_read_once(T, monkeypatch, B, H, Hkv, D, P, S, bk, bv, gs):
     # With B >= 2 sequences over a shared prefix the prefix is read once per
@@ -438,7 +443,7 @@ def test_decode_rejects_unreadable_layouts(T):
     q = T.DeviceArray((1, 12, 1, 128), np.uint16)
     out = T.DeviceArray((1, 12, 1, 128), np.uint16)
     seg = T.affine_seg((q.ptr,) * 3, (q.ptr,) * 3, 1, 1)
-    for args in [(1, 10, 2, 128, 64, 4, 4), (1, 10, 2, 128, 64, 3, 3), (1, 12, 12, 96, 32, 4, 4),
+    for args in [(1, 66, 2, 128, 64, 4, 4), (1, 68, 2, 128, 64, 3, 3), (1, 12, 12, 96, 32, 4, 4),
                  (1, 12, 12, 128, 64, 7, 7), (1, 12, 12, 128, 64, 5, 4), (1, 12, 12, 128, 64, 6, 8)]:
         with pytest.raises(T.TqkvError) as e:
             T.decode_attend_affine(q.ptr, *args, 1.0, [seg], out.ptr)

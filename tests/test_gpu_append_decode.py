@@ -102,6 +102,7 @@ def want_of(q, K, V, gs, bk, bv, scale):
     (1, 16, 8, 256, 4, 4, 100, 3, True, 32),    # group size 32 (16 A rows)
     (2, 32, 8, 128, 6, 6, 40, 2, True, 32),     # group size 32, 4 heads a KV head
     (1, 16, 8, 128, 8, 4, 70, 2, True, 128),    # group size 128
+    (1, 32, 2, 128, 4, 4, 50, 2, True, 64),     # 16 heads a KV head: two launches
 ])
 def test_growing(T, B, Hq, Hkv, D, bk, bv, prefill, steps, prealloc, gs):
     assert T.decode_kernel_name(Hq, Hkv, D, gs, bk, bv) == "mfma"
