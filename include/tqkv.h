@@ -169,8 +169,11 @@ typedef struct tqkv_affine_seg {
  * q: bf16 [B, H, 1, D]; out: bf16 [B, H, 1, D]. Query head h reads KV head
  * h / (H / H_kv). (bits_k, bits_v): 3, 4 or 8 bits each in any pair, or 2,
  * 5 or 6 bits for both; group_size in {32, 64, 128}; D in {64, 128, 256,
- * 512}; H / H_kv in {1, 2, 3, 4, 6, 8} (6 or 8 heads of a 2/3/5/6-bit cache
- * are served as two launches of half the heads). n_segs in {1, 2}.
+ * 512}; H / H_kv from 1 to 32 (the reference's limit): groups of 1, 2, 3, 4,
+ * 6 or 8 heads in one launch (6 or 8 heads of a 2/3/5/6-bit cache as two
+ * launches of half the heads), any other group as launches of its largest
+ * such divisor, each launch reading the keys once (16 heads: two of 8).
+ * n_segs in {1, 2}.
  * workspace: device scratch of tqkv_decode_workspace_size() bytes for the
  * split partials, or NULL to use a buffer the library keeps per device (grown
  * on demand); calls that share a workspace must not overlap in time. One
@@ -293,8 +296,8 @@ size_t tqkv_sparse_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
 
 /*
  * Which decode kernel tqkv_decode_attend_affine runs for a layout: "mfma"
- * (scores on the matrix cores; group_size 64, D in {64, 128, 256},
- * H / H_kv in {1, 2, 4, 8} with H / H_kv * D / 64 <= 16), "dot2" (every other
+ * (scores on the matrix cores; group_size 32, 64 or 128, D in {64, 128, 256},
+ * heads a launch in {1, 2, 4, 8} with heads * D / group_size <= 16), "dot2" (every other
  * supported layout, or any layout when the environment variable
  * TQKV_DECODE_KERNEL=dot2 is set), or "" (unsupported). No counterpart in the
  * reference; for tests and benchmarks.
