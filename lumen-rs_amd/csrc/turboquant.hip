@@ -1231,7 +1231,7 @@ int32_t launch_cb(int G, dim3 grid, hipStream_t st, const float* qr, int H, cons
                          po, pm, pl, ksg, krn, pq, m);                                        \
     break;
   switch (G) {
-    TQKV_CB(1) TQKV_CB(2) TQKV_CB(4) TQKV_CB(8)
+    TQKV_CB(1) TQKV_CB(2) TQKV_CB(4) TQKV_CB(8) TQKV_CB(16)
     default: return fail(TQKV_EUNSUPPORTED, "codebook decode with %d query heads per KV head", G);
   }
 #undef TQKV_CB
@@ -1379,7 +1379,8 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
     case 64: rc = tq::launch_cb<64>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
     case 128: rc = tq::launch_cb<128>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
     case 256: rc = tq::launch_cb<256>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
-    default: return fail(TQKV_EUNSUPPORTED, "codebook decode D=%d not in {64,128,256}", D);
+    case 512: rc = tq::launch_cb<512>(G, grid, st, qr, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
+    default: return fail(TQKV_EUNSUPPORTED, "codebook decode D=%d not in {64,128,256,512}", D);
   }
   if (rc) return rc;
   hipLaunchKernelGGL(tq::cb_merge_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256),

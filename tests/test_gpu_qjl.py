@@ -133,7 +133,11 @@ def test_gpu_path_variance_threshold(T):
 
 
 @pytest.mark.parametrize("B,H,Hkv,D,N,bits,m", [(2, 8, 2, 128, 300, 4, 64), (1, 4, 4, 64, 700, 3, 96),
-                                               (1, 16, 8, 256, 1100, 4, 1024)])
+                                               (1, 16, 8, 256, 1100, 4, 1024),
+                                               # Gemma 4 full attention (turboquant.rs:1638-1650):
+                                               # 16 heads a KV head at D = 512
+                                               (1, 32, 2, 512, 700, 4, 64),
+                                               (2, 32, 2, 128, 300, 3, 32)])
 def test_codebook_decode_with_qjl(T, B, H, Hkv, D, N, bits, m):
     print(f"[qjl-decode] B={B} H={H}/{Hkv} D={D} N={N} bits={bits} m={m}", flush=True)
     R, phi = T.rotation_matrix(D, 42), T.qjl_matrix(D, m, 43)
