@@ -297,7 +297,9 @@ size_t tqkv_sparse_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
 /*
  * Which decode kernel tqkv_decode_attend_affine runs for a layout: "mfma"
  * (scores on the matrix cores; group_size 32, 64 or 128, D in {64, 128, 256},
- * heads a launch in {1, 2, 4, 8} with heads * D / group_size <= 16), "dot2" (every other
+ * heads a launch in {1, 2, 4, 8} with heads * D / group_size <= 16), "tiles"
+ * (head dim 512: the prefill tile kernel with f16 operands, a sequence's
+ * heads as one block's rows), "dot2" (every other
  * supported layout, or any layout when the environment variable
  * TQKV_DECODE_KERNEL=dot2 is set), or "" (unsupported). No counterpart in the
  * reference; for tests and benchmarks.

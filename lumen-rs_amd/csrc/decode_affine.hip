@@ -14,6 +14,12 @@ int32_t shared_prefix_partials(const uint16_t* q, int B, int H, int H_kv, int D,
                                int split_len, int n_part, float* part_o, float* part_m,
                                float* part_l, hipStream_t st);
 int shared_prefix_block_rows(int D);
+bool tile_decode_supported(int D, int bk, int bv);
+int tile_decode_rows();
+int32_t tile_decode(const uint16_t* q, int B, int H, int H_kv, int D, int gs, int bk, int bv,
+                    float scale, const tqkv_affine_seg* segs, int n_segs, int n_splits,
+                    int split_len, int n_part, float* part_o, float* part_m, float* part_l,
+                    uint16_t* out, hipStream_t st);
 }  // namespace prefill
 namespace decode {
 namespace {
@@ -265,6 +271,18 @@ int group_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows = 0) {
   return 0;
 }
 
+// Head dim 512 decodes through the tile kernel (the prefill kernel's f16
+// variant, a sequence's heads as the rows of a block): its scores and
+// values run on the matrix cores, where the dot2 kernel spends a 64-lane
+// reduction per token and head at that width (measured 3-9x slower). No
+// fused append there (that needs the MFMA decode kernel), and
+// TQKV_DECODE_KERNEL=dot2 keeps the dot2 kernel.
+bool use_tile(int D, int bk, int bv, int G, bool app) {
+  const char* env = getenv("TQKV_DECODE_KERNEL");
+  if (env && strcmp(env, "dot2") == 0) return false;
+  return D == 512 && !app && G <= 32 && prefill::tile_decode_supported(D, bk, bv);
+}
+
 int kernel_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows) {
   KernelFn fn = pick(D, bk, bv, G, gs, max_rows);
   if (!fn || fn == pick_mfma_only(D, bk, bv, G, gs)) return G;
@@ -282,6 +300,7 @@ extern "C" const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t 
                                                int32_t group_size, int32_t bits_k,
                                                int32_t bits_v) {
   if (H <= 0 || H_kv <= 0 || H % H_kv != 0) return "";
+  if (use_tile(D, bits_k, bits_v, H / H_kv, false)) return "tiles";
   const int Gp = group_heads(D, bits_k, bits_v, H / H_kv, group_size);
   if (!Gp) return "";
   KernelFn fn = pick(D, bits_k, bits_v, Gp, group_size);
@@ -316,6 +335,7 @@ struct AppendDst {
 // How a decode call splits its keys, and the workspace bytes that needs (0:
 // none). Only the segments' lengths and shared flags matter.
 struct DecodePlan {
+  bool tile = false;  // the tile kernel (use_tile), splits as below
   bool shared_path = false;
   // Shared prefix read once: prefix splits, then the suffix's.
   int sp_p = 0, split_len_p = 0, sp_s = 0;
@@ -374,9 +394,10 @@ uint32_t* merge_counters(int64_t units) {
 }
 
 // Gk: the query heads one decode launch serves (kernel_heads).
-// waves: the launch's wavefronts a workgroup (decode_waves).
+// waves: the launch's wavefronts a workgroup (decode_waves); tile: the
+// tile kernel decodes (use_tile).
 DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, int waves,
-                       const tqkv_affine_seg* segs, int n_segs, bool app) {
+                       const tqkv_affine_seg* segs, int n_segs, bool app, bool tile = false) {
   DecodePlan pl;
   const int G = H / H_kv;
   const int64_t total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
@@ -401,6 +422,24 @@ DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, int waves,
     pl.n_part = pl.sp_p + pl.sp_s;
     pl.inline_merge = pl.sp_s > 0 && pl.n_part <= kInlineMergeMax && inline_merge_enabled();
     pl.need = size_t(B) * H * pl.n_part * row * sizeof(float);
+    return pl;
+  }
+  if (tile) {
+    // About 256 workgroups (one a CU: the tile kernel's LDS holds one),
+    // never under 256 keys a split.
+    const int rows = prefill::tile_decode_rows();
+    const int64_t units = int64_t(B) * H_kv * ((G + rows - 1) / rows);
+    int64_t want = (256 + units - 1) / units;
+    const int64_t most = (total + 255) / 256;
+    if (want > most) want = most;
+    if (want < 1) want = 1;
+    int64_t len = (total + want - 1) / want;
+    len = (len + 63) / 64 * 64;
+    pl.tile = true;
+    pl.split_len = len;
+    pl.n_splits = int((total + len - 1) / len);
+    pl.n_part = pl.n_splits;
+    pl.need = pl.n_splits > 1 ? size_t(B) * H * pl.n_splits * row * sizeof(float) : 0;
     return pl;
   }
   plan_splits(B, H_kv, waves, total, &pl.n_splits, &pl.split_len);
@@ -428,16 +467,17 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
   // launches cover the group).
   const int Gp = group_heads(D, bits_k, bits_v, G, group_size, max_rows);
   KernelFn fn = Gp ? pick(D, bits_k, bits_v, Gp, group_size, max_rows) : nullptr;
-  if (!fn)
+  const bool tile = use_tile(D, bits_k, bits_v, G, app != nullptr);
+  if (!fn && !tile)
     return fail(TQKV_EUNSUPPORTED, "decode layout D=%d bits_k=%d bits_v=%d gqa=%d", D, bits_k,
                 bits_v, G);
-  const bool mfma = fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size);
+  const bool mfma = fn && fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size);
   const int epl = epl_rt(bits_k, bits_v, Gp);
-  if (!mfma && group_size < epl)
+  if (!tile && !mfma && group_size < epl)
     return fail(TQKV_EUNSUPPORTED, "group_size=%d below %d", group_size, epl);
   // Heads a launch: Gp, or half of it where the dot2 kernel takes 6 or 8
   // heads of 2/3/5/6-bit caches as two launches (each launch reads the keys).
-  const int Gk = kernel_heads(D, bits_k, bits_v, Gp, group_size, max_rows);
+  const int Gk = Gp ? kernel_heads(D, bits_k, bits_v, Gp, group_size, max_rows) : G;
 
   Args a{};
   a.q = q;
@@ -484,7 +524,7 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
 
   const int waves = decode_waves(D, bits_k, bits_v, Gk, group_size, mfma);
   a.out = out;
-  const DecodePlan pl = plan_decode(B, H, H_kv, D, Gk, waves, segs, n_segs, app != nullptr);
+  const DecodePlan pl = plan_decode(B, H, H_kv, D, Gk, waves, segs, n_segs, app != nullptr, tile);
   void* ws = workspace;
   if (pl.need > 0) {
     if (!ws) {
@@ -497,6 +537,20 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
   // Each launch that merges in-kernel counts in a chunk of its own.
   auto counters = [&]() { return pl.inline_merge ? merge_counters(int64_t(B) * H_kv) : nullptr; };
 
+  if (pl.tile) {
+    float* po = static_cast<float*>(ws);
+    float* pm = po ? po + size_t(B) * H * pl.n_part * D : nullptr;
+    float* pl_ = pm ? pm + size_t(B) * H * pl.n_part : nullptr;
+    if (int32_t rc = prefill::tile_decode(q, B, H, H_kv, D, group_size, bits_k, bits_v, scale,
+                                          segs, n_segs, pl.n_splits, int(pl.split_len),
+                                          pl.n_part, po, pm, pl_, out, st))
+      return rc;
+    if (pl.n_splits > 1) {
+      launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
+      TQKV_LAUNCHED();
+    }
+    return ok();
+  }
   bool merged = false;  // the decode launches merged in-kernel
   if (pl.shared_path) {
     Args s = a;
@@ -596,13 +650,15 @@ size_t decode_need_bytes(int B, int H, int H_kv, int D, int group_size, int bits
   if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv != 0 || n_segs < 1 || n_segs > 2) return 0;
   int64_t max_rows = 0;
   for (int i = 0; i < n_segs; ++i) max_rows = segs[i].n > max_rows ? segs[i].n : max_rows;
-  const int Gp = group_heads(D, bits_k, bits_v, H / H_kv, group_size, max_rows);
-  if (!Gp) return 0;
-  const int Gk = kernel_heads(D, bits_k, bits_v, Gp, group_size, max_rows);
-  KernelFn fn = pick(D, bits_k, bits_v, Gp, group_size, max_rows);
+  const int G = H / H_kv;
+  const int Gp = group_heads(D, bits_k, bits_v, G, group_size, max_rows);
+  const bool tile = use_tile(D, bits_k, bits_v, G, app);
+  if (!Gp && !tile) return 0;
+  const int Gk = Gp ? kernel_heads(D, bits_k, bits_v, Gp, group_size, max_rows) : G;
+  KernelFn fn = Gp ? pick(D, bits_k, bits_v, Gp, group_size, max_rows) : nullptr;
   const bool mfma = fn && fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size);
   return plan_decode(B, H, H_kv, D, Gk, decode_waves(D, bits_k, bits_v, Gk, group_size, mfma),
-                     segs, n_segs, app).need;
+                     segs, n_segs, app, tile).need;
 }
 }  // namespace tqkv
 

@@ -95,6 +95,59 @@ namespace prefill {
 // (rows (b, g) of a KV head), the prefix's keys are split over the grid,
 // and each split's (o, m, l) go to slots [0, n_splits) of the decode's
 // partials [B, H, n_part]. Rows b * H + h line up with the decode kernel's.
+bool tile_decode_supported(int D, int bk, int bv) { return D == 512 && pick(D, bk, bv, true); }
+int tile_decode_rows() { return Shape<512, true>::kRows; }
+
+// Decode through the tile kernel (f16 operands): each sequence's G query
+// heads of a KV head are the rows of one block (one position, L = 1), the
+// keys of up to two segments split over the grid; with n_splits > 1 each
+// split's (o, m, l) go to slots [0, n_splits) of the decode's partials
+// [B, H, n_part] (the decode's merge finishes), else the block writes out.
+// Serves head_dim 512, which no decode kernel takes on the matrix cores.
+int32_t tile_decode(const uint16_t* q, int B, int H, int H_kv, int D, int gs, int bk, int bv,
+                    float scale, const tqkv_affine_seg* segs, int n_segs, int n_splits,
+                    int split_len, int n_part, float* part_o, float* part_m, float* part_l,
+                    uint16_t* out, hipStream_t st) {
+  KernelFn fn = pick(D, bk, bv, true);
+  if (!fn || D != 512) return fail(TQKV_EUNSUPPORTED, "tile decode D=%d bits %d/%d", D, bk, bv);
+  Args a{};
+  a.q = q;
+  a.out = out;
+  a.qs_b = int64_t(H) * D;
+  a.qs_h = D;
+  a.qs_l = int64_t(H) * D;
+  a.H = H;
+  a.H_kv = H_kv;
+  a.G = H / H_kv;
+  a.L = 1;
+  a.gs = gs;
+  a.causal = 0;
+  a.qscale = scale * kLog2e;
+  for (int i = 0; i < n_segs; ++i) {
+    const tqkv_affine_seg& sg = segs[i];
+    a.seg[i] = Seg{sg.k_packed, sg.k_scales, sg.k_biases, sg.v_packed, sg.v_scales, sg.v_biases,
+                   sg.cap, sg.shared ? 0 : int64_t(H_kv) * sg.cap};
+  }
+  if (n_segs == 1) a.seg[1] = a.seg[0];
+  a.n0 = segs[0].n;
+  a.total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
+  a.n_splits = n_splits;
+  a.split_len = split_len;
+  a.split_base = 0;
+  a.n_part = n_part;
+  a.part_o = n_splits > 1 ? part_o : nullptr;
+  a.part_m = n_splits > 1 ? part_m : nullptr;
+  a.part_l = n_splits > 1 ? part_l : nullptr;
+  using S = Shape<512, true>;
+  const int64_t blocks = (a.G + S::kRows - 1) / S::kRows;
+  a.n_blocks = int(blocks);
+  const int64_t grid = blocks * n_splits * H_kv * int64_t(B);
+  if (grid > 0x7fffffff) return fail(TQKV_EINVAL_SHAPE, "grid too large");
+  hipLaunchKernelGGL(fn, dim3(unsigned(grid)), dim3(S::kThreads), 0, st, a);
+  TQKV_LAUNCHED();
+  return TQKV_OK;
+}
+
 int shared_prefix_block_rows(int D) {
   switch (D) {
     case 64: return Shape<64, true>::kRows;

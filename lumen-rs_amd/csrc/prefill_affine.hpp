@@ -123,7 +123,7 @@ struct Shape {
   // Tiles whose raw words are in flight in registers while a tile is
   // computed. The f16 (decode) variant serves few query rows, so a tile's
   // compute is short and the loads must run further ahead to keep HBM busy.
-  static constexpr int kSets = H16 ? 2 : 1;
+  static constexpr int kSets = H16 && D <= 256 ? 2 : 1;
   static constexpr int kBufs = D == 512 ? 1 : 2;      // LDS tile buffers
   static constexpr int kWavesPerEu = D == 512 ? 1 : 2;
   static_assert(kPer * kThreads == 4 * D, "whole loader tasks per thread");

@@ -4,6 +4,8 @@
 
 namespace tqkv {
 namespace prefill {
-KernelFn pick_d512(int bk, int bv, bool h16) { return h16 ? nullptr : pick_for<512, false>(bk, bv); }
+KernelFn pick_d512(int bk, int bv, bool h16) {
+  return h16 ? pick_for<512, true>(bk, bv) : pick_for<512, false>(bk, bv);
+}
 }  // namespace prefill
 }  // namespace tqkv

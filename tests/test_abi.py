@@ -48,7 +48,7 @@ def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 3, 3) == "mfma"  # config 2
     assert tqkv.decode_kernel_name(32, 8, 128, 64, 4, 4) == "mfma"  # configs 1 and 3
     assert tqkv.decode_kernel_name(32, 8, 128, 64, 8, 4) == "mfma"  # config 4
-    assert tqkv.decode_kernel_name(16, 2, 512, 64, 8, 8) == "dot2"
+    assert tqkv.decode_kernel_name(16, 2, 512, 64, 8, 8) == "tiles"  # D = 512: tile kernel
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 5, 5) == "mfma"  # bit-anchored windows
     assert tqkv.decode_kernel_name(32, 8, 128, 64, 6, 6) == "mfma"  # Gemma's 6-bit cache
     assert tqkv.decode_kernel_name(32, 4, 128, 64, 3, 3) == "dot2"  # 8 heads: two launches
@@ -59,7 +59,7 @@ def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 7, 7) == ""
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 5, 4) == ""
     assert tqkv.decode_kernel_name(20, 4, 128, 64, 4, 4) == "mfma"  # 5 heads: 5 launches of 1
-    assert tqkv.decode_kernel_name(32, 2, 512, 64, 4, 4) == "dot2"  # Gemma 4 full attention
+    assert tqkv.decode_kernel_name(32, 2, 512, 64, 4, 4) == "tiles"  # Gemma 4 full attention
     assert tqkv.decode_kernel_name(32, 2, 128, 64, 4, 4) == "mfma"  # 16 heads: 2 launches of 8
     assert tqkv.decode_kernel_name(66, 2, 128, 64, 4, 4) == ""  # 33 heads: past the limit
     monkeypatch.setenv("TQKV_DECODE_KERNEL", "dot2")
