@@ -117,7 +117,13 @@ template <int D, bool H16>
 struct Shape {
   static constexpr int kWaves = (D == 64 || D == 512) ? 4 : 8;
   static constexpr int kRW = (D >= 256 || H16) ? 16 : 32;
-  static constexpr int kRows = kWaves * kRW;
+  // D = 512 with f16 operands (decode: a sequence's heads at one position)
+  // splits the output channels instead of the rows: every wavefront takes
+  // the block's rows, scores all of D, and accumulates a quarter of the
+  // channels (its O accumulators fit the register file; one wavefront
+  // holding all 512 spilled).
+  static constexpr bool kChanSplit = H16 && D == 512;
+  static constexpr int kRows = kChanSplit ? kRW : kWaves * kRW;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kPer = 4 * D / kThreads;
   // Tiles whose raw words are in flight in registers while a tile is
@@ -458,7 +464,12 @@ __global__ __launch_bounds__((Shape<D, H16>::kThreads))
 __attribute__((amdgpu_waves_per_eu(Shape<D, H16>::kWavesPerEu)))
 void prefill_affine_kernel(const Args a) {
   constexpr int kWaves = Shape<D, H16>::kWaves, RW = Shape<D, H16>::kRW, kRows = Shape<D, H16>::kRows;
-  constexpr int NR = RW / 16, ND = D / 32, NT = D / 16;
+  constexpr int NR = RW / 16, ND = D / 32;
+  constexpr bool CS = Shape<D, H16>::kChanSplit;
+  // Output channel tiles of 16 this wavefront accumulates, from t_base on;
+  // RWO: rows between wavefronts (0 when they share the rows).
+  constexpr int NT = CS ? D / 16 / kWaves : D / 16;
+  constexpr int RWO = CS ? 0 : RW;
   constexpr int KSTR = kKStride<D>, VSTR = kVStride;
   constexpr int kPer = Shape<D, H16>::kPer, kThreads = Shape<D, H16>::kThreads;
   constexpr int kBufs = Shape<D, H16>::kBufs;
@@ -471,6 +482,7 @@ void prefill_affine_kernel(const Args a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave, lr = lane % 16, lg = lane / 16;
+  const int t_base = CS ? wave * NT : 0;
   // Workgroup i runs on XCD i % 8 (round-robin dispatch). Consecutive
   // logical blocks, which share a (batch row, KV head) and so its keys, are
   // placed on one XCD's L2; within a unit the longest key ranges go first.
@@ -501,7 +513,7 @@ void prefill_affine_kernel(const Args a) {
   bool rvalid[NR];
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
-    const int64_t r = row0 + wave * RW + 16 * j + lr;
+    const int64_t r = row0 + wave * RWO + 16 * j + lr;
     rvalid[j] = r < rows;
     const int64_t rr = rvalid[j] ? r : rows - 1;
     const int64_t l = rr / a.G, g = rr % a.G;
@@ -602,7 +614,7 @@ void prefill_affine_kernel(const Args a) {
     // work in opposite orders, so one's dequantization (VALU) runs while the
     // other's products (MFMA) do.
     const bool dequant_first = wave >= kWaves / 2;
-    const bool live = row0 + int64_t(wave) * RW < rows;
+    const bool live = row0 + int64_t(wave) * RWO < rows;
     // One tile: S holds tile t + 1's words, which go into the other LDS
     // buffer (last read in the previous tile, before the barrier that ended
     // it); S then fetches tile t + 1 + NS.
@@ -707,7 +719,7 @@ void prefill_affine_kernel(const Args a) {
           }
   #pragma unroll
           for (int t2 = 0; t2 < NT; ++t2) {
-            const uint16_t* vrow = Vt + (16 * t2 + lr) * VSTR + 32 * u + 4 * lg;
+            const uint16_t* vrow = Vt + (16 * (t_base + t2) + lr) * VSTR + 32 * u + 4 * lg;
             const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
             const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
             const op8_t va = __builtin_bit_cast(op8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
@@ -756,14 +768,14 @@ void prefill_affine_kernel(const Args a) {
     tot = xor32_sum(xor16_sum(tot));
     if (!rvalid[j]) continue;
     if (a.part_o) {
-      const int64_t r = row0 + wave * RW + 16 * j + lr;
+      const int64_t r = row0 + wave * RWO + 16 * j + lr;
       const int64_t l = r / a.G, h = int64_t(kvh) * a.G + r % a.G;
       const int64_t slot = ((int64_t(b) * a.L + l) * a.H + h) * a.n_part + a.split_base + split;
       float* po = a.part_o + slot * D;
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2)
-        *reinterpret_cast<f4_t*>(po + 16 * t2 + 4 * lg) = o[t2][j];
-      if (lg == 0) {
+        *reinterpret_cast<f4_t*>(po + 16 * (t_base + t2) + 4 * lg) = o[t2][j];
+      if (lg == 0 && (!CS || wave == 0)) {
         a.part_m[slot] = m[j];
         a.part_l[slot] = tot;
       }
@@ -772,7 +784,7 @@ void prefill_affine_kernel(const Args a) {
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2) {
         const f4_t v = o[t2][j] * inv;
-        *reinterpret_cast<u32x2_t*>(a.out + orow[j] + 16 * t2 + 4 * lg) =
+        *reinterpret_cast<u32x2_t*>(a.out + orow[j] + 16 * (t_base + t2) + 4 * lg) =
             u32x2_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
       }
     }
