@@ -381,6 +381,33 @@ def test_decode_reference_fused_kernel_cases(T, kernel, H, Hkv, D, N, bits):
     check_close(got, wf)
 
 
+@pytest.mark.parametrize("B,H,Hkv,D,n1,n2,shared,bk,bv", [
+    (2, 16, 2, 512, 700, 333, False, 4, 4),   # a ring view: two segments of one cache
+    (1, 32, 2, 512, 1500, 90, True, 8, 8),    # one sequence over a shared prefix
+    (2, 8, 2, 128, 513, 200, False, 4, 8),
+])
+def test_decode_two_segments(T, kernel, B, H, Hkv, D, n1, n2, shared, bk, bv):
+    """Two segments in one softmax on every decode path (the D = 512 tile
+    kernel included): the oracle over their concatenation."""
+    print(f"[decode-2seg] B={B} H={H}/{Hkv} D={D} n={n1}+{n2} shared={shared} "
+          f"kernel={T.decode_kernel_name(H, Hkv, D, 64, bk, bv)}", flush=True)
+    gs = 64
+    q = kv_bf16((B, H, 1, D), 31 + D, std=D ** -0.5 * 4)
+    b1 = 1 if shared else B
+    k1, v1 = kv_bf16((b1, Hkv, n1, D), 32), kv_bf16((b1, Hkv, n1, D), 33)
+    k2, v2 = kv_bf16((B, Hkv, n2, D), 34), kv_bf16((B, Hkv, n2, D), 35)
+    (k1h, k1d), (v1h, v1d) = _cache(k1, gs, bk, n1 + 7), _cache(v1, gs, bv, n1 + 7)
+    (k2h, k2d), (v2h, v2d) = _cache(k2, gs, bk, n2 + 3), _cache(v2, gs, bv, n2 + 3)
+    got = run_decode(T, q, [(k1d, v1d, n1 + 7, n1, shared), (k2d, v2d, n2 + 3, n2, False)], B,
+                     H, Hkv, D, gs, bk, bv, 1.0)
+    cat = lambda a, b: np.concatenate([np.broadcast_to(a, (B,) + a.shape[1:]), b], axis=2)
+    kfull = tuple(cat(a, b) for a, b in zip(k1h, k2h))
+    vfull = tuple(cat(a, b) for a, b in zip(v1h, v2h))
+    wf, _, _ = O.attend_affine(q, kfull, vfull, gs, bk, bv, 1.0)
+    wm, _, _ = O.attend_affine(q, kfull, vfull, gs, bk, bv, 1.0, dequant="bf16")
+    check_close(got, wf, wm)
+
+
 def test_decode_shared_prefix_plus_suffix(T, kernel):
     # sdpa_split semantics (native_attention.rs:174-208): one softmax over a
     # shared batch-1 prefix and each row's own suffix.
