@@ -125,12 +125,18 @@ int32_t tile_decode(const uint16_t* q, int B, int H, int H_kv, int D, int gs, in
   a.qscale = scale * kLog2e;
   for (int i = 0; i < n_segs; ++i) {
     const tqkv_affine_seg& sg = segs[i];
+    // Rows of a slab are addressed with 32-bit word offsets.
+    if (sg.cap > 0 && sg.cap * int64_t(D) * (bk > bv ? bk : bv) / 32 >= (int64_t(1) << 32))
+      return fail(TQKV_EINVAL_SHAPE, "segment %d: cap=%lld rows too large", i, (long long)sg.cap);
     a.seg[i] = Seg{sg.k_packed, sg.k_scales, sg.k_biases, sg.v_packed, sg.v_scales, sg.v_biases,
                    sg.cap, sg.shared ? 0 : int64_t(H_kv) * sg.cap};
   }
   if (n_segs == 1) a.seg[1] = a.seg[0];
   a.n0 = segs[0].n;
   a.total = segs[0].n + (n_segs == 2 ? segs[1].n : 0);
+  if (a.total > (int64_t(1) << 31) - 2 * kTile)
+    return fail(TQKV_EINVAL_SHAPE, "%lld keys exceed the kernel's 32-bit key index",
+                (long long)a.total);
   a.n_splits = n_splits;
   a.split_len = split_len;
   a.split_base = 0;
