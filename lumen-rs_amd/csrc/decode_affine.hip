@@ -192,7 +192,6 @@ int max_splits(int B, int H_kv, int64_t total) {
   return want < 1 ? 1 : int(want);
 }
 
-
 // Workgroups of the shared-prefix pass: one per CU of an MI355X (256). The
 // pass holds one workgroup per CU, and each workgroup's fixed costs (query
 // load, first tile, partials) favour one long key range per CU over several
@@ -256,8 +255,6 @@ KernelFn pick_mfma_only(int D, int bk, int bv, int G, int gs) {
   return nullptr;
 }
 
-// Query heads one launch serves: the group's G, or G / 2 where the dot2
-// kernel takes the group in two launches (split_heads).
 // The heads a KV head that one kernel instantiation is picked for: G where
 // a kernel takes G heads, else (G up to 32, the reference's limit,
 // native_quant_attention.rs:253) the largest divisor of G a kernel takes,
@@ -283,6 +280,8 @@ bool use_tile(int D, int bk, int bv, int G, bool app) {
   return D == 512 && !app && G <= 32 && prefill::tile_decode_supported(D, bk, bv);
 }
 
+// Query heads one launch serves: the group's G, or G / 2 where the dot2
+// kernel takes the group in two launches (split_heads).
 int kernel_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows) {
   KernelFn fn = pick(D, bk, bv, G, gs, max_rows);
   if (!fn || fn == pick_mfma_only(D, bk, bv, G, gs)) return G;

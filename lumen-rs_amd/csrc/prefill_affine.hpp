@@ -128,7 +128,8 @@ struct Shape {
   static constexpr int kPer = 4 * D / kThreads;
   // Tiles whose raw words are in flight in registers while a tile is
   // computed. The f16 (decode) variant serves few query rows, so a tile's
-  // compute is short and the loads must run further ahead to keep HBM busy.
+  // compute is short and the loads must run further ahead to keep HBM busy
+  // (one set at D = 512, where two measured slower).
   static constexpr int kSets = H16 && D <= 256 ? 2 : 1;
   static constexpr int kBufs = D == 512 ? 1 : 2;      // LDS tile buffers
   static constexpr int kWavesPerEu = D == 512 ? 1 : 2;
