@@ -572,7 +572,12 @@ void prefill_affine_kernel(const Args a) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int task = tid + i * kThreads, r = task % (2 * D);
-      tv[i] = wave * kWave + i * kThreads >= 2 * D;
+      // A task's kind is wave-uniform; where 2D is a multiple of the
+      // workgroup it depends on i alone, so the compiler folds each task's
+      // pointers to K's or V's (D = 512: 8 tasks a thread would otherwise
+      // hold 48 pointers in scalar registers and spill them).
+      tv[i] = (2 * D) % kThreads == 0 ? i * kThreads >= 2 * D
+                                       : wave * kWave + i * kThreads >= 2 * D;
       tkey[i] = r % kTile;
       trun[i] = r / kTile;
       tp[i].w0 = tv[i] ? vp.w0 : kp.w0;
