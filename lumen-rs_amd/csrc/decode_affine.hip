@@ -261,7 +261,15 @@ KernelFn pick_mfma_only(int D, int bk, int bv, int G, int gs) {
 // run as G / divisor launches that each read the keys once (Gemma 4's
 // full-attention layers: 16 heads a KV head). 0 when none applies.
 int group_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows = 0) {
-  if (pick(D, bk, bv, G, gs, max_rows)) return G;
+  KernelFn whole = pick(D, bk, bv, G, gs, max_rows);
+  // Where only the dot2 kernel takes the whole group, two MFMA launches of
+  // half the heads (each reading the keys) beat it: 8 heads at D = 256,
+  // 4-bit, 8,192 keys: 2 x 50.7 against 222 us.
+  if (whole && whole != pick_mfma_only(D, bk, bv, G, gs) && G % 2 == 0 &&
+      pick(D, bk, bv, G / 2, gs, max_rows) == pick_mfma_only(D, bk, bv, G / 2, gs) &&
+      pick_mfma_only(D, bk, bv, G / 2, gs))
+    return G / 2;
+  if (whole) return G;
   if (G > 32) return 0;
   for (int d : {8, 6, 4, 3, 2, 1})
     if (d < G && G % d == 0 && pick(D, bk, bv, d, gs, max_rows)) return d;

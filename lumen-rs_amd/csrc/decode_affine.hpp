@@ -649,14 +649,15 @@ constexpr int epl_for() {
 // same function): 8, two a SIMD with at most 256 registers each, or 4 (one
 // a SIMD, up to 512) where the cross-wave merge buffer (waves x G x D
 // floats) would pass 32 KB of LDS, or where a wavefront's accumulators
-// outgrow 256 registers by far: the MFMA kernel's G x D/gs = 16 A rows
-// (600 registers spilled at 8 wavefronts; 4 measured 1.2-1.5x faster) and
+// outgrow 256 registers by far: the MFMA kernel's G x D/gs = 16 A rows,
+// G x D = 1024 value accumulators or 8 heads (30-600 registers spilled at
+// 8 wavefronts; 4 measured 1.2-1.5x faster) and
 // the dot2 kernel's G heads x EPL channels above 64 (200-700 spilled; 4
 // measured 2.7-3.2x faster). At G x EPL = 64 the few spills of 8
 // wavefronts cost less than the lost occupancy (8 measured 10-25% faster).
 constexpr int decode_waves(int D, int bk, int bv, int G, int gs, bool mfma) {
   return G * D > 1024 ? 4
-         : mfma       ? (G * (D / gs) >= 16 ? 4 : 8)
+         : mfma       ? (G * (D / gs) >= 16 || G * D >= 1024 || G >= 8 ? 4 : 8)
                       : (G * epl_of(bk, bv, G) > 64 ? 4 : 8);
 }
 

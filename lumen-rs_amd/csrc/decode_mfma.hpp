@@ -52,8 +52,10 @@ constexpr bool has_plan() {
 
 template <int D, int BK, int BV, int G, int NG>
 constexpr bool mfma_layout_ok() {
+  // G * D <= 1024: the value accumulators (G x D/8 a lane) fit a
+  // wavefront's registers (at 2048, 700+ spilled even with four wavefronts).
   return (D == 64 || D == 128 || D == 256) && has_plan<BK, D / 4>() && has_plan<BV, D / 8>() &&
-         G * NG <= 16 && (D / NG) % (D / 8) == 0;
+         G * NG <= 16 && G * D <= 1024 && (D / NG) % (D / 8) == 0;
 }
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;

@@ -55,12 +55,13 @@ def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):
     assert tqkv.decode_kernel_name(16, 8, 256, 32, 4, 4) == "mfma"  # gs32 (16 A rows)
     assert tqkv.decode_kernel_name(32, 8, 128, 32, 6, 6) == "mfma"
     assert tqkv.decode_kernel_name(16, 8, 128, 128, 8, 4) == "mfma"
-    assert tqkv.decode_kernel_name(32, 8, 256, 32, 4, 4) == "dot2"  # 32 A rows
+    assert tqkv.decode_kernel_name(32, 8, 256, 32, 4, 4) == "mfma"  # 32 A rows: 2 launches of 16
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 7, 7) == ""
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 5, 4) == ""
     assert tqkv.decode_kernel_name(20, 4, 128, 64, 4, 4) == "mfma"  # 5 heads: 5 launches of 1
     assert tqkv.decode_kernel_name(32, 2, 512, 64, 4, 4) == "tiles"  # Gemma 4 full attention
     assert tqkv.decode_kernel_name(32, 2, 128, 64, 4, 4) == "mfma"  # 16 heads: 2 launches of 8
     assert tqkv.decode_kernel_name(66, 2, 128, 64, 4, 4) == ""  # 33 heads: past the limit
+    assert tqkv.decode_kernel_name(64, 8, 256, 64, 4, 4) == "mfma"  # 8 heads: 2 MFMA launches of 4
     monkeypatch.setenv("TQKV_DECODE_KERNEL", "dot2")
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 3, 3) == "dot2"

@@ -323,6 +323,7 @@ DECODE_CASES = [
     (2, 32, 2, 128, 1500, 4, 4, 64, 0),      # 16 heads a KV head: two launches of 8
     (1, 20, 4, 128, 700, 8, 8, 64, 0),       # 5 heads a KV head: five launches of 1
     (1, 32, 1, 256, 900, 3, 3, 64, 0),       # 32 heads on one KV head
+    (2, 64, 8, 256, 900, 4, 4, 64, 0),       # 8 heads at D = 256: two MFMA launches of 4
 ]
 
 

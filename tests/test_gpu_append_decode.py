@@ -103,6 +103,7 @@ def want_of(q, K, V, gs, bk, bv, scale):
     (2, 32, 8, 128, 6, 6, 40, 2, True, 32),     # group size 32, 4 heads a KV head
     (1, 16, 8, 128, 8, 4, 70, 2, True, 128),    # group size 128
     (1, 32, 2, 128, 4, 4, 50, 2, True, 64),     # 16 heads a KV head: two launches
+    (1, 64, 8, 256, 4, 4, 60, 2, True, 64),     # 8 heads at D = 256: two MFMA launches
 ])
 def test_growing(T, B, Hq, Hkv, D, bk, bv, prefill, steps, prealloc, gs):
     assert T.decode_kernel_name(Hq, Hkv, D, gs, bk, bv) == "mfma"
