@@ -471,6 +471,11 @@ void prefill_affine_kernel(const Args a) {
   // RWO: rows between wavefronts (0 when they share the rows).
   constexpr int NT = CS ? D / 16 / kWaves : D / 16;
   constexpr int RWO = CS ? 0 : RW;
+  // Channel-split scores: each wavefront reduces its quarter of D (NDW
+  // k-steps from its own quarter of Q and K) and the four partial score
+  // tiles meet in LDS, summed in wavefront order (the same bits in every
+  // wavefront).
+  constexpr int NDW = CS ? ND / kWaves : ND;
   constexpr int KSTR = kKStride<D>, VSTR = kVStride;
   constexpr int kPer = Shape<D, H16>::kPer, kThreads = Shape<D, H16>::kThreads;
   constexpr int kBufs = Shape<D, H16>::kBufs;
@@ -479,11 +484,13 @@ void prefill_affine_kernel(const Args a) {
   // t + 1 is written after every wavefront has read tile t.
   __shared__ __attribute__((aligned(16))) uint16_t Ks2[kBufs][kTile * KSTR];
   __shared__ __attribute__((aligned(16))) uint16_t Vt2[kBufs][D * VSTR];
+  __shared__ f4_t s_part[CS ? kWaves : 1][CS ? 4 : 1][kWave];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave, lr = lane % 16, lg = lane / 16;
   const int t_base = CS ? wave * NT : 0;
+  const int s_base = CS ? wave * NDW : 0;
   // Workgroup i runs on XCD i % 8 (round-robin dispatch). Consecutive
   // logical blocks, which share a (batch row, KV head) and so its keys, are
   // placed on one XCD's L2; within a unit the longest key ranges go first.
@@ -509,7 +516,7 @@ void prefill_affine_kernel(const Args a) {
   }
 
   using op8_t = std::conditional_t<H16, h8_t, bf8_t>;
-  op8_t qf[NR][ND];
+  op8_t qf[NR][NDW];
   int64_t qabs[NR], orow[NR];
   bool rvalid[NR];
 #pragma unroll
@@ -521,9 +528,10 @@ void prefill_affine_kernel(const Args a) {
     qabs[j] = a.q_start + l;
     orow[j] = int64_t(b) * a.qs_b + (int64_t(kvh) * a.G + g) * a.qs_h + l * a.qs_l;
 #pragma unroll
-    for (int s = 0; s < ND; ++s)
+    for (int s = 0; s < NDW; ++s)
     {
-      const bf8_t x = *reinterpret_cast<const bf8_t*>(a.q + orow[j] + 32 * s + 8 * lg);
+      const bf8_t x =
+          *reinterpret_cast<const bf8_t*>(a.q + orow[j] + 32 * (s_base + s) + 8 * lg);
       if constexpr (H16) {
         // bf16 -> f16 is exact for |q| in f16's normal range.
 #pragma unroll
@@ -644,14 +652,28 @@ void prefill_affine_kernel(const Args a) {
   #pragma unroll
           for (int j = 0; j < NR; ++j) sc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
   #pragma unroll
-        for (int s = 0; s < ND; ++s)
+        for (int s = 0; s < NDW; ++s)
   #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const op8_t ka = *reinterpret_cast<const op8_t*>(Ks + (16 * i + lr) * KSTR + 32 * s + 8 * lg);
+            const op8_t ka = *reinterpret_cast<const op8_t*>(
+                Ks + (16 * i + lr) * KSTR + 32 * (s_base + s) + 8 * lg);
   #pragma unroll
             for (int j = 0; j < NR; ++j)
               sc[i][j] = mma<H16>(ka, qf[j][s], sc[i][j]);
           }
+        if constexpr (CS) {
+          // Every wavefront of the block is live here (they share the rows).
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) s_part[wave][i][lane] = sc[i][0];
+          __syncthreads();
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            f4_t tot = s_part[0][i][lane];
+  #pragma unroll
+            for (int w = 1; w < kWaves; ++w) tot += s_part[w][i][lane];
+            sc[i][0] = tot;
+          }
+        }
 
         // Mask: only on tiles some row of the block sees in part. Key offset
         // o in the tile is visible to a row iff lo <= o <= hi.
