@@ -18,8 +18,8 @@
 // effective under a causal or sliding mask).
 //
 // Per key tile (64 keys): the workgroup's threads each take one run of 32
-// codes of one key (bits words) for K and for V, dequantize it and write K
-// row-major [key][D] and V transposed [D][key] into LDS; the next tile's
+// codes of one key (bits words) for K and for V, dequantize it and write
+// both row-major [key][D] into LDS; the next tile's
 // words are fetched into registers while the matrix cores work on this one.
 // Each wavefront owns RW query rows:
 //   S^T = K . Q^T: A = K rows from LDS (ds_read_b128), B = the wavefront's Q
@@ -33,7 +33,9 @@
 //   O^T += V^T . P^T: the score registers of key tiles 2u and 2u + 1 are,
 //   rounded to bf16, exactly the B operand (k slot 8(l / 16) + s holds key
 //   32u + 4(l / 16) + s, s < 4, or 32u + 16 + 4(l / 16) + s - 4); the A
-//   operand reads the same keys of V^T with two ds_read_b64.
+//   operand takes the same keys of V^T from the row-major V tile with two
+//   transposing ds_read_b64_tr_b16 (the V stores are four 16-byte stores a
+//   run, where a transposed tile took 32 two-byte stores).
 // Only tiles that some row of the block can see are visited, and the
 // per-element mask runs only on tiles that are not wholly visible.
 #pragma once
@@ -50,13 +52,12 @@ namespace prefill {
 constexpr int kWave = 64;
 constexpr int kTile = 64;  // keys per tile
 constexpr int kXcds = 8;   // accelerator dies (each with its own L2) on MI355X
-// LDS row strides (bf16 elements). K rows: D + 8 keeps ds_read_b128 rows
-// 16-byte aligned and 8 consecutive rows on distinct banks. V^T rows:
-// kTile + 4 = 34 dwords, so the 16 rows one ds_read_b64 touches start on
-// distinct even banks.
+// LDS row stride (bf16 elements) of the K and V tiles, both row-major
+// [key][D]: D + 8 keeps ds_read_b128 rows 16-byte aligned and 8
+// consecutive rows on distinct banks.
 template <int D>
 constexpr int kKStride = D + 8;
-constexpr int kVStride = kTile + 4;
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kTau = 8.0f;
 
@@ -386,24 +387,13 @@ __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int k
   for (int i = 0; i < 4; ++i) d[i] = u32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
 }
 
-// Writes a V task into column `key` of V^T, channels [32 run, 32 run + 32).
-// Keys past the end are zero (0 * v stays finite).
+// Writes a V task into LDS like a K task: row `key` of V, channels
+// [32 run, 32 run + 32), four 16-byte stores. The products read V^T from it
+// with gfx950's transposing ds_read_b64_tr_b16. Keys past the end are zero
+// (0 * v stays finite).
 template <int D, int BITS, bool H16, int NW>
-__device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vt, int key, int run) {
-  constexpr int VSTR = kVStride;
-  uint32_t v[16];
-  if (st.ok) {
-    dequant_run<BITS, H16>(st.w, st.s | (st.b << 16), v);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = 0u;
-  }
-  uint16_t* d = Vt + (run * 32) * VSTR + key;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    d[(2 * i) * VSTR] = uint16_t(v[i]);
-    d[(2 * i + 1) * VSTR] = uint16_t(v[i] >> 16);
-  }
+__device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vs, int key, int run) {
+  store_k<D, BITS, H16>(st, Vs, key, run);
 }
 
 // The V tasks' stage registers: their own set, or the K tasks' set.
@@ -422,6 +412,16 @@ __device__ __forceinline__ f4_t mma(V a, V b, f4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   else
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// gfx950's transposing LDS read: the 16 lanes of a group each name 4
+// consecutive 16-bit values of a 4 x 16 block (lane i: row i / 4, columns
+// 4 (i % 4) + [0, 4)); lane i receives column i of the block's 4 rows.
+typedef short s4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2_t tr_read(const uint16_t* p) {
+  const s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4_t*)(p));
+  return __builtin_bit_cast(u32x2_t, v);
 }
 
 // acc + both halves of a packed pair (v_dot2 against a (1, 1) splat).
@@ -476,14 +476,14 @@ void prefill_affine_kernel(const Args a) {
   // tiles meet in LDS, summed in wavefront order (the same bits in every
   // wavefront).
   constexpr int NDW = CS ? ND / kWaves : ND;
-  constexpr int KSTR = kKStride<D>, VSTR = kVStride;
+  constexpr int KSTR = kKStride<D>;
   constexpr int kPer = Shape<D, H16>::kPer, kThreads = Shape<D, H16>::kThreads;
   constexpr int kBufs = Shape<D, H16>::kBufs;
   // Two tile buffers: tile t is read from one while tile t + 1 is written
   // into the other, so a tile costs one barrier. One buffer (D = 512): tile
   // t + 1 is written after every wavefront has read tile t.
   __shared__ __attribute__((aligned(16))) uint16_t Ks2[kBufs][kTile * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt2[kBufs][D * VSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt2[kBufs][kTile * KSTR];
   __shared__ f4_t s_part[CS ? kWaves : 1][CS ? 4 : 1][kWave];
 
   const int tid = threadIdx.x;
@@ -747,9 +747,15 @@ void prefill_affine_kernel(const Args a) {
           }
   #pragma unroll
           for (int t2 = 0; t2 < NT; ++t2) {
-            const uint16_t* vrow = Vt + (16 * (t_base + t2) + lr) * VSTR + 32 * u + 4 * lg;
-            const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vrow);
-            const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vrow + 16);
+            // Lane lr of group lg supplies row 32u + 4lg + lr/4 and channels
+            // 16 tt + 4(lr % 4) + [0, 4); the transposing read hands it
+            // channel 16 tt + lr of keys 32u + 4lg + [0, 4) (and + 16 for
+            // the second read): the A operand of V^T for the k slots the
+            // score registers fill.
+            const uint16_t* vrow = Vt + (32 * u + 4 * lg + lr / 4) * KSTR +
+                                   16 * (t_base + t2) + 4 * (lr % 4);
+            const u32x2_t lo = tr_read(vrow);
+            const u32x2_t hi = tr_read(vrow + 16 * KSTR);
             const op8_t va = __builtin_bit_cast(op8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
   #pragma unroll
             for (int j = 0; j < NR; ++j)
