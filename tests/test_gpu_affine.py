@@ -216,14 +216,35 @@ def test_quantize_rejects_bad_layouts(T):
     assert e.value.status == T.EINVAL_SHAPE
 
 
-def test_dequantize_bit_exact(T):
-    x = kv_bf16((2, 40, 256), 9, frac=0.01, mult=10.0)
-    wpk, wsc, wbi = O.affine_quantize(x, 64, 3)
-    out = T.DeviceArray((2, 40, 256), np.uint16)
+@pytest.mark.parametrize("dim,gs,bits,rows", [
+    (256, 64, 3, 80), (128, 64, 4, 77), (128, 32, 2, 9), (64, 64, 5, 33), (256, 128, 6, 21),
+    (512, 64, 8, 7), (32, 32, 3, 101), (1024, 128, 5, 3), (128, 128, 6, 65)])
+def test_dequantize_bit_exact(T, dim, gs, bits, rows):
+    """Eight values a thread (16-byte aligned output) against the oracle's
+    mlx::dequantize, at every width and 32-1024 channels."""
+    x = kv_bf16((1, rows, dim), 9 + bits, frac=0.01, mult=10.0)
+    wpk, wsc, wbi = O.affine_quantize(x, gs, bits)
+    out = T.DeviceArray((1, rows, dim), np.uint16)
     pk, sc, bi = T.DeviceArray.of(wpk), T.DeviceArray.of(wsc), T.DeviceArray.of(wbi)
-    T.affine_dequantize(pk.ptr, sc.ptr, bi.ptr, 80, 256, 64, 3, out.ptr)
+    T.affine_dequantize(pk.ptr, sc.ptr, bi.ptr, rows, dim, gs, bits, out.ptr)
     T.hip().sync()
-    assert np.array_equal(out.numpy(), O.affine_dequantize(wpk, wsc, wbi, 64, 3))
+    assert np.array_equal(out.numpy(), O.affine_dequantize(wpk, wsc, wbi, gs, bits))
+
+
+def test_dequantize_unaligned_output(T):
+    """An output one bf16 past a 16-byte boundary takes the one-value path:
+    the same bits, nothing written outside the rows."""
+    rows, dim, gs, bits = 19, 128, 64, 3
+    x = kv_bf16((1, rows, dim), 31, frac=0.01, mult=10.0)
+    wpk, wsc, wbi = O.affine_quantize(x, gs, bits)
+    buf = T.DeviceArray.of(np.full(rows * dim + 16, 0x7777, np.uint16))
+    pk, sc, bi = T.DeviceArray.of(wpk), T.DeviceArray.of(wsc), T.DeviceArray.of(wbi)
+    T.affine_dequantize(pk.ptr, sc.ptr, bi.ptr, rows, dim, gs, bits, buf.ptr + 2)
+    T.hip().sync()
+    got = buf.numpy()
+    want = O.affine_dequantize(wpk, wsc, wbi, gs, bits).reshape(-1)
+    assert np.array_equal(got[1:1 + rows * dim], want)
+    assert got[0] == 0x7777 and np.all(got[1 + rows * dim:] == 0x7777)
 
 
 # ------------------------------------------------------------------ decode
