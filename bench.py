@@ -50,13 +50,14 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget for the baseline sample")
     ap.add_argument("--workload", choices=("decode", "prefill", "append", "decode1", "prefix",
-                                           "layers", "sparse"), default="decode",
+                                           "layers", "sparse", "codebook"), default="decode",
                     help="decode: config 2 (the headline); prefill: config 3's 2048-token "
                          "chunk attention; append: config 0's quantize round trip (affine, "
                          "affine+rotation, TurboQuant codebook); decode1: config 1's "
                          "single-sequence decode; layers: config 3's 30-layer stack (chunked "
                          "prefill, then decode steps); prefix: config 4's shared-prefix decode; "
-                         "sparse: config 2's shape with page-sparse decode")
+                         "sparse: config 2's shape with page-sparse decode; codebook: config "
+                         "2's shape over a TurboQuant codebook cache")
     ap.add_argument("--two-launch", action="store_true",
                     help="decode steps append with the quantize kernel and then attend (two "
                          "launches) instead of the decode kernel quantizing the new token "
@@ -81,7 +82,8 @@ def main():
     hip = T.hip()
     hip._ok(hip.h.hipSetDevice(0), "hipSetDevice")
     others = {"prefill": prefill_main, "append": append_main, "decode1": decode1_main,
-              "prefix": prefix_main, "layers": layers_main, "sparse": sparse_main}
+              "prefix": prefix_main, "layers": layers_main, "sparse": sparse_main,
+              "codebook": codebook_main}
     if args.workload in others:
         others[args.workload](T, hip, args)
         return
@@ -943,6 +945,63 @@ def sparse_main(T, hip, args):
              "page bounds + select + decode_mfma_kernel<256,3,3,2,4,8,paged>", alg_b, att_ms),
         {"digest_ms_once": round(digest_ms, 4), "dense_bytes_per_step": int(dense_b),
          "dense_equivalent_gbps": round(dense_b / (att_ms * 1e-3) / 1e9, 1)}, settle, steps)
+    print(json.dumps(result))
+
+
+def codebook_main(T, hip, args):
+    """Config 2's shape (B=32, 16 / 8 heads, D=256, 32,768-token context) over
+    a TurboQuant codebook cache (the GPU TurboQuant caches' attention,
+    turboquant.rs:763-923): 3-bit Lloyd-Max codes as one byte each plus an
+    f32 sigma a vector, for K and V, stored rotated. A step is one
+    tqkv_decode_attend_codebook call (query rotated, attention over
+    centroid * sigma, output rotated back). Not the headline metric (a
+    different cache format): reported beside it. Bytes: the codes and sigmas
+    of K and V, Q, O and R."""
+    B, H, HKV, D, N, BITS = 32, 16, 8, 256, args.context, 3
+    stream = hip.stream()
+    slabs = B * HKV
+    settle = 32 if args.settle is None else max(0, args.settle)
+    steps = 50 if args.steps is None else args.steps
+    rng = np.random.default_rng(7)
+    codes = {}
+    sigmas = {}
+    for name in ("k", "v"):
+        c = T.DeviceArray((slabs, N, D), np.uint8)
+        one = rng.integers(0, 1 << BITS, size=(N, D), dtype=np.uint8)
+        for sl in range(slabs):  # one slab's codes, rolled per slab
+            hip.copy_in(c.ptr + sl * N * D, np.roll(one, sl, axis=0))
+        codes[name] = c
+        sigmas[name] = T.DeviceArray.of(
+            rng.uniform(0.5, 2.0, size=(slabs, N)).astype(np.float32))
+    cent = T.DeviceArray.of(T.lloyd_max(BITS)[1].astype(np.float32))
+    R = T.DeviceArray.of(T.rotation_matrix(D, 42))
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.synth_bf16(q.ptr, B * H, D, 33, 0.0, 1.0, stream)
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    wsb = T.decode_codebook_workspace_size(B, H, D, N)
+    ws = T.DeviceArray((wsb,), np.uint8)
+
+    def call():
+        T.decode_attend_codebook(q.ptr, B, H, HKV, D, D ** -0.5, R.ptr, cent.ptr, BITS, cent.ptr,
+                                 BITS, codes["k"].ptr, sigmas["k"].ptr, codes["v"].ptr,
+                                 sigmas["v"].ptr, N, N, out.ptr, ws.ptr, wsb, stream)
+
+    for _ in range(settle + args.warmup):
+        call()
+    hip.sync()
+    ms = _loop_ms(hip, stream, call, steps)
+    o = (out.numpy().astype(np.uint32) << 16).view(np.float32)
+    assert np.all(np.isfinite(o)) and np.abs(o).max() > 0, "codebook output is not sane"
+    alg = 2 * slabs * N * (D + 4) + 2 * B * H * D * 2 + D * D * 4
+    result = _line(
+        "codebook-cache decode tokens/s @ B=32, 32K ctx", B / (ms * 1e-3), "tokens/s", ms, args,
+        "bf16 in/out, f32 arithmetic",
+        {"workload": "config 2's shape (B=32, 16/8 heads, D=256, 32K context) over a TurboQuant "
+                     "codebook cache: 3-bit Lloyd-Max codes (u8) + f32 sigma, K and V rotated",
+         "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "context": N,
+         "bits_k": BITS, "bits_v": BITS},
+        _hbm(alg / (ms * 1e-3) / 1e9, "one call: cb_rotate_q_kernel + cb_decode_kernel<256,2,false> + cb_merge_kernel", alg, ms),
+        {"workspace_bytes": wsb}, settle, steps)
     print(json.dumps(result))
 
 

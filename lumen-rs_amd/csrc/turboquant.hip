@@ -1009,14 +1009,21 @@ namespace {
 
 constexpr int kCbTile = 64;  // tokens per step of a wavefront
 
-// q_rot[b, h, :] = R q[b, h, :] in f32.
+// q_rot[b, h, :] = R q[b, h, :] in f32. A wavefront takes one output at a
+// time: its lanes read row i of R (coalesced) against the query, then sum
+// across the lanes. blockDim: a multiple of 64.
 __global__ void cb_rotate_q_kernel(const uint16_t* __restrict__ q, const float* __restrict__ R,
                                    int D, float* __restrict__ qr) {
   const int64_t bh = blockIdx.x;
-  for (int i = threadIdx.x; i < D; i += blockDim.x) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  for (int i = wave; i < D; i += waves) {
     float acc = 0.0f;
-    for (int j = 0; j < D; ++j) acc = fmaf(R[int64_t(i) * D + j], bf16_to_f32(q[bh * D + j]), acc);
-    qr[bh * D + i] = acc;
+    for (int j = lane; j < D; j += kWave)
+      acc = fmaf(R[int64_t(i) * D + j], bf16_to_f32(q[bh * D + j]), acc);
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (lane == 0) qr[bh * D + i] = acc;
   }
 }
 
@@ -1095,6 +1102,19 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
 #pragma unroll
     for (int k = 0; k < PER; ++k) acc[h][k] = 0.0f;
   }
+  // D <= 256: the lane's key row of the next tile loads while this tile's
+  // softmax and values run (16 B a load, D / 16 registers of 4 words).
+  constexpr bool kAhead = D <= 256;
+  constexpr int KW = kAhead ? D / 16 : 1;
+  uint4 kn[KW];
+  auto load_keys = [&](int64_t at) {
+    if (at < t1) {
+      const uint8_t* row = kc + (slab + at) * D;
+#pragma unroll
+      for (int i = 0; i < KW; ++i) kn[i] = *reinterpret_cast<const uint4*>(row + 16 * i);
+    }
+  };
+  if constexpr (kAhead) load_keys(t0 + lane);
   for (int64_t base = t0; base < t1; base += kCbTile) {
     const int64_t t = base + lane;
     const bool valid = t < t1;
@@ -1103,8 +1123,9 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     for (int h = 0; h < G; ++h) sc[h] = 0.0f;
     if (valid) {
       const uint8_t* row = kc + (slab + t) * D;
+#pragma unroll(kAhead ? D / 16 : 1)
       for (int d = 0; d < D; d += 16) {
-        const uint4 w = *reinterpret_cast<const uint4*>(row + d);
+        const uint4 w = kAhead ? kn[d / 16] : *reinterpret_cast<const uint4*>(row + d);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
@@ -1142,6 +1163,7 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
         }
       }
     }
+    if constexpr (kAhead) load_keys(t + kCbTile);  // this tile's keys are scored
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float mx = valid ? sc[h] : -INFINITY;

@@ -127,6 +127,9 @@ _SIGS = {
     "tqkv_tq_scores_two_stage": (I32, [P, P, P, P, P, P, P, I32, I32, I64, P, P]),
     "tqkv_qjl_encode_stage2": (I32, [P, P, P, I64, I32, I32, P, P, P]),
     "tqkv_qjl_apply_correction": (I32, [P, P, P, P, I64, I32, I32, P, P]),
+    "tqkv_decode_attend_codebook": (I32, [P, I32, I32, I32, I32, F32, P, P, I32, P, I32, P, P,
+                                          P, P, I64, I64, P, P, SZ, P]),
+    "tqkv_decode_codebook_workspace_size": (SZ, [I32, I32, I32, I64]),
     "tqkv_decode_attend_codebook_qjl": (I32, [P, I32, I32, I32, I32, F32, P, P, I32, P, I32, P, P,
                                               P, P, P, I32, P, P, I64, I64, P, P, SZ, P]),
     "tqkv_tq_values": (I32, [P, P, P, P, P, I32, I64, P, P]),
@@ -687,6 +690,19 @@ def tq_encode(x, x_is_bf16, n_slabs, s, dim, R, bnd, cent, bits, phi, m, codes, 
     check(lib().tqkv_tq_encode(x, int(x_is_bf16), n_slabs, s, dim, R, bnd, cent, bits, phi, m,
                                codes, sigma, signs, rnorm, s if dst_cap is None else dst_cap,
                                dst_start, stream))
+
+
+def decode_attend_codebook(q, B, H, H_kv, D, scale, rotation, cent_k, bits_k, cent_v, bits_v,
+                           k_codes, k_sigma, v_codes, v_sigma, cap, n, out, workspace=None,
+                           workspace_bytes=0, stream=None):
+    """Fused decode attention over a codebook cache; device pointers."""
+    check(lib().tqkv_decode_attend_codebook(q, B, H, H_kv, D, scale, rotation, cent_k, bits_k,
+                                            cent_v, bits_v, k_codes, k_sigma, v_codes, v_sigma,
+                                            cap, n, out, workspace, workspace_bytes, stream))
+
+
+def decode_codebook_workspace_size(B, H, D, total_tokens):
+    return int(lib().tqkv_decode_codebook_workspace_size(B, H, D, total_tokens))
 
 
 def codebook_dequantize(codes, sigma, centroids, bits, rows, dim, out, stream=None):
