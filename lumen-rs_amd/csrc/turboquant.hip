@@ -1009,21 +1009,27 @@ namespace {
 
 constexpr int kCbTile = 64;  // tokens per step of a wavefront
 
-// q_rot[b, h, :] = R q[b, h, :] in f32. A wavefront takes one output at a
-// time: its lanes read row i of R (coalesced) against the query, then sum
-// across the lanes. blockDim: a multiple of 64.
+// q_rot[b, h, :] = R q[b, h, :] in f32. A wavefront takes four outputs at
+// a time: its lanes read rows i of R (coalesced) against the query, then sum
+// across the lanes. blockDim: a multiple of 64 with D a multiple of 4 x its
+// wavefronts.
 __global__ void cb_rotate_q_kernel(const uint16_t* __restrict__ q, const float* __restrict__ R,
                                    int D, float* __restrict__ qr) {
   const int64_t bh = blockIdx.x;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int waves = blockDim.x / kWave;
-  for (int i = wave; i < D; i += waves) {
-    float acc = 0.0f;
-    for (int j = lane; j < D; j += kWave)
-      acc = fmaf(R[int64_t(i) * D + j], bf16_to_f32(q[bh * D + j]), acc);
+  for (int i0 = 4 * wave; i0 < D; i0 += 4 * waves) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = lane; j < D; j += kWave) {
+      const float x = bf16_to_f32(q[bh * D + j]);
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
-    if (lane == 0) qr[bh * D + i] = acc;
+      for (int r = 0; r < 4; ++r) acc[r] = fmaf(R[int64_t(i0 + r) * D + j], x, acc[r]);
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += __shfl_xor(acc[r], off, kWave);
+    if (lane < 4) qr[bh * D + i0 + lane] = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
   }
 }
 
@@ -1123,7 +1129,7 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     for (int h = 0; h < G; ++h) sc[h] = 0.0f;
     if (valid) {
       const uint8_t* row = kc + (slab + t) * D;
-#pragma unroll(kAhead ? D / 16 : 1)
+#pragma unroll KW
       for (int d = 0; d < D; d += 16) {
         const uint4 w = kAhead ? kn[d / 16] : *reinterpret_cast<const uint4*>(row + d);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -1218,18 +1224,26 @@ __global__ void cb_merge_kernel(const float* __restrict__ part_o, const float* _
   const float* pl = part_l + bh * n_splits;
   float mx = -INFINITY;
   for (int s = 0; s < n_splits; ++s) mx = fmaxf(mx, pm[s]);
+  // Each split's weight once (the same exp2f of the same argument as a
+  // per-element evaluation; empty splits are skipped by their max).
+  float* s_w = s_o + D;
+  for (int s = threadIdx.x; s < n_splits; s += blockDim.x)
+    s_w[s] = pm[s] != -INFINITY ? exp2f(pm[s] - mx) : 0.0f;
+  __syncthreads();
   float ls = 0.0f;
   for (int s = 0; s < n_splits; ++s)
-    if (pm[s] != -INFINITY) ls += pl[s] * exp2f(pm[s] - mx);
+    if (pm[s] != -INFINITY) ls += pl[s] * s_w[s];
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float os = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < n_splits; ++s)
-      if (pm[s] != -INFINITY) os += part_o[(bh * n_splits + s) * D + d] * exp2f(pm[s] - mx);
+      if (pm[s] != -INFINITY) os += part_o[(bh * n_splits + s) * D + d] * s_w[s];
     s_o[d] = ls > 0.0f ? os / ls : 0.0f;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < D; i += blockDim.x) {
     float acc = 0.0f;
+#pragma unroll 8
     for (int j = 0; j < D; ++j) acc = fmaf(R[int64_t(j) * D + i], s_o[j], acc);
     out[bh * D + i] = f32_to_bf16(acc);
   }
@@ -1406,7 +1420,8 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
   }
   if (rc) return rc;
   hipLaunchKernelGGL(tq::cb_merge_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256),
-                     size_t(D) * sizeof(float), st, po, pm, pl, n_splits, D, rotation, out);
+                     size_t(D + n_splits) * sizeof(float), st, po, pm, pl, n_splits, D, rotation,
+                     out);
   TQKV_LAUNCHED();
   return ok();
 }
