@@ -344,3 +344,41 @@ def test_codebook_cache_append_and_decode(T, bits, qjl_words):
     cos = (got.ravel() @ orig.ravel()) / (np.linalg.norm(got) * np.linalg.norm(orig))
     print(f"[codebook-decode] cos_vs_unquantized={cos:.4f}", flush=True)
     assert cos > {8: 0.995, 4: 0.9, 3: 0.85}[bits]
+
+
+@pytest.mark.parametrize("B,Hkv,G,D,N,bits", [(16, 8, 2, 128, 2100, 3), (32, 4, 4, 64, 1500, 4),
+                                              (2, 4, 2, 256, 1300, 3)])
+def test_codebook_decode_direct(T, B, Hkv, G, D, N, bits):
+    """tqkv_decode_attend_codebook on codes and sigmas it is handed, against
+    f64 attention over centroid * sigma in the rotated basis, rotated back;
+    128 or more (batch row, KV head) units take 1024-token splits, fewer take
+    512."""
+    H = G * Hkv
+    rng = np.random.default_rng(B * 1000 + D + bits)
+    kc = rng.integers(0, 1 << bits, size=(B, Hkv, N, D), dtype=np.uint8)
+    vc = rng.integers(0, 1 << bits, size=(B, Hkv, N, D), dtype=np.uint8)
+    ks = rng.uniform(0.5, 2.0, size=(B, Hkv, N)).astype(np.float32)
+    vs = rng.uniform(0.5, 2.0, size=(B, Hkv, N)).astype(np.float32)
+    q = kv_bf16((B, H, 1, D), 71 + D)
+    R = T.rotation_matrix(D, 42)
+    _, cent = T.lloyd_max(bits)
+    cf = cent.astype(np.float32)
+    d = {n: T.DeviceArray.of(a) for n, a in
+         dict(q=q, kc=kc, vc=vc, ks=ks, vs=vs, R=R, c=cf).items()}
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    wsb = T.decode_codebook_workspace_size(B, H, D, N)
+    ws = T.DeviceArray((wsb,), np.uint8)
+    T.decode_attend_codebook(d["q"].ptr, B, H, Hkv, D, D ** -0.5, d["R"].ptr, d["c"].ptr, bits,
+                             d["c"].ptr, bits, d["kc"].ptr, d["ks"].ptr, d["vc"].ptr, d["vs"].ptr,
+                             N, N, out.ptr, ws.ptr, wsb)
+    T.hip().sync()
+    c64 = cf.astype(np.float64)
+    Kr = c64[kc] * ks[..., None]
+    Vr = c64[vc] * vs[..., None]
+    qr = O.bf16_to_f32(q).reshape(B, H, D).astype(np.float64) @ R.astype(np.float64).T
+    want = attention_f64(qr, Kr, Vr, D ** -0.5, G) @ R.astype(np.float64)
+    got = O.bf16_to_f32(out.numpy()).reshape(B, H, D)
+    err = np.abs(got - want)
+    print(f"[codebook-direct] B={B} Hkv={Hkv} D={D} max_abs={err.max():.3e} "
+          f"mean_abs={err.mean():.3e}", flush=True)
+    assert err.max() <= 2e-2 and err.mean() <= 1e-3
