@@ -314,8 +314,10 @@ const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t D, int32_t 
  * the query is rotated, attention runs over centroid[c] * sigma in the
  * rotated basis, and the output returns through R^T. rotation f32 [D, D],
  * centroids f32 [2^bits] (device). D in {64, 128, 256, 512}; H / H_kv in
- * {1, 2, 4, 8, 16}. workspace: tqkv_decode_codebook_workspace_size() bytes, or
- * NULL for the library's per-device buffer.
+ * {1, 2, 4, 8, 16}. v_codes 4-byte aligned at D >= 256, 2-byte at D = 128
+ * (TQKV_EINVAL_ARG otherwise). workspace:
+ * tqkv_decode_codebook_workspace_size() bytes, or NULL for the library's
+ * per-device buffer.
  */
 int32_t tqkv_decode_attend_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv,
                                     int32_t D, float scale, const float* rotation,

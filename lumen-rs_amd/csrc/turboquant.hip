@@ -1062,7 +1062,7 @@ constexpr int kMaxQjl = 1024;
 
 // One workgroup of one wavefront per (split, KV head, batch row): partial
 // softmax state over its tokens for the G query heads. Scores: lane = token;
-// values: lane = channels (D / 64 each). QJL: each key's score gains the
+// values: lane = D / 64 consecutive channels. QJL: each key's score gains the
 // QJL estimate of q . r from its residual signs (estimate_correction,
 // qjl.rs:86-118; the two-stage scores of compressor.rs:122-159), with the
 // query's projection in LDS.
@@ -1189,12 +1189,24 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
       s_p[h][lane] = valid ? p * vs[slab + t] : 0.0f;
     }
     __syncthreads();
+    // Values: lane takes channels PER * lane .. + PER - 1 (one PER-byte load
+    // of each token's row; the wavefront reads the row whole).
     const int cnt = int(t1 - base < kCbTile ? t1 - base : kCbTile);
+    const uint8_t* vrow = vc + (slab + base) * D + PER * lane;
     for (int j = 0; j < cnt; ++j) {
-      const uint8_t* row = vc + (slab + base + j) * D;
+      uint32_t cw[(PER + 3) / 4];
+      if constexpr (PER == 1) {
+        cw[0] = vrow[int64_t(j) * D];
+      } else if constexpr (PER == 2) {
+        cw[0] = *reinterpret_cast<const uint16_t*>(vrow + int64_t(j) * D);
+      } else {
+#pragma unroll
+        for (int w = 0; w < PER / 4; ++w)
+          cw[w] = *reinterpret_cast<const uint32_t*>(vrow + int64_t(j) * D + 4 * w);
+      }
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
-        const float c = s_cv[row[lane + k * kWave]];
+        const float c = s_cv[(cw[k / 4] >> (8 * (k % 4))) & 0xffu];
 #pragma unroll
         for (int h = 0; h < G; ++h) acc[h][k] = fmaf(s_p[h][j], c, acc[h][k]);
       }
@@ -1205,7 +1217,7 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
   for (int h = 0; h < G; ++h) {
     const int64_t row = (int64_t(b) * H + kvh * G + h) * n_splits + split;
 #pragma unroll
-    for (int k = 0; k < PER; ++k) part_o[row * D + lane + k * kWave] = acc[h][k];
+    for (int k = 0; k < PER; ++k) part_o[row * D + PER * lane + k] = acc[h][k];
     if (lane == 0) {
       part_m[row] = m[h];
       part_l[row] = l[h];
@@ -1378,6 +1390,10 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
                 (long long)cap);
   if (bits_k < 1 || bits_k > 8 || bits_v < 1 || bits_v > 8)
     return fail(TQKV_EUNSUPPORTED, "bits %d/%d", bits_k, bits_v);
+  // A lane loads D / 64 value codes at once (up to 4-byte words).
+  const int v_align = D >= 256 ? 4 : D >= 128 ? 2 : 1;
+  if (reinterpret_cast<uintptr_t>(v_codes) % v_align != 0)
+    return fail(TQKV_EINVAL_ARG, "v_codes must be %d-byte aligned", v_align);
   const int G = H / H_kv;
   // Splits of 512 tokens (at most 64); with 128 or more (batch row, KV head)
   // units the grid fills the chip with splits of 1024 (at most 32), which

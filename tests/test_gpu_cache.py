@@ -382,3 +382,19 @@ def test_codebook_decode_direct(T, B, Hkv, G, D, N, bits):
     print(f"[codebook-direct] B={B} Hkv={Hkv} D={D} max_abs={err.max():.3e} "
           f"mean_abs={err.mean():.3e}", flush=True)
     assert err.max() <= 2e-2 and err.mean() <= 1e-3
+
+
+def test_codebook_decode_rejects_unaligned_values(T):
+    """A lane loads its value codes 4 bytes at a time at D = 256: a value
+    code pointer off that alignment is refused before any launch."""
+    B, Hkv, H, D, N = 1, 1, 2, 256, 64
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    codes = T.DeviceArray((N * D + 4,), np.uint8)
+    sig = T.DeviceArray((N,), np.float32)
+    R = T.DeviceArray.of(T.rotation_matrix(D, 42))
+    cent = T.DeviceArray.of(T.lloyd_max(3)[1].astype(np.float32))
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    with pytest.raises(T.TqkvError) as e:
+        T.decode_attend_codebook(q.ptr, B, H, Hkv, D, 1.0, R.ptr, cent.ptr, 3, cent.ptr, 3,
+                                 codes.ptr, sig.ptr, codes.ptr + 1, sig.ptr, N, N, out.ptr)
+    assert e.value.status == T.EINVAL_ARG
