@@ -564,9 +564,30 @@ def append_main(T, hip, args):
             T.tq_encode(x[n].ptr, True, slabs, S, D, R.ptr, dbnd.ptr, dcen.ptr, BITS, phi.ptr, M,
                         codes[n].ptr, sig[n].ptr, sgn[n].ptr, rn[n].ptr, stream=stream)
 
+    # The reference GPU cache's encode (mode 1: y = bf16(x R), its default
+    # for K and V), the codebook rows back to bf16 (the codebook cache's
+    # prefill), and the codes packed into stage1_packed u64 words.
+    inner = T.DeviceArray.of(np.asarray(bnd[1:-1]).astype(np.float32))
+    pw = T.packed_words(D, BITS)
+    packed = {n: T.DeviceArray((slabs * S, pw), np.uint64) for n in ("k", "v")}
+
+    def tq_gpu():
+        for n in ("k", "v"):
+            T.tq_encode_gpu_path(x[n].ptr, slabs, S, D, R.ptr, 1, False, inner.ptr, BITS,
+                                 codes[n].ptr, sig[n].ptr, stream=stream)
+
+    def cb_deq():
+        for n in ("k", "v"):
+            T.codebook_dequantize(codes[n].ptr, sig[n].ptr, dcen.ptr, BITS, slabs * S, D,
+                                  deq[n].ptr, stream)
+
+    def pack():
+        for n in ("k", "v"):
+            T.pack_codes(codes[n].ptr, slabs * S, D, BITS, packed[n].ptr, stream)
+
     settle = 16 if args.settle is None else max(0, args.settle)
     for _ in range(settle + args.warmup):
-        quant(), dequant(), rotq(), rotq_k(), rotq_two(), tq()
+        quant(), dequant(), rotq(), rotq_k(), rotq_two(), tq(), tq_gpu(), cb_deq(), pack()
     hip.sync()
     n = args.steps
     ms_q = _loop_ms(hip, stream, quant, n)
@@ -576,6 +597,11 @@ def append_main(T, hip, args):
     ms_r2 = _loop_ms(hip, stream, rotq_two, n)
     rot_flop = 2 * slabs * S * D * D  # K only: V is not rotated (gemma4_moe.rs:4154-4173)
     ms_t = _loop_ms(hip, stream, tq, max(3, n // 5))
+    ms_g = _loop_ms(hip, stream, tq_gpu, n)
+    ms_c = _loop_ms(hip, stream, cb_deq, n)
+    ms_p = _loop_ms(hip, stream, pack, n)
+    cb_bytes = 2 * slabs * S * (D + 4)  # u8 codes + f32 sigma, K and V
+    pk_bytes = 2 * slabs * S * (D + pw * 8)
     in_bytes = 2 * slabs * S * D * 2
     q_bytes = 2 * slabs * S * (words * 4 + 2 * groups * 2)
     tq_bytes = 2 * slabs * S * (D + 4 + M // 8 + 4)
@@ -612,7 +638,21 @@ def append_main(T, hip, args):
                                "bytes": in_bytes + tq_bytes, "qjl_m": M,
                                "note": "compress_one restated bit-exactly: sequential f32 "
                                        "sums, four lanes per vector, R and Phi from LDS; "
-                                       "VALU-bound (unfused mul + add)"}},
+                                       "VALU-bound (unfused mul + add)"},
+         "turboquant_encode_gpu_path": {
+             "ms": round(ms_g, 5), "tokens_per_s": round(S / (ms_g * 1e-3), 1),
+             "bytes": in_bytes + cb_bytes,
+             "gbps": round((in_bytes + cb_bytes) / (ms_g * 1e-3) / 1e9, 1),
+             "note": "tqkv_tq_encode_gpu_path mode 1 (y = bf16(x R), sigma, bf16(y / sigma) "
+                     "against f32 inner boundaries), K and V"},
+         "codebook_dequantize": {
+             "ms": round(ms_c, 5), "bytes": cb_bytes + in_bytes,
+             "gbps": round((cb_bytes + in_bytes) / (ms_c * 1e-3) / 1e9, 1),
+             "note": "tqkv_codebook_dequantize: bf16(centroid * sigma) rows of K and V"},
+         "pack_codes": {
+             "ms": round(ms_p, 5), "bytes": pk_bytes,
+             "gbps": round(pk_bytes / (ms_p * 1e-3) / 1e9, 1),
+             "note": "tqkv_pack_codes: u8 codes of K and V to stage1_packed u64 words"}},
         settle)
     if not args.no_cpu_baseline:
         O, threads = _oracle()

@@ -623,59 +623,74 @@ __global__ void tq_values_kernel(const float* __restrict__ R, Codes code,
 // rotate_and_lloyd_max_quantize_stage1_fused, :720-745), M = R or R^T
 // (transpose). sigma = sqrt(sum y^2 / D); code = the number of inner
 // boundaries b (ascending, f32) with b <= bf16(y / sigma) (the level scan of
-// lloyd_max_boundaries_inner, :310-331). One wavefront per row, lane l
-// holding channels l + 64 k: the rotation is tq_rotate_rows_kernel's fmaf
-// chain over j from 0.0; the sum of squares runs over k in each lane, then
-// over the lanes by an xor butterfly 32, 16, ..., 1 (MLX's own reduction
-// order is not in the reference; this one is fixed, and the oracle
-// restates it).
+// lloyd_max_boundaries_inner, :310-331). One wavefront per kEncRows rows,
+// lane l holding channels l + 64 k of each (each load of M serves them
+// all): the rotation is tq_rotate_rows_kernel's fmaf chain over j from 0.0;
+// the sum of squares runs over k in each lane, then over the lanes by an
+// xor butterfly 32, 16, ..., 1 (MLX's own reduction order is not in the
+// reference; this one is fixed, and the oracle restates it).
+constexpr int kEncRows = 4;
 template <int D>
 __global__ __launch_bounds__(kWave) void tq_encode_gpu_kernel(
-    const uint16_t* __restrict__ x, int64_t s, const float* __restrict__ R, int mode,
-    int transpose, const float* __restrict__ inner, int n_inner, uint8_t* __restrict__ codes,
-    float* __restrict__ sigma, int64_t dst_cap, int64_t dst_start) {
+    const uint16_t* __restrict__ x, int64_t s, int64_t rows, const float* __restrict__ R,
+    int mode, int transpose, const float* __restrict__ inner, int n_inner,
+    uint8_t* __restrict__ codes, float* __restrict__ sigma, int64_t dst_cap, int64_t dst_start) {
   constexpr int PER = D / kWave;
-  __shared__ float xs[D];
+  __shared__ float xs[kEncRows][D];
   __shared__ float bnd[256];
-  const int64_t r = blockIdx.x;
+  const int64_t r0 = int64_t(blockIdx.x) * kEncRows;
+  const int nr = rows - r0 < kEncRows ? int(rows - r0) : kEncRows;
   const int lane = threadIdx.x;
-  for (int i = lane; i < D; i += kWave) xs[i] = bf16_to_f32(x[r * D + i]);
+  for (int q = 0; q < kEncRows; ++q)
+    for (int i = lane; i < D; i += kWave)
+      xs[q][i] = q < nr ? bf16_to_f32(x[(r0 + q) * D + i]) : 0.0f;
   for (int i = lane; i < n_inner; i += kWave) bnd[i] = inner[i];
   __syncthreads();
-  float y[PER];
+  float y[kEncRows][PER];
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int i = lane + k * kWave;
     if (mode == 0) {
-      y[k] = xs[i];
+#pragma unroll
+      for (int q = 0; q < kEncRows; ++q) y[q][k] = xs[q][i];
     } else {
-      float acc = 0.0f;
-      for (int j = 0; j < D; ++j)
-        acc = fmaf(xs[j], transpose ? R[int64_t(i) * D + j] : R[int64_t(j) * D + i], acc);
-      y[k] = mode == 1 ? bf16_to_f32(f32_to_bf16(acc)) : acc;
+      float acc[kEncRows] = {};
+      for (int j = 0; j < D; ++j) {
+        const float rv = transpose ? R[int64_t(i) * D + j] : R[int64_t(j) * D + i];
+#pragma unroll
+        for (int q = 0; q < kEncRows; ++q) acc[q] = fmaf(xs[q][j], rv, acc[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < kEncRows; ++q)
+        y[q][k] = mode == 1 ? bf16_to_f32(f32_to_bf16(acc[q])) : acc[q];
     }
   }
-  float p = 0.0f;
 #pragma unroll
-  for (int k = 0; k < PER; ++k) p = add(p, mul(y[k], y[k]));
+  for (int q = 0; q < kEncRows; ++q) {
+    if (q >= nr) break;
+    const int64_t r = r0 + q;
+    float p = 0.0f;
 #pragma unroll
-  for (int off = kWave / 2; off >= 1; off >>= 1) p = add(p, __shfl_xor(p, off, kWave));
-  const float sg = sqrt_rn(div_rn(p, float(D)));
-  const int64_t dst = (r / s) * dst_cap + dst_start + r % s;
+    for (int k = 0; k < PER; ++k) p = add(p, mul(y[q][k], y[q][k]));
 #pragma unroll
-  for (int k = 0; k < PER; ++k) {
-    const float xn = bf16_to_f32(f32_to_bf16(div_rn(y[k], sg)));
-    int lo = 0, hi = n_inner;
-    while (lo < hi) {
-      const int mid = (lo + hi) / 2;
-      if (bnd[mid] <= xn)
-        lo = mid + 1;
-      else
-        hi = mid;
+    for (int off = kWave / 2; off >= 1; off >>= 1) p = add(p, __shfl_xor(p, off, kWave));
+    const float sg = sqrt_rn(div_rn(p, float(D)));
+    const int64_t dst = (r / s) * dst_cap + dst_start + r % s;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const float xn = bf16_to_f32(f32_to_bf16(div_rn(y[q][k], sg)));
+      int lo = 0, hi = n_inner;
+      while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (bnd[mid] <= xn)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      codes[dst * D + lane + k * kWave] = uint8_t(lo);
     }
-    codes[dst * D + lane + k * kWave] = uint8_t(lo);
+    if (lane == 0) sigma[dst] = sg;
   }
-  if (lane == 0) sigma[dst] = sg;
 }
 
 // y = x R (x bf16 [rows, D] -> bf16): the GPU path's rotate_last_axis
@@ -777,9 +792,10 @@ extern "C" int32_t tqkv_tq_encode_gpu_path(const uint16_t* x, int64_t n_slabs, i
   const int n_inner = (1 << bits) - 1;
 #define TQKV_ENC(DIM)                                                                       \
   case DIM:                                                                                  \
-    hipLaunchKernelGGL(tq_encode_gpu_kernel<DIM>, dim3(unsigned(rows)), dim3(kWave), 0, st, x, \
-                       s, rotation, mode, transpose ? 1 : 0, boundaries_inner, n_inner, codes,  \
-                       sigma, dst_cap, dst_start);                                            \
+    hipLaunchKernelGGL(tq_encode_gpu_kernel<DIM>,                                            \
+                       dim3(unsigned((rows + kEncRows - 1) / kEncRows)), dim3(kWave), 0, st, x,  \
+                       s, rows, rotation, mode, transpose ? 1 : 0, boundaries_inner, n_inner,    \
+                       codes, sigma, dst_cap, dst_start);                                       \
     break;
   switch (dim) {
     TQKV_ENC(64) TQKV_ENC(128) TQKV_ENC(256) TQKV_ENC(512)
