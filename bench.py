@@ -585,9 +585,21 @@ def append_main(T, hip, args):
         for n in ("k", "v"):
             T.pack_codes(codes[n].ptr, slabs * S, D, BITS, packed[n].ptr, stream)
 
+    # QJL stage 2 of the keys on the device (qjl_encode_stage2_packed and
+    # qjl_apply_correction_packed): residual signs of K against a bf16
+    # reconstruction (here the affine dequantize's rows), then K_eff.
+    def qjl_enc():
+        T.qjl_encode_stage2(x["k"].ptr, deq["k"].ptr, phi.ptr, slabs * S, D, M, sgn["k"].ptr,
+                            rn["k"].ptr, stream)
+
+    def qjl_fix():
+        T.qjl_apply_correction(deq["k"].ptr, sgn["k"].ptr, rn["k"].ptr, phi.ptr, slabs * S, D, M,
+                               rot["v"].ptr, stream)
+
     settle = 16 if args.settle is None else max(0, args.settle)
     for _ in range(settle + args.warmup):
         quant(), dequant(), rotq(), rotq_k(), rotq_two(), tq(), tq_gpu(), cb_deq(), pack()
+        qjl_enc(), qjl_fix()
     hip.sync()
     n = args.steps
     ms_q = _loop_ms(hip, stream, quant, n)
@@ -600,6 +612,11 @@ def append_main(T, hip, args):
     ms_g = _loop_ms(hip, stream, tq_gpu, n)
     ms_c = _loop_ms(hip, stream, cb_deq, n)
     ms_p = _loop_ms(hip, stream, pack, n)
+    ms_je = _loop_ms(hip, stream, qjl_enc, n)
+    ms_jf = _loop_ms(hip, stream, qjl_fix, n)
+    sg_bytes = slabs * S * (M // 8 + 4)  # sign words + residual norm, keys
+    je_bytes = 2 * slabs * S * D * 2 + sg_bytes
+    jf_bytes = 2 * slabs * S * D * 2 + sg_bytes
     cb_bytes = 2 * slabs * S * (D + 4)  # u8 codes + f32 sigma, K and V
     pk_bytes = 2 * slabs * S * (D + pw * 8)
     in_bytes = 2 * slabs * S * D * 2
@@ -652,7 +669,14 @@ def append_main(T, hip, args):
          "pack_codes": {
              "ms": round(ms_p, 5), "bytes": pk_bytes,
              "gbps": round(pk_bytes / (ms_p * 1e-3) / 1e9, 1),
-             "note": "tqkv_pack_codes: u8 codes of K and V to stage1_packed u64 words"}},
+             "note": "tqkv_pack_codes: u8 codes of K and V to stage1_packed u64 words"},
+         "qjl_stage2": {
+             "encode_ms": round(ms_je, 5), "encode_bytes": je_bytes,
+             "encode_gbps": round(je_bytes / (ms_je * 1e-3) / 1e9, 1),
+             "apply_ms": round(ms_jf, 5), "apply_bytes": jf_bytes,
+             "apply_gbps": round(jf_bytes / (ms_jf * 1e-3) / 1e9, 1), "qjl_m": M,
+             "note": "tqkv_qjl_encode_stage2 (residual signs and norms of K) and "
+                     "tqkv_qjl_apply_correction (K_eff rows), keys only"}},
         settle)
     if not args.no_cpu_baseline:
         O, threads = _oracle()

@@ -535,65 +535,89 @@ __global__ void tq_scores_two_stage_kernel(const float* __restrict__ rq,
 }
 
 // The GPU TurboQuant path's stage 2 (turboquant.rs:592-622): one wavefront
-// per row; residual = f32(K_rot) - f32(K_dq), r_norm = sqrt(sum r^2) in
-// channel order, sign bit i = (sum_d r_d * Phi[i][d] >= 0), sums from +0.0.
+// per kQjlRows rows (each load of Phi serves them all); residual =
+// f32(K_rot) - f32(K_dq), r_norm = sqrt(sum r^2) in channel order, sign bit
+// i = (sum_d r_d * Phi[i][d] >= 0), sums from +0.0.
+constexpr int kQjlRows = 4;
 __global__ __launch_bounds__(kWave) void qjl_encode_stage2_kernel(
     const uint16_t* __restrict__ k_rot, const uint16_t* __restrict__ k_dq,
-    const float* __restrict__ phi, int D, int m, uint32_t* __restrict__ signs,
+    const float* __restrict__ phi, int D, int m, int64_t rows, uint32_t* __restrict__ signs,
     float* __restrict__ rnorm) {
-  extern __shared__ float s_r[];
-  const int64_t t = blockIdx.x;
+  extern __shared__ float s_r[];  // kQjlRows x D residuals
+  const int64_t t0 = int64_t(blockIdx.x) * kQjlRows;
+  const int nr = rows - t0 < kQjlRows ? int(rows - t0) : kQjlRows;
   const int lane = threadIdx.x;
-  for (int d = lane; d < D; d += kWave)
-    s_r[d] = __fsub_rn(bf16_to_f32(k_rot[t * D + d]), bf16_to_f32(k_dq[t * D + d]));
+  for (int q = 0; q < kQjlRows; ++q)
+    for (int d = lane; d < D; d += kWave)
+      s_r[q * D + d] = q < nr ? __fsub_rn(bf16_to_f32(k_rot[(t0 + q) * D + d]),
+                                          bf16_to_f32(k_dq[(t0 + q) * D + d]))
+                              : 0.0f;
   __syncthreads();
-  if (lane == 0) {
+  if (lane < nr) {
     float ss = 0.0f;
-    for (int d = 0; d < D; ++d) ss = add(ss, mul(s_r[d], s_r[d]));
-    rnorm[t] = sqrt_rn(ss);
+    for (int d = 0; d < D; ++d) ss = add(ss, mul(s_r[lane * D + d], s_r[lane * D + d]));
+    rnorm[t0 + lane] = sqrt_rn(ss);
   }
   const int words = (m + 31) / 32;
   for (int base = 0; base < m; base += kWave) {
     const int row = base + lane;
-    bool bit = false;
+    float acc[kQjlRows] = {};
     if (row < m) {
       const float* p = phi + int64_t(row) * D;
-      float acc = 0.0f;
-      for (int d = 0; d < D; ++d) acc = add(acc, mul(s_r[d], p[d]));
-      bit = acc >= 0.0f;
+      for (int d = 0; d < D; ++d) {
+        const float pv = p[d];
+#pragma unroll
+        for (int q = 0; q < kQjlRows; ++q) acc[q] = add(acc[q], mul(s_r[q * D + d], pv));
+      }
     }
-    const uint64_t ball = __ballot(bit);
-    if (lane == 0) {
-      const int w0 = base / 32;
-      signs[t * words + w0] = uint32_t(ball);
-      if (w0 + 1 < words) signs[t * words + w0 + 1] = uint32_t(ball >> 32);
+#pragma unroll
+    for (int q = 0; q < kQjlRows; ++q) {
+      if (q >= nr) break;
+      const uint64_t ball = __ballot(row < m && acc[q] >= 0.0f);
+      if (lane == 0) {
+        const int w0 = base / 32;
+        signs[(t0 + q) * words + w0] = uint32_t(ball);
+        if (w0 + 1 < words) signs[(t0 + q) * words + w0 + 1] = uint32_t(ball >> 32);
+      }
     }
   }
 }
 
 // qjl_apply_correction_packed / _to_k_dq (turboquant.rs:624-691): one
-// thread per (row, channel); K_eff = bf16(K_dq + bf16((sum_i sign_i *
-// Phi[i][d]) * (r_norm * sqrt(pi/2) / sqrt(m)))), the sum from +0.0 in i
-// order.
+// thread per (kQjlRows rows, channel), each load of Phi serving the rows;
+// K_eff = bf16(K_dq + bf16((sum_i sign_i * Phi[i][d]) * (r_norm *
+// sqrt(pi/2) / sqrt(m)))), the sum from +0.0 in i order.
 __global__ void qjl_apply_correction_kernel(const uint16_t* __restrict__ k_dq,
                                             const uint32_t* __restrict__ signs,
                                             const float* __restrict__ rnorm,
                                             const float* __restrict__ phi, int D, int m,
                                             int64_t rows, uint16_t* __restrict__ k_eff) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * D) return;
-  const int64_t t = i / D;
+  const int64_t groups = (rows + kQjlRows - 1) / kQjlRows;
+  if (i >= groups * D) return;
+  const int64_t t0 = (i / D) * kQjlRows;
   const int d = int(i % D);
+  const int nr = rows - t0 < kQjlRows ? int(rows - t0) : kQjlRows;
   const int words = (m + 31) / 32;
-  const uint32_t* sg = signs + t * words;
-  float acc = 0.0f;
+  float acc[kQjlRows] = {};
   for (int row = 0; row < m; ++row) {
     const float p = phi[int64_t(row) * D + d];
-    acc = add(acc, ((sg[row / 32] >> (row % 32)) & 1u) ? p : -p);
+#pragma unroll
+    for (int q = 0; q < kQjlRows; ++q) {
+      if (q < nr) {
+        const uint32_t w = signs[(t0 + q) * words + row / 32];
+        acc[q] = add(acc[q], ((w >> (row % 32)) & 1u) ? p : -p);
+      }
+    }
   }
   const float sc = div_rn(sqrt_rn(1.57079632679489661923f), sqrt_rn(float(m)));
-  const float corr = bf16_to_f32(f32_to_bf16(mul(acc, mul(rnorm[t], sc))));
-  k_eff[i] = f32_to_bf16(add(bf16_to_f32(k_dq[i]), corr));
+#pragma unroll
+  for (int q = 0; q < kQjlRows; ++q) {
+    if (q >= nr) break;
+    const int64_t t = t0 + q;
+    const float corr = bf16_to_f32(f32_to_bf16(mul(acc[q], mul(rnorm[t], sc))));
+    k_eff[t * D + d] = f32_to_bf16(add(bf16_to_f32(k_dq[t * D + d]), corr));
+  }
 }
 
 // attend_values: output channel i sums, token by token in order and channel
@@ -849,9 +873,10 @@ extern "C" int32_t tqkv_qjl_encode_stage2(const uint16_t* k_rot, const uint16_t*
   if (!k_rot || !k_dq || !qjl || !signs || !rnorm) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (rows < 0 || rows > 0x7fffffffLL || dim <= 0 || dim > 4096 || m <= 0)
     return fail(TQKV_EINVAL_SHAPE, "rows=%lld dim=%d m=%d", (long long)rows, dim, m);
-  hipLaunchKernelGGL(qjl_encode_stage2_kernel, dim3(unsigned(rows)), dim3(kWave),
-                     size_t(dim) * sizeof(float), reinterpret_cast<hipStream_t>(stream), k_rot,
-                     k_dq, qjl, dim, m, signs, rnorm);
+  hipLaunchKernelGGL(qjl_encode_stage2_kernel, dim3(unsigned((rows + kQjlRows - 1) / kQjlRows)),
+                     dim3(kWave), size_t(kQjlRows) * size_t(dim) * sizeof(float),
+                     reinterpret_cast<hipStream_t>(stream), k_rot, k_dq, qjl, dim, m, rows, signs,
+                     rnorm);
   TQKV_LAUNCHED();
   return ok();
 }
@@ -864,7 +889,7 @@ extern "C" int32_t tqkv_qjl_apply_correction(const uint16_t* k_dq, const uint32_
   if (!k_dq || !signs || !rnorm || !qjl || !k_eff) return fail(TQKV_EINVAL_ARG, "null pointer");
   if (rows < 0 || dim <= 0 || m <= 0)
     return fail(TQKV_EINVAL_SHAPE, "rows=%lld dim=%d m=%d", (long long)rows, dim, m);
-  const int64_t blocks = (rows * dim + 255) / 256;
+  const int64_t blocks = ((rows + kQjlRows - 1) / kQjlRows * dim + 255) / 256;
   if (blocks > 0x7fffffffLL) return fail(TQKV_EINVAL_SHAPE, "too many rows");
   hipLaunchKernelGGL(qjl_apply_correction_kernel, dim3(unsigned(blocks)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), k_dq, signs, rnorm, qjl, dim, m, rows,
