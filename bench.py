@@ -618,6 +618,30 @@ def append_main(T, hip, args):
     je_bytes = 2 * slabs * S * D * 2 + sg_bytes
     jf_bytes = 2 * slabs * S * D * 2 + sg_bytes
     cb_bytes = 2 * slabs * S * (D + 4)  # u8 codes + f32 sigma, K and V
+    # The KVCache trait object (SimpleCache semantics over the device):
+    # host f32 vectors in and out, so these times include the copies across
+    # PCIe and the call's synchronization. One head of the layer.
+    kvc = T.KVCache(D, bits=BITS, qjl_m=M, seed=42)
+    kf = (x["k"].numpy()[0].astype(np.uint32) << 16).view(np.float32)
+    vf = (x["v"].numpy()[0].astype(np.uint32) << 16).view(np.float32)
+    t_s = time.perf_counter()
+    kvc.store(0, 0, kf, vf)
+    kv_store_s = time.perf_counter() - t_s
+    qv = kf[7] * np.float32(0.5)
+    kvc.attend_keys(0, 0, qv)
+    reps = 20
+    t_s = time.perf_counter()
+    for _ in range(reps):
+        scv = kvc.attend_keys(0, 0, qv)
+    kv_keys_us = (time.perf_counter() - t_s) / reps * 1e6
+    wv = np.exp(scv - scv.max()).astype(np.float32)
+    wv /= wv.sum()
+    kvc.attend_values(0, 0, wv)
+    t_s = time.perf_counter()
+    for _ in range(reps):
+        kvc.attend_values(0, 0, wv)
+    kv_values_us = (time.perf_counter() - t_s) / reps * 1e6
+    kvc.close()
     pk_bytes = 2 * slabs * S * (D + pw * 8)
     in_bytes = 2 * slabs * S * D * 2
     q_bytes = 2 * slabs * S * (words * 4 + 2 * groups * 2)
@@ -676,7 +700,13 @@ def append_main(T, hip, args):
              "apply_ms": round(ms_jf, 5), "apply_bytes": jf_bytes,
              "apply_gbps": round(jf_bytes / (ms_jf * 1e-3) / 1e9, 1), "qjl_m": M,
              "note": "tqkv_qjl_encode_stage2 (residual signs and norms of K) and "
-                     "tqkv_qjl_apply_correction (K_eff rows), keys only"}},
+                     "tqkv_qjl_apply_correction (K_eff rows), keys only"},
+         "kvcache_trait": {
+             "store_vectors_per_s": round(S / kv_store_s, 1),
+             "attend_keys_us": round(kv_keys_us, 1), "attend_values_us": round(kv_values_us, 1),
+             "vectors": S, "qjl_m": M,
+             "note": "tqkv_kvcache_store / _attend_keys / _attend_values on one head: host f32 "
+                     "in and out, PCIe and the synchronizing return included (host clock)"}},
         settle)
     if not args.no_cpu_baseline:
         O, threads = _oracle()
