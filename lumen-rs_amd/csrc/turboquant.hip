@@ -600,14 +600,17 @@ __global__ void qjl_apply_correction_kernel(const uint16_t* __restrict__ k_dq,
   const int nr = rows - t0 < kQjlRows ? int(rows - t0) : kQjlRows;
   const int words = (m + 31) / 32;
   float acc[kQjlRows] = {};
-  for (int row = 0; row < m; ++row) {
-    const float p = phi[int64_t(row) * D + d];
+  for (int w0 = 0; w0 < words; ++w0) {
+    // The rows' sign words for Phi rows 32 w0 .. + 31, loaded once.
+    uint32_t sw[kQjlRows];
 #pragma unroll
-    for (int q = 0; q < kQjlRows; ++q) {
-      if (q < nr) {
-        const uint32_t w = signs[(t0 + q) * words + row / 32];
-        acc[q] = add(acc[q], ((w >> (row % 32)) & 1u) ? p : -p);
-      }
+    for (int q = 0; q < kQjlRows; ++q) sw[q] = q < nr ? signs[(t0 + q) * words + w0] : 0u;
+    const int row_end = m - 32 * w0 < 32 ? m : 32 * w0 + 32;
+    for (int row = 32 * w0; row < row_end; ++row) {
+      const float p = phi[int64_t(row) * D + d];
+#pragma unroll
+      for (int q = 0; q < kQjlRows; ++q)
+        if (q < nr) acc[q] = add(acc[q], ((sw[q] >> (row % 32)) & 1u) ? p : -p);
     }
   }
   const float sc = div_rn(sqrt_rn(1.57079632679489661923f), sqrt_rn(float(m)));
