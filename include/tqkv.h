@@ -50,7 +50,10 @@ typedef struct ihipStream_t* tqkv_stream;
 const char* tqkv_status_string(int32_t status);
 /* Detail of the last failing call on this thread ("" if none). */
 const char* tqkv_last_error(void);
-/* ABI version, major * 10000 + minor * 100 + patch. */
+/* ABI version, major * 10000 + minor * 100 + patch: tqkv_version() returns
+ * the TQKV_ABI_VERSION this header declares. 0.2.0 added tqkv_cache_config's
+ * encode and reserved fields (its size went from 64 to 72 bytes). */
+#define TQKV_ABI_VERSION 200
 int32_t tqkv_version(void);
 /* Frees the scratch the library keeps per device for calls given no
  * workspace (no counterpart in the reference). The scratch grows by at
@@ -59,6 +62,9 @@ int32_t tqkv_version(void);
  * scratch to finish its work, then frees it all. The next call that needs
  * scratch allocates again. */
 int32_t tqkv_scratch_release(void);
+/* Bytes of that scratch the library holds now, over every device (current
+ * buffers and outgrown ones not yet released). Host bookkeeping only. */
+size_t tqkv_scratch_bytes(void);
 
 /* ======================================================================
  * Stateless kernels
@@ -129,7 +135,10 @@ int32_t tqkv_affine_quantize_kv_rotated(const uint16_t* k, const uint16_t* v, in
 /*
  * mlx::dequantize(packed, scales, biases, group_size, bits) to bf16, as the
  * reference's prefill fallback uses it (gemma4_moe.rs:2394-2399):
- * out = bf16(bf16(scale * code) + bias). rows = number of [dim] rows.
+ * out = bf16(fma(scale, code, bias)), one rounding of the f32 multiply-add
+ * (MLX's dequantize as the reference's qwen4exp_tiny fixture records it,
+ * reference/mtp_outputs.safetensors mtp_embedded). rows = number of [dim]
+ * rows.
  */
 int32_t tqkv_affine_dequantize(const uint32_t* packed, const uint16_t* scales,
                                const uint16_t* biases, int64_t rows, int32_t dim,
@@ -235,8 +244,8 @@ int32_t tqkv_decode_attend_affine_append(
  *
  * tqkv_page_digest_affine: key_min / key_max [n_slabs, max_pages, dim] bf16
  * get, for pages [page_from, page_to) of every slab, the elementwise min and
- * max over the page's 64 mlx::dequantize'd keys (bf16(bf16(scale * code) +
- * bias)). Digesting only the newly filled pages keeps the digest current, as
+ * max over the page's 64 mlx::dequantize'd keys (bf16(fma(scale, code,
+ * bias))). Digesting only the newly filled pages keeps the digest current, as
  * page_digest does.
  */
 int32_t tqkv_page_digest_affine(const uint32_t* k_packed, const uint16_t* k_scales,
@@ -306,6 +315,13 @@ size_t tqkv_sparse_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
  */
 const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
                                     int32_t bits_k, int32_t bits_v);
+/* The same for a context whose longest segment holds max_rows rows: the
+ * MFMA kernel addresses a (batch row, KV head)'s rows through 32-bit byte
+ * offsets, so from max_rows * D >= 2^31 on the dot2 kernel serves the
+ * layout (and a fused append, which needs the MFMA kernel, runs as two
+ * calls). Host arithmetic only. */
+const char* tqkv_decode_kernel_for_rows(int32_t H, int32_t H_kv, int32_t D, int32_t group_size,
+                                        int32_t bits_k, int32_t bits_v, int64_t max_rows);
 
 /*
  * Fused decode attention over a codebook cache (the GPU TurboQuant caches'
@@ -353,8 +369,8 @@ int32_t tqkv_decode_attend_codebook_qjl(const uint16_t* q, int32_t B, int32_t H,
  * Prefill-chunk attention over affine-packed K/V on the matrix cores:
  * softmax(scale * Q K^T + mask) V for a chunk of L query rows per head.
  * Replaces dequantized_prefill_attention (gemma4_moe.rs:2382-2411): K and V
- * dequantize as mlx::dequantize does for bf16 (bf16(bf16(scale * code) +
- * bias)), then attention runs with bf16 operands and f32 accumulation. When
+ * dequantize as mlx::dequantize does for bf16 (bf16(fma(scale, code,
+ * bias)), one rounding), then attention runs with bf16 operands and f32 accumulation. When
  * 8 or more 256-row blocks share a KV head, the keys are dequantized once
  * into the library's per-device scratch (2 * B * H_kv * keys * D * 2 bytes,
  * at most 4 GiB; larger contexts dequantize in every block instead, in LDS)

@@ -388,7 +388,7 @@ __global__ __launch_bounds__(kRT) void affine_quantize_rot_kernel(const RArgs a)
   }
 }
 
-// mlx::dequantize (bf16(bf16(scale * code) + bias)), one value a thread: the
+// mlx::dequantize (bf16(fma(scale, code, bias)), one rounding), one value a thread: the
 // path for an output that is not 16-byte aligned.
 __global__ void affine_dequantize_kernel(const uint32_t* __restrict__ packed,
                                          const uint16_t* __restrict__ scales,
@@ -406,8 +406,7 @@ __global__ void affine_dequantize_kernel(const uint32_t* __restrict__ packed,
   const int groups = dim / gs;
   const float sc = bf16_to_f32(scales[r * groups + e / gs]);
   const float bi = bf16_to_f32(biases[r * groups + e / gs]);
-  const float prod = bf16_to_f32(f32_to_bf16(sc * float(code)));
-  out[i] = f32_to_bf16(prod + bi);
+  out[i] = f32_to_bf16(fmaf(sc, float(code), bi));
 }
 
 // The same values eight at a time: a thread takes 8 consecutive values of a
@@ -437,8 +436,7 @@ __global__ __launch_bounds__(256) void affine_dequantize8_kernel(
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t code = uint32_t(win >> (e * bits)) & ((1u << bits) - 1);
-    const float prod = bf16_to_f32(f32_to_bf16(sc * float(code)));
-    const uint32_t v = f32_to_bf16(prod + bi);
+    const uint32_t v = f32_to_bf16(fmaf(sc, float(code), bi));
     if (e % 2 == 0)
       o[e / 2] = v;
     else

@@ -1071,8 +1071,10 @@ int32_t tqkv_cache_append_decode(tqkv_cache* c, const uint16_t* k, const uint16_
   if (c->cur[0].cap != c->cur[3].cap)
     return fail(TQKV_EINVAL_ARG, "K and V buffers of different capacity");
   // The decode must not fail once the update is committed (its row is only
-  // written by the decode kernel): the workspace it will need is settled
-  // first, from the segment lengths it will attend.
+  // written by the decode kernel): the kernel it will pick and the
+  // workspace it will need are settled first, from the segment lengths it
+  // will attend (a segment too long for the MFMA kernel's 32-bit offsets
+  // takes the dot2 kernel, which cannot append: two calls then).
   {
     tqkv_affine_seg vs[2]{};
     int vn = 0;
@@ -1086,6 +1088,12 @@ int32_t tqkv_cache_append_decode(tqkv_cache* c, const uint16_t* k, const uint16_
       vs[vn++].n = p.write_at;
       vs[vn++].n = p.view - p.write_at - 1;
     }
+    int64_t max_rows = 0;
+    for (int i = 0; i < vn; ++i) max_rows = vs[i].n > max_rows ? vs[i].n : max_rows;
+    if (strcmp(tqkv_decode_kernel_for_rows(H, g.kv_heads, g.k_dim, g.group_size, g.bits_k,
+                                           g.bits_v, max_rows),
+               "mfma") != 0)
+      return two_calls();
     const size_t need = decode_need_bytes(g.batch, H, g.kv_heads, g.k_dim, g.group_size,
                                           g.bits_k, g.bits_v, vs, vn, true);
     if (need > 0) {

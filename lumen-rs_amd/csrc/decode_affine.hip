@@ -1,9 +1,7 @@
 // Host side of the fused affine decode: split planning, workspace, dispatch.
 // The kernel itself (and its design notes) is in decode_affine.hpp.
-#include <atomic>
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
 
 #include "decode_mfma.hpp"
 
@@ -303,15 +301,21 @@ int kernel_heads(int D, int bk, int bv, int G, int gs, int64_t max_rows) {
 using namespace tqkv;
 using namespace tqkv::decode;
 
+extern "C" const char* tqkv_decode_kernel_for_rows(int32_t H, int32_t H_kv, int32_t D,
+                                                   int32_t group_size, int32_t bits_k,
+                                                   int32_t bits_v, int64_t max_rows) {
+  if (H <= 0 || H_kv <= 0 || H % H_kv != 0 || max_rows < 0) return "";
+  if (use_tile(D, bits_k, bits_v, H / H_kv, false)) return "tiles";
+  const int Gp = group_heads(D, bits_k, bits_v, H / H_kv, group_size, max_rows);
+  if (!Gp) return "";
+  KernelFn fn = pick(D, bits_k, bits_v, Gp, group_size, max_rows);
+  return fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size) ? "mfma" : "dot2";
+}
+
 extern "C" const char* tqkv_decode_kernel_name(int32_t H, int32_t H_kv, int32_t D,
                                                int32_t group_size, int32_t bits_k,
                                                int32_t bits_v) {
-  if (H <= 0 || H_kv <= 0 || H % H_kv != 0) return "";
-  if (use_tile(D, bits_k, bits_v, H / H_kv, false)) return "tiles";
-  const int Gp = group_heads(D, bits_k, bits_v, H / H_kv, group_size);
-  if (!Gp) return "";
-  KernelFn fn = pick(D, bits_k, bits_v, Gp, group_size);
-  return fn == pick_mfma_only(D, bits_k, bits_v, Gp, group_size) ? "mfma" : "dot2";
+  return tqkv_decode_kernel_for_rows(H, H_kv, D, group_size, bits_k, bits_v, 0);
 }
 
 extern "C" size_t tqkv_decode_workspace_size(int32_t B, int32_t H, int32_t H_kv, int32_t D,
@@ -351,54 +355,8 @@ struct DecodePlan {
   int n_splits = 1;
   int64_t split_len = 0;
   int n_part = 1;
-  // The last workgroup of each unit merges (no merge launch): n_part slots
-  // of at most kInlineMergeMax, behind a launch that writes slots.
-  bool inline_merge = false;
   size_t need = 0;
 };
-
-// TQKV_INLINE_MERGE=1 merges in-kernel. Off by default: on MI355X the last
-// workgroup's counter round trip and its reads of the partials past the
-// L2 cost as much as the merge launch they replace (config 1: 17.0 against
-// 16.5 us a step; config 3: 0.517 against 0.506 ms).
-bool inline_merge_enabled() {
-  const char* e = getenv("TQKV_INLINE_MERGE");
-  return e && strcmp(e, "1") == 0;
-}
-
-// Unit counters of the in-kernel merge: a file-scope device array (zero at
-// load; every merge sets its counter back to zero), handed out in chunks of
-// kRingChunk counters, one chunk a launch, round robin over kRingChunks, so
-// launches in flight on different streams count in different chunks (a
-// chunk comes round again only after kRingChunks - 1 later launches).
-constexpr int kRingChunk = 4096;   // most units (batch rows x KV heads) a launch
-constexpr int kRingChunks = 256;
-static __device__ __attribute__((used)) uint32_t merge_ring[kRingChunk * kRingChunks];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_ring_mu;
-uint32_t* g_ring[kMaxDevices] = {};
-std::atomic<uint32_t> g_ring_next{0};
-
-// A chunk of the current device's counters, or null (the merge launch then
-// runs instead).
-uint32_t* merge_counters(int64_t units) {
-  if (units > kRingChunk) return nullptr;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  uint32_t* base = nullptr;
-  {
-    std::lock_guard<std::mutex> lock(g_ring_mu);
-    if (!g_ring[dev]) {
-      void* p = nullptr;
-      if (hipGetSymbolAddress(&p, HIP_SYMBOL(merge_ring)) != hipSuccess || !p) return nullptr;
-      g_ring[dev] = static_cast<uint32_t*>(p);
-    }
-    base = g_ring[dev];
-  }
-  const uint32_t c = g_ring_next.fetch_add(1, std::memory_order_relaxed) % kRingChunks;
-  return base + size_t(c) * kRingChunk;
-}
 
 // Gk: the query heads one decode launch serves (kernel_heads).
 // waves: the launch's wavefronts a workgroup (decode_waves); tile: the
@@ -427,7 +385,6 @@ DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, int waves,
       pl.split_len_s = 64;
     }
     pl.n_part = pl.sp_p + pl.sp_s;
-    pl.inline_merge = pl.sp_s > 0 && pl.n_part <= kInlineMergeMax && inline_merge_enabled();
     pl.need = size_t(B) * H * pl.n_part * row * sizeof(float);
     return pl;
   }
@@ -451,7 +408,6 @@ DecodePlan plan_decode(int B, int H, int H_kv, int D, int Gk, int waves,
   }
   plan_splits(B, H_kv, waves, total, &pl.n_splits, &pl.split_len);
   pl.n_part = pl.n_splits;
-  pl.inline_merge = pl.n_splits > 1 && pl.n_part <= kInlineMergeMax && inline_merge_enabled();
   pl.need = pl.n_splits > 1 ? size_t(B) * H * pl.n_splits * row * sizeof(float) : 0;
   return pl;
 }
@@ -541,8 +497,6 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     }
   }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // Each launch that merges in-kernel counts in a chunk of its own.
-  auto counters = [&]() { return pl.inline_merge ? merge_counters(int64_t(B) * H_kv) : nullptr; };
 
   if (pl.tile) {
     float* po = static_cast<float*>(ws);
@@ -558,7 +512,6 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     }
     return ok();
   }
-  bool merged = false;  // the decode launches merged in-kernel
   if (pl.shared_path) {
     Args s = a;
     s.seg[0] = a.seg[1];
@@ -582,17 +535,13 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
       s.part_m = pm;
       s.part_l = pl_;
       for (s.h_off = 0; s.h_off < G; s.h_off += Gk) {
-        s.merge_cnt = counters();
-        merged = s.merge_cnt != nullptr;
         hipLaunchKernelGGL(fn, dim3(unsigned(pl.sp_s), unsigned(H_kv), unsigned(B)),
                            dim3(kWave * waves), 0, st, s);
         TQKV_LAUNCHED();
       }
     }
-    if (!merged) {
-      launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
-      TQKV_LAUNCHED();
-    }
+    launch_merge(po, pm, pl_, pl.n_part, D, int64_t(B) * H, out, st);
+    TQKV_LAUNCHED();
     return ok();
   }
 
@@ -606,13 +555,11 @@ int32_t decode_affine(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, int
     a.part_l = a.part_m + size_t(B) * H * a.n_splits;
   }
   for (a.h_off = 0; a.h_off < G; a.h_off += Gk) {
-    a.merge_cnt = a.n_splits > 1 ? counters() : nullptr;
-    merged = a.merge_cnt != nullptr;
     hipLaunchKernelGGL(fn, dim3(unsigned(a.n_splits), unsigned(H_kv), unsigned(B)),
                        dim3(kWave * waves), 0, st, a);
     TQKV_LAUNCHED();
   }
-  if (a.n_splits > 1 && !merged) {
+  if (a.n_splits > 1) {
     launch_merge(a.part_o, a.part_m, a.part_l, a.n_splits, D, int64_t(B) * H, out, st);
     TQKV_LAUNCHED();
   }

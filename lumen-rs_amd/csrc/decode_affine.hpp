@@ -25,10 +25,7 @@
 // writes the normalized bf16 output itself: the decode is one launch. Else
 // each workgroup writes its split's unnormalized partial and a small second
 // kernel merges the splits, as native_quant_attention.rs:190-207 does in its
-// pass 2. (A last-arriving-workgroup merge, merge_if_last below, is built:
-// with device-scope fences it wrote back and invalidated L2 on this
-// multi-XCD part, with coherent relaxed accesses and a counter it costs
-// about what the launch does, so it is opt-in.)
+// pass 2.
 //
 // Decode is HBM-bound (~1 dot2 per 2 codes per head), so the kernel uses VALU
 // dot products, not MFMA. f16 denormals must be preserved (the default mode).
@@ -97,110 +94,7 @@ struct Args {
   float* part_o;  // [B, H, n_part, D]
   float* part_m;  // [B, H, n_part]
   float* part_l;  // [B, H, n_part]
-  // In-kernel merge (merge_cnt null: a merge launch follows): the last of a
-  // unit's n_splits workgroups of this launch merges all n_part slots of
-  // the heads the launch serves into out. merge_cnt[b * H_kv + kvh] counts
-  // the unit's finished workgroups; it is zero before the launch and the
-  // merging workgroup sets it back to zero.
-  uint32_t* merge_cnt;
 };
-
-// Partial slots written and read device-wide without a cache writeback:
-// relaxed agent-scope atomic accesses are coherent per location across
-// every XCD's L2 (the stores write through, the loads miss the CU's L1),
-// which a release/acquire pair would otherwise buy with an L2 writeback and
-// invalidate.
-__device__ __forceinline__ void store_partial(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_partial(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Most partial slots the in-kernel merge takes (more: a merge launch).
-constexpr int kInlineMergeMax = 32;
-
-// Called by every thread of a workgroup after its partial slots are
-// stored: counts the workgroup in its unit and, in the unit's last one,
-// merges the n_part slots of heads [h_off, h_off + G) into out exactly as
-// decode_merge_small_kernel does (the same order of operations, so the
-// same bits). NT: threads of the workgroup.
-template <int G, int D, int NT>
-__device__ __forceinline__ void merge_if_last(const Args& a, int b, int kvh) {
-  __shared__ int s_last;
-  __shared__ float s_pm[G][kInlineMergeMax], s_pl[G][kInlineMergeMax];
-  // Every wavefront's partial stores are complete (the barrier waits for
-  // its outstanding memory operations) before the unit counts this one.
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* cnt = a.merge_cnt + int64_t(b) * a.H_kv + kvh;
-    const uint32_t done =
-        __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    s_last = done == uint32_t(a.n_splits);
-    // The unit's last workgroup: no other one touches the counter again in
-    // this launch, so it goes back to zero for the counter's next use.
-    if (s_last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  const int np = a.n_part;
-  const int64_t bh0 = int64_t(b) * a.H + int64_t(kvh) * a.Gt + a.h_off;
-  for (int i = threadIdx.x; i < G * np; i += NT) {
-    const int h = i / np, s = i - h * np;
-    s_pm[h][s] = load_partial(a.part_m + (bh0 + h) * np + s);
-    s_pl[h][s] = load_partial(a.part_l + (bh0 + h) * np + s);
-  }
-  constexpr int K = (G * D + NT - 1) / NT;  // outputs a thread
-  if constexpr (K <= 2) {
-    // Every load is issued before any is used (one trip to memory): each
-    // thread's outputs' partials into registers beside the (max, sum) loads.
-    float o[K][kInlineMergeMax];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int i = threadIdx.x + k * NT;
-      const float* po = a.part_o + (bh0 + i / D) * np * D + i % D;
-#pragma unroll
-      for (int s = 0; s < kInlineMergeMax; ++s)
-        o[k][s] = i < G * D && s < np ? load_partial(po + int64_t(s) * D) : 0.0f;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int i = threadIdx.x + k * NT;
-      if (i >= G * D) break;
-      const int h = i / D, d = i - h * D;
-      float mx = -INFINITY;
-      for (int s = 0; s < np; ++s) mx = fmaxf(mx, s_pm[h][s]);
-      float ls = 0.0f, os = 0.0f;
-#pragma unroll
-      for (int s = 0; s < kInlineMergeMax; ++s) {
-        if (s >= np) break;
-        const float m = s_pm[h][s];
-        const float w = m == -INFINITY ? 0.0f : exp2f(m - mx);
-        ls += w * s_pl[h][s];
-        os += w * o[k][s];
-      }
-      a.out[(bh0 + h) * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
-    }
-  } else {
-    __syncthreads();
-    for (int i = threadIdx.x; i < G * D; i += NT) {
-      const int h = i / D, d = i - h * D;
-      float mx = -INFINITY;
-      for (int s = 0; s < np; ++s) mx = fmaxf(mx, s_pm[h][s]);
-      float ls = 0.0f, os = 0.0f;
-      const float* po = a.part_o + (bh0 + h) * np * D + d;
-#pragma unroll 8
-      for (int s = 0; s < np; ++s) {
-        const float m = s_pm[h][s];
-        const float w = m == -INFINITY ? 0.0f : exp2f(m - mx);
-        ls += w * s_pl[h][s];
-        os += w * load_partial(po + int64_t(s) * D);
-      }
-      a.out[(bh0 + h) * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
-    }
-  }
-}
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
@@ -611,22 +505,13 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_affine_kernel(Args a) {
       a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
     } else {
       const int64_t row = bh * a.n_part + a.split_base + split;
-      if (a.merge_cnt) {  // read by a workgroup of this launch
-        store_partial(a.part_o + row * D + d, os);
-        if (d == 0) {
-          store_partial(a.part_m + row, mx);
-          store_partial(a.part_l + row, ls);
-        }
-      } else {  // read by the merge launch
-        a.part_o[row * D + d] = os;
-        if (d == 0) {
-          a.part_m[row] = mx;
-          a.part_l[row] = ls;
-        }
+      a.part_o[row * D + d] = os;
+      if (d == 0) {
+        a.part_m[row] = mx;
+        a.part_l[row] = ls;
       }
     }
   }
-  if (a.merge_cnt && a.n_part > 1) merge_if_last<G, D, kWave * kWaves>(a, b, kvh);
 }
 
 using KernelFn = void (*)(Args);

@@ -763,22 +763,13 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
       a.out[bh * D + d] = f32_to_bf16(ls > 0.0f ? os / ls : 0.0f);
     } else {
       const int64_t row = bh * a.n_part + a.split_base + split;
-      if (a.merge_cnt) {  // read by a workgroup of this launch
-        store_partial(a.part_o + row * D + d, os);
-        if (d == 0) {
-          store_partial(a.part_m + row, mx);
-          store_partial(a.part_l + row, ls);
-        }
-      } else {  // read by the merge launch
-        a.part_o[row * D + d] = os;
-        if (d == 0) {
-          a.part_m[row] = mx;
-          a.part_l[row] = ls;
-        }
+      a.part_o[row * D + d] = os;
+      if (d == 0) {
+        a.part_m[row] = mx;
+        a.part_l[row] = ls;
       }
     }
   }
-  if (a.merge_cnt && a.n_part > 1) merge_if_last<G, D, kWave * kWaves>(a, b, kvh);
 }
 
 // The MFMA kernel for a layout, or nullptr where it does not apply (the dot2

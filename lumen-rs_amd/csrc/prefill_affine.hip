@@ -26,10 +26,12 @@ KernelFn pick(int D, int bk, int bv, bool h16 = false) {
 }
 
 // Dequantize-once: keys [0, total) of every (batch row, KV head), K into kd
-// and V into vd as bf16 rows [B * H_kv, total, D], with mlx::dequantize's
-// arithmetic (bf16(bf16(scale * code) + bias)). Grid: (row chunks, slab,
-// K or V); a thread writes 8 consecutive values of one row (one 16-byte
-// store). Keys [0, n0) come from segment 0, the rest from segment 1.
+// as bf16 rows [B * H_kv, total, D] with mlx::dequantize's arithmetic
+// (bf16(fma(scale, code, bias)), one rounding), V into vd as the prefill
+// kernel's V operands (those bf16 values times 2^-kVShift, in f16; see
+// v_operand_run). Grid: (row chunks, slab, K or V); a thread writes 8
+// consecutive values of one row (one 16-byte store). Keys [0, n0) come from
+// segment 0, the rest from segment 1.
 template <int D>
 __global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int bk, int bv,
                                                               uint16_t* kd, uint16_t* vd) {
@@ -47,8 +49,9 @@ __global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int 
   const int bits = isv ? bv : bk;
   const uint32_t* pw = (isv ? s.vw : s.kw) + src * (D * bits / 32);
   const int groups = D / a.gs, g = e0 / a.gs;
-  const float sc = bf16_to_f32((isv ? s.vs : s.ks)[src * groups + g]);
-  const float bi = bf16_to_f32((isv ? s.vb : s.kb)[src * groups + g]);
+  const float down = isv ? kVDown : 1.0f;
+  const float sc = bf16_to_f32((isv ? s.vs : s.ks)[src * groups + g]) * down;
+  const float bi = bf16_to_f32((isv ? s.vb : s.kb)[src * groups + g]) * down;
   // The 8 codes start on a byte (8 * bits bits from bit e0 * bits) and, at
   // every width, end within the next 64 bits of the word holding their
   // first bit: two loads, the second only when they run into it.
@@ -60,8 +63,8 @@ __global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int 
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t code = uint32_t(win >> (e * bits)) & ((1u << bits) - 1);
-    const float prod = bf16_to_f32(f32_to_bf16(sc * float(code)));
-    const uint32_t v = f32_to_bf16(prod + bi);
+    uint32_t v = f32_to_bf16(fmaf(sc, float(code), bi));
+    if (isv) v = __builtin_bit_cast(uint16_t, _Float16(bf16_to_f32(uint16_t(v))));
     if (e % 2 == 0)
       out[e / 2] = v;
     else
@@ -343,7 +346,7 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
                    int64_t(H_kv) * a.total};
     p.seg[1] = p.seg[0];
     p.n0 = a.total;
-    hipLaunchKernelGGL(pick(D, kPreBits, kPreBits), dim3(unsigned(grid)), dim3(threads), 0, st,
+    hipLaunchKernelGGL(pick(D, kPreBits, kPreF16), dim3(unsigned(grid)), dim3(threads), 0, st,
                        p);
     TQKV_LAUNCHED();
     return ok();

@@ -2,8 +2,16 @@
 //
 // What it computes (the reference's dequantized_prefill_attention,
 // gemma4_moe.rs:2382-2411): K and V are dequantized the way mlx::dequantize
-// does for bf16 (each of scale * code and + bias rounds to bf16), then
-// softmax(scale * Q K^T + mask) V with bf16 operands and f32 accumulation.
+// does for bf16 (scale * code + bias as one f32 multiply-add, rounded once
+// to bf16), then softmax(scale * Q K^T + mask) V with f32 accumulation.
+// Operands of the prefill variant: Q K^T in bf16 (the products of bf16
+// values are exact in f32), P V in f16: the weights P and the dequantized
+// bf16 values of V, the latter scaled by 2^-kVShift so |v| up to 2^24
+// stays inside f16's range (the output scales back). f16 weights carry 11
+// significant bits where the reference's bf16 SDPA rounds them to 8, so the
+// output stays within the f32-level band of the exact result. The f16
+// variant (decode over a shared prefix, head dim 512 decode) takes every
+// operand in f16.
 // The mask is build_causal_mask_abs (native_attention.rs:545-622) in absolute
 // positions: query row l sits at q_start + l, key k at k_start + k, and key k
 // is visible to query l iff k_abs <= q_abs and, with a window W,
@@ -28,10 +36,10 @@
 //   Online softmax per row: the 64-key maximum is a 16-value local max plus
 //   two lane exchanges (l ^ 16, l ^ 32); the running maximum may lag the true
 //   one by up to kTau (log2 units), so the O accumulators are rescaled only
-//   when some row moves by more. Row sums (of the bf16-rounded weights, one
+//   when some row moves by more. Row sums (of the f16-rounded weights, one
 //   v_dot2 per pair) stay per lane until the end.
 //   O^T += V^T . P^T: the score registers of key tiles 2u and 2u + 1 are,
-//   rounded to bf16, exactly the B operand (k slot 8(l / 16) + s holds key
+//   rounded to f16, exactly the B operand (k slot 8(l / 16) + s holds key
 //   32u + 4(l / 16) + s, s < 4, or 32u + 16 + 4(l / 16) + s - 4); the A
 //   operand takes the same keys of V^T from the row-major V tile with two
 //   transposing ds_read_b64_tr_b16 (the V stores are four 16-byte stores a
@@ -60,6 +68,12 @@ constexpr int kKStride = D + 8;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kTau = 8.0f;
+// V operands of the prefill variant hold v * 2^-kVShift in f16: |v| below
+// 65504 * 2^8 (about 1.68e7) fits, and values under 2^-6 in magnitude, which
+// become f16 subnormals, move by at most 2^-17.
+constexpr int kVShift = 8;
+constexpr float kVDown = 1.0f / float(1 << kVShift);
+constexpr float kVUp = float(1 << kVShift);
 
 typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -190,11 +204,6 @@ __device__ __forceinline__ uint32_t pack_h16(float lo, float hi) {
 }
 __device__ __forceinline__ h2_t as_h2(uint32_t x) { return __builtin_bit_cast(h2_t, x); }
 
-// Operand packing of a kernel variant: bf16 (the reference's prefill
-// arithmetic) or f16 (three more significand bits, for decode use).
-template <bool H16>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi);
-
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   const f2_t f = {lo, hi};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf2_t));
@@ -209,6 +218,21 @@ struct Stage {
   uint32_t s, b;  // bf16 bits; combined only when used, so the loads stay in flight
   bool ok;
 };
+
+// Width 16 stands for keys dequantized beforehand: rows of D bf16 values
+// (mlx::dequantize's bits; bf16 caches; codebook rows). Width 17: rows of D
+// f16 values already in the prefill variant's V operand form (bf16 values
+// times 2^-kVShift, written once per (batch row, KV head) by
+// dequantize_rows_kernel), which the loaders copy into LDS as they are.
+constexpr int kPreBits = 16;
+constexpr int kPreF16 = 17;
+template <int BITS>
+constexpr bool is_rows() { return BITS == kPreBits || BITS == kPreF16; }
+// 32-bit words of a loader task's run of 32 values.
+template <int BITS>
+constexpr int run_words() { return is_rows<BITS>() ? 16 : BITS; }
+static_assert(run_words<kPreBits>() == 16 && run_words<kPreF16>() == 16 && run_words<3>() == 3,
+              "a run of 32 16-bit values is 16 words; a row of D is D / 2");
 
 // Where the workgroup's loads start: the (batch row, KV head) slab of each
 // segment (uniform, so it stays in scalar registers); rows and the thread's
@@ -231,14 +255,11 @@ __device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, cons
   const int64_t r0 = int64_t(b) * s0.b_stride + int64_t(kvh) * s0.cap;
   const int64_t r1 = int64_t(b) * s1.b_stride + int64_t(kvh) * s1.cap;
   const int groups = D / gs;
-  return SlabPtrs{w0 + r0 * (D * BITS / 32), w1 + r1 * (D * BITS / 32), sc0 + r0 * groups,
+  // Words a row: D * BITS / 32 for codes, D / 2 for rows of 16-bit values.
+  constexpr int kRowWords = D * run_words<BITS>() / 32;
+  return SlabPtrs{w0 + r0 * kRowWords, w1 + r1 * kRowWords, sc0 + r0 * groups,
                   sc1 + r1 * groups,         bi0 + r0 * groups,         bi1 + r1 * groups};
 }
-
-// Width 16 stands for keys dequantized beforehand: rows of D bf16 values
-// (mlx::dequantize's bits, written once per (batch row, KV head) by
-// dequantize_rows_kernel), which the loaders copy into LDS as they are.
-constexpr int kPreBits = 16;
 
 // Loads run `run` of key kk (counted across both segments) of K or V.
 template <int D, int BITS, int NW>
@@ -246,8 +267,8 @@ __device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, con
                                            int run) {
   st.ok = kk < a.total;
   if (!st.ok) return;
-  if constexpr (BITS == kPreBits) {  // one segment of bf16 rows, no scales
-    load_words<BITS>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
+  if constexpr (is_rows<BITS>()) {  // one segment of 16-bit rows, no scales
+    load_words<16>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
     st.s = st.b = 0u;
   } else {
     const bool first = kk < a.n0;
@@ -295,15 +316,11 @@ __device__ __forceinline__ void run_codes(const uint32_t* w, float* f) {
   }
 }
 
-template <>
-__device__ __forceinline__ uint32_t pack2<false>(float lo, float hi) { return pack_bf16(lo, hi); }
-template <>
-__device__ __forceinline__ uint32_t pack2<true>(float lo, float hi) { return pack_h16(lo, hi); }
 
 // Dequantization of a run, two codes at a time; out[i] holds codes 2i (low
-// half) and 2i + 1. bf16: mlx::dequantize, bf16(bf16(scale * code) + bias):
-// scale * code is exact in f32 (8-bit by at most 8-bit significands), so
-// each rounding is a single RNE conversion, as in MLX's bf16 arithmetic.
+// half) and 2i + 1. bf16: mlx::dequantize, bf16(fma(scale, code, bias)):
+// one multiply-add in f32 (the product is exact, 8-bit by at most 8-bit
+// significands) and one RNE conversion, as MLX's kernel computes it.
 // f16: scale * code + bias in f32 (one rounding), then to f16.
 // f16 dequantization of 8- and 4-bit runs in packed f16 arithmetic, two
 // codes an instruction: a byte permute puts code c under the f16 exponent of
@@ -351,6 +368,8 @@ __device__ __forceinline__ void dequant_run(const uint32_t* w, uint32_t sb, uint
     static_assert(!H16, "dequantized rows are bf16");
 #pragma unroll
     for (int i = 0; i < 16; ++i) out[i] = w[i];
+  } else if constexpr (BITS == kPreF16) {
+    static_assert(BITS != kPreF16, "f16 rows are V operands only");
   } else if constexpr (H16 && (BITS == 8 || BITS == 4)) {
     dequant_run_h16<BITS>(w, sb, out);
   } else {
@@ -362,9 +381,7 @@ __device__ __forceinline__ void dequant_run(const uint32_t* w, uint32_t sb, uint
       if constexpr (H16) {
         out[i] = pack_h16(s * f[2 * i] + bias, s * f[2 * i + 1] + bias);
       } else {
-        const uint32_t m = pack_bf16(s * f[2 * i], s * f[2 * i + 1]);
-        out[i] = pack_bf16(__uint_as_float(m << 16) + bias,
-                           __uint_as_float(m & 0xffff0000u) + bias);
+        out[i] = pack_bf16(fmaf(s, f[2 * i], bias), fmaf(s, f[2 * i + 1], bias));
       }
     }
   }
@@ -391,9 +408,51 @@ __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int k
 // [32 run, 32 run + 32), four 16-byte stores. The products read V^T from it
 // with gfx950's transposing ds_read_b64_tr_b16. Keys past the end are zero
 // (0 * v stays finite).
+// The prefill variant's V operands of a run: mlx::dequantize's bf16 value
+// times 2^-kVShift, as f16 (exact from the bf16 value wherever the product
+// is an f16 normal). The scale and bias are scaled first, which scales the
+// fused multiply-add's result exactly, and the bf16 rounding commutes with
+// the power of two.
+template <int BITS>
+__device__ __forceinline__ void v_operand_run(const uint32_t* w, uint32_t sb, uint32_t* out) {
+  if constexpr (BITS == kPreF16) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[i] = w[i];
+  } else if constexpr (BITS == kPreBits) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      out[i] = pack_h16(__uint_as_float(w[i] << 16) * kVDown,
+                        __uint_as_float(w[i] & 0xffff0000u) * kVDown);
+  } else {
+    float f[32];
+    run_codes<BITS>(w, f);
+    const float s = __uint_as_float(sb << 16) * kVDown;
+    const float bias = __uint_as_float(sb & 0xffff0000u) * kVDown;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t m = pack_bf16(fmaf(s, f[2 * i], bias), fmaf(s, f[2 * i + 1], bias));
+      out[i] = pack_h16(__uint_as_float(m << 16), __uint_as_float(m & 0xffff0000u));
+    }
+  }
+}
+
 template <int D, int BITS, bool H16, int NW>
 __device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vs, int key, int run) {
-  store_k<D, BITS, H16>(st, Vs, key, run);
+  if constexpr (H16) {
+    store_k<D, BITS, H16>(st, Vs, key, run);
+  } else {
+    constexpr int KSTR = kKStride<D>;
+    uint32_t v[16];
+    if (st.ok) {
+      v_operand_run<BITS>(st.w, st.s | (st.b << 16), v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = 0u;
+    }
+    u32x4_t* d = reinterpret_cast<u32x4_t*>(Vs + key * KSTR + run * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = u32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+  }
 }
 
 // The V tasks' stage registers: their own set, or the K tasks' set.
@@ -570,9 +629,10 @@ void prefill_affine_kernel(const Args a) {
     // (The bf16 prefill variant shares one set: it has no registers to
     // spare, and its long tiles hide the wait behind the other wavefront.)
     constexpr bool kSplit = H16;
-    constexpr int NW = BK > BV ? BK : BV;
-    Stage<kSplit ? BK : NW> stk[NS][kPer];
-    Stage<kSplit ? BV : NW> stv_own[kSplit ? NS : 1][kPer];
+    constexpr int WK = run_words<BK>(), WV = run_words<BV>();
+    constexpr int NW = WK > WV ? WK : WV;
+    Stage<kSplit ? WK : NW> stk[NS][kPer];
+    Stage<kSplit ? WV : NW> stv_own[kSplit ? NS : 1][kPer];
     auto& stv = v_stages<kSplit>(stk, stv_own);
     SlabPtrs tp[kPer];
     bool tv[kPer];
@@ -732,18 +792,18 @@ void prefill_affine_kernel(const Args a) {
 
   #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          op8_t pb[NR];
+          h8_t pb[NR];
   #pragma unroll
           for (int j = 0; j < NR; ++j) {
             const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
-            const u32x4_t w = {pack2<H16>(p0[0], p0[1]), pack2<H16>(p0[2], p0[3]),
-                               pack2<H16>(p1[0], p1[1]), pack2<H16>(p1[2], p1[3])};
-            pb[j] = __builtin_bit_cast(op8_t, w);
+            const u32x4_t w = {pack_h16(p0[0], p0[1]), pack_h16(p0[2], p0[3]),
+                               pack_h16(p1[0], p1[1]), pack_h16(p1[2], p1[3])};
+            pb[j] = __builtin_bit_cast(h8_t, w);
             // The row sum counts the weights as rounded for the matrix cores,
             // so the output stays an exact convex combination of them.
   #pragma unroll
             for (int e = 0; e < 4; ++e)
-              lsum[j] = sum2<H16>(w[e], lsum[j]);
+              lsum[j] = sum2<true>(w[e], lsum[j]);
           }
   #pragma unroll
           for (int t2 = 0; t2 < NT; ++t2) {
@@ -756,10 +816,10 @@ void prefill_affine_kernel(const Args a) {
                                    16 * (t_base + t2) + 4 * (lr % 4);
             const u32x2_t lo = tr_read(vrow);
             const u32x2_t hi = tr_read(vrow + 16 * KSTR);
-            const op8_t va = __builtin_bit_cast(op8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
+            const h8_t va = __builtin_bit_cast(h8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
   #pragma unroll
             for (int j = 0; j < NR; ++j)
-              o[t2][j] = mma<H16>(va, pb[j], o[t2][j]);
+              o[t2][j] = mma<true>(va, pb[j], o[t2][j]);
           }
         }
       }
@@ -801,6 +861,8 @@ void prefill_affine_kernel(const Args a) {
     float tot = lsum[j];
     tot = xor32_sum(xor16_sum(tot));
     if (!rvalid[j]) continue;
+    // The prefill variant's V operands were scaled by 2^-kVShift.
+    const float vup = H16 ? 1.0f : kVUp;
     if (a.part_o) {
       const int64_t r = row0 + wave * RWO + 16 * j + lr;
       const int64_t l = r / a.G, h = int64_t(kvh) * a.G + r % a.G;
@@ -808,13 +870,13 @@ void prefill_affine_kernel(const Args a) {
       float* po = a.part_o + slot * D;
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2)
-        *reinterpret_cast<f4_t*>(po + 16 * (t_base + t2) + 4 * lg) = o[t2][j];
+        *reinterpret_cast<f4_t*>(po + 16 * (t_base + t2) + 4 * lg) = o[t2][j] * vup;
       if (lg == 0 && (!CS || wave == 0)) {
         a.part_m[slot] = m[j];
         a.part_l[slot] = tot;
       }
     } else {
-      const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+      const float inv = tot > 0.0f ? vup / tot : 0.0f;
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2) {
         const f4_t v = o[t2][j] * inv;
@@ -827,9 +889,9 @@ void prefill_affine_kernel(const Args a) {
 
 typedef void (*KernelFn)(Args);
 
-// The kernel for (D, bits_k, bits_v), bits in {2, 3, 4, 5, 6, 8}, or both
-// kPreBits for keys dequantized beforehand; null if unsupported. h16: the
-// f16-operand variant.
+// The kernel for (D, bits_k, bits_v), bits in {2, 3, 4, 5, 6, 8}, or
+// (kPreBits, kPreBits) / (kPreBits, kPreF16) for rows dequantized
+// beforehand; null if unsupported. h16: the f16-operand variant.
 KernelFn pick_d64(int bk, int bv, bool h16);
 KernelFn pick_d128(int bk, int bv, bool h16);
 KernelFn pick_d256(int bk, int bv, bool h16);
@@ -850,8 +912,10 @@ KernelFn pick_bv(int bv) {
 
 template <int D, bool H16>
 KernelFn pick_for(int bk, int bv) {
-  if constexpr (!H16)
+  if constexpr (!H16) {
     if (bk == kPreBits && bv == kPreBits) return prefill_affine_kernel<D, kPreBits, kPreBits, false>;
+    if (bk == kPreBits && bv == kPreF16) return prefill_affine_kernel<D, kPreBits, kPreF16, false>;
+  }
   switch (bk) {
     case 2: return pick_bv<D, 2, H16>(bv);
     case 3: return pick_bv<D, 3, H16>(bv);

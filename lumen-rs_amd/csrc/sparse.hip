@@ -3,8 +3,8 @@
 //
 // Page digest (PageDigest / page_digest, native_cache.rs:352-364, 407-445):
 // the elementwise min and max over each full 64-token page of the keys. The
-// keys of an affine cache are its mlx::dequantize'd rows, bf16(bf16(scale *
-// code) + bias), so min and max are exact bf16 values. One workgroup per
+// keys of an affine cache are its mlx::dequantize'd rows, bf16(fma(scale,
+// code, bias)) rounded once, so min and max are exact bf16 values. One workgroup per
 // (slab, page), one thread per channel: the 64 rows' codes of a channel come
 // from the same words for every thread of a group, so the reads coalesce.
 //
@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void digest_kernel(
       const int64_t r = slab * cap + page * kPage + t;
       const float s = bf16_to_f32(ks[r * groups + g]), b = bf16_to_f32(kb[r * groups + g]);
       const float c = float(code_at(kw + r * words, d, bits));
-      const float v = bf16_to_f32(f32_to_bf16(bf16_to_f32(f32_to_bf16(s * c)) + b));
+      const float v = bf16_to_f32(f32_to_bf16(fmaf(s, c, b)));
       mn = fminf(mn, v);
       mx = fmaxf(mx, v);
     }

@@ -28,6 +28,7 @@ struct Scratch {
   void* ptr = nullptr;
   size_t bytes = 0;
   std::vector<void*> retired;  // outgrown buffers, freed by tqkv_scratch_release
+  size_t retired_bytes = 0;
 };
 std::mutex g_scratch_mu;
 std::vector<Scratch> g_scratch;
@@ -55,7 +56,10 @@ int32_t scratch_for_current_device(size_t bytes, void** out) {
         return fail(TQKV_ENOMEM, "scratch hipMalloc of %zu bytes failed", bytes);
       }
     }
-    if (s.ptr) s.retired.push_back(s.ptr);
+    if (s.ptr) {
+      s.retired.push_back(s.ptr);
+      s.retired_bytes += s.bytes;
+    }
     s.ptr = p;
     s.bytes = want;
   }
@@ -74,12 +78,20 @@ int32_t scratch_release_all() {
     TQKV_HIP(hipDeviceSynchronize());
     for (void* p : s.retired) (void)hipFree(p);
     s.retired.clear();
+    s.retired_bytes = 0;
     (void)hipFree(s.ptr);
     s.ptr = nullptr;
     s.bytes = 0;
   }
   TQKV_HIP(hipSetDevice(dev));
   return TQKV_OK;
+}
+
+size_t scratch_held_bytes() {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  size_t n = 0;
+  for (const Scratch& s : g_scratch) n += s.bytes + s.retired_bytes;
+  return n;
 }
 
 }  // namespace tqkv
@@ -107,6 +119,8 @@ int32_t tqkv_scratch_release(void) {
   return tqkv::ok();
 }
 
-int32_t tqkv_version(void) { return 100; }
+size_t tqkv_scratch_bytes(void) { return tqkv::scratch_held_bytes(); }
+
+int32_t tqkv_version(void) { return TQKV_ABI_VERSION; }
 
 }  // extern "C"

@@ -1434,10 +1434,13 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
                 (long long)cap);
   if (bits_k < 1 || bits_k > 8 || bits_v < 1 || bits_v > 8)
     return fail(TQKV_EUNSUPPORTED, "bits %d/%d", bits_k, bits_v);
-  // A lane loads D / 64 value codes at once (up to 4-byte words).
+  // A lane loads D / 64 value codes at once (up to 4-byte words); key rows
+  // are read 16 bytes a load (rows of D >= 64 bytes keep that alignment).
   const int v_align = D >= 256 ? 4 : D >= 128 ? 2 : 1;
   if (reinterpret_cast<uintptr_t>(v_codes) % v_align != 0)
     return fail(TQKV_EINVAL_ARG, "v_codes must be %d-byte aligned", v_align);
+  if (reinterpret_cast<uintptr_t>(k_codes) % 16 != 0)
+    return fail(TQKV_EINVAL_ARG, "k_codes must be 16-byte aligned");
   const int G = H / H_kv;
   // Splits of 512 tokens (at most 64); with 128 or more (batch row, KV head)
   // units the grid fills the chip with splits of 1024 (at most 32), which

@@ -14,6 +14,7 @@ pub const TQKV_EDEVICE: i32 = 4;
 pub const TQKV_ENOMEM: i32 = 5;
 pub const TQKV_EINVAL_ARG: i32 = 6;
 pub const TQKV_ECORRUPT: i32 = 7;
+pub const TQKV_ABI_VERSION: i32 = 200;
 pub const TQKV_NOALLOC_SCRATCH_BYTES: i32 = 33554432;
 pub const TQKV_CACHE_BF16: i32 = 0;
 pub const TQKV_CACHE_AFFINE: i32 = 1;
@@ -115,6 +116,7 @@ extern "C" {
     pub fn tqkv_last_error() -> *const c_char;
     pub fn tqkv_version() -> i32;
     pub fn tqkv_scratch_release() -> i32;
+    pub fn tqkv_scratch_bytes() -> usize;
     pub fn tqkv_affine_quantize(x: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits: i32, packed: *mut u32, scales: *mut u16, biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_quantize_kv(k: *const u16, v: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits_k: i32, bits_v: i32, k_packed: *mut u32, k_scales: *mut u16, k_biases: *mut u16, v_packed: *mut u32, v_scales: *mut u16, v_biases: *mut u16, dst_cap: i64, dst_start: i64, stream: tqkv_stream) -> i32;
     pub fn tqkv_affine_quantize_rotated(x: *const u16, n_slabs: i64, s: i64, dim: i32, group_size: i32, bits: i32, rotation: *const f32, packed: *mut u32, scales: *mut u16, biases: *mut u16, dst_cap: i64, dst_start: i64, rotated: *mut u16, stream: tqkv_stream) -> i32;
@@ -131,6 +133,7 @@ extern "C" {
     pub fn tqkv_decode_attend_affine_sparse(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, scale: f32, seg: *const tqkv_affine_seg, key_min: *const u16, key_max: *const u16, max_pages: i64, pages: i64, keep: i32, out: *mut u16, chosen_out: *mut i32, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
     pub fn tqkv_sparse_workspace_size(B: i32, H: i32, H_kv: i32, D: i32, total_tokens: i64, keep: i32) -> usize;
     pub fn tqkv_decode_kernel_name(H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32) -> *const c_char;
+    pub fn tqkv_decode_kernel_for_rows(H: i32, H_kv: i32, D: i32, group_size: i32, bits_k: i32, bits_v: i32, max_rows: i64) -> *const c_char;
     pub fn tqkv_decode_attend_codebook(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, scale: f32, rotation: *const f32, centroids_k: *const f32, bits_k: i32, centroids_v: *const f32, bits_v: i32, k_codes: *const u8, k_sigma: *const f32, v_codes: *const u8, v_sigma: *const f32, cap: i64, n: i64, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;
     pub fn tqkv_decode_codebook_workspace_size(B: i32, H: i32, D: i32, total_tokens: i64) -> usize;
     pub fn tqkv_decode_attend_codebook_qjl(q: *const u16, B: i32, H: i32, H_kv: i32, D: i32, scale: f32, rotation: *const f32, centroids_k: *const f32, bits_k: i32, centroids_v: *const f32, bits_v: i32, k_codes: *const u8, k_sigma: *const f32, k_signs: *const u32, k_rnorm: *const f32, qjl: *const f32, qjl_m: i32, v_codes: *const u8, v_sigma: *const f32, cap: i64, n: i64, out: *mut u16, workspace: *mut c_void, workspace_bytes: usize, stream: tqkv_stream) -> i32;

@@ -92,6 +92,7 @@ _SIGS = {
                                             I64, I64, I32, I64, P, P, SZ, P]),
     "tqkv_prefill_workspace_size": (SZ, [I32, I32, I32, I64]),
     "tqkv_scratch_release": (I32, []),
+    "tqkv_scratch_bytes": (SZ, []),
     "tqkv_empty_launch": (I32, [I32, P]),
     "tqkv_decode_attend_affine": (I32, [P, I32, I32, I32, I32, I32, I32, I32, F32,
                                         ctypes.POINTER(AffineSeg), I32, P, P, SZ, P]),
@@ -105,6 +106,7 @@ _SIGS = {
                                          P]),
     "tqkv_decode_workspace_size": (SZ, [I32, I32, I32, I32, I64]),
     "tqkv_decode_kernel_name": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32]),
+    "tqkv_decode_kernel_for_rows": (ctypes.c_char_p, [I32, I32, I32, I32, I32, I32, I64]),
     "tqkv_page_digest_affine": (I32, [P, P, P, I64, I64, I32, I32, I32, I64, I64, P, P, I64, P]),
     "tqkv_sparse_keep_pages": (I64, [I64]),
     "tqkv_page_select": (I32, [P, I32, I32, I32, I32, P, P, I64, I64, I32, P, P, SZ, P]),
@@ -441,6 +443,11 @@ def scratch_release():
     check(lib().tqkv_scratch_release())
 
 
+def scratch_bytes():
+    """Bytes of per-device scratch the library holds (tqkv_scratch_bytes)."""
+    return int(lib().tqkv_scratch_bytes())
+
+
 def empty_launch(workgroups=256, stream=None):
     check(lib().tqkv_empty_launch(workgroups, stream))
 
@@ -448,6 +455,11 @@ def empty_launch(workgroups=256, stream=None):
 def decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v):
     """"mfma", "dot2" or "" (unsupported) for a decode layout."""
     return lib().tqkv_decode_kernel_name(H, H_kv, D, gs, bits_k, bits_v).decode()
+
+
+def decode_kernel_for_rows(H, H_kv, D, gs, bits_k, bits_v, max_rows):
+    """The decode kernel for a context whose longest segment holds max_rows."""
+    return lib().tqkv_decode_kernel_for_rows(H, H_kv, D, gs, bits_k, bits_v, max_rows).decode()
 
 
 def page_digest_affine(kt, n_slabs, cap, dim, gs, bits, page_from, page_to, key_min, key_max,

@@ -116,9 +116,10 @@ void oracle_attend_bf16(const uint16_t* q, const uint16_t* K, const uint16_t* V,
 
 // Affine-quantized K/V triples [B, H_kv, N, .] dequantized, then attended.
 // dequant_f32 = 0: mlx::dequantize to bf16 (the reference's prefill path,
-// gemma4_moe.rs:2394-2399) with two bf16 roundings; 1: exact f32
-// scale * code + bias (its decode paths); 2: mlx::dequantize read as one
-// rounding of the f32 result. K and V may use different bit widths.
+// gemma4_moe.rs:2394-2399), one rounding of the fused f32 multiply-add; 1:
+// exact f32 scale * code + bias (its decode paths); 2: mlx::dequantize read
+// as two bf16 roundings (the secondary reading). K and V may use different
+// bit widths.
 void oracle_attend_affine(const uint16_t* q, const uint32_t* kw, const uint16_t* ks,
                           const uint16_t* kb, const uint32_t* vw, const uint16_t* vs,
                           const uint16_t* vb, int B, int H, int H_kv, int L, size_t N, int D,

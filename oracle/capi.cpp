@@ -197,10 +197,24 @@ void oracle_affine_dequantize(const uint32_t* packed, const uint16_t* scales,
                               uint16_t* out) {
   affine_dequantize_rows(packed, scales, biases, rows, dim, gs, bits, out);
 }
-void oracle_affine_dequantize_one_rounding(const uint32_t* packed, const uint16_t* scales,
-                                           const uint16_t* biases, size_t rows, int dim, int gs,
-                                           int bits, uint16_t* out) {
+void oracle_affine_dequantize_two_roundings(const uint32_t* packed, const uint16_t* scales,
+                                            const uint16_t* biases, size_t rows, int dim, int gs,
+                                            int bits, uint16_t* out) {
   affine_dequantize_rows(packed, scales, biases, rows, dim, gs, bits, out, true);
+}
+void oracle_affine_quantize_f32(const float* w, size_t rows, int dim, int gs, int bits,
+                                uint32_t* packed, float* scales, float* biases, int round_mode,
+                                int wmax0, int clip_low) {
+  AffineOpts ao;
+  ao.round = round_mode ? RoundMode::HalfEven : RoundMode::HalfAway;
+  ao.wmax_starts_at_zero = wmax0 != 0;
+  ao.clip_low = clip_low != 0;
+  affine_quantize_rows_f32(w, rows, dim, gs, bits, packed, scales, biases, ao);
+}
+void oracle_affine_dequantize_f32(const uint32_t* packed, const float* scales,
+                                  const float* biases, size_t rows, int dim, int gs, int bits,
+                                  float* out) {
+  affine_dequantize_rows_f32(packed, scales, biases, rows, dim, gs, bits, out);
 }
 void oracle_write_code(uint32_t* words, size_t i, int bits, uint32_t code) {
   write_code(words, i, bits, code);

@@ -138,13 +138,20 @@ struct AffineOpts {
 void affine_quantize_rows(const uint16_t* w, size_t rows, int dim, int gs, int bits,
                           uint32_t* packed, uint16_t* scales, uint16_t* biases,
                           const AffineOpts& o = AffineOpts());
-// MLX dequantize: bf16(bf16(scale * code) + bias), two bf16 roundings (the
-// restatement), or with one_rounding bf16(scale * code + bias) from f32
-// arithmetic, the other reading of MLX's kernel. Nothing in the reference
-// records either, so tests that depend on this rounding check both.
+// The same over f32 rows with f32 scales and biases (MLX's quantize of an
+// f32 tensor; w_min starts from FLT_MAX in the Metal kernel).
+void affine_quantize_rows_f32(const float* w, size_t rows, int dim, int gs, int bits,
+                              uint32_t* packed, float* scales, float* biases,
+                              const AffineOpts& o = AffineOpts());
+// MLX dequantize to bf16: bf16(fma(scale, code, bias)), one rounding (what
+// the reference's fixture records for MLX's kernel, see affine.cpp), or
+// with two_roundings bf16(bf16(scale * code) + bias), the secondary reading.
 void affine_dequantize_rows(const uint32_t* packed, const uint16_t* scales,
                             const uint16_t* biases, size_t rows, int dim, int gs,
-                            int bits, uint16_t* out, bool one_rounding = false);
+                            int bits, uint16_t* out, bool two_roundings = false);
+// MLX dequantize of an f32-scaled table: fmaf(scale, code, bias).
+void affine_dequantize_rows_f32(const uint32_t* packed, const float* scales, const float* biases,
+                                size_t rows, int dim, int gs, int bits, float* out);
 uint32_t read_code(const uint32_t* words, size_t i, int bits);
 // Code i of an LSB-first u32 stream (offload/lowbit.rs:220-240 write_code).
 void write_code(uint32_t* words, size_t i, int bits, uint32_t code);

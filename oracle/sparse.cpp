@@ -4,8 +4,8 @@
 // PageDigest (native_cache.rs:352-364, page_digest :407-445): elementwise
 // min and max of the keys over each full 64-token page, [B, H_kv, pages, D].
 // The reference digests the bf16 keys its attention reads; the keys of an
-// affine cache here are its mlx::dequantize'd rows (bf16(bf16(s c) + b)),
-// so min and max are exact bf16 values.
+// affine cache here are its mlx::dequantize'd rows (bf16(fma(s, c, b)),
+// one rounding), so min and max are exact bf16 values.
 //
 // sdpa_page_sparse (native_attention.rs:210-291): per (batch row, KV head),
 // page p's bound is the max over the KV head's query group of

@@ -53,7 +53,9 @@ def lib():
             "oracle_attend_values": (None, [P, P, SZ, P, P, P, P, P]),
             "oracle_affine_quantize": (None, [P, SZ, I, I, I, P, P, P, I, I, I]),
             "oracle_affine_dequantize": (None, [P, P, P, SZ, I, I, I, P]),
-            "oracle_affine_dequantize_one_rounding": (None, [P, P, P, SZ, I, I, I, P]),
+            "oracle_affine_dequantize_two_roundings": (None, [P, P, P, SZ, I, I, I, P]),
+            "oracle_affine_quantize_f32": (None, [P, SZ, I, I, I, P, P, P, I, I, I]),
+            "oracle_affine_dequantize_f32": (None, [P, P, P, SZ, I, I, I, P]),
             "oracle_write_code": (None, [P, SZ, I, U32]),
             "oracle_read_code": (U32, [P, SZ, I]),
             "oracle_mask_allowed": (I, [SZ, SZ, L]),
@@ -179,16 +181,43 @@ def affine_quantize(w_bf16, gs, bits, round_mode=0, wmax0=1, clip_low=0):
     return packed, scales, biases
 
 
-def affine_dequantize(packed, scales, biases, gs, bits, one_rounding=False):
-    """mlx::dequantize to bf16: two bf16 roundings (the restatement), or
-    one_rounding=True, the other reading (f32 arithmetic, one rounding)."""
+def affine_dequantize(packed, scales, biases, gs, bits, two_roundings=False):
+    """mlx::dequantize to bf16: bf16(fma(scale, code, bias)), one rounding
+    (what the reference's qwen4exp_tiny fixture records for MLX), or with
+    two_roundings=True bf16(bf16(scale * code) + bias), the secondary
+    reading."""
     d = packed.shape[-1] * 32 // bits
     rows = packed.size // packed.shape[-1]
     out = np.empty(packed.shape[:-1] + (d,), np.uint16)
-    fn = lib().oracle_affine_dequantize_one_rounding if one_rounding \
+    fn = lib().oracle_affine_dequantize_two_roundings if two_roundings \
         else lib().oracle_affine_dequantize
     fn(ptr(np.ascontiguousarray(packed)), ptr(np.ascontiguousarray(scales)),
        ptr(np.ascontiguousarray(biases)), rows, d, gs, bits, ptr(out))
+    return out
+
+
+def affine_quantize_f32(w, gs, bits, round_mode=0, wmax0=1, clip_low=0):
+    """MLX's quantize of f32 rows: (packed u32, scales f32, biases f32)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    d = w.shape[-1]
+    rows = w.size // d
+    packed = np.zeros(w.shape[:-1] + (d * bits // 32,), np.uint32)
+    scales = np.zeros(w.shape[:-1] + (d // gs,), np.float32)
+    biases = np.zeros_like(scales)
+    lib().oracle_affine_quantize_f32(ptr(w), rows, d, gs, bits, ptr(packed), ptr(scales),
+                                     ptr(biases), round_mode, wmax0, clip_low)
+    return packed, scales, biases
+
+
+def affine_dequantize_f32(packed, scales, biases, gs, bits):
+    """MLX's dequantize of an f32-scaled table: fmaf(scale, code, bias)."""
+    d = packed.shape[-1] * 32 // bits
+    rows = packed.size // packed.shape[-1]
+    out = np.empty(packed.shape[:-1] + (d,), np.float32)
+    lib().oracle_affine_dequantize_f32(ptr(np.ascontiguousarray(packed, np.uint32)),
+                                       ptr(np.ascontiguousarray(scales, np.float32)),
+                                       ptr(np.ascontiguousarray(biases, np.float32)), rows, d,
+                                       gs, bits, ptr(out))
     return out
 
 
@@ -261,8 +290,9 @@ def attend_bf16(q, K, V, scale, causal=False, q_start=0, first_held=0, window=-1
 def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0, first_held=0,
                   window=-1, dequant="f32"):
     """dequant="f32": exact scale * code + bias (the reference's decode paths);
-    "bf16": mlx::dequantize to bf16 first (its prefill path), two roundings;
-    "bf16_1r": the same read as one rounding of the f32 result."""
+    "bf16": mlx::dequantize to bf16 first (its prefill path), one rounding of
+    the fused multiply-add; "bf16_2r": the same read as two bf16 roundings
+    (the secondary reading)."""
     B, H, Lq, D = q.shape
     Hkv, N = kt[0].shape[1], kt[0].shape[2]
     of = np.empty((B, H, Lq, D), np.float32)
@@ -272,7 +302,7 @@ def attend_affine(q, kt, vt, gs, bits_k, bits_v, scale, causal=False, q_start=0,
     lib().oracle_attend_affine(ptr(np.ascontiguousarray(q)), *[ptr(a) for a in c], B, H, Hkv, Lq,
                                N, D, gs, bits_k, bits_v, scale, int(causal), q_start, first_held,
                                window, ptr(of), ptr(ob), ptr(lse),
-                               {"bf16": 0, "f32": 1, "bf16_1r": 2}[dequant])
+                               {"bf16": 0, "f32": 1, "bf16_2r": 2}[dequant])
     return of, ob, lse
 
 

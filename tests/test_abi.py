@@ -26,7 +26,37 @@ def test_status_strings_without_a_gpu():
     import tqkv
     assert tqkv.status_name(tqkv.EUNSUPPORTED) == "TQKV_EUNSUPPORTED"
     assert tqkv.status_name(12345) == "TQKV_UNKNOWN"
-    assert tqkv.lib().tqkv_version() >= 100
+    assert tqkv.lib().tqkv_version() == 200
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """The ctypes mirrors of the header's structs have the C compiler's sizes
+    and field offsets, and the library reports the header's ABI version."""
+    import ctypes
+    import subprocess
+    import tqkv
+    structs = {"tqkv_cache_config": tqkv.CacheConfig, "tqkv_cache_view": tqkv.CacheView,
+               "tqkv_cache_state": tqkv.CacheState, "tqkv_tq_config": tqkv.TqConfig}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "tqkv.h"', "int main(void) {",
+             '  printf("version %d\\n", TQKV_ABI_VERSION);']
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in py._fields_:
+            lines.append(f'  printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "abi.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "abi"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {tuple(l.split()[:-1]): int(l.split()[-1]) for l in out if l}
+    assert got[("version",)] == tqkv.lib().tqkv_version()
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for fname, _ in py._fields_:
+            assert got[(cname, fname)] == getattr(py, fname).offset, (cname, fname)
+    assert got[("tqkv_cache_config", "size")] == 72
 
 
 def test_argument_checks_come_before_any_launch():
@@ -65,3 +95,19 @@ def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):
     assert tqkv.decode_kernel_name(64, 8, 256, 64, 4, 4) == "mfma"  # 8 heads: 2 MFMA launches of 4
     monkeypatch.setenv("TQKV_DECODE_KERNEL", "dot2")
     assert tqkv.decode_kernel_name(16, 8, 256, 64, 3, 3) == "dot2"
+
+
+def test_long_segments_take_the_dot2_kernel(monkeypatch):
+    """The MFMA kernel addresses a unit's rows with 32-bit byte offsets: a
+    segment of max_rows rows with max_rows * D >= 2^31 takes the dot2 kernel,
+    and tqkv_cache_append_decode checks this with the real segment lengths
+    before it commits an update (a fused append needs the MFMA kernel)."""
+    import tqkv
+    monkeypatch.delenv("TQKV_DECODE_KERNEL", raising=False)
+    for D in (64, 128, 256):
+        edge = (1 << 31) // D
+        assert tqkv.decode_kernel_for_rows(16, 8, D, 64, 4, 4, edge - 1) == "mfma"
+        assert tqkv.decode_kernel_for_rows(16, 8, D, 64, 4, 4, edge) == "dot2"
+    assert tqkv.decode_kernel_for_rows(16, 8, 256, 64, 4, 4, 0) == \
+        tqkv.decode_kernel_name(16, 8, 256, 64, 4, 4)
+    assert tqkv.decode_kernel_for_rows(16, 8, 256, 64, 4, 4, -1) == ""

@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+from bars import check_bf16
 from inputs import kv_bf16
 
 pytestmark = pytest.mark.gpu
@@ -73,17 +74,7 @@ class Twin:
 
 
 def check_close(got_bf16, want_f32):
-    """The decode bar (2e-2 max-abs, 1e-3 mean-abs) on the error beyond the
-    bf16 rounding of the output itself: contexts of a few keys give outputs of
-    magnitude 1-8 (single value rows with outlier channels), where rounding
-    alone averages ~1e-3."""
-    got = O.bf16_to_f32(got_bf16).astype(np.float64)
-    raw = np.abs(got - want_f32)
-    half_ulp = 0.5 * 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want_f32), 2.0 ** -126))) - 7)
-    err = np.maximum(raw - half_ulp, 0.0)
-    print(f"[append-decode] max_abs={raw.max():.3e} mean_abs={raw.mean():.3e} "
-          f"beyond rounding: max={err.max():.3e} mean={err.mean():.3e}", flush=True)
-    assert err.max() <= 2e-2 and err.mean() <= 1e-3
+    check_bf16(got_bf16, want_f32, "append-decode")
 
 
 def want_of(q, K, V, gs, bk, bv, scale):

@@ -15,13 +15,12 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+from bars import check_bf16
 from inputs import kv_bf16
 from test_oracle_golden import RECORDED
 
 pytestmark = pytest.mark.gpu
 
-MAX_ABS = 2e-2
-MEAN_ABS = 1e-3
 
 
 @pytest.fixture(scope="module")
@@ -163,12 +162,7 @@ def test_rewind_refusals(T):
 
 
 def check_close(got_bf16, want_f32):
-    got = O.bf16_to_f32(got_bf16).astype(np.float64)
-    raw = np.abs(got - want_f32)
-    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want_f32), 2.0 ** -126))) - 7)
-    err = np.maximum(raw - 0.5 * ulp, 0.0)
-    print(f"[cache-decode] max_abs={raw.max():.3e} mean_abs={raw.mean():.3e}", flush=True)
-    assert err.max() <= MAX_ABS and raw.mean() <= MEAN_ABS
+    check_bf16(got_bf16, want_f32, "cache-decode")
 
 
 def decode(T, cache, q, H_, scale):
@@ -332,10 +326,9 @@ def test_codebook_cache_append_and_decode(T, bits, qjl_words):
                                      R, phi[:m], m, D ** -0.5).astype(np.float64)
     else:
         want = attention_f64(qr, Kr, Vr, D ** -0.5, Hq // Hkv) @ R.astype(np.float64)  # R^T o
-    got = O.bf16_to_f32(decode(T, c, q, Hq, D ** -0.5)).reshape(B, Hq, D)
-    err = np.abs(got - want)
-    print(f"[codebook-decode] bits={bits} max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
-    assert err.max() <= 2e-2 and err.mean() <= 1e-3
+    got_b = decode(T, c, q, Hq, D ** -0.5).reshape(B, Hq, D)
+    check_bf16(got_b, want, f"codebook-decode bits={bits}")
+    got = O.bf16_to_f32(got_b)
     # A coarse sanity bar against attention over the unquantized K/V (the
     # output averages many values, so codebook noise weighs more in it than
     # in any one score).
@@ -377,11 +370,7 @@ def test_codebook_decode_direct(T, B, Hkv, G, D, N, bits):
     Vr = c64[vc] * vs[..., None]
     qr = O.bf16_to_f32(q).reshape(B, H, D).astype(np.float64) @ R.astype(np.float64).T
     want = attention_f64(qr, Kr, Vr, D ** -0.5, G) @ R.astype(np.float64)
-    got = O.bf16_to_f32(out.numpy()).reshape(B, H, D)
-    err = np.abs(got - want)
-    print(f"[codebook-direct] B={B} Hkv={Hkv} D={D} max_abs={err.max():.3e} "
-          f"mean_abs={err.mean():.3e}", flush=True)
-    assert err.max() <= 2e-2 and err.mean() <= 1e-3
+    check_bf16(out.numpy().reshape(B, H, D), want, f"codebook-direct B={B} Hkv={Hkv} D={D}")
 
 
 def test_codebook_decode_rejects_unaligned_values(T):
@@ -398,3 +387,20 @@ def test_codebook_decode_rejects_unaligned_values(T):
         T.decode_attend_codebook(q.ptr, B, H, Hkv, D, 1.0, R.ptr, cent.ptr, 3, cent.ptr, 3,
                                  codes.ptr, sig.ptr, codes.ptr + 1, sig.ptr, N, N, out.ptr)
     assert e.value.status == T.EINVAL_ARG
+
+
+def test_codebook_decode_rejects_unaligned_keys(T):
+    """Key rows are read 16 bytes a load: a key code pointer off that
+    alignment is refused before any launch (values aligned)."""
+    B, Hkv, H, D, N = 1, 1, 2, 128, 64
+    q = T.DeviceArray((B, H, 1, D), np.uint16)
+    codes = T.DeviceArray((N * D + 16,), np.uint8)
+    sig = T.DeviceArray((N,), np.float32)
+    R = T.DeviceArray.of(T.rotation_matrix(D, 42))
+    cent = T.DeviceArray.of(T.lloyd_max(3)[1].astype(np.float32))
+    out = T.DeviceArray((B, H, 1, D), np.uint16)
+    for off in (2, 8):
+        with pytest.raises(T.TqkvError) as e:
+            T.decode_attend_codebook(q.ptr, B, H, Hkv, D, 1.0, R.ptr, cent.ptr, 3, cent.ptr, 3,
+                                     codes.ptr + off, sig.ptr, codes.ptr, sig.ptr, N, N, out.ptr)
+        assert e.value.status == T.EINVAL_ARG

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+from bars import check_bf16
 from inputs import kv_bf16
 
 pytestmark = pytest.mark.gpu
@@ -29,16 +30,7 @@ def T():
 
 
 def check(got_bf16, want, tag):
-    got = O.bf16_to_f32(got_bf16).astype(np.float64)
-    want = np.asarray(want, np.float64)
-    raw = np.abs(got - want)
-    big = np.ones(want.shape, bool)
-    half = 0.5 * 2.0 ** (np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
-    err = np.where(big, np.maximum(raw - half, 0.0), raw)
-    print(f"[cb-prefill] {tag}: max_abs={raw.max():.3e} bar_err={err.max():.3e} "
-          f"mean_abs={raw.mean():.3e}", flush=True)
-    assert np.all(np.isfinite(got))
-    assert err.max() <= 2e-2 and raw.mean() <= 1e-3
+    check_bf16(got_bf16, want, f"cb-prefill {tag}")
 
 
 def dequant(cent, codes, sigma):

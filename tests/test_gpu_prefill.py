@@ -4,8 +4,8 @@ dequantization the reference's prefill path uses (mlx::dequantize to bf16,
 gemma4_moe.rs:2394-2399) and its absolute-position mask
 (build_causal_mask_abs, native_attention.rs:545-622).
 
-Bar: 2e-2 max-abs (beyond half a bf16 step of the expected value) and 1e-3
-mean-abs, as for decode. Cases cover the reference's prefill branches
+Bar: 2e-2 max-abs and 1e-3 mean-abs in bf16 (|got - RN_bf16(expected)|,
+tests/bars.py), as for decode. Cases cover the reference's prefill branches
 (causal aligned, sliding window over a rotating view, unmasked), GQA groups
 that do not divide the 128-row block (G = 3), rows that see no key, a shared
 prefix segment, every head dim the kernel takes and mixed K/V widths, and the
@@ -18,13 +18,10 @@ import pytest
 
 import oracle_lib as O
 from inputs import kv_bf16
-from test_gpu_affine import _cache, bf16_ulp
+from bars import check_bf16
+from test_gpu_affine import _cache
 
 pytestmark = pytest.mark.gpu
-
-MAX_ABS = 2e-2
-MEAN_ABS = 1e-3
-
 
 @pytest.fixture(scope="module")
 def T():
@@ -34,36 +31,20 @@ def T():
 
 
 def want_mlx(q, kh, vh, gs, bk, bv, scale, **kw):
-    """The oracle under both readings of mlx::dequantize's bf16 rounding
-    (two roundings, or one of the f32 result): nothing in the reference
-    records which one MLX performs, so the kernel must meet the bar against
-    either."""
+    """The oracle over the mlx::dequantize'd cache (one rounding of the fused
+    multiply-add, as the reference's fixture records MLX's kernel), and over
+    the secondary reading (two bf16 roundings), printed only."""
     return tuple(O.attend_affine(q, kh, vh, gs, bk, bv, scale, dequant=d, **kw)[0]
-                 for d in ("bf16", "bf16_1r"))
+                 for d in ("bf16", "bf16_2r"))
 
 
 def check(got_bf16, wants, tag):
-    """The bar (max-abs beyond half a bf16 step of the expected value, and
-    mean-abs; the raw max-abs is printed: the bf16 softmax weights of the
-    product, the reference SDPA's own operand type, move an output by up to
-    2^-8 of its value range, which on x10 outlier channels passes 2e-2 raw)
-    against the restatement's two-rounding dequantization; against
-    the other reading, the bar beyond the two readings' own difference,
-    which on a sharp softmax (a few keys carrying all the weight) exceeds
-    the bar by itself: there parity depends on which rounding MLX performs,
-    which nothing in the reference records."""
+    """The bar in bf16 (bars.check_bf16) against the primary reading; the
+    raw distance to the secondary reading is printed beside it."""
+    check_bf16(got_bf16, wants[0], f"prefill {tag}")
     got = O.bf16_to_f32(got_bf16).astype(np.float64)
-    assert np.all(np.isfinite(got))
-    wants = wants if isinstance(wants, tuple) else (wants,)
-    for i, want_f32 in enumerate(wants):
-        raw = np.abs(got - want_f32)
-        gap = np.abs(np.asarray(want_f32, np.float64) - wants[0]) if i else np.zeros_like(raw)
-        big = np.ones(np.shape(want_f32), bool)
-        err = np.where(big, np.maximum(raw - 0.5 * bf16_ulp(want_f32), 0.0), raw) - gap
-        print(f"[prefill] {tag} candidate {i}: max_abs={raw.max():.3e} "
-              f"bar_err={err.max():.3e} mean_abs={raw.mean():.3e} "
-              f"candidate_gap_max={gap.max():.3e}", flush=True)
-        assert err.max() <= MAX_ABS and raw.mean() <= MEAN_ABS + gap.mean()
+    print(f"[prefill {tag}] secondary reading: max_abs={np.abs(got - wants[1]).max():.3e}",
+          flush=True)
 
 
 def run(T, q, segs_host, B, H, Hkv, L, D, gs, bk, bv, scale, q_start, k_start, causal, window):

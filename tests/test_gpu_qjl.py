@@ -18,6 +18,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
+from bars import check_bf16
 from inputs import kv_bf16
 
 pytestmark = pytest.mark.gpu
@@ -174,7 +175,4 @@ def test_codebook_decode_with_qjl(T, B, H, Hkv, D, N, bits, m):
     want = O.attend_codebook_qjl(q, sh(kc.numpy(), D), sh(ks.numpy()), sh(ksg.numpy(), W),
                                  sh(krn.numpy()), sh(vc.numpy(), D), sh(vs.numpy()), cf, cf, R,
                                  phi, m, D ** -0.5)
-    got = O.bf16_to_f32(out.numpy()).reshape(B, H, D)
-    err = np.abs(got - want)
-    print(f"[qjl-decode] max_abs={err.max():.3e} mean_abs={err.mean():.3e}", flush=True)
-    assert err.max() <= 2e-2 and err.mean() <= 1e-3
+    check_bf16(out.numpy().reshape(B, H, D), want, "qjl-decode")

@@ -54,16 +54,17 @@ def test_digest_bit_exact_in_pieces(T, D, gs, bits):
     gmin, gmax = kmin.numpy(), kmax.numpy()
     assert np.array_equal(gmin[:, :, :pages], wmin) and np.array_equal(gmax[:, :, :pages], wmax)
     assert np.all(gmin[:, :, pages:] == 0x7777) and np.all(gmax[:, :, pages:] == 0x7777)
-    # Bit-exact with the oracle's reading of mlx::dequantize (two bf16
-    # roundings). Under the other reading (one rounding of the f32 result)
-    # a page's min / max moves by at most the largest difference between the
-    # two readings over the page's keys at that channel (min and max are
-    # 1-Lipschitz in the largest difference): the digest stays within it.
+    # Bit-exact with the oracle's reading of mlx::dequantize (one rounding
+    # of the fused multiply-add). Against the secondary reading (two bf16
+    # roundings) a page's min / max moves by at most the largest difference
+    # between the two readings over the page's keys at that channel (min and
+    # max are 1-Lipschitz in the largest difference): the digest stays
+    # within it.
     tr = tuple(a[:, :, :pages * PAGE] for a in kh)
-    dq1 = O.bf16_to_f32(O.affine_dequantize(*tr, gs, bits, one_rounding=True)).astype(np.float64)
-    dq2 = O.bf16_to_f32(O.affine_dequantize(*tr, gs, bits)).astype(np.float64)
+    dq1 = O.bf16_to_f32(O.affine_dequantize(*tr, gs, bits)).astype(np.float64)
+    dq2 = O.bf16_to_f32(O.affine_dequantize(*tr, gs, bits, two_roundings=True)).astype(np.float64)
     gap = np.abs(dq1 - dq2).reshape(B, Hkv, pages, PAGE, D).max(axis=3)
-    pg = dq1.reshape(B, Hkv, pages, PAGE, D)
+    pg = dq2.reshape(B, Hkv, pages, PAGE, D)
     for got, alt in ((gmin, pg.min(axis=3)), (gmax, pg.max(axis=3))):
         g = O.bf16_to_f32(got[:, :, :pages]).astype(np.float64)
         assert np.all(np.abs(g - alt) <= gap)

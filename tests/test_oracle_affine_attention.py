@@ -83,16 +83,17 @@ def test_half_way_ties_round_away_from_zero(bits):
     assert not np.array_equal(p2, p)
 
 
-def test_dequantize_candidates_differ():
-    # The two readings of mlx::dequantize (two bf16 roundings, or one of the
-    # f32 result) must disagree on ordinary inputs, or checking prefill and
-    # the page digest against both would test nothing; where they agree with
-    # each other they agree with the exact value rounded once.
+def test_dequantize_readings_differ():
+    # The primary reading of mlx::dequantize (one rounding of the fused
+    # multiply-add, what the reference's qwen4exp_tiny fixture records) and
+    # the secondary one (two bf16 roundings) must disagree on ordinary
+    # inputs, or the fixture test would not tell them apart at bf16; the
+    # primary equals the exact value rounded once.
     w = _bf16_normal((256, 256), 5, std=3.0)
     for bits in (3, 4, 8):
         p, s, b = O.affine_quantize(w, 64, bits)
-        two = O.affine_dequantize(p, s, b, 64, bits)
-        one = O.affine_dequantize(p, s, b, 64, bits, one_rounding=True)
+        one = O.affine_dequantize(p, s, b, 64, bits)
+        two = O.affine_dequantize(p, s, b, 64, bits, two_roundings=True)
         assert np.mean(two != one) > 0.01
         c = _codes(p, bits, 256).reshape(256, 4, 64).astype(np.float64)
         prod = (O.bf16_to_f32(s)[..., None] * c).reshape(256, 256)
@@ -131,13 +132,18 @@ def test_affine_error_bound_and_edge_snapping(bits):
 
 
 def test_affine_dequantize_matches_definition():
+    # Primary: one rounding of scale * code + bias (exact in f64 here, the
+    # product being exact); secondary: each operation rounded to bf16.
     w = _bf16_normal((8, 128), 3)
     p, s, b = O.affine_quantize(w, 64, 4)
-    d = O.bf16_to_f32(O.affine_dequantize(p, s, b, 64, 4))
-    c = _codes(p, 4, 128).reshape(8, 2, 64).astype(np.float32)
-    sc = O.bf16_to_f32(O.bf16_from_f32(O.bf16_to_f32(s)[..., None] * c))
-    want = O.bf16_to_f32(O.bf16_from_f32(sc + O.bf16_to_f32(b)[..., None])).reshape(8, 128)
-    assert np.array_equal(d, want)
+    c = _codes(p, 4, 128).reshape(8, 2, 64).astype(np.float64)
+    sf = O.bf16_to_f32(s)[..., None].astype(np.float64)
+    bf = O.bf16_to_f32(b)[..., None].astype(np.float64)
+    one = O.bf16_to_f32(O.affine_dequantize(p, s, b, 64, 4))
+    assert np.array_equal(one, O.bf16_to_f32(O.bf16_from_f32((sf * c + bf).reshape(8, 128))))
+    two = O.bf16_to_f32(O.affine_dequantize(p, s, b, 64, 4, two_roundings=True))
+    sc = O.bf16_to_f32(O.bf16_from_f32(sf * c))
+    assert np.array_equal(two, O.bf16_to_f32(O.bf16_from_f32(sc + bf)).reshape(8, 128))
 
 
 @pytest.mark.parametrize("q_len,offset,window,want", [

@@ -55,6 +55,34 @@ def test_noalloc_matches_workspace_entry(T, B, H, Hkv, D, bits, sizes):
         check_close(got, want)
 
 
+def test_noalloc_holds_no_library_scratch(T):
+    """What the entry is for: on a shape that splits (config 1's layout, ~32
+    splits a unit, so partials and a merge) it allocates nothing: with the
+    library's scratch released first, the call leaves it empty. The same
+    decode through the workspace-less entry then does allocate scratch (the
+    check can see an allocation)."""
+    B, H, Hkv, D, bits, N = 1, 32, 8, 128, 4, 8192
+    q = kv_bf16((B, H, 1, D), 301)
+    k = kv_bf16((B, Hkv, N, D), 302, frac=0.01, mult=10.0)
+    v = kv_bf16((B, Hkv, N, D), 303, frac=0.01, mult=10.0)
+    (kh, kd), (vh, vd) = _cache(k, 64, bits, N), _cache(v, 64, bits, N)
+    dq = T.DeviceArray.of(q)
+    segs = [T.affine_seg(tuple(a.ptr for a in kd), tuple(a.ptr for a in vd), N, N)]
+    o1 = T.DeviceArray((B, H, 1, D), np.uint16)
+    o2 = T.DeviceArray((B, H, 1, D), np.uint16)
+    T.hip().sync()
+    T.scratch_release()
+    assert T.scratch_bytes() == 0
+    T.decode_attend_affine_noalloc(dq.ptr, B, H, Hkv, D, 64, bits, bits, D ** -0.5, segs, o1.ptr)
+    T.hip().sync()
+    assert T.scratch_bytes() == 0, "the no-allocation entry created library scratch"
+    T.decode_attend_affine(dq.ptr, B, H, Hkv, D, 64, bits, bits, D ** -0.5, segs, o2.ptr)
+    T.hip().sync()
+    assert T.scratch_bytes() > 0, "this shape should split and use scratch"
+    assert np.array_equal(o1.numpy(), o2.numpy())
+    T.scratch_release()
+
+
 def test_noalloc_shared_prefix(T):
     # A prefix stored once for every sequence (read once per KV head) plus
     # each sequence's suffix: prefix partials, suffix partials, one merge.
