@@ -326,7 +326,7 @@ def _port_baseline(fn1, tok1, fnn, tokn, threads, budget_s, sample):
 
 
 PEAK_BF16_TFLOPS = 2500.0
-PREFILL_METRIC = "quantized-KV prefill chunk attention tokens/s (MFMA bf16)"
+PREFILL_METRIC = "quantized-KV prefill chunk attention tokens/s (MFMA)"
 
 
 def visible_pairs(L, N, q_start, k_start, window):
@@ -413,7 +413,7 @@ def prefill_main(T, hip, args):
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "settle_steps": settle,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic",
+        "dtype": "bf16 in/out, bf16 Q K^T, f16 P V, f32 accumulate", "data": "synthetic",
         "config": {
             "workload": "BASELINE config 3: one 2048-token prefill chunk attention of a "
                         "global layer at 16,384 keys (causal), over a 4-bit gs64 cache",
@@ -424,7 +424,7 @@ def prefill_main(T, hip, args):
             "bound": "mfma", "achieved": round(tf_g, 1), "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(tf_g / PEAK_BF16_TFLOPS, 4), "traffic": None,
             "kernel": "tqkv_prefill_attend_affine call: dequantize_rows_kernel<128> (the "
-                      "keys once, as bf16) + prefill_affine_kernel<128,16,16>",
+                      "keys once: K bf16, V f16 operands) + prefill_affine_kernel<128,16,17>",
             "alg_flops_per_launch": fl_g, "avg_launch_ms": round(ms_g, 5),
         },
         "sliding_layer_chunk": {
