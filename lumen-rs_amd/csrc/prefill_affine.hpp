@@ -261,12 +261,14 @@ __device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, cons
                   sc1 + r1 * groups,         bi0 + r0 * groups,         bi1 + r1 * groups};
 }
 
-// Loads run `run` of key kk (counted across both segments) of K or V.
+// Loads run `run` of key kk (counted across both segments) of K or V. A key
+// past the end loads the last key instead (ok = false: it is stored as
+// zeros), so the load is issued unconditionally.
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, const Args& a, int kk,
                                            int run) {
   st.ok = kk < a.total;
-  if (!st.ok) return;
+  kk = st.ok ? kk : int(a.total) - 1;
   if constexpr (is_rows<BITS>()) {  // one segment of 16-bit rows, no scales
     load_words<16>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
     st.s = st.b = 0u;
@@ -620,8 +622,7 @@ void prefill_affine_kernel(const Args a) {
                                          a.seg[0].vs, a.seg[1].vs, a.seg[0].vb, a.seg[1].vb,
                                          a.gs, b, kvh);
     // Task i of this thread: tid + i * kThreads; the first 2D tasks are K
-    // runs, the rest V runs (a whole wavefront takes one kind, so the kind
-    // and its pointers are uniform).
+    // runs, the rest V runs.
     constexpr int NS = Shape<D, H16>::kSets;
     // K and V tasks keep their words in separate registers: with one shared
     // set the two load paths meet in register copies that must wait for the
@@ -634,72 +635,82 @@ void prefill_affine_kernel(const Args a) {
     Stage<kSplit ? WK : NW> stk[NS][kPer];
     Stage<kSplit ? WV : NW> stv_own[kSplit ? NS : 1][kPer];
     auto& stv = v_stages<kSplit>(stk, stv_own);
-    SlabPtrs tp[kPer];
-    bool tv[kPer];
+    // A task's kind (K or V run) goes by its index where 2D is a multiple of
+    // the workgroup (the compiler then folds each task's pointers to K's or
+    // V's: D = 512 holds 8 tasks a thread), else by wavefront, with one task
+    // a thread.
+    constexpr bool kKindByTask = (2 * D) % kThreads == 0;
+    static_assert(kKindByTask || kPer == 1, "a kind by wavefront means one task a thread");
     int tkey[kPer], trun[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int task = tid + i * kThreads, r = task % (2 * D);
-      // A task's kind is wave-uniform; where 2D is a multiple of the
-      // workgroup it depends on i alone, so the compiler folds each task's
-      // pointers to K's or V's (D = 512: 8 tasks a thread would otherwise
-      // hold 48 pointers in scalar registers and spill them).
-      tv[i] = (2 * D) % kThreads == 0 ? i * kThreads >= 2 * D
-                                       : wave * kWave + i * kThreads >= 2 * D;
       tkey[i] = r % kTile;
       trun[i] = r / kTile;
-      tp[i].w0 = tv[i] ? vp.w0 : kp.w0;
-      tp[i].w1 = tv[i] ? vp.w1 : kp.w1;
-      tp[i].s0 = tv[i] ? vp.s0 : kp.s0;
-      tp[i].s1 = tv[i] ? vp.s1 : kp.s1;
-      tp[i].b0 = tv[i] ? vp.b0 : kp.b0;
-      tp[i].b1 = tv[i] ? vp.b1 : kp.b1;
     }
-#define TQKV_LOAD_TILE(S, T)                                                     \
-  _Pragma("unroll") for (int i = 0; i < kPer; ++i) {                             \
-    if (tv[i])                                                                   \
-      load_stage<D, BV>(stv[S][i], tp[i], a, (T) * kTile + tkey[i], trun[i]);    \
-    else                                                                         \
-      load_stage<D, BK>(stk[S][i], tp[i], a, (T) * kTile + tkey[i], trun[i]);    \
-  }
-#define TQKV_STORE_TILE(S, BUF)                                                  \
-  _Pragma("unroll") for (int i = 0; i < kPer; ++i) {                             \
-    if (tv[i])                                                                   \
-      store_v<D, BV, H16>(stv[S][i], Vt2[BUF], tkey[i], trun[i]);                \
-    else                                                                         \
-      store_k<D, BK, H16>(stk[S][i], Ks2[BUF], tkey[i], trun[i]);                \
-  }
-    TQKV_LOAD_TILE(0, int(t_lo))
-    // Everything loaded so far (the Q fragments, the first tile) has landed:
-    // without this the compiler's loop-carried wait analysis keeps the Q
-    // loads pending and makes every tile's MFMAs wait for the next tile's
-    // prefetch. (vmcnt(0); expcnt and lgkmcnt unchanged.)
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    TQKV_STORE_TILE(0, 0)
-    // Tile t_lo + 1 + k into set (k + 1) % NS: tile x sits in set
-    // (x - t_lo) % NS until it is dequantized.
-    static_for<NS>([&](auto k) {
-      if (t_lo + 1 + k.value <= t_hi) {
-        TQKV_LOAD_TILE((k.value + 1) % NS, int(t_lo) + 1 + k.value)
-      }
-    });
-    __syncthreads();
     // The two wavefronts on a SIMD (w and w + kWaves / 2) take the tile's
     // work in opposite orders, so one's dequantization (VALU) runs while the
     // other's products (MFMA) do.
     const bool dequant_first = wave >= kWaves / 2;
     const bool live = row0 + int64_t(wave) * RWO < rows;
-    // One tile: S holds tile t + 1's words, which go into the other LDS
-    // buffer (last read in the previous tile, before the barrier that ended
-    // it); S then fetches tile t + 1 + NS.
-    auto tile = [&](int t, int cur, auto set) __attribute__((always_inline)) {
-      constexpr int S = decltype(set)::value;
-      if (kBufs == 2 && dequant_first && t < t_hi) {
-        TQKV_STORE_TILE(S, cur ^ 1)
-        if (t + NS < t_hi + 1) {
-          TQKV_LOAD_TILE(S, t + 1 + NS)
+    // The tile loop, compiled once per kind of this wavefront's tasks (VW:
+    // V runs) where the kind goes by wavefront. Every load in it is
+    // unconditional: a key past the end re-reads the last key (load_stage)
+    // and a tile past the last re-reads the last tile (into a set that is
+    // never dequantized for use), and the loop runs whole rounds of NS tiles
+    // with the past-the-end ones computing nothing. The compiler's wait
+    // counts then know exactly which loads are outstanding, and NS tiles of
+    // words stay in flight: a branch around a load makes it wait for all of
+    // them.
+    auto run = [&](auto vw, auto dqf) __attribute__((always_inline)) {
+      constexpr bool VW = decltype(vw)::value;
+      constexpr bool DQF = decltype(dqf)::value;  // this wavefront dequantizes first
+      auto load_tile = [&](auto set, int64_t tt) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        const int tc = int(tt < t_hi ? tt : t_hi);
+        static_for<kPer>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          constexpr bool KV = kKindByTask ? i * kThreads >= 2 * D : VW;
+          if constexpr (KV)
+            load_stage<D, BV>(stv[S][i], vp, a, tc * kTile + tkey[i], trun[i]);
+          else
+            load_stage<D, BK>(stk[S][i], kp, a, tc * kTile + tkey[i], trun[i]);
+        });
+      };
+      auto store_tile = [&](auto set, int buf) __attribute__((always_inline)) {
+        constexpr int S = decltype(set)::value;
+        static_for<kPer>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          constexpr bool KV = kKindByTask ? i * kThreads >= 2 * D : VW;
+          if constexpr (KV)
+            store_v<D, BV, H16>(stv[S][i], Vt2[buf], tkey[i], trun[i]);
+          else
+            store_k<D, BK, H16>(stk[S][i], Ks2[buf], tkey[i], trun[i]);
+        });
+      };
+      load_tile(std::integral_constant<int, 0>{}, t_lo);
+      // Everything loaded so far (the Q fragments, the first tile) has
+      // landed: without this the compiler's loop-carried wait analysis keeps
+      // the Q loads pending and makes every tile's MFMAs wait for the next
+      // tile's prefetch. (vmcnt(0); expcnt and lgkmcnt unchanged.)
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      store_tile(std::integral_constant<int, 0>{}, 0);
+      // Tile t_lo + 1 + k into set (k + 1) % NS: tile x sits in set
+      // (x - t_lo) % NS until it is dequantized.
+      static_for<NS>([&](auto k) {
+        load_tile(std::integral_constant<int, (decltype(k)::value + 1) % NS>{},
+                  t_lo + 1 + decltype(k)::value);
+      });
+      __syncthreads();
+      // One tile: set S holds tile t + 1's words, which go into the other
+      // LDS buffer (last read in the previous tile, before the barrier that
+      // ended it); S then fetches tile t + 1 + NS.
+      auto tile = [&](int64_t t, int cur, auto set) __attribute__((always_inline)) {
+        if constexpr (kBufs == 2 && DQF) {
+          store_tile(set, cur ^ 1);
+          load_tile(set, t + 1 + NS);
         }
-      }
+        if (t <= t_hi) {
       const uint16_t* Ks = Ks2[cur];
       const uint16_t* Vt = Vt2[cur];
       // A wavefront whose rows are all past the end (a short block) only
@@ -823,39 +834,49 @@ void prefill_affine_kernel(const Args a) {
           }
         }
       }
-      if constexpr (kBufs == 2) {
-        if (!dequant_first && t < t_hi) {
-          TQKV_STORE_TILE(S, cur ^ 1)
-          if (t + NS < t_hi + 1) {
-            TQKV_LOAD_TILE(S, t + 1 + NS)
-          }
         }
-      } else {
-        __syncthreads();  // every wavefront is done with this tile's LDS
-        if (t < t_hi) {
-          TQKV_STORE_TILE(S, 0)
-          if (t + NS < t_hi + 1) {
-            TQKV_LOAD_TILE(S, t + 1 + NS)
+        if constexpr (kBufs == 2) {
+          if constexpr (!DQF) {
+            store_tile(set, cur ^ 1);
+            load_tile(set, t + 1 + NS);
           }
+        } else {
+          __syncthreads();  // every wavefront is done with this tile's LDS
+          store_tile(set, 0);
+          load_tile(set, t + 1 + NS);
         }
-      }
-      __syncthreads();
-    };
-    // Unrolled over the stage sets so each one stays in named registers.
-    int t = int(t_lo), cur = 0;
-    while (t <= int(t_hi)) {
-      static_for<NS>([&](auto k) {
-        if (t <= int(t_hi)) {
-          tile(t, cur, std::integral_constant<int, (k.value + 1) % NS>{});
-          ++t;
+        __syncthreads();
+      };
+      // Whole rounds of NS tiles, unrolled over the stage sets so each one
+      // stays in named registers.
+      const int64_t rounds = (t_hi - t_lo + NS) / NS;
+      int cur = 0;
+      for (int64_t it = 0; it < rounds; ++it) {
+        static_for<NS>([&](auto k) {
+          tile(t_lo + it * NS + decltype(k)::value, cur,
+               std::integral_constant<int, (decltype(k)::value + 1) % NS>{});
           cur ^= kBufs - 1;
-        }
-      });
+        });
+      }
+    };
+    // One copy of the loop per (task kind, order) a wavefront can have: the
+    // two arms of a runtime branch would load into the same registers, and
+    // the copies where they meet would wait for every load in flight.
+    auto by_order = [&](auto vw) __attribute__((always_inline)) {
+      if (kBufs == 2 && dequant_first)
+        run(vw, std::true_type{});
+      else
+        run(vw, std::false_type{});
+    };
+    if constexpr (kKindByTask) {
+      by_order(std::false_type{});
+    } else {
+      if (wave * kWave >= 2 * D)
+        by_order(std::true_type{});
+      else
+        by_order(std::false_type{});
     }
   }
-#undef TQKV_STORE_TILE
-
-#undef TQKV_LOAD_TILE
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     float tot = lsum[j];
