@@ -78,6 +78,7 @@ constexpr float kVUp = float(1 << kVShift);
 typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
 typedef float f2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
@@ -138,7 +139,15 @@ struct Shape {
   // channels (its O accumulators fit the register file; one wavefront
   // holding all 512 spilled).
   static constexpr bool kChanSplit = H16 && D == 512;
-  static constexpr int kRows = kChanSplit ? kRW : kWaves * kRW;
+  // D <= 256 with f16 operands (decode over a shared prefix: a block holds
+  // a KV head's B x G query rows, 32 at config 4) splits the keys instead:
+  // the wavefronts form groups of 16 rows times kKQ quarters of every 64-key
+  // tile, so every wavefront carries scores and products (with whole
+  // 16-row slices, two of eight did and bounded the pass); the quarters'
+  // softmax states meet in LDS at the end.
+  static constexpr bool kKeySplit = H16 && D <= 256;
+  static constexpr int kKQ = kKeySplit ? 4 : 1;
+  static constexpr int kRows = kChanSplit ? kRW : kWaves / kKQ * kRW;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int kPer = 4 * D / kThreads;
   // Tiles whose raw words are in flight in registers while a tile is
@@ -485,6 +494,13 @@ __device__ __forceinline__ u32x2_t tr_read(const uint16_t* p) {
   return __builtin_bit_cast(u32x2_t, v);
 }
 
+// Marks a block that runs on few tiles (the element mask of partially
+// visible tiles, the accumulator rescale when a row's maximum moves): with
+// it the compiler keeps the block behind its wave-uniform branch instead of
+// turning it into selects that every tile executes (measured: ~190 of ~380
+// VALU instructions a tile at head dim 128).
+__device__ __forceinline__ void keep_branch() { asm volatile(""); }
+
 // acc + both halves of a packed pair (v_dot2 against a (1, 1) splat).
 template <bool H16>
 __device__ __forceinline__ float sum2(uint32_t w, float acc) {
@@ -528,6 +544,11 @@ void prefill_affine_kernel(const Args a) {
   constexpr int kWaves = Shape<D, H16>::kWaves, RW = Shape<D, H16>::kRW, kRows = Shape<D, H16>::kRows;
   constexpr int NR = RW / 16, ND = D / 32;
   constexpr bool CS = Shape<D, H16>::kChanSplit;
+  // Key split: this wavefront's row group rg and key quarter kq (rows
+  // rg * RW + [0, RW), keys 16 kq + [0, 16) of every tile).
+  constexpr bool KS = Shape<D, H16>::kKeySplit;
+  constexpr int KQ = Shape<D, H16>::kKQ, RG = kWaves / KQ;
+  static_assert(!KS || RW == 16, "a key-split wavefront holds 16 rows");
   // Output channel tiles of 16 this wavefront accumulates, from t_base on;
   // RWO: rows between wavefronts (0 when they share the rows).
   constexpr int NT = CS ? D / 16 / kWaves : D / 16;
@@ -543,8 +564,12 @@ void prefill_affine_kernel(const Args a) {
   // Two tile buffers: tile t is read from one while tile t + 1 is written
   // into the other, so a tile costs one barrier. One buffer (D = 512): tile
   // t + 1 is written after every wavefront has read tile t.
-  __shared__ __attribute__((aligned(16))) uint16_t Ks2[kBufs][kTile * KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt2[kBufs][kTile * KSTR];
+  // K tiles then V tiles, one array: after the last tile the key split
+  // merges its quarters' accumulators in the same memory.
+  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[2][kBufs][kTile * KSTR];
+  auto& Ks2 = s_tiles[0];
+  auto& Vt2 = s_tiles[1];
+  __shared__ float s_km[KS ? kWaves : 1][16], s_kl[KS ? kWaves : 1][16];
   __shared__ f4_t s_part[CS ? kWaves : 1][CS ? 4 : 1][kWave];
 
   const int tid = threadIdx.x;
@@ -552,6 +577,9 @@ void prefill_affine_kernel(const Args a) {
   const int lane = tid % kWave, lr = lane % 16, lg = lane / 16;
   const int t_base = CS ? wave * NT : 0;
   const int s_base = CS ? wave * NDW : 0;
+  const int kq = KS ? wave / RG : 0;
+  // First row of this wavefront within the block.
+  const int wrow = KS ? (wave % RG) * RW : wave * RWO;
   // Workgroup i runs on XCD i % 8 (round-robin dispatch). Consecutive
   // logical blocks, which share a (batch row, KV head) and so its keys, are
   // placed on one XCD's L2; within a unit the longest key ranges go first.
@@ -582,7 +610,7 @@ void prefill_affine_kernel(const Args a) {
   bool rvalid[NR];
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
-    const int64_t r = row0 + wave * RWO + 16 * j + lr;
+    const int64_t r = row0 + wrow + 16 * j + lr;
     rvalid[j] = r < rows;
     const int64_t rr = rvalid[j] ? r : rows - 1;
     const int64_t l = rr / a.G, g = rr % a.G;
@@ -652,7 +680,74 @@ void prefill_affine_kernel(const Args a) {
     // work in opposite orders, so one's dequantization (VALU) runs while the
     // other's products (MFMA) do.
     const bool dequant_first = wave >= kWaves / 2;
-    const bool live = row0 + int64_t(wave) * RWO < rows;
+    const bool live = row0 + wrow < rows;
+    // A key-split wavefront's share of tile t (buffer cur): S^T of its 16
+    // keys by its 16 rows (D / 32 products), the online softmax over them,
+    // and O^T += V^T P^T as D / 16 products of 16 x 16 x 16 whose k slots are
+    // the 16 keys: the score registers are exactly the B operand, and one
+    // transposing read gives the A operand of 4 keys x 16 channels a lane
+    // group.
+    auto ks_tile = [&](int64_t t, int cur) __attribute__((always_inline)) {
+      if constexpr (KS) {
+        const uint16_t* Ks = Ks2[cur];
+        const uint16_t* Vt = Vt2[cur];
+        f4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < NDW; ++s) {
+          const op8_t ka =
+              *reinterpret_cast<const op8_t*>(Ks + (16 * kq + lr) * KSTR + 32 * s + 8 * lg);
+          sc = mma<H16>(ka, qf[0][s], sc);
+        }
+        const int64_t kbase = a.k_start + int64_t(t) * kTile;
+        const int rem = a.total - int64_t(t) * kTile < kTile ? int(a.total - int64_t(t) * kTile) : kTile;
+        const bool full = rem == kTile &&
+                          (!a.causal || (kbase + kTile - 1 <= qa_lo &&
+                                         (a.window < 0 || qa_hi < kbase + a.window)));
+        if (!full) {
+          keep_branch();
+          int hi = rem - 1, lo = 0;
+          if (a.causal) {
+            const int64_t dq = qabs[0] - kbase;
+            if (dq < hi) hi = dq < -1 ? -1 : int(dq);
+            if (a.window >= 0) {
+              const int64_t first = dq - a.window + 1;
+              lo = first < 0 ? 0 : (first > kTile ? kTile : int(first));
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int o2 = 16 * kq + 4 * lg + r;
+            if (o2 < lo || o2 > hi) sc[r] = -INFINITY;
+          }
+        }
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = xor32_max(xor16_max(mx));
+        mx *= a.qscale;
+        const bool up = mx > m[0] + kTau;
+        if (__any(up)) {
+          keep_branch();
+          const float mn = up ? mx : m[0];
+          const float alpha = up ? __builtin_amdgcn_exp2f(m[0] - mn) : 1.0f;
+          lsum[0] *= alpha;
+#pragma unroll
+          for (int t2 = 0; t2 < NT; ++t2) o[t2][0] *= alpha;
+          m[0] = mn;
+        }
+        const float nm = m[0] == -INFINITY ? 0.0f : -m[0];
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], a.qscale, nm));
+        const uint32_t w0 = pack_h16(p[0], p[1]), w1 = pack_h16(p[2], p[3]);
+        lsum[0] = sum2<true>(w1, sum2<true>(w0, lsum[0]));
+        const h4_t pb = __builtin_bit_cast(h4_t, u32x2_t{w0, w1});
+#pragma unroll
+        for (int t2 = 0; t2 < NT; ++t2) {
+          const h4_t va = __builtin_bit_cast(
+              h4_t, tr_read(Vt + (16 * kq + 4 * lg + lr / 4) * KSTR + 16 * t2 + 4 * (lr % 4)));
+          o[t2][0] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[t2][0], 0, 0, 0);
+        }
+      }
+    };
     // The tile loop, compiled once per kind of this wavefront's tasks (VW:
     // V runs) where the kind goes by wavefront. Every load in it is
     // unconditional: a key past the end re-reads the last key (load_stage)
@@ -716,7 +811,9 @@ void prefill_affine_kernel(const Args a) {
       // A wavefront whose rows are all past the end (a short block) only
       // dequantizes.
       if (live) {
-
+        if constexpr (KS) {
+          ks_tile(t, cur);
+        } else {
         f4_t sc[4][NR];
   #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -754,6 +851,7 @@ void prefill_affine_kernel(const Args a) {
                           (!a.causal || (kbase + kTile - 1 <= qa_lo &&
                                          (a.window < 0 || qa_hi < kbase + a.window)));
         if (!full) {
+          keep_branch();
   #pragma unroll
           for (int j = 0; j < NR; ++j) {
             int hi = rem - 1, lo = 0;
@@ -785,6 +883,7 @@ void prefill_affine_kernel(const Args a) {
           mx *= a.qscale;  // qscale > 0: the max of the scaled scores
           const bool up = mx > m[j] + kTau;
           if (__any(up)) {
+            keep_branch();
             const float mn = up ? mx : m[j];
             const float alpha = up ? __builtin_amdgcn_exp2f(m[j] - mn) : 1.0f;
             lsum[j] *= alpha;
@@ -833,6 +932,7 @@ void prefill_affine_kernel(const Args a) {
               o[t2][j] = mma<true>(va, pb[j], o[t2][j]);
           }
         }
+        }
       }
         }
         if constexpr (kBufs == 2) {
@@ -877,6 +977,71 @@ void prefill_affine_kernel(const Args a) {
         by_order(std::false_type{});
     }
   }
+  if constexpr (KS) {
+    // The key quarters' (m, l, O) of each row meet in LDS (the tile memory,
+    // free after the last tile's barrier); wavefront (row group, kq) then
+    // combines its group's rows over channels [kq D / KQ, (kq + 1) D / KQ):
+    // lane i takes row i / 4 and D / 16 consecutive channels.
+    const float tot = xor32_sum(xor16_sum(lsum[0]));
+    float* so = reinterpret_cast<float*>(&s_tiles[0][0][0]);  // [kWaves][16][D]
+    static_assert(sizeof(s_tiles) >= sizeof(float) * kWaves * 16 * D, "merge space");
+    __syncthreads();
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2)
+      *reinterpret_cast<f4_t*>(so + (wave * 16 + lr) * D + 16 * t2 + 4 * lg) = o[t2][0];
+    if (lg == 0) {
+      s_km[wave][lr] = m[0];
+      s_kl[wave][lr] = tot;
+    }
+    __syncthreads();
+    constexpr int CPL = D / 16;  // channels a lane
+    const int rr = lane / 4, c0 = kq * (D / KQ) + (lane % 4) * CPL;
+    const int rgp = wave % RG;
+    const int64_t r = row0 + rgp * RW + rr;
+    if (r < rows) {
+      float mk[KQ], mx = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        mk[q] = s_km[q * RG + rgp][rr];
+        mx = fmaxf(mx, mk[q]);
+      }
+      float fk[KQ], lt = 0.0f;
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        fk[q] = mk[q] == -INFINITY ? 0.0f : exp2f(mk[q] - mx);
+        lt += fk[q] * s_kl[q * RG + rgp][rr];
+      }
+      float ov[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < KQ; ++q) acc += fk[q] * so[((q * RG + rgp) * 16 + rr) * D + c0 + c];
+        ov[c] = acc;
+      }
+      const int64_t l = r / a.G, g = r % a.G;
+      if (a.part_o) {
+        const int64_t slot =
+            ((int64_t(b) * a.L + l) * a.H + int64_t(kvh) * a.G + g) * a.n_part + a.split_base + split;
+        float* po = a.part_o + slot * D + c0;
+#pragma unroll
+        for (int c = 0; c < CPL; c += 4)
+          *reinterpret_cast<f4_t*>(po + c) = f4_t{ov[c], ov[c + 1], ov[c + 2], ov[c + 3]};
+        if (kq == 0 && lane % 4 == 0) {
+          a.part_m[slot] = mx;
+          a.part_l[slot] = lt;
+        }
+      } else {
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        uint16_t* dst = a.out + int64_t(b) * a.qs_b + (int64_t(kvh) * a.G + g) * a.qs_h + l * a.qs_l + c0;
+#pragma unroll
+        for (int c = 0; c < CPL; c += 4)
+          *reinterpret_cast<u32x2_t*>(dst + c) =
+              u32x2_t{pack_bf16(ov[c] * inv, ov[c + 1] * inv), pack_bf16(ov[c + 2] * inv, ov[c + 3] * inv)};
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     float tot = lsum[j];
@@ -885,7 +1050,7 @@ void prefill_affine_kernel(const Args a) {
     // The prefill variant's V operands were scaled by 2^-kVShift.
     const float vup = H16 ? 1.0f : kVUp;
     if (a.part_o) {
-      const int64_t r = row0 + wave * RWO + 16 * j + lr;
+      const int64_t r = row0 + wrow + 16 * j + lr;
       const int64_t l = r / a.G, h = int64_t(kvh) * a.G + r % a.G;
       const int64_t slot = ((int64_t(b) * a.L + l) * a.H + h) * a.n_part + a.split_base + split;
       float* po = a.part_o + slot * D;
