@@ -712,37 +712,59 @@ __global__ __launch_bounds__(kWave* kWaves) void decode_mfma_kernel(Args a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h][vcd.e] = fmaf(acc[h][vcd.e], unscale, bacc[h]);
   });
-  // The 8 token-pair groups (lanes vp = lane / 8) summed as a butterfly:
-  // lane ^ 8 by DPP row_ror:8 within each row of 16, lane ^ 16 and lane ^ 32
-  // by gfx950's v_permlane16_swap / v_permlane32_swap of a value with
-  // itself (the two halves they return are the lane's and its partner's).
-  auto xor_sum = [](float v) {
-    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, true));
-    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
-                                                      false, false);
-    v = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
-    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
-                                                      false, false);
-    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
-  };
+  // The 8 token-pair groups (lanes vp = lane / 8) summed as a
+  // reduce-scatter: each lane ends with a quarter of the wavefront's sums.
+  // v_permlane16_swap of two different registers (A, B) hands even 16-lane
+  // rows their own and their lane ^ 16 partner's A and odd rows the same of
+  // B, so one swap and one add fold both halves of a pair of values, each
+  // into the rows that keep it; v_permlane32_swap does the same for lane ^
+  // 32; the NQ values left are then summed over lane ^ 8 by DPP row_ror:8.
+  // Lane bits (4, 5) = (b4, b5) keep the sums of value indices
+  // i + 2 NQ b4 + NQ b5, i < NQ (acc[h][e] at h * EV + e, then l[h]).
+  // (A butterfly over all G * (EV + 1) values took about three times the
+  // instructions.)
+  constexpr int NV = G * EV + G, NQ = (NV + 3) / 4;
+  float vsum[4 * NQ];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    l[h] = xor_sum(l[h]);
 #pragma unroll
-    for (int e = 0; e < EV; ++e) acc[h][e] = xor_sum(acc[h][e]);
+    for (int e = 0; e < EV; ++e) vsum[h * EV + e] = acc[h][e];
+    vsum[G * EV + h] = l[h];
+  }
+#pragma unroll
+  for (int k = NV; k < 4 * NQ; ++k) vsum[k] = 0.0f;
+  float half[2 * NQ];
+#pragma unroll
+  for (int i = 0; i < 2 * NQ; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(vsum[i]),
+                                                    __float_as_uint(vsum[i + 2 * NQ]), false, false);
+    half[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float quarter[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(half[i]),
+                                                    __float_as_uint(half[i + NQ]), false, false);
+    quarter[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    quarter[i] += __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(quarter[i]), 0x128, 0xf, 0xf, true));
   }
 
   __shared__ float s_m[kWaves][G], s_l[kWaves][G];
   __shared__ float s_acc[kWaves][G][D];
-  if (vp == 0) {
+  if (lane == 0) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      if (vc == 0) {
-        s_m[wave][h] = m[h] + ev[h];  // the reference of l and acc
-        s_l[wave][h] = l[h];
-      }
+    for (int h = 0; h < G; ++h) s_m[wave][h] = m[h] + ev[h];  // the reference of l and acc
+  }
+  if ((lane & 8) == 0) {  // lanes ^ 8 hold the same sums
+    const int k0 = 2 * NQ * ((lane >> 4) & 1) + NQ * ((lane >> 5) & 1);
 #pragma unroll
-      for (int e = 0; e < EV; ++e) s_acc[wave][h][ve0 + e] = acc[h][e];
+    for (int i = 0; i < NQ; ++i) {
+      const int k = k0 + i;
+      if (k < G * EV)
+        s_acc[wave][k / EV][ve0 + k % EV] = quarter[i];
+      else if (k < NV && vc == 0)
+        s_l[wave][k - G * EV] = quarter[i];
     }
   }
   __syncthreads();
