@@ -79,7 +79,24 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
       if (d >= D) break;
       const float* po = part_o + (bh * n_splits + c0) * D + d;
       float acc = os[k];
-      for (int s = 0; s < n; ++s) acc += wgt[s] * po[int64_t(s) * D];
+      // Sixteen slots' loads issued before any is used (a load a slot in
+      // turn paid the L2 round trip per slot: 5.4 us for 36 slots).
+      int s = 0;
+      for (; s + 16 <= n; s += 16) {
+        float x[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) x[u] = po[int64_t(s + u) * D];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) acc += wgt[s + u] * x[u];
+      }
+      for (; s + 4 <= n; s += 4) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = po[int64_t(s + u) * D];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc += wgt[s + u] * x[u];
+      }
+      for (; s < n; ++s) acc += wgt[s] * po[int64_t(s) * D];
       os[k] = acc;
     }
   }
