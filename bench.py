@@ -406,6 +406,11 @@ def prefill_main(T, hip, args):
     ms_per_step = total_ms / args.steps
     o = (out.numpy().astype(np.uint32) << 16).view(np.float32)
     assert np.all(np.isfinite(o)) and np.abs(o).max() > 0, "prefill output is not sane"
+    # HBM bytes of one global-chunk call at this shape, from the FETCH_SIZE
+    # (x 2.000) and WRITE_SIZE (x 1.000) passes of
+    # profiles/prefill_affine_config3.md: dequantize-once 83.94 MB read +
+    # 268.44 MB written, attention 335.88 MB read + 67.11 MB written.
+    traffic = 755356672 if (B, L, N_G) == (4, 2048, 16384) else None
     result = {
         "metric": PREFILL_METRIC,
         "value": round(B * L / (ms_per_step * 1e-3), 1),
@@ -422,7 +427,10 @@ def prefill_main(T, hip, args):
         },
         "roofline": {
             "bound": "mfma", "achieved": round(tf_g, 1), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tf_g / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "unit": "TFLOP/s", "frac": round(tf_g / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+            "traffic_source": ("profile-derived, not counted in this run: the counter passes "
+                               "of profiles/prefill_affine_config3.md (both launches of the "
+                               "call)" if traffic is not None else None),
             "kernel": "tqkv_prefill_attend_affine call: dequantize_rows_kernel<128> (the "
                       "keys once: K bf16, V f16 operands) + prefill_affine_kernel<128,16,17>",
             "alg_flops_per_launch": fl_g, "avg_launch_ms": round(ms_g, 5),
@@ -909,6 +917,20 @@ def prefix_main(T, hip, args):
     ctx = ctx0 + (steps + 1) / 2.0
     unique = P * HKV * row + B * HKV * ctx * row + 2 * B * H * D * 2
     naive = B * HKV * (P + ctx) * row + 2 * B * H * D * 2
+    # HBM bytes per call from the FETCH_SIZE (x 2.000) and WRITE_SIZE (x 1.000)
+    # passes of profiles/prefix_shared_config4.md at this command's default
+    # steps: prefix pass 113.70 MB + suffix decode 59.41 MB + merge 4.99 MB =
+    # 178.11 MB against 165.06 MB algorithmic, 1.07903 per algorithmic byte
+    # (the excess is the partial results written and read back by the merge).
+    traffic = int(unique * 1.07903) if steps == 128 and fused else None
+    hbm = _hbm(unique / (dec_ms * 1e-3) / 1e9,
+               "shared-prefix decode call: prefix pass (prefill kernel, f16 tiles) + suffix "
+               "decode (" + T.decode_kernel_name(H, HKV, D, GS, BK, BV) + ") + merge", unique,
+               dec_ms, traffic)
+    if traffic is not None:
+        hbm["traffic_source"] = ("profile-derived, not counted in this run: the counter passes "
+                                 "of profiles/prefix_shared_config4.md give 1.07903 HBM bytes "
+                                 "per algorithmic byte")
     result = _line(
         "prefix-shared quantized-KV decode tokens/s", B / (total / steps * 1e-3), "tokens/s",
         total / steps, args, "bf16 in/out, f16 operands, f32 accumulate",
@@ -916,9 +938,7 @@ def prefix_main(T, hip, args):
                      "own tokens, 32/8 heads, D=128, K 8-bit / V 4-bit gs64, 128 decode steps",
          "batch": B, "q_heads": H, "kv_heads": HKV, "head_dim": D, "prefix": P, "suffix": S0,
          "bits_k": BK, "bits_v": BV, "group_size": GS, "launches_per_step": 3 if fused else 4},
-        _hbm(unique / (dec_ms * 1e-3) / 1e9,
-             "shared-prefix decode call: prefix pass (prefill kernel, f16 tiles) + suffix "
-             "decode (" + T.decode_kernel_name(H, HKV, D, GS, BK, BV) + ") + merge", unique, dec_ms),
+        hbm,
         {"naive_bytes_per_step": int(naive),
          "naive_gbps": round(naive / (dec_ms * 1e-3) / 1e9, 1),
          "per_sequence_path_ms_per_step": round(per_seq_ms, 5),

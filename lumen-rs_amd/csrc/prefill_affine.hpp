@@ -60,11 +60,17 @@ namespace prefill {
 constexpr int kWave = 64;
 constexpr int kTile = 64;  // keys per tile
 constexpr int kXcds = 8;   // accelerator dies (each with its own L2) on MI355X
-// LDS row stride (bf16 elements) of the K and V tiles, both row-major
-// [key][D]: D + 8 keeps ds_read_b128 rows 16-byte aligned and 8
-// consecutive rows on distinct banks.
+// LDS row stride (16-bit elements) of the K and V tiles, both row-major
+// [key][D]. D + 16 (rows 32 bytes past a multiple of 128) leaves both reads
+// of the products free of bank conflicts, as counted on gfx950
+// (SQ_LDS_BANK_CONFLICT of each access pattern alone): the K operand's
+// ds_read_b128 (16 rows x 2 chunks a half-wavefront) and V's transposing
+// ds_read_b64_tr_b16 (8 rows x 32 bytes a half-wavefront). The loader's
+// 16-byte stores (64 consecutive rows, one chunk) then conflict 2-way; D + 8
+// made the stores conflict-free but cost 4 cycles per K read and 2 per V
+// read, 4x more conflict cycles a tile.
 template <int D>
-constexpr int kKStride = D + 8;
+constexpr int kKStride = D + 16;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kTau = 8.0f;
@@ -157,6 +163,15 @@ struct Shape {
   static constexpr int kSets = H16 && D <= 256 ? 2 : 1;
   static constexpr int kBufs = D == 512 ? 1 : 2;      // LDS tile buffers
   static constexpr int kWavesPerEu = D == 512 ? 1 : 2;
+  // The bf16 prefill at D = 128 (two wavefronts a SIMD, 32 rows each):
+  // the second wavefront of each SIMD (waves kWaves / 2..) multiplies a
+  // tile's P by V one tile late, before the next tile's scores. Both
+  // wavefronts of a SIMD leave each tile's barrier together; in this order
+  // one's softmax (VALU) meets the other's products (matrix cores) instead
+  // of both doing the same phase at once. V then needs three LDS buffers
+  // (tile t - 1 read late, t read, t + 1 written); D = 256 has no room.
+  static constexpr bool kDeferPV = !H16 && D == 128;
+  static constexpr int kVBufs = kDeferPV ? 3 : kBufs;
   static_assert(kPer * kThreads == 4 * D, "whole loader tasks per thread");
 };
 
@@ -560,15 +575,17 @@ void prefill_affine_kernel(const Args a) {
   constexpr int NDW = CS ? ND / kWaves : ND;
   constexpr int KSTR = kKStride<D>;
   constexpr int kPer = Shape<D, H16>::kPer, kThreads = Shape<D, H16>::kThreads;
-  constexpr int kBufs = Shape<D, H16>::kBufs;
+  constexpr int kBufs = Shape<D, H16>::kBufs, kVBufs = Shape<D, H16>::kVBufs;
+  constexpr bool kDeferPV = Shape<D, H16>::kDeferPV;
   // Two tile buffers: tile t is read from one while tile t + 1 is written
   // into the other, so a tile costs one barrier. One buffer (D = 512): tile
-  // t + 1 is written after every wavefront has read tile t.
+  // t + 1 is written after every wavefront has read tile t. Three V buffers
+  // where P V runs one tile late on half the wavefronts.
   // K tiles then V tiles, one array: after the last tile the key split
   // merges its quarters' accumulators in the same memory.
-  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[2][kBufs][kTile * KSTR];
-  auto& Ks2 = s_tiles[0];
-  auto& Vt2 = s_tiles[1];
+  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[kBufs + kVBufs][kTile * KSTR];
+  auto Ks2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[c][0]; };
+  auto Vt2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[kBufs + c][0]; };
   __shared__ float s_km[KS ? kWaves : 1][16], s_kl[KS ? kWaves : 1][16];
   __shared__ f4_t s_part[CS ? kWaves : 1][CS ? 4 : 1][kWave];
 
@@ -687,10 +704,10 @@ void prefill_affine_kernel(const Args a) {
     // the 16 keys: the score registers are exactly the B operand, and one
     // transposing read gives the A operand of 4 keys x 16 channels a lane
     // group.
-    auto ks_tile = [&](int64_t t, int cur) __attribute__((always_inline)) {
+    auto ks_tile = [&](int64_t t, int cur, int vc) __attribute__((always_inline)) {
       if constexpr (KS) {
-        const uint16_t* Ks = Ks2[cur];
-        const uint16_t* Vt = Vt2[cur];
+        const uint16_t* Ks = Ks2(cur);
+        const uint16_t* Vt = Vt2(vc);
         f4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int s = 0; s < NDW; ++s) {
@@ -772,15 +789,15 @@ void prefill_affine_kernel(const Args a) {
             load_stage<D, BK>(stk[S][i], kp, a, tc * kTile + tkey[i], trun[i]);
         });
       };
-      auto store_tile = [&](auto set, int buf) __attribute__((always_inline)) {
+      auto store_tile = [&](auto set, int kbuf, int vbuf) __attribute__((always_inline)) {
         constexpr int S = decltype(set)::value;
         static_for<kPer>([&](auto I) {
           constexpr int i = decltype(I)::value;
           constexpr bool KV = kKindByTask ? i * kThreads >= 2 * D : VW;
           if constexpr (KV)
-            store_v<D, BV, H16>(stv[S][i], Vt2[buf], tkey[i], trun[i]);
+            store_v<D, BV, H16>(stv[S][i], Vt2(vbuf), tkey[i], trun[i]);
           else
-            store_k<D, BK, H16>(stk[S][i], Ks2[buf], tkey[i], trun[i]);
+            store_k<D, BK, H16>(stk[S][i], Ks2(kbuf), tkey[i], trun[i]);
         });
       };
       load_tile(std::integral_constant<int, 0>{}, t_lo);
@@ -789,7 +806,7 @@ void prefill_affine_kernel(const Args a) {
       // the Q loads pending and makes every tile's MFMAs wait for the next
       // tile's prefetch. (vmcnt(0); expcnt and lgkmcnt unchanged.)
       __builtin_amdgcn_s_waitcnt(0x0F70);
-      store_tile(std::integral_constant<int, 0>{}, 0);
+      store_tile(std::integral_constant<int, 0>{}, 0, 0);
       // Tile t_lo + 1 + k into set (k + 1) % NS: tile x sits in set
       // (x - t_lo) % NS until it is dequantized.
       static_for<NS>([&](auto k) {
@@ -797,23 +814,54 @@ void prefill_affine_kernel(const Args a) {
                   t_lo + 1 + decltype(k)::value);
       });
       __syncthreads();
-      // One tile: set S holds tile t + 1's words, which go into the other
-      // LDS buffer (last read in the previous tile, before the barrier that
+      // P V of one tile: the packed weights pp[u][j] (keys 32u + [0, 32) of
+      // rows 16j + [0, 16)) times V^T from buffer Vt.
+      auto pv_tile = [&](const h8_t (&pp)[2][NR], const uint16_t* Vt) __attribute__((always_inline)) {
+  #pragma unroll
+        for (int u = 0; u < 2; ++u)
+  #pragma unroll
+          for (int t2 = 0; t2 < NT; ++t2) {
+            // Lane lr of group lg supplies row 32u + 4lg + lr/4 and channels
+            // 16 tt + 4(lr % 4) + [0, 4); the transposing read hands it
+            // channel 16 tt + lr of keys 32u + 4lg + [0, 4) (and + 16 for
+            // the second read): the A operand of V^T for the k slots the
+            // score registers fill.
+            const uint16_t* vrow = Vt + (32 * u + 4 * lg + lr / 4) * KSTR +
+                                   16 * (t_base + t2) + 4 * (lr % 4);
+            const u32x2_t lo = tr_read(vrow);
+            const u32x2_t hi = tr_read(vrow + 16 * KSTR);
+            const h8_t va = __builtin_bit_cast(h8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
+  #pragma unroll
+            for (int j = 0; j < NR; ++j)
+              o[t2][j] = mma<true>(va, pp[u][j], o[t2][j]);
+          }
+      };
+      // This wavefront multiplies by V one tile late (the second wavefront of
+      // each SIMD): pprev holds the previous tile's packed weights.
+      constexpr bool DEFER = kDeferPV && DQF;
+      static_assert(!kDeferPV || NS == 1, "one tile a round where P V runs late");
+      h8_t pprev[2][NR];
+      auto vnext = [](int c) { return kVBufs == 3 ? (c == 2 ? 0 : c + 1) : (c ^ (kVBufs - 1)); };
+      auto vprev = [](int c) { return c == 0 ? kVBufs - 1 : c - 1; };
+      // One tile: set S holds tile t + 1's words, which go into the next
+      // LDS buffers (last read in an earlier tile, before the barrier that
       // ended it); S then fetches tile t + 1 + NS.
-      auto tile = [&](int64_t t, int cur, auto set) __attribute__((always_inline)) {
+      auto tile = [&](int64_t t, int cur, int vc, auto set) __attribute__((always_inline)) {
         if constexpr (kBufs == 2 && DQF) {
-          store_tile(set, cur ^ 1);
+          store_tile(set, cur ^ 1, vnext(vc));
           load_tile(set, t + 1 + NS);
         }
         if (t <= t_hi) {
-      const uint16_t* Ks = Ks2[cur];
-      const uint16_t* Vt = Vt2[cur];
+      const uint16_t* Ks = Ks2(cur);
       // A wavefront whose rows are all past the end (a short block) only
       // dequantizes.
       if (live) {
         if constexpr (KS) {
-          ks_tile(t, cur);
+          ks_tile(t, cur, vc);
         } else {
+        if constexpr (DEFER) {
+          if (t > t_lo) pv_tile(pprev, Vt2(vprev(vc)));
+        }
         f4_t sc[4][NR];
   #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -901,48 +949,31 @@ void prefill_affine_kernel(const Args a) {
 
 
   #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          h8_t pb[NR];
+        for (int u = 0; u < 2; ++u)
   #pragma unroll
           for (int j = 0; j < NR; ++j) {
             const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
             const u32x4_t w = {pack_h16(p0[0], p0[1]), pack_h16(p0[2], p0[3]),
                                pack_h16(p1[0], p1[1]), pack_h16(p1[2], p1[3])};
-            pb[j] = __builtin_bit_cast(h8_t, w);
+            pprev[u][j] = __builtin_bit_cast(h8_t, w);
             // The row sum counts the weights as rounded for the matrix cores,
             // so the output stays an exact convex combination of them.
   #pragma unroll
             for (int e = 0; e < 4; ++e)
               lsum[j] = sum2<true>(w[e], lsum[j]);
           }
-  #pragma unroll
-          for (int t2 = 0; t2 < NT; ++t2) {
-            // Lane lr of group lg supplies row 32u + 4lg + lr/4 and channels
-            // 16 tt + 4(lr % 4) + [0, 4); the transposing read hands it
-            // channel 16 tt + lr of keys 32u + 4lg + [0, 4) (and + 16 for
-            // the second read): the A operand of V^T for the k slots the
-            // score registers fill.
-            const uint16_t* vrow = Vt + (32 * u + 4 * lg + lr / 4) * KSTR +
-                                   16 * (t_base + t2) + 4 * (lr % 4);
-            const u32x2_t lo = tr_read(vrow);
-            const u32x2_t hi = tr_read(vrow + 16 * KSTR);
-            const h8_t va = __builtin_bit_cast(h8_t, u32x4_t{lo.x, lo.y, hi.x, hi.y});
-  #pragma unroll
-            for (int j = 0; j < NR; ++j)
-              o[t2][j] = mma<true>(va, pb[j], o[t2][j]);
-          }
-        }
+        if constexpr (!DEFER) pv_tile(pprev, Vt2(vc));
         }
       }
         }
         if constexpr (kBufs == 2) {
           if constexpr (!DQF) {
-            store_tile(set, cur ^ 1);
+            store_tile(set, cur ^ 1, vnext(vc));
             load_tile(set, t + 1 + NS);
           }
         } else {
           __syncthreads();  // every wavefront is done with this tile's LDS
-          store_tile(set, 0);
+          store_tile(set, 0, 0);
           load_tile(set, t + 1 + NS);
         }
         __syncthreads();
@@ -950,13 +981,19 @@ void prefill_affine_kernel(const Args a) {
       // Whole rounds of NS tiles, unrolled over the stage sets so each one
       // stays in named registers.
       const int64_t rounds = (t_hi - t_lo + NS) / NS;
-      int cur = 0;
+      int cur = 0, vc = 0;
       for (int64_t it = 0; it < rounds; ++it) {
         static_for<NS>([&](auto k) {
-          tile(t_lo + it * NS + decltype(k)::value, cur,
+          tile(t_lo + it * NS + decltype(k)::value, cur, vc,
                std::integral_constant<int, (decltype(k)::value + 1) % NS>{});
           cur ^= kBufs - 1;
+          vc = vnext(vc);
         });
+      }
+      // The last tile's P V: its V buffer is not written again (the loader's
+      // last store went to the buffer after it).
+      if constexpr (DEFER) {
+        if (live) pv_tile(pprev, Vt2(vprev(vc)));
       }
     };
     // One copy of the loop per (task kind, order) a wavefront can have: the
@@ -983,7 +1020,7 @@ void prefill_affine_kernel(const Args a) {
     // combines its group's rows over channels [kq D / KQ, (kq + 1) D / KQ):
     // lane i takes row i / 4 and D / 16 consecutive channels.
     const float tot = xor32_sum(xor16_sum(lsum[0]));
-    float* so = reinterpret_cast<float*>(&s_tiles[0][0][0]);  // [kWaves][16][D]
+    float* so = reinterpret_cast<float*>(&s_tiles[0][0]);  // [kWaves][16][D]
     static_assert(sizeof(s_tiles) >= sizeof(float) * kWaves * 16 * D, "merge space");
     __syncthreads();
 #pragma unroll
