@@ -168,8 +168,13 @@ struct Shape {
   // tile's P by V one tile late, before the next tile's scores. Both
   // wavefronts of a SIMD leave each tile's barrier together; in this order
   // one's softmax (VALU) meets the other's products (matrix cores) instead
-  // of both doing the same phase at once. V then needs three LDS buffers
-  // (tile t - 1 read late, t read, t + 1 written); D = 256 has no room.
+  // of both doing the same phase at once (measured on gfx950: a wavefront
+  // issuing back-to-back products leaves the other on its SIMD about one
+  // v_exp_f32 or two FMAs per product). A strict two-phase ping-pong (a
+  // barrier between products and softmax) measured slower: a wavefront's
+  // own LDS reads then stall its products with nothing to fill the gap.
+  // V needs three LDS buffers (tile t - 1 read late, t read, t + 1
+  // written); D = 256 has no room for them.
   static constexpr bool kDeferPV = !H16 && D == 128;
   static constexpr int kVBufs = kDeferPV ? 3 : kBufs;
   static_assert(kPer * kThreads == 4 * D, "whole loader tasks per thread");
@@ -240,7 +245,6 @@ template <int NW>
 struct Stage {
   uint32_t w[NW];
   uint32_t s, b;  // bf16 bits; combined only when used, so the loads stay in flight
-  bool ok;
 };
 
 // Width 16 stands for keys dequantized beforehand: rows of D bf16 values
@@ -286,13 +290,13 @@ __device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, cons
 }
 
 // Loads run `run` of key kk (counted across both segments) of K or V. A key
-// past the end loads the last key instead (ok = false: it is stored as
-// zeros), so the load is issued unconditionally.
+// past the end loads the last key instead, so the load is issued
+// unconditionally; the tile keeps that key's (finite) values, which every
+// consumer masks: its scores are -inf, so its weight is exactly 0.
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, const Args& a, int kk,
                                            int run) {
-  st.ok = kk < a.total;
-  kk = st.ok ? kk : int(a.total) - 1;
+  kk = min(kk, int(a.total) - 1);  // 32-bit: a cache holds fewer than 2^31 keys
   if constexpr (is_rows<BITS>()) {  // one segment of 16-bit rows, no scales
     load_words<16>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
     st.s = st.b = 0u;
@@ -414,17 +418,11 @@ __device__ __forceinline__ void dequant_run(const uint32_t* w, uint32_t sb, uint
 }
 
 // Writes a K task into LDS: row `key` of K at channels [32 run, 32 run + 32).
-// Keys past the end are zero (their scores are masked).
 template <int D, int BITS, bool H16, int NW>
 __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int key, int run) {
   constexpr int KSTR = kKStride<D>;
   uint32_t v[16];
-  if (st.ok) {
-    dequant_run<BITS, H16>(st.w, st.s | (st.b << 16), v);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = 0u;
-  }
+  dequant_run<BITS, H16>(st.w, st.s | (st.b << 16), v);
   u32x4_t* d = reinterpret_cast<u32x4_t*>(Ks + key * KSTR + run * 32);
 #pragma unroll
   for (int i = 0; i < 4; ++i) d[i] = u32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
@@ -432,8 +430,7 @@ __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int k
 
 // Writes a V task into LDS like a K task: row `key` of V, channels
 // [32 run, 32 run + 32), four 16-byte stores. The products read V^T from it
-// with gfx950's transposing ds_read_b64_tr_b16. Keys past the end are zero
-// (0 * v stays finite).
+// with gfx950's transposing ds_read_b64_tr_b16.
 // The prefill variant's V operands of a run: mlx::dequantize's bf16 value
 // times 2^-kVShift, as f16 (exact from the bf16 value wherever the product
 // is an f16 normal). The scale and bias are scaled first, which scales the
@@ -469,12 +466,7 @@ __device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vs, int k
   } else {
     constexpr int KSTR = kKStride<D>;
     uint32_t v[16];
-    if (st.ok) {
-      v_operand_run<BITS>(st.w, st.s | (st.b << 16), v);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = 0u;
-    }
+    v_operand_run<BITS>(st.w, st.s | (st.b << 16), v);
     u32x4_t* d = reinterpret_cast<u32x4_t*>(Vs + key * KSTR + run * 32);
 #pragma unroll
     for (int i = 0; i < 4; ++i) d[i] = u32x4_t{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
@@ -532,13 +524,21 @@ __device__ __forceinline__ float sum2(uint32_t w, float acc) {
 // (v_permlane32_swap) of a value with itself returns the lane's and its
 // partner's halves, with no LDS round trip (a ds_bpermute shuffle would sit
 // on the path from the scores to the softmax).
+// The maximum of two scores as one v_max_f32: fmaxf on the swapped values
+// costs a v_max_f32 x, x (NaN quieting) on each first, which finite
+// scores never need.
+__device__ __forceinline__ float max_raw(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 __device__ __forceinline__ float xor16_max(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_raw(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor16_sum(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -648,15 +648,34 @@ void prefill_affine_kernel(const Args a) {
     }
   }
 
-  float m[NR], lsum[NR];
+  // Per row slot: the running maximum m (log2 units), nm = -m (0 while no
+  // key is visible) and thr, the raw score above which m must move (a tile
+  // compares its raw maximum with it; all three change only on a rescale).
+  float m[NR], nm[NR], thr[NR], lsum[NR];
   f4_t o[NT][NR];
+  const float iqs = 1.0f / a.qscale;
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
     m[j] = -INFINITY;
+    nm[j] = 0.0f;
+    thr[j] = -INFINITY;
     lsum[j] = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; ++t) o[t][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
   }
+  // A rescale of row slot j to the tile maximum mx (raw), on the lanes with
+  // up set: the accumulators and sum scale by 2^(m - m'), then the state
+  // moves. qscale > 0, so mx * qscale is the maximum of the scaled scores.
+  auto rescale = [&](int j, bool up, float mx) __attribute__((always_inline)) {
+    const float mn = up ? mx * a.qscale : m[j];
+    const float alpha = up ? __builtin_amdgcn_exp2f(m[j] - mn) : 1.0f;
+    lsum[j] *= alpha;
+#pragma unroll
+    for (int t2 = 0; t2 < NT; ++t2) o[t2][j] *= alpha;
+    m[j] = mn;
+    nm[j] = mn == -INFINITY ? 0.0f : -mn;
+    thr[j] = (mn + kTau) * iqs;
+  };
 
   if (kk_lo <= kk_hi) {
     const int64_t t_lo = kk_lo / kTile, t_hi = kk_hi / kTile;
@@ -739,21 +758,16 @@ void prefill_affine_kernel(const Args a) {
         }
         float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mx = xor32_max(xor16_max(mx));
-        mx *= a.qscale;
-        const bool up = mx > m[0] + kTau;
+        // The running maximum may lag the true one by up to kTau: it moves
+        // only when some row's raw maximum passes its threshold.
+        const bool up = mx > thr[0];
         if (__any(up)) {
           keep_branch();
-          const float mn = up ? mx : m[0];
-          const float alpha = up ? __builtin_amdgcn_exp2f(m[0] - mn) : 1.0f;
-          lsum[0] *= alpha;
-#pragma unroll
-          for (int t2 = 0; t2 < NT; ++t2) o[t2][0] *= alpha;
-          m[0] = mn;
+          rescale(0, up, mx);
         }
-        const float nm = m[0] == -INFINITY ? 0.0f : -m[0];
         float p[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], a.qscale, nm));
+        for (int r = 0; r < 4; ++r) p[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], a.qscale, nm[0]));
         const uint32_t w0 = pack_h16(p[0], p[1]), w1 = pack_h16(p[2], p[3]);
         lsum[0] = sum2<true>(w1, sum2<true>(w0, lsum[0]));
         const h4_t pb = __builtin_bit_cast(h4_t, u32x2_t{w0, w1});
@@ -836,33 +850,10 @@ void prefill_affine_kernel(const Args a) {
               o[t2][j] = mma<true>(va, pp[u][j], o[t2][j]);
           }
       };
-      // This wavefront multiplies by V one tile late (the second wavefront of
-      // each SIMD): pprev holds the previous tile's packed weights.
-      constexpr bool DEFER = kDeferPV && DQF;
-      static_assert(!kDeferPV || NS == 1, "one tile a round where P V runs late");
-      h8_t pprev[2][NR];
-      auto vnext = [](int c) { return kVBufs == 3 ? (c == 2 ? 0 : c + 1) : (c ^ (kVBufs - 1)); };
-      auto vprev = [](int c) { return c == 0 ? kVBufs - 1 : c - 1; };
-      // One tile: set S holds tile t + 1's words, which go into the next
-      // LDS buffers (last read in an earlier tile, before the barrier that
-      // ended it); S then fetches tile t + 1 + NS.
-      auto tile = [&](int64_t t, int cur, int vc, auto set) __attribute__((always_inline)) {
-        if constexpr (kBufs == 2 && DQF) {
-          store_tile(set, cur ^ 1, vnext(vc));
-          load_tile(set, t + 1 + NS);
-        }
-        if (t <= t_hi) {
-      const uint16_t* Ks = Ks2(cur);
-      // A wavefront whose rows are all past the end (a short block) only
-      // dequantizes.
-      if (live) {
-        if constexpr (KS) {
-          ks_tile(t, cur, vc);
-        } else {
-        if constexpr (DEFER) {
-          if (t > t_lo) pv_tile(pprev, Vt2(vprev(vc)));
-        }
-        f4_t sc[4][NR];
+      // S^T of one tile: the K operand from buffer Ks against the
+      // wavefront's Q fragments (channel split: the partial tiles of the
+      // wavefronts summed through LDS).
+      auto score_tile = [&](const uint16_t* Ks, f4_t (&sc)[4][NR]) __attribute__((always_inline)) {
   #pragma unroll
         for (int i = 0; i < 4; ++i)
   #pragma unroll
@@ -890,7 +881,11 @@ void prefill_affine_kernel(const Args a) {
             sc[i][0] = tot;
           }
         }
-
+      };
+      // The online softmax of tile t's scores: the mask, the running
+      // maximum (and the rescale when it moves), then the weights rounded
+      // to f16 into pp and their row sums.
+      auto softmax_tile = [&](int64_t t, f4_t (&sc)[4][NR], h8_t (&pp)[2][NR]) __attribute__((always_inline)) {
         // Mask: only on tiles some row of the block sees in part. Key offset
         // o in the tile is visible to a row iff lo <= o <= hi.
         const int64_t kbase = a.k_start + int64_t(t) * kTile;
@@ -928,23 +923,18 @@ void prefill_affine_kernel(const Args a) {
   #pragma unroll
             for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[i][j][r]);
           mx = xor32_max(xor16_max(mx));
-          mx *= a.qscale;  // qscale > 0: the max of the scaled scores
-          const bool up = mx > m[j] + kTau;
+          // The running maximum may lag the true one by up to kTau: it
+          // moves only when some row's raw maximum passes its threshold.
+          const bool up = mx > thr[j];
           if (__any(up)) {
             keep_branch();
-            const float mn = up ? mx : m[j];
-            const float alpha = up ? __builtin_amdgcn_exp2f(m[j] - mn) : 1.0f;
-            lsum[j] *= alpha;
-  #pragma unroll
-            for (int t2 = 0; t2 < NT; ++t2) o[t2][j] *= alpha;
-            m[j] = mn;
+            rescale(j, up, mx);
           }
-          const float nm = m[j] == -INFINITY ? 0.0f : -m[j];
   #pragma unroll
           for (int i = 0; i < 4; ++i)
   #pragma unroll
             for (int r = 0; r < 4; ++r)
-              sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm));
+              sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm[j]));
         }
 
 
@@ -955,16 +945,54 @@ void prefill_affine_kernel(const Args a) {
             const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
             const u32x4_t w = {pack_h16(p0[0], p0[1]), pack_h16(p0[2], p0[3]),
                                pack_h16(p1[0], p1[1]), pack_h16(p1[2], p1[3])};
-            pprev[u][j] = __builtin_bit_cast(h8_t, w);
+            pp[u][j] = __builtin_bit_cast(h8_t, w);
             // The row sum counts the weights as rounded for the matrix cores,
             // so the output stays an exact convex combination of them.
   #pragma unroll
             for (int e = 0; e < 4; ++e)
               lsum[j] = sum2<true>(w[e], lsum[j]);
           }
-        if constexpr (!DEFER) pv_tile(pprev, Vt2(vc));
+      };
+      auto vnext = [](int c) { return kVBufs == 3 ? (c == 2 ? 0 : c + 1) : (c ^ (kVBufs - 1)); };
+      auto vprev = [](int c) { return c == 0 ? kVBufs - 1 : c - 1; };
+      // The second wavefront of each SIMD multiplies by V one tile late:
+      // pprev then carries the previous tile's packed weights.
+      constexpr bool DEFER = kDeferPV && DQF;
+      static_assert(!kDeferPV || NS == 1, "one tile a round where P V runs late");
+      h8_t pprev[2][NR];
+      // One tile: set S holds tile t + 1's words, which go into the next
+      // LDS buffers (last read in an earlier tile, before the barrier that
+      // ended it); S then fetches tile t + 1 + NS.
+      auto tile = [&](int64_t t, int cur, int vc, auto set) __attribute__((always_inline)) {
+        if constexpr (kBufs == 2 && DQF) {
+          store_tile(set, cur ^ 1, vnext(vc));
+          load_tile(set, t + 1 + NS);
         }
-      }
+        if (t <= t_hi) {
+          // A wavefront whose rows are all past the end (a short block)
+          // only dequantizes.
+          if (live) {
+            if constexpr (KS) {
+              ks_tile(t, cur, vc);
+            } else {
+              // The products run at the higher wave priority where the two
+              // wavefronts of a SIMD alternate phases, so the matrix cores
+              // are fed first.
+              if constexpr (kDeferPV) __builtin_amdgcn_s_setprio(1);
+              if constexpr (DEFER) {
+                if (t > t_lo) pv_tile(pprev, Vt2(vprev(vc)));
+              }
+              f4_t sc[4][NR];
+              score_tile(Ks2(cur), sc);
+              if constexpr (kDeferPV) __builtin_amdgcn_s_setprio(0);
+              softmax_tile(t, sc, pprev);
+              if constexpr (!DEFER) {
+                if constexpr (kDeferPV) __builtin_amdgcn_s_setprio(1);
+                pv_tile(pprev, Vt2(vc));
+                if constexpr (kDeferPV) __builtin_amdgcn_s_setprio(0);
+              }
+            }
+          }
         }
         if constexpr (kBufs == 2) {
           if constexpr (!DQF) {
