@@ -29,49 +29,65 @@ KernelFn pick(int D, int bk, int bv, bool h16 = false) {
 // as bf16 rows [B * H_kv, total, D] with mlx::dequantize's arithmetic
 // (bf16(fma(scale, code, bias)), one rounding), V into vd as the prefill
 // kernel's V operands (those bf16 values times 2^-kVShift, in f16; see
-// v_operand_run). Grid: (row chunks, slab, K or V); a thread writes 8
-// consecutive values of one row (one 16-byte store). Keys [0, n0) come from
-// segment 0, the rest from segment 1.
-template <int D>
-__global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int bk, int bv,
+// v_operand_run). Grid: (row-run chunks, slab, K and/or V); a thread takes
+// one run of 32 values of one row: its BITS words in one or two wide loads,
+// its group's scale and bias (a run never straddles a group: gs is a
+// multiple of 32), four 16-byte stores. kinds: 1 = K, 2 = V, 3 = both
+// (blockIdx.z picks). Keys [0, n0) come from segment 0, the rest from
+// segment 1.
+template <int D, int BITS>
+__global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int kinds,
                                                               uint16_t* kd, uint16_t* vd) {
-  constexpr int kPerRow = D / 8;
+  constexpr int kRuns = D / 32;
   const uint32_t j = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t row = j / kPerRow;
+  const uint32_t row = j / kRuns;
   if (row >= uint32_t(a.total)) return;
-  const int c8 = int(j % kPerRow), e0 = 8 * c8;
+  const int run = int(j % kRuns);
   const int slab = int(blockIdx.y), bb = slab / a.H_kv, kv = slab % a.H_kv;
-  const bool isv = blockIdx.z != 0;
+  const bool isv = kinds == 3 ? blockIdx.z != 0 : kinds == 2;
   const bool first = row < uint32_t(a.n0);
   const Seg& s = a.seg[first ? 0 : 1];
   const int64_t src = int64_t(bb) * s.b_stride + int64_t(kv) * s.cap +
                       (first ? row : row - uint32_t(a.n0));
-  const int bits = isv ? bv : bk;
-  const uint32_t* pw = (isv ? s.vw : s.kw) + src * (D * bits / 32);
-  const int groups = D / a.gs, g = e0 / a.gs;
-  const float down = isv ? kVDown : 1.0f;
-  const float sc = bf16_to_f32((isv ? s.vs : s.ks)[src * groups + g]) * down;
-  const float bi = bf16_to_f32((isv ? s.vb : s.kb)[src * groups + g]) * down;
-  // The 8 codes start on a byte (8 * bits bits from bit e0 * bits) and, at
-  // every width, end within the next 64 bits of the word holding their
-  // first bit: two loads, the second only when they run into it.
-  const int bit0 = e0 * bits, sh = bit0 % 32;
-  uint64_t win = pw[bit0 / 32];
-  if (sh + 8 * bits > 32) win |= uint64_t(pw[bit0 / 32 + 1]) << 32;
-  win >>= sh;
-  uint32_t out[4];
+  const uint32_t* pw = (isv ? s.vw : s.kw) + src * (D * BITS / 32) + run * BITS;
+  const int64_t g = src * (D / a.gs) + (run * 32) / a.gs;
+  const uint32_t sb = uint32_t((isv ? s.vs : s.ks)[g]) | (uint32_t((isv ? s.vb : s.kb)[g]) << 16);
+  uint32_t w[BITS], out[16];
+  load_words<BITS>(w, pw);
+  if (isv)
+    v_operand_run<BITS>(w, sb, out);
+  else
+    dequant_run<BITS, false>(w, sb, out);
+  uint4* d = reinterpret_cast<uint4*>((isv ? vd : kd) + (int64_t(slab) * a.total + row) * D + run * 32);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t code = uint32_t(win >> (e * bits)) & ((1u << bits) - 1);
-    uint32_t v = f32_to_bf16(fmaf(sc, float(code), bi));
-    if (isv) v = __builtin_bit_cast(uint16_t, _Float16(bf16_to_f32(uint16_t(v))));
-    if (e % 2 == 0)
-      out[e / 2] = v;
-    else
-      out[e / 2] |= v << 16;
+  for (int i = 0; i < 4; ++i) d[i] = uint4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+}
+
+template <int D>
+void launch_dequantize_rows(const Args& a, int bits, int kinds, dim3 grid, hipStream_t st,
+                            uint16_t* kd, uint16_t* vd) {
+  switch (bits) {
+    case 2: hipLaunchKernelGGL((dequantize_rows_kernel<D, 2>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
+    case 3: hipLaunchKernelGGL((dequantize_rows_kernel<D, 3>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
+    case 4: hipLaunchKernelGGL((dequantize_rows_kernel<D, 4>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
+    case 5: hipLaunchKernelGGL((dequantize_rows_kernel<D, 5>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
+    case 6: hipLaunchKernelGGL((dequantize_rows_kernel<D, 6>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
+    default: hipLaunchKernelGGL((dequantize_rows_kernel<D, 8>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
   }
-  *reinterpret_cast<uint4*>((isv ? vd : kd) + (int64_t(slab) * a.total + row) * D + e0) =
-      uint4{out[0], out[1], out[2], out[3]};
+}
+
+// Both halves of the dequantize-once pass: one launch when K and V share a
+// width, else one each.
+template <int D>
+void dequantize_rows(const Args& a, int bk, int bv, int64_t slabs, hipStream_t st, uint16_t* kd,
+                     uint16_t* vd) {
+  const unsigned chunks = unsigned((a.total * (D / 32) + 255) / 256);
+  if (bk == bv) {
+    launch_dequantize_rows<D>(a, bk, 3, dim3(chunks, unsigned(slabs), 2), st, kd, vd);
+  } else {
+    launch_dequantize_rows<D>(a, bk, 1, dim3(chunks, unsigned(slabs), 1), st, kd, vd);
+    launch_dequantize_rows<D>(a, bv, 2, dim3(chunks, unsigned(slabs), 1), st, kd, vd);
+  }
 }
 
 // Row blocks sharing one (batch row, KV head) from which the keys are
@@ -319,24 +335,11 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
     uint16_t* kd = static_cast<uint16_t*>(ws);
     uint16_t* vd = kd + size_t(slabs) * size_t(a.total) * size_t(D);
     if (slabs > 65535) return fail(TQKV_EINVAL_SHAPE, "B * H_kv = %lld slabs", (long long)slabs);
-    const dim3 dq_grid(unsigned((a.total * (D / 8) + 255) / 256), unsigned(slabs), 2);
     switch (D) {
-      case 64:
-        hipLaunchKernelGGL(dequantize_rows_kernel<64>, dq_grid, dim3(256), 0, st, a, bits_k,
-                           bits_v, kd, vd);
-        break;
-      case 128:
-        hipLaunchKernelGGL(dequantize_rows_kernel<128>, dq_grid, dim3(256), 0, st, a, bits_k,
-                           bits_v, kd, vd);
-        break;
-      case 256:
-        hipLaunchKernelGGL(dequantize_rows_kernel<256>, dq_grid, dim3(256), 0, st, a, bits_k,
-                           bits_v, kd, vd);
-        break;
-      default:
-        hipLaunchKernelGGL(dequantize_rows_kernel<512>, dq_grid, dim3(256), 0, st, a, bits_k,
-                           bits_v, kd, vd);
-        break;
+      case 64: dequantize_rows<64>(a, bits_k, bits_v, slabs, st, kd, vd); break;
+      case 128: dequantize_rows<128>(a, bits_k, bits_v, slabs, st, kd, vd); break;
+      case 256: dequantize_rows<256>(a, bits_k, bits_v, slabs, st, kd, vd); break;
+      default: dequantize_rows<512>(a, bits_k, bits_v, slabs, st, kd, vd); break;
     }
     TQKV_LAUNCHED();
     Args p = a;
