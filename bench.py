@@ -408,9 +408,9 @@ def prefill_main(T, hip, args):
     assert np.all(np.isfinite(o)) and np.abs(o).max() > 0, "prefill output is not sane"
     # HBM bytes of one global-chunk call at this shape, from the FETCH_SIZE
     # (x 2.000) and WRITE_SIZE (x 1.000) passes of
-    # profiles/prefill_affine_config3.md: dequantize-once 83.94 MB read +
+    # profiles/prefill_affine_config3.md: dequantize-once 75.55 MB read +
     # 268.44 MB written, attention 335.88 MB read + 67.11 MB written.
-    traffic = 755356672 if (B, L, N_G) == (4, 2048, 16384) else None
+    traffic = 746973184 if (B, L, N_G) == (4, 2048, 16384) else None
     result = {
         "metric": PREFILL_METRIC,
         "value": round(B * L / (ms_per_step * 1e-3), 1),
@@ -431,7 +431,7 @@ def prefill_main(T, hip, args):
             "traffic_source": ("profile-derived, not counted in this run: the counter passes "
                                "of profiles/prefill_affine_config3.md (both launches of the "
                                "call)" if traffic is not None else None),
-            "kernel": "tqkv_prefill_attend_affine call: dequantize_rows_kernel<128> (the "
+            "kernel": "tqkv_prefill_attend_affine call: dequantize_rows_kernel<128,4> (the "
                       "keys once: K bf16, V f16 operands) + prefill_affine_kernel<128,16,17>",
             "alg_flops_per_launch": fl_g, "avg_launch_ms": round(ms_g, 5),
         },
