@@ -33,10 +33,11 @@
 //   S^T = K . Q^T: A = K rows from LDS (ds_read_b128), B = the wavefront's Q
 //   rows held in registers for the whole kernel; lane l ends up with the
 //   scores of query row l % 16 for keys 16i + 4(l / 16) + r.
-//   Online softmax per row: the 64-key maximum is a 16-value local max plus
-//   two lane exchanges (l ^ 16, l ^ 32); the running maximum may lag the true
-//   one by up to kTau (log2 units), so the O accumulators are rescaled only
-//   when some row moves by more. Row sums (of the f16-rounded weights, one
+//   Online softmax per row: the running maximum may lag the true one by up
+//   to kTau (log2 units), so the O accumulators are rescaled only when some
+//   row moves by more; a lane compares its own 16-key maximum with the
+//   row's threshold, and only when some lane passes it are the row's lanes
+//   combined (two lane exchanges, l ^ 16 and l ^ 32). Row sums (of the f16-rounded weights, one
 //   v_dot2 per pair) stay per lane until the end.
 //   O^T += V^T . P^T: the score registers of key tiles 2u and 2u + 1 are,
 //   rounded to f16, exactly the B operand (k slot 8(l / 16) + s holds key
@@ -623,21 +624,27 @@ void prefill_affine_kernel(const Args a) {
 
   using op8_t = std::conditional_t<H16, h8_t, bf8_t>;
   op8_t qf[NR][NDW];
-  int64_t qabs[NR], orow[NR];
-  bool rvalid[NR];
+  // Row slot j of this lane: row r of the block's (query, head) rows, held
+  // as its query index within the chunk (ql, 32-bit; the Q and output row
+  // offsets are recomputed where they are used, off the tile loop).
+  int ql[NR];
+  auto row_of = [&](int j) __attribute__((always_inline)) { return row0 + wrow + 16 * j + lr; };
+  auto orow_of = [&](int64_t r) __attribute__((always_inline)) {
+    const int64_t rr = r < rows ? r : rows - 1;
+    const int64_t l = rr / a.G, g = rr % a.G;
+    return int64_t(b) * a.qs_b + (int64_t(kvh) * a.G + g) * a.qs_h + l * a.qs_l;
+  };
 #pragma unroll
   for (int j = 0; j < NR; ++j) {
-    const int64_t r = row0 + wrow + 16 * j + lr;
-    rvalid[j] = r < rows;
-    const int64_t rr = rvalid[j] ? r : rows - 1;
-    const int64_t l = rr / a.G, g = rr % a.G;
-    qabs[j] = a.q_start + l;
-    orow[j] = int64_t(b) * a.qs_b + (int64_t(kvh) * a.G + g) * a.qs_h + l * a.qs_l;
+    const int64_t r = row_of(j);
+    const int64_t rr = r < rows ? r : rows - 1;
+    ql[j] = int(rr / a.G);
+    const int64_t orow = orow_of(r);
 #pragma unroll
     for (int s = 0; s < NDW; ++s)
     {
       const bf8_t x =
-          *reinterpret_cast<const bf8_t*>(a.q + orow[j] + 32 * (s_base + s) + 8 * lg);
+          *reinterpret_cast<const bf8_t*>(a.q + orow + 32 * (s_base + s) + 8 * lg);
       if constexpr (H16) {
         // bf16 -> f16 is exact for |q| in f16's normal range.
 #pragma unroll
@@ -743,7 +750,7 @@ void prefill_affine_kernel(const Args a) {
           keep_branch();
           int hi = rem - 1, lo = 0;
           if (a.causal) {
-            const int64_t dq = qabs[0] - kbase;
+            const int64_t dq = a.q_start + ql[0] - kbase;
             if (dq < hi) hi = dq < -1 ? -1 : int(dq);
             if (a.window >= 0) {
               const int64_t first = dq - a.window + 1;
@@ -882,9 +889,33 @@ void prefill_affine_kernel(const Args a) {
           }
         }
       };
+      // The weights of tile t: exp2 of each scaled score less its row's
+      // running maximum, rounded to f16 into pp, their sums added to acc.
+      auto weigh = [&](f4_t (&sc)[4][NR], h8_t (&pp)[2][NR], float (&acc)[NR]) __attribute__((always_inline)) {
+  #pragma unroll
+        for (int j = 0; j < NR; ++j)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i)
+  #pragma unroll
+            for (int r = 0; r < 4; ++r)
+              sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm[j]));
+  #pragma unroll
+        for (int u = 0; u < 2; ++u)
+  #pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
+            const u32x4_t w = {pack_h16(p0[0], p0[1]), pack_h16(p0[2], p0[3]),
+                               pack_h16(p1[0], p1[1]), pack_h16(p1[2], p1[3])};
+            pp[u][j] = __builtin_bit_cast(h8_t, w);
+            // The row sum counts the weights as rounded for the matrix cores,
+            // so the output stays an exact convex combination of them.
+  #pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[j] = sum2<true>(w[e], acc[j]);
+          }
+      };
       // The online softmax of tile t's scores: the mask, the running
-      // maximum (and the rescale when it moves), then the weights rounded
-      // to f16 into pp and their row sums.
+      // maximum (and the rescale when it moves), then the weights.
       auto softmax_tile = [&](int64_t t, f4_t (&sc)[4][NR], h8_t (&pp)[2][NR]) __attribute__((always_inline)) {
         // Mask: only on tiles some row of the block sees in part. Key offset
         // o in the tile is visible to a row iff lo <= o <= hi.
@@ -899,7 +930,7 @@ void prefill_affine_kernel(const Args a) {
           for (int j = 0; j < NR; ++j) {
             int hi = rem - 1, lo = 0;
             if (a.causal) {
-              const int64_t dq = qabs[j] - kbase;  // the row's own offset
+              const int64_t dq = a.q_start + ql[j] - kbase;  // the row's own offset
               if (dq < hi) hi = dq < -1 ? -1 : int(dq);
               if (a.window >= 0) {
                 const int64_t first = dq - a.window + 1;
@@ -917,41 +948,22 @@ void prefill_affine_kernel(const Args a) {
         }
   #pragma unroll
         for (int j = 0; j < NR; ++j) {
+          // The lane's maximum over its 16 keys of the row. The running
+          // maximum may lag the true one by up to kTau: it moves only when
+          // the row's raw maximum passes its threshold, which needs some
+          // lane's to pass it; only then are the row's four lanes combined.
           float mx = -INFINITY;
   #pragma unroll
           for (int i = 0; i < 4; ++i)
   #pragma unroll
             for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[i][j][r]);
-          mx = xor32_max(xor16_max(mx));
-          // The running maximum may lag the true one by up to kTau: it
-          // moves only when some row's raw maximum passes its threshold.
-          const bool up = mx > thr[j];
-          if (__any(up)) {
+          if (__any(mx > thr[j])) {
             keep_branch();
-            rescale(j, up, mx);
+            mx = xor32_max(xor16_max(mx));
+            rescale(j, mx > thr[j], mx);
           }
-  #pragma unroll
-          for (int i = 0; i < 4; ++i)
-  #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              sc[i][j][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i][j][r], a.qscale, nm[j]));
         }
-
-
-  #pragma unroll
-        for (int u = 0; u < 2; ++u)
-  #pragma unroll
-          for (int j = 0; j < NR; ++j) {
-            const f4_t p0 = sc[2 * u][j], p1 = sc[2 * u + 1][j];
-            const u32x4_t w = {pack_h16(p0[0], p0[1]), pack_h16(p0[2], p0[3]),
-                               pack_h16(p1[0], p1[1]), pack_h16(p1[2], p1[3])};
-            pp[u][j] = __builtin_bit_cast(h8_t, w);
-            // The row sum counts the weights as rounded for the matrix cores,
-            // so the output stays an exact convex combination of them.
-  #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              lsum[j] = sum2<true>(w[e], lsum[j]);
-          }
+        weigh(sc, pp, lsum);
       };
       auto vnext = [](int c) { return kVBufs == 3 ? (c == 2 ? 0 : c + 1) : (c ^ (kVBufs - 1)); };
       auto vprev = [](int c) { return c == 0 ? kVBufs - 1 : c - 1; };
@@ -1111,7 +1123,7 @@ void prefill_affine_kernel(const Args a) {
   for (int j = 0; j < NR; ++j) {
     float tot = lsum[j];
     tot = xor32_sum(xor16_sum(tot));
-    if (!rvalid[j]) continue;
+    if (row_of(j) >= rows) continue;
     // The prefill variant's V operands were scaled by 2^-kVShift.
     const float vup = H16 ? 1.0f : kVUp;
     if (a.part_o) {
@@ -1131,7 +1143,7 @@ void prefill_affine_kernel(const Args a) {
 #pragma unroll
       for (int t2 = 0; t2 < NT; ++t2) {
         const f4_t v = o[t2][j] * inv;
-        *reinterpret_cast<u32x2_t*>(a.out + orow[j] + 16 * (t_base + t2) + 4 * lg) =
+        *reinterpret_cast<u32x2_t*>(a.out + orow_of(row_of(j)) + 16 * (t_base + t2) + 4 * lg) =
             u32x2_t{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
       }
     }
