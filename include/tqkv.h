@@ -411,7 +411,9 @@ int32_t tqkv_prefill_attend_affine_ws(const uint16_t* q, int32_t B, int32_t H, i
                                       int32_t causal, int64_t window, uint16_t* out,
                                       void* workspace, size_t workspace_bytes,
                                       tqkv_stream stream);
-/* Bytes of the prefill's dequantize-once rows: 2 * B * H_kv * keys * D * 2. */
+/* Bytes of the prefill's dequantize-once rows: 2 * B * H_kv * rows * D * 2,
+ * rows = keys, rounded up to a multiple of 64 at D = 128 (V is held there as
+ * 64-key tiles). */
 size_t tqkv_prefill_workspace_size(int32_t B, int32_t H_kv, int32_t D, int64_t total_keys);
 
 /* Bytes of workspace tqkv_decode_attend_affine needs for this shape. */

@@ -26,25 +26,34 @@ KernelFn pick(int D, int bk, int bv, bool h16 = false) {
 }
 
 // Dequantize-once: keys [0, total) of every (batch row, KV head), K into kd
-// as bf16 rows [B * H_kv, total, D] with mlx::dequantize's arithmetic
+// as bf16 rows [B * H_kv, slab_rows, D] with mlx::dequantize's arithmetic
 // (bf16(fma(scale, code, bias)), one rounding), V into vd as the prefill
 // kernel's V operands (those bf16 values times 2^-kVShift, in f16; see
-// v_operand_run). Grid: (row-run chunks, slab, K and/or V); a thread takes
-// one run of 32 values of one row: its BITS words in one or two wide loads,
-// its group's scale and bias (a run never straddles a group: gs is a
-// multiple of 32). A wavefront's 64 runs are 4 KB of consecutive rows;
-// they pass through LDS so that each of the wavefront's four 16-byte store
-// instructions writes 1 KB contiguously (measured on MI355X: 64-byte
-// strided 16-byte stores reach 3.5 TB/s, contiguous ones 7.0). kinds: 1 =
-// K, 2 = V, 3 = both (blockIdx.z picks). Keys [0, n0) come from segment 0,
-// the rest from segment 1.
+// v_operand_run): rows like K, or with vt (D = 128) transposed 64-key tiles
+// (width kPreF16T; slab_rows a multiple of 64, zeros past the last key).
+// Grid: (row-run chunks, slab, K and/or V); a thread takes one run of 32
+// values of one row: its BITS words in one or two wide loads, its group's
+// scale and bias (a run never straddles a group: gs is a multiple of 32).
+// A wavefront's 64 runs are 4 KB of consecutive rows; they pass through LDS
+// so that each of the wavefront's four 16-byte store instructions writes 1
+// KB contiguously (measured on MI355X: 64-byte strided 16-byte stores reach
+// 3.5 TB/s, contiguous ones 7.0). A V^T tile is a workgroup's 256 runs (64
+// keys at D = 128), transposed through LDS with the transposing read, its
+// 16 KB written 1 KB a store instruction. kinds: 1 = K, 2 = V, 3 = both
+// (blockIdx.z picks). Keys [0, n0) come from segment 0, the rest from
+// segment 1.
 template <int D, int BITS>
 __global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int kinds,
+                                                              int64_t slab_rows, int vt,
                                                               uint16_t* kd, uint16_t* vd) {
   constexpr int kRuns = D / 32;
   static_assert(64 % kRuns == 0, "a wavefront covers whole rows");
   constexpr int kChunkRows = D / 8;  // 16-byte chunks a row
-  __shared__ uint4 s_t[4][256];      // a wavefront's 64 runs x 4 chunks
+  constexpr int KSTR = kKStride<D>;
+  // A wavefront's 64 runs x 4 chunks each (rows), or the tile's 64 keys
+  // row-major at the prefill kernel's stride (V^T).
+  constexpr int kLds = D == 128 ? 64 * KSTR / 8 : 1024;
+  __shared__ uint4 s_buf[kLds];
   const int wv = threadIdx.x / 64, l = threadIdx.x % 64;
   const uint32_t j = blockIdx.x * 256u + threadIdx.x;
   const uint32_t total = uint32_t(a.total);
@@ -67,48 +76,92 @@ __global__ __launch_bounds__(256) void dequantize_rows_kernel(const Args a, int 
     v_operand_run<BITS>(w, sb, out);
   else
     dequant_run<BITS, false>(w, sb, out);
+  if constexpr (D == 128) {
+    if (isv && vt) {  // (block-uniform)
+      // Keys past the end are zeros: their weights are exactly 0, and 0
+      // times a zero operand stays 0.
+      const int key = int(threadIdx.x) / kRuns;
+      uint4* d = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(s_buf) + key * KSTR + run * 32);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        d[i] = row < total ? uint4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]}
+                           : uint4{0u, 0u, 0u, 0u};
+      __syncthreads();
+      // Store pass (u, tt) of wavefront wv: lane (grp, lr) takes channel
+      // 16 tt + lr of keys 32 u + 4 grp + [0, 4) and 32 u + 16 + 4 grp +
+      // [0, 4) (two transposing reads), the 16 bytes at slot 8 grp of V^T
+      // row u D + 16 tt + lr; the wavefront's 64 chunks are 16 whole rows.
+      const int grp = l / 16, lr = l % 16;
+      uint4* tile = reinterpret_cast<uint4*>(vd + (int64_t(slab) * slab_rows + int64_t(blockIdx.x) * kTile) * D);
+      const uint16_t* sv = reinterpret_cast<const uint16_t*>(s_buf);
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int pass = 4 * wv + it, u = pass / 8, tt = pass % 8;
+        const uint16_t* vrow = sv + (32 * u + 4 * grp + lr / 4) * KSTR + 16 * tt + 4 * (lr % 4);
+        const u32x2_t lo = tr_read(vrow);
+        const u32x2_t hi = tr_read(vrow + 16 * KSTR);
+        tile[(u * D + 16 * tt + lr) * 4 + grp] = uint4{lo.x, lo.y, hi.x, hi.y};
+      }
+      return;
+    }
+  }
   // Lane l's run is chunks 4 l .. 4 l + 3 of the wavefront's block; store i
   // of lane l writes chunk 64 i + l. The exchange stays inside one
   // wavefront, so a wavefront-scope fence orders it (no workgroup barrier).
+  uint4* s_t = s_buf + 256 * wv;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    s_t[wv][4 * l + i] = uint4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
+    s_t[4 * l + i] = uint4{out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]};
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const uint32_t row0 = (blockIdx.x * 256u + wv * 64u) / kRuns;
-  uint4* d = reinterpret_cast<uint4*>((isv ? vd : kd) + (int64_t(slab) * a.total + row0) * D);
+  uint4* d = reinterpret_cast<uint4*>((isv ? vd : kd) + (int64_t(slab) * slab_rows + row0) * D);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int c = 64 * i + l;
-    if (row0 + uint32_t(c / kChunkRows) < total) d[c] = s_t[wv][c];
+    if (row0 + uint32_t(c / kChunkRows) < total) d[c] = s_t[c];
   }
 }
 
 template <int D>
-void launch_dequantize_rows(const Args& a, int bits, int kinds, dim3 grid, hipStream_t st,
-                            uint16_t* kd, uint16_t* vd) {
+void launch_dequantize_rows(const Args& a, int bits, int kinds, int64_t slab_rows, int vt,
+                            dim3 grid, hipStream_t st, uint16_t* kd, uint16_t* vd) {
+#define TQKV_DQ(B)                                                                            \
+  hipLaunchKernelGGL((dequantize_rows_kernel<D, B>), grid, dim3(256), 0, st, a, kinds, slab_rows, \
+                     vt, kd, vd)
   switch (bits) {
-    case 2: hipLaunchKernelGGL((dequantize_rows_kernel<D, 2>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
-    case 3: hipLaunchKernelGGL((dequantize_rows_kernel<D, 3>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
-    case 4: hipLaunchKernelGGL((dequantize_rows_kernel<D, 4>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
-    case 5: hipLaunchKernelGGL((dequantize_rows_kernel<D, 5>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
-    case 6: hipLaunchKernelGGL((dequantize_rows_kernel<D, 6>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
-    default: hipLaunchKernelGGL((dequantize_rows_kernel<D, 8>), grid, dim3(256), 0, st, a, kinds, kd, vd); break;
+    case 2: TQKV_DQ(2); break;
+    case 3: TQKV_DQ(3); break;
+    case 4: TQKV_DQ(4); break;
+    case 5: TQKV_DQ(5); break;
+    case 6: TQKV_DQ(6); break;
+    default: TQKV_DQ(8); break;
   }
+#undef TQKV_DQ
+}
+
+// V as transposed tiles (width kPreF16T) at this head dim.
+constexpr bool v_tiles(int D) { return D == 128; }
+// Rows a slab of the dequantize-once scratch holds: total, padded to whole
+// 64-key tiles where V is tiled (K shares the stride).
+int64_t once_slab_rows(int D, int64_t total) {
+  return v_tiles(D) ? (total + kTile - 1) / kTile * kTile : total;
 }
 
 // Both halves of the dequantize-once pass: one launch when K and V share a
-// width, else one each.
+// width, else one each. (At D = 128 a chunk of 256 runs is one 64-key tile.)
 template <int D>
 void dequantize_rows(const Args& a, int bk, int bv, int64_t slabs, hipStream_t st, uint16_t* kd,
                      uint16_t* vd) {
   const unsigned chunks = unsigned((a.total * (D / 32) + 255) / 256);
+  const int64_t sr = once_slab_rows(D, a.total);
+  const int vt = v_tiles(D) ? 1 : 0;
   if (bk == bv) {
-    launch_dequantize_rows<D>(a, bk, 3, dim3(chunks, unsigned(slabs), 2), st, kd, vd);
+    launch_dequantize_rows<D>(a, bk, 3, sr, vt, dim3(chunks, unsigned(slabs), 2), st, kd, vd);
   } else {
-    launch_dequantize_rows<D>(a, bk, 1, dim3(chunks, unsigned(slabs), 1), st, kd, vd);
-    launch_dequantize_rows<D>(a, bv, 2, dim3(chunks, unsigned(slabs), 1), st, kd, vd);
+    launch_dequantize_rows<D>(a, bk, 1, sr, vt, dim3(chunks, unsigned(slabs), 1), st, kd, vd);
+    launch_dequantize_rows<D>(a, bv, 2, sr, vt, dim3(chunks, unsigned(slabs), 1), st, kd, vd);
   }
 }
 
@@ -343,7 +396,8 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
   // TQKV_PREFILL_DEQUANT_ONCE=0 / 1 forces the choice (tests compare them).
   const char* once_env = getenv("TQKV_PREFILL_DEQUANT_ONCE");
   const int64_t slabs = int64_t(B) * H_kv;
-  const size_t need = 2 * size_t(slabs) * size_t(a.total) * size_t(D) * 2;
+  const int64_t slab_rows = once_slab_rows(D, a.total);
+  const size_t need = 2 * size_t(slabs) * size_t(slab_rows) * size_t(D) * 2;
   // With a caller workspace (the _ws entry) the dequantized rows go there
   // when it holds them, else every block dequantizes for itself.
   const bool fits = library_scratch || (workspace && workspace_bytes >= need);
@@ -355,7 +409,7 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
     if (library_scratch)
       if (int32_t rc = scratch_for_current_device(need, &ws)) return rc;
     uint16_t* kd = static_cast<uint16_t*>(ws);
-    uint16_t* vd = kd + size_t(slabs) * size_t(a.total) * size_t(D);
+    uint16_t* vd = kd + size_t(slabs) * size_t(slab_rows) * size_t(D);
     if (slabs > 65535) return fail(TQKV_EINVAL_SHAPE, "B * H_kv = %lld slabs", (long long)slabs);
     switch (D) {
       case 64: dequantize_rows<64>(a, bits_k, bits_v, slabs, st, kd, vd); break;
@@ -367,12 +421,12 @@ int32_t prefill_launch(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, in
     Args p = a;
     const uint16_t* none = kd;  // scales and biases: never read at this width
     p.seg[0] = Seg{reinterpret_cast<const uint32_t*>(kd), none, none,
-                   reinterpret_cast<const uint32_t*>(vd), none, none, a.total,
-                   int64_t(H_kv) * a.total};
+                   reinterpret_cast<const uint32_t*>(vd), none, none, slab_rows,
+                   int64_t(H_kv) * slab_rows};
     p.seg[1] = p.seg[0];
     p.n0 = a.total;
-    hipLaunchKernelGGL(pick(D, kPreBits, kPreF16), dim3(unsigned(grid)), dim3(threads), 0, st,
-                       p);
+    hipLaunchKernelGGL(pick(D, kPreBits, v_tiles(D) ? kPreF16T : kPreF16), dim3(unsigned(grid)),
+                       dim3(threads), 0, st, p);
     TQKV_LAUNCHED();
     return ok();
   }
@@ -397,7 +451,7 @@ extern "C" int32_t tqkv_prefill_attend_affine(const uint16_t* q, int32_t B, int3
 extern "C" size_t tqkv_prefill_workspace_size(int32_t B, int32_t H_kv, int32_t D,
                                               int64_t total_keys) {
   if (B <= 0 || H_kv <= 0 || D <= 0 || total_keys <= 0) return 0;
-  return 2 * size_t(B) * size_t(H_kv) * size_t(total_keys) * size_t(D) * 2;
+  return 2 * size_t(B) * size_t(H_kv) * size_t(once_slab_rows(D, total_keys)) * size_t(D) * 2;
 }
 
 extern "C" int32_t tqkv_prefill_attend_affine_ws(

@@ -253,10 +253,23 @@ struct Stage {
 // f16 values already in the prefill variant's V operand form (bf16 values
 // times 2^-kVShift, written once per (batch row, KV head) by
 // dequantize_rows_kernel), which the loaders copy into LDS as they are.
+// Width 18 (D = 128): the same V operands as transposed 64-key tiles, the
+// slab padded to whole tiles (zeros past the last key). Tile t is 2 D rows
+// of 32 values: row u D + c holds channel c of keys 64 t + 32 u + [0, 32)
+// in the order of the P operand's k slots (slot 8 g + s: key 4 g + s for
+// s < 4, 16 + 4 g + s - 4 else), so the products read V^T with one 16-byte
+// LDS read where the row-major tile takes two transposing reads.
 constexpr int kPreBits = 16;
 constexpr int kPreF16 = 17;
+constexpr int kPreF16T = 18;
 template <int BITS>
-constexpr bool is_rows() { return BITS == kPreBits || BITS == kPreF16; }
+constexpr bool is_rows() { return BITS == kPreBits || BITS == kPreF16 || BITS == kPreF16T; }
+// Row stride of a V^T tile in LDS (elements): 96 bytes. Counted with
+// gfx950's bank rules (16-byte reads served 32 lanes at a time over 128
+// dword banks; 16-byte stores 8 lanes at a time over 32), the P V operand
+// reads are then conflict-free and a loader store costs 8 conflict cycles;
+// at 80 bytes the reads would cost 4 each.
+constexpr int kVtStr = 48;
 // 32-bit words of a loader task's run of 32 values.
 template <int BITS>
 constexpr int run_words() { return is_rows<BITS>() ? 16 : BITS; }
@@ -297,6 +310,13 @@ __device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, cons
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, const Args& a, int kk,
                                            int run) {
+  if constexpr (BITS == kPreF16T) {  // row kk % 64 + 64 run of tile kk / 64
+    static_assert(D == 128, "transposed V tiles at head dim 128");
+    load_words<16>(st.w, p.w0 + (uint32_t(kk / kTile) * (D * 32) +
+                                 uint32_t(kk % kTile + kTile * run) * 16));
+    st.s = st.b = 0u;
+    return;
+  }
   kk = min(kk, int(a.total) - 1);  // 32-bit: a cache holds fewer than 2^31 keys
   if constexpr (is_rows<BITS>()) {  // one segment of 16-bit rows, no scales
     load_words<16>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
@@ -439,7 +459,7 @@ __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int k
 // the power of two.
 template <int BITS>
 __device__ __forceinline__ void v_operand_run(const uint32_t* w, uint32_t sb, uint32_t* out) {
-  if constexpr (BITS == kPreF16) {
+  if constexpr (BITS == kPreF16 || BITS == kPreF16T) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) out[i] = w[i];
   } else if constexpr (BITS == kPreBits) {
@@ -464,6 +484,11 @@ template <int D, int BITS, bool H16, int NW>
 __device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vs, int key, int run) {
   if constexpr (H16) {
     store_k<D, BITS, H16>(st, Vs, key, run);
+  } else if constexpr (BITS == kPreF16T) {  // row key + 64 run of the V^T tile
+    u32x4_t* d = reinterpret_cast<u32x4_t*>(Vs + (key + kTile * run) * kVtStr);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      d[i] = u32x4_t{st.w[4 * i], st.w[4 * i + 1], st.w[4 * i + 2], st.w[4 * i + 3]};
   } else {
     constexpr int KSTR = kKStride<D>;
     uint32_t v[16];
@@ -584,7 +609,14 @@ void prefill_affine_kernel(const Args a) {
   // where P V runs one tile late on half the wavefronts.
   // K tiles then V tiles, one array: after the last tile the key split
   // merges its quarters' accumulators in the same memory.
-  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[kBufs + kVBufs][kTile * KSTR];
+  // V^T tiles (width 18) are 2 D rows at kVtStr.
+  constexpr bool VT = BV == kPreF16T;
+  static_assert(!VT || (D == 128 && !H16 && !KS && !CS), "V^T tiles: the bf16 variant at D = 128");
+  // (Buffers of one size, a two-dimensional array: with buffer offsets
+  // computed from a flat array the compiler keeps more addresses live and
+  // spills.)
+  constexpr int kBufElems = VT ? 2 * D * kVtStr : kTile * KSTR;
+  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[kBufs + kVBufs][kBufElems];
   auto Ks2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[c][0]; };
   auto Vt2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[kBufs + c][0]; };
   __shared__ float s_km[KS ? kWaves : 1][16], s_kl[KS ? kWaves : 1][16];
@@ -838,6 +870,35 @@ void prefill_affine_kernel(const Args a) {
       // P V of one tile: the packed weights pp[u][j] (keys 32u + [0, 32) of
       // rows 16j + [0, 16)) times V^T from buffer Vt.
       auto pv_tile = [&](const h8_t (&pp)[2][NR], const uint16_t* Vt) __attribute__((always_inline)) {
+        if constexpr (VT) {
+          // Four operands read ahead of their products: one 16-byte read
+          // feeds two products, too little to cover the read's latency.
+  #pragma unroll
+          for (int u = 0; u < 2; ++u)
+  #pragma unroll
+            for (int t0 = 0; t0 < NT; t0 += 4) {
+              h8_t va[4];
+  #pragma unroll
+              for (int k = 0; k < 4; ++k)
+                va[k] = *reinterpret_cast<const h8_t*>(
+                    Vt + (u * D + 16 * (t_base + t0 + k) + lr) * kVtStr + 8 * lg);
+  #pragma unroll
+              for (int k = 0; k < 4; ++k)
+  #pragma unroll
+                for (int j = 0; j < NR; ++j)
+                  o[t0 + k][j] = mma<true>(va[k], pp[u][j], o[t0 + k][j]);
+            }
+          // The order for the scheduler: four reads, then a read after
+          // every two products, so four stay in flight.
+          __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+  #pragma unroll
+          for (int k = 0; k < 2 * NT - 4; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+          return;
+        }
   #pragma unroll
         for (int u = 0; u < 2; ++u)
   #pragma unroll
@@ -1178,6 +1239,8 @@ KernelFn pick_for(int bk, int bv) {
   if constexpr (!H16) {
     if (bk == kPreBits && bv == kPreBits) return prefill_affine_kernel<D, kPreBits, kPreBits, false>;
     if (bk == kPreBits && bv == kPreF16) return prefill_affine_kernel<D, kPreBits, kPreF16, false>;
+    if constexpr (D == 128)
+      if (bk == kPreBits && bv == kPreF16T) return prefill_affine_kernel<D, kPreBits, kPreF16T, false>;
   }
   switch (bk) {
     case 2: return pick_bv<D, 2, H16>(bv);

@@ -278,6 +278,9 @@ def test_prefill_with_caller_workspace(T, monkeypatch):
     T.scratch_release()
     need = T.prefill_workspace_size(B, Hkv, D, N)
     assert need == 2 * B * Hkv * N * D * 2
+    # Head dim 128 keeps V as 64-key tiles: a slab rounds up to whole tiles.
+    assert T.prefill_workspace_size(B, Hkv, D, N - 3) == need
+    assert T.prefill_workspace_size(B, Hkv, 64, N - 3) == 2 * B * Hkv * (N - 3) * 64 * 2
     dq = T.DeviceArray.of(q)
     segs = [T.affine_seg(tuple(a.ptr for a in kk), tuple(a.ptr for a in vv), c, n, sh)
             for (kk, vv, c, n, sh) in segs_host]
