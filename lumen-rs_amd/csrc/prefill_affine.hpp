@@ -936,6 +936,17 @@ void prefill_affine_kernel(const Args a) {
             for (int j = 0; j < NR; ++j)
               sc[i][j] = mma<H16>(ka, qf[j][s], sc[i][j]);
           }
+        if constexpr (VT) {
+          // Eight K reads first, then one after every two products (eight
+          // in flight; left to itself the scheduler keeps two).
+          __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+  #pragma unroll
+          for (int k = 0; k < 4 * NDW - 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+        }
         if constexpr (CS) {
           // Every wavefront of the block is live here (they share the rows).
   #pragma unroll
