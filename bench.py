@@ -432,7 +432,8 @@ def prefill_main(T, hip, args):
                                "of profiles/prefill_affine_config3.md (both launches of the "
                                "call)" if traffic is not None else None),
             "kernel": "tqkv_prefill_attend_affine call: dequantize_rows_kernel<128,4> (the "
-                      "keys once: K bf16, V f16 operands) + prefill_affine_kernel<128,16,17>",
+                      "keys once: K bf16 rows, V f16 operands as transposed 64-key tiles) + "
+                      "prefill_affine_kernel<128,16,18>",
             "alg_flops_per_launch": fl_g, "avg_launch_ms": round(ms_g, 5),
         },
         "sliding_layer_chunk": {
