@@ -70,6 +70,12 @@ def test_workspace_size_is_host_arithmetic():
     n = tqkv.decode_workspace_size(32, 16, 8, 256, 32768)
     assert n > 32 * 16 * 256 * 4
     assert tqkv.decode_workspace_size(0, 16, 8, 256, 10) == 0
+    # The prefill's dequantize-once rows: K and V, 2 bytes a value; at head
+    # dim 128 a slab holds whole 64-key tiles.
+    assert tqkv.prefill_workspace_size(4, 8, 128, 16384) == 2 * 4 * 8 * 16384 * 128 * 2
+    assert tqkv.prefill_workspace_size(4, 8, 128, 3071) == 2 * 4 * 8 * 3072 * 128 * 2
+    assert tqkv.prefill_workspace_size(1, 2, 256, 3071) == 2 * 1 * 2 * 3071 * 256 * 2
+    assert tqkv.prefill_workspace_size(1, 2, 128, 0) == 0
 
 
 def test_baseline_layouts_take_the_mfma_kernel(monkeypatch):

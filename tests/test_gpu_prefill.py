@@ -261,13 +261,14 @@ def test_prefill_dequantize_once_two_segments_by_default(T, monkeypatch):
     check(got, want, "once, two segments")
 
 
-def test_prefill_with_caller_workspace(T, monkeypatch):
+@pytest.mark.parametrize("N", [1024, 1021])
+def test_prefill_with_caller_workspace(T, monkeypatch, N):
     """tqkv_prefill_attend_affine_ws: with a workspace that holds the
     dequantized rows, without one (every block dequantizes), and after the
     library's scratch is released: the same bits as the library-scratch
-    entry."""
+    entry. 1021 keys end in a partial V tile (the slab pads to 1024)."""
     monkeypatch.delenv("TQKV_PREFILL_DEQUANT_ONCE", raising=False)
-    B, H, Hkv, D, L, N, gs, bk, bv = 1, 32, 8, 128, 256, 1024, 64, 4, 4
+    B, H, Hkv, D, L, gs, bk, bv = 1, 32, 8, 128, 256, 64, 4, 4
     q = kv_bf16((B, H, L, D), 31)
     k = kv_bf16((B, Hkv, N, D), 32, frac=0.01, mult=10.0)
     v = kv_bf16((B, Hkv, N, D), 33, frac=0.01, mult=10.0)
@@ -277,10 +278,9 @@ def test_prefill_with_caller_workspace(T, monkeypatch):
     want = run(T, q, segs_host, B, H, Hkv, L, D, gs, bk, bv, scale, N - L, 0, True, -1)
     T.scratch_release()
     need = T.prefill_workspace_size(B, Hkv, D, N)
-    assert need == 2 * B * Hkv * N * D * 2
     # Head dim 128 keeps V as 64-key tiles: a slab rounds up to whole tiles.
-    assert T.prefill_workspace_size(B, Hkv, D, N - 3) == need
-    assert T.prefill_workspace_size(B, Hkv, 64, N - 3) == 2 * B * Hkv * (N - 3) * 64 * 2
+    assert need == 2 * B * Hkv * 1024 * D * 2
+    assert T.prefill_workspace_size(B, Hkv, 64, N) == 2 * B * Hkv * N * 64 * 2
     dq = T.DeviceArray.of(q)
     segs = [T.affine_seg(tuple(a.ptr for a in kk), tuple(a.ptr for a in vv), c, n, sh)
             for (kk, vv, c, n, sh) in segs_host]
