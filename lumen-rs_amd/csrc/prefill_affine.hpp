@@ -264,12 +264,37 @@ constexpr int kPreF16 = 17;
 constexpr int kPreF16T = 18;
 template <int BITS>
 constexpr bool is_rows() { return BITS == kPreBits || BITS == kPreF16 || BITS == kPreF16T; }
-// Row stride of a V^T tile in LDS (elements): 96 bytes. Counted with
-// gfx950's bank rules (16-byte reads served 32 lanes at a time over 128
-// dword banks; 16-byte stores 8 lanes at a time over 32), the P V operand
-// reads are then conflict-free and a loader store costs 8 conflict cycles;
-// at 80 bytes the reads would cost 4 each.
-constexpr int kVtStr = 48;
+// Tiles of widths 16 and 18 at D = 128 go from HBM straight into LDS
+// (global_load_lds_dwordx4: each 16-byte lane load lands at the wavefront's
+// LDS base + 16 x lane, so a load instruction fills 1 KB of LDS in lane
+// order, and the loader picks each lane's source). The tiles sit in LDS
+// unpadded, 16-byte chunks permuted within their rows so that the operand
+// reads are conflict-free under gfx950's bank rules (16-byte reads served
+// 32 lanes at a time over 128 dword banks): K row r (256 bytes) keeps its
+// chunk c at position c ^ (r mod 16); V^T row R (64 bytes) keeps chunk c
+// at c ^ (2 x bit 3 of R).
+__device__ __forceinline__ uint32_t k_chunk_pos(uint32_t r, uint32_t c) { return c ^ (r & 15u); }
+__device__ __forceinline__ uint32_t vt_chunk_pos(uint32_t R, uint32_t c) { return c ^ (((R >> 3) & 1u) << 1); }
+// The LDS address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+// One global_load_lds_dwordx4: 16 bytes from each lane's src to LDS
+// [lds + 16 lane, lds + 16 lane + 16). Written as assembly so that the
+// compiler does not treat every later LDS read of the tile array as
+// waiting on it (it cannot tell the tile buffers apart); the kernel waits
+// for these loads itself (vmcnt(0)) before the barrier that publishes the
+// tile. M0 carries the LDS base; the kernels that use this set nothing
+// else in M0. An SALU write of M0 needs one wait state before an LDS DMA
+// reads it (the s_nop; the compiler pads the same way for its own).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobbers: see above
+__device__ __forceinline__ void lds_dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src),
+               "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 // 32-bit words of a loader task's run of 32 values.
 template <int BITS>
 constexpr int run_words() { return is_rows<BITS>() ? 16 : BITS; }
@@ -310,13 +335,6 @@ __device__ __forceinline__ SlabPtrs slabs_for(const Seg& s0, const Seg& s1, cons
 template <int D, int BITS, int NW>
 __device__ __forceinline__ void load_stage(Stage<NW>& st, const SlabPtrs& p, const Args& a, int kk,
                                            int run) {
-  if constexpr (BITS == kPreF16T) {  // row kk % 64 + 64 run of tile kk / 64
-    static_assert(D == 128, "transposed V tiles at head dim 128");
-    load_words<16>(st.w, p.w0 + (uint32_t(kk / kTile) * (D * 32) +
-                                 uint32_t(kk % kTile + kTile * run) * 16));
-    st.s = st.b = 0u;
-    return;
-  }
   kk = min(kk, int(a.total) - 1);  // 32-bit: a cache holds fewer than 2^31 keys
   if constexpr (is_rows<BITS>()) {  // one segment of 16-bit rows, no scales
     load_words<16>(st.w, p.w0 + (uint32_t(kk) * (D / 2) + run * 16));
@@ -459,7 +477,7 @@ __device__ __forceinline__ void store_k(const Stage<NW>& st, uint16_t* Ks, int k
 // the power of two.
 template <int BITS>
 __device__ __forceinline__ void v_operand_run(const uint32_t* w, uint32_t sb, uint32_t* out) {
-  if constexpr (BITS == kPreF16 || BITS == kPreF16T) {
+  if constexpr (BITS == kPreF16) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) out[i] = w[i];
   } else if constexpr (BITS == kPreBits) {
@@ -484,11 +502,6 @@ template <int D, int BITS, bool H16, int NW>
 __device__ __forceinline__ void store_v(const Stage<NW>& st, uint16_t* Vs, int key, int run) {
   if constexpr (H16) {
     store_k<D, BITS, H16>(st, Vs, key, run);
-  } else if constexpr (BITS == kPreF16T) {  // row key + 64 run of the V^T tile
-    u32x4_t* d = reinterpret_cast<u32x4_t*>(Vs + (key + kTile * run) * kVtStr);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      d[i] = u32x4_t{st.w[4 * i], st.w[4 * i + 1], st.w[4 * i + 2], st.w[4 * i + 3]};
   } else {
     constexpr int KSTR = kKStride<D>;
     uint32_t v[16];
@@ -609,16 +622,21 @@ void prefill_affine_kernel(const Args a) {
   // where P V runs one tile late on half the wavefronts.
   // K tiles then V tiles, one array: after the last tile the key split
   // merges its quarters' accumulators in the same memory.
-  // V^T tiles (width 18) are 2 D rows at kVtStr.
+  // V^T tiles (width 18; K bf16 rows with them): loaded straight into LDS,
+  // unpadded, chunks permuted (k_chunk_pos, vt_chunk_pos).
   constexpr bool VT = BV == kPreF16T;
-  static_assert(!VT || (D == 128 && !H16 && !KS && !CS), "V^T tiles: the bf16 variant at D = 128");
+  static_assert(!VT || (D == 128 && BK == kPreBits && !H16 && !KS && !CS && kWaves == 8),
+                "V^T tiles: the bf16 variant at D = 128");
   // (Buffers of one size, a two-dimensional array: with buffer offsets
   // computed from a flat array the compiler keeps more addresses live and
   // spills.)
-  constexpr int kBufElems = VT ? 2 * D * kVtStr : kTile * KSTR;
-  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[kBufs + kVBufs][kBufElems];
+  constexpr int kBufElems = VT ? kTile * D : kTile * KSTR;
+  // The V^T variant loads two tiles ahead straight into LDS: three K and
+  // four V buffers (112 KiB).
+  constexpr int KBN = VT ? 3 : kBufs, VBN = VT ? 4 : kVBufs;
+  __shared__ __attribute__((aligned(16))) uint16_t s_tiles[KBN + VBN][kBufElems];
   auto Ks2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[c][0]; };
-  auto Vt2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[kBufs + c][0]; };
+  auto Vt2 = [&](int c) __attribute__((always_inline)) { return &s_tiles[KBN + c][0]; };
   __shared__ float s_km[KS ? kWaves : 1][16], s_kl[KS ? kWaves : 1][16];
   __shared__ f4_t s_part[CS ? kWaves : 1][CS ? 4 : 1][kWave];
 
@@ -853,19 +871,74 @@ void prefill_affine_kernel(const Args a) {
             store_k<D, BK, H16>(stk[S][i], Ks2(kbuf), tkey[i], trun[i]);
         });
       };
-      load_tile(std::integral_constant<int, 0>{}, t_lo);
-      // Everything loaded so far (the Q fragments, the first tile) has
-      // landed: without this the compiler's loop-carried wait analysis keeps
-      // the Q loads pending and makes every tile's MFMAs wait for the next
-      // tile's prefetch. (vmcnt(0); expcnt and lgkmcnt unchanged.)
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      store_tile(std::integral_constant<int, 0>{}, 0, 0);
-      // Tile t_lo + 1 + k into set (k + 1) % NS: tile x sits in set
-      // (x - t_lo) % NS until it is dequantized.
-      static_for<NS>([&](auto k) {
-        load_tile(std::integral_constant<int, (decltype(k)::value + 1) % NS>{},
-                  t_lo + 1 + decltype(k)::value);
-      });
+      // V^T tiles: tile tt's K and V^T straight into LDS buffers kb and vb,
+      // this wavefront's four 1 KB quarters-of-an-eighth (K chunks 2 w and
+      // 2 w + 1 of the tile's 16, the same of V^T). Lane l of K chunk j
+      // fills row r = 4 j + l / 16 at position l % 16 with the row's chunk
+      // k_chunk_pos(r, l % 16) (rows past the last key re-read it: their
+      // scores are masked); of V^T chunk j, row R = 16 j + l / 4 at position
+      // l % 4 (V^T tiles are whole, zeros past the last key).
+      uint32_t dma_kr[2], dma_kc[2], dma_v[2];
+      if constexpr (VT) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint32_t j = uint32_t(2 * wave + i);
+          dma_kr[i] = 4 * j + uint32_t(lane) / 16;
+          dma_kc[i] = 16 * k_chunk_pos(dma_kr[i], uint32_t(lane) % 16);
+          const uint32_t R = 16 * j + uint32_t(lane) / 4;
+          dma_v[i] = R * 64 + 16 * vt_chunk_pos(R, uint32_t(lane) % 4);
+        }
+      }
+      auto dma_tile = [&](int64_t tt, int kb, int vb) __attribute__((always_inline)) {
+        if constexpr (VT) {
+          const uint32_t tc = uint32_t(tt < t_hi ? tt : t_hi);
+          const uint32_t klds = __builtin_amdgcn_readfirstlane(lds_addr(Ks2(kb)));
+          const uint32_t vlds = __builtin_amdgcn_readfirstlane(lds_addr(Vt2(vb)));
+          const char* kbase = reinterpret_cast<const char*>(kp.w0);
+          const char* vbase = reinterpret_cast<const char*>(vp.w0) + size_t(tc) * (kTile * D * 2);
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const uint32_t row = min(tc * kTile + dma_kr[i], uint32_t(a.total) - 1);
+            lds_dma16(kbase + size_t(row) * (D * 2) + dma_kc[i], klds + uint32_t(2 * wave + i) * 1024);
+          }
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            lds_dma16(vbase + dma_v[i], vlds + uint32_t(2 * wave + i) * 1024);
+        }
+      };
+      // Operand read offsets in the V^T variant's unpadded tiles (elements):
+      // K chunk 4 s + lg of row lr (+ 16 i rows), V^T chunk lg of row lr
+      // (+ u D + 16 t2 rows: bit 3 of the row is bit 3 of lr).
+      int kco[NDW], vco = 0;
+      if constexpr (VT) {
+#pragma unroll
+        for (int s2 = 0; s2 < NDW; ++s2)
+          kco[s2] = lr * D + 8 * int(k_chunk_pos(uint32_t(lr), uint32_t(4 * s2 + lg)));
+        vco = lr * 32 + 8 * int(vt_chunk_pos(uint32_t(lr), uint32_t(lg)));
+      }
+      if constexpr (VT) {
+        // The Q fragments and the first tile have landed before the loop;
+        // the second tile is in flight.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        dma_tile(t_lo, 0, 0);
+        dma_tile(t_lo + 1, 1, 1);
+        __builtin_amdgcn_s_waitcnt(0x0F74);
+      } else {
+        load_tile(std::integral_constant<int, 0>{}, t_lo);
+        // Everything loaded so far (the Q fragments, the first tile) has
+        // landed: without this the compiler's loop-carried wait analysis
+        // keeps the Q loads pending and makes every tile's MFMAs wait for
+        // the next tile's prefetch. (vmcnt(0); expcnt and lgkmcnt
+        // unchanged.)
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        store_tile(std::integral_constant<int, 0>{}, 0, 0);
+        // Tile t_lo + 1 + k into set (k + 1) % NS: tile x sits in set
+        // (x - t_lo) % NS until it is dequantized.
+        static_for<NS>([&](auto k) {
+          load_tile(std::integral_constant<int, (decltype(k)::value + 1) % NS>{},
+                    t_lo + 1 + decltype(k)::value);
+        });
+      }
       __syncthreads();
       // P V of one tile: the packed weights pp[u][j] (keys 32u + [0, 32) of
       // rows 16j + [0, 16)) times V^T from buffer Vt.
@@ -881,7 +954,7 @@ void prefill_affine_kernel(const Args a) {
   #pragma unroll
               for (int k = 0; k < 4; ++k)
                 va[k] = *reinterpret_cast<const h8_t*>(
-                    Vt + (u * D + 16 * (t_base + t0 + k) + lr) * kVtStr + 8 * lg);
+                    Vt + (u * D + 16 * (t_base + t0 + k)) * 32 + vco);
   #pragma unroll
               for (int k = 0; k < 4; ++k)
   #pragma unroll
@@ -930,8 +1003,11 @@ void prefill_affine_kernel(const Args a) {
         for (int s = 0; s < NDW; ++s)
   #pragma unroll
           for (int i = 0; i < 4; ++i) {
+            // (V^T tiles: K rows unpadded, chunk 4 s + lg of row 16 i + lr
+            // at its permuted position.)
             const op8_t ka = *reinterpret_cast<const op8_t*>(
-                Ks + (16 * i + lr) * KSTR + 32 * (s_base + s) + 8 * lg);
+                VT ? Ks + 16 * i * D + kco[s]
+                   : Ks + (16 * i + lr) * KSTR + 32 * (s_base + s) + 8 * lg);
   #pragma unroll
             for (int j = 0; j < NR; ++j)
               sc[i][j] = mma<H16>(ka, qf[j][s], sc[i][j]);
@@ -1037,8 +1113,9 @@ void prefill_affine_kernel(const Args a) {
         }
         weigh(sc, pp, lsum);
       };
-      auto vnext = [](int c) { return kVBufs == 3 ? (c == 2 ? 0 : c + 1) : (c ^ (kVBufs - 1)); };
-      auto vprev = [](int c) { return c == 0 ? kVBufs - 1 : c - 1; };
+      auto vnext = [](int c) { return VBN >= 3 ? (c == VBN - 1 ? 0 : c + 1) : (c ^ (VBN - 1)); };
+      auto vprev = [](int c) { return c == 0 ? VBN - 1 : c - 1; };
+      auto knext = [](int c) { return KBN == 3 ? (c == 2 ? 0 : c + 1) : (c ^ (KBN - 1)); };
       // The second wavefront of each SIMD multiplies by V one tile late:
       // pprev then carries the previous tile's packed weights.
       constexpr bool DEFER = kDeferPV && DQF;
@@ -1048,7 +1125,12 @@ void prefill_affine_kernel(const Args a) {
       // LDS buffers (last read in an earlier tile, before the barrier that
       // ended it); S then fetches tile t + 1 + NS.
       auto tile = [&](int64_t t, int cur, int vc, auto set) __attribute__((always_inline)) {
-        if constexpr (kBufs == 2 && DQF) {
+        if constexpr (VT) {
+          // Tile t + 2 into the buffers after the next (K: tile t - 1's, read
+          // before the barrier that ended it; V: tile t - 2's, whose late
+          // P V ran at the start of tile t - 1), in flight for two tiles.
+          dma_tile(t + 2, knext(knext(cur)), vnext(vnext(vc)));
+        } else if constexpr (kBufs == 2 && DQF) {
           store_tile(set, cur ^ 1, vnext(vc));
           load_tile(set, t + 1 + NS);
         }
@@ -1078,7 +1160,11 @@ void prefill_affine_kernel(const Args a) {
             }
           }
         }
-        if constexpr (kBufs == 2) {
+        if constexpr (VT) {
+          // This wavefront's part of tile t + 1 is in LDS (the four newest
+          // loads are tile t + 2's). (vmcnt(4); expcnt and lgkmcnt unchanged.)
+          __builtin_amdgcn_s_waitcnt(0x0F74);
+        } else if constexpr (kBufs == 2) {
           if constexpr (!DQF) {
             store_tile(set, cur ^ 1, vnext(vc));
             load_tile(set, t + 1 + NS);
@@ -1098,7 +1184,7 @@ void prefill_affine_kernel(const Args a) {
         static_for<NS>([&](auto k) {
           tile(t_lo + it * NS + decltype(k)::value, cur, vc,
                std::integral_constant<int, (decltype(k)::value + 1) % NS>{});
-          cur ^= kBufs - 1;
+          cur = knext(cur);
           vc = vnext(vc);
         });
       }
@@ -1107,6 +1193,9 @@ void prefill_affine_kernel(const Args a) {
       if constexpr (DEFER) {
         if (live) pv_tile(pprev, Vt2(vprev(vc)));
       }
+      // The re-loads of the last tile past the end land before the
+      // workgroup's LDS is released.
+      if constexpr (VT) __builtin_amdgcn_s_waitcnt(0x0F70);
     };
     // One copy of the loop per (task kind, order) a wavefront can have: the
     // two arms of a runtime branch would load into the same registers, and
