@@ -37,14 +37,18 @@
 //   to kTau (log2 units), so the O accumulators are rescaled only when some
 //   row moves by more; a lane compares its own 16-key maximum with the
 //   row's threshold, and only when some lane passes it are the row's lanes
-//   combined (two lane exchanges, l ^ 16 and l ^ 32). Row sums (of the f16-rounded weights, one
-//   v_dot2 per pair) stay per lane until the end.
+//   combined (two lane exchanges, l ^ 16 and l ^ 32). Row sums (of the
+//   f16-rounded weights, one v_dot2 per pair) stay per lane until the end.
 //   O^T += V^T . P^T: the score registers of key tiles 2u and 2u + 1 are,
 //   rounded to f16, exactly the B operand (k slot 8(l / 16) + s holds key
 //   32u + 4(l / 16) + s, s < 4, or 32u + 16 + 4(l / 16) + s - 4); the A
 //   operand takes the same keys of V^T from the row-major V tile with two
 //   transposing ds_read_b64_tr_b16 (the V stores are four 16-byte stores a
 //   run, where a transposed tile took 32 two-byte stores).
+// Keys dequantized beforehand (widths 16, 17, 18 below) skip the
+// dequantization: the loader copies their rows. With V^T tiles (width 18,
+// D = 128) the tiles go from HBM straight into LDS two tiles ahead, and
+// the A operand of P V is one 16-byte read.
 // Only tiles that some row of the block can see are visited, and the
 // per-element mask runs only on tiles that are not wholly visible.
 #pragma once
