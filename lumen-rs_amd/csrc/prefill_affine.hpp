@@ -268,7 +268,8 @@ constexpr int kPreF16 = 17;
 constexpr int kPreF16T = 18;
 template <int BITS>
 constexpr bool is_rows() { return BITS == kPreBits || BITS == kPreF16 || BITS == kPreF16T; }
-// Tiles of widths 16 and 18 at D = 128 go from HBM straight into LDS
+// The V^T variant (width 16 K rows with width 18 V^T tiles, D = 128) loads
+// its tiles from HBM straight into LDS
 // (global_load_lds_dwordx4: each 16-byte lane load lands at the wavefront's
 // LDS base + 16 x lane, so a load instruction fills 1 KB of LDS in lane
 // order, and the loader picks each lane's source). The tiles sit in LDS
@@ -287,8 +288,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // [lds + 16 lane, lds + 16 lane + 16). Written as assembly so that the
 // compiler does not treat every later LDS read of the tile array as
 // waiting on it (it cannot tell the tile buffers apart); the kernel waits
-// for these loads itself (vmcnt(0)) before the barrier that publishes the
-// tile. M0 carries the LDS base; the kernels that use this set nothing
+// for these loads itself (s_waitcnt vmcnt) before the barrier that
+// publishes the tile. M0 carries the LDS base; the kernels that use this set nothing
 // else in M0. An SALU write of M0 needs one wait state before an LDS DMA
 // reads it (the s_nop; the compiler pads the same way for its own).
 #pragma clang diagnostic push
@@ -876,8 +877,8 @@ void prefill_affine_kernel(const Args a) {
         });
       };
       // V^T tiles: tile tt's K and V^T straight into LDS buffers kb and vb,
-      // this wavefront's four 1 KB quarters-of-an-eighth (K chunks 2 w and
-      // 2 w + 1 of the tile's 16, the same of V^T). Lane l of K chunk j
+      // this wavefront's four 1 KB pieces (K chunks 2 w and 2 w + 1 of the
+      // tile's 16, the same of V^T). Lane l of K chunk j
       // fills row r = 4 j + l / 16 at position l % 16 with the row's chunk
       // k_chunk_pos(r, l % 16) (rows past the last key re-read it: their
       // scores are masked); of V^T chunk j, row R = 16 j + l / 4 at position
