@@ -73,6 +73,7 @@ PREFILL_CASES = [
     (1, 16, 2, 512, 40, 600, 4, 4, 64, 560, 0, True, -1, None),      # D = 512 (Gemma 4 global)
     (2, 8, 4, 512, 70, 300, 8, 6, 128, 230, 0, True, 100, 1.0),      # D = 512, window, 8/6-bit
     (1, 16, 2, 512, 96, 450, 3, 5, 32, 354, 0, True, -1, None),      # D = 512, 12 row blocks
+    (1, 8, 2, 128, 50, 40, 4, 4, 64, 0, 0, True, -1, None),          # fewer keys than a tile
 ]
 
 
@@ -207,7 +208,7 @@ def test_cache_prefill_rejects(T):
     assert e.value.status == T.EINVAL_SHAPE
 
 
-@pytest.mark.parametrize("case", [0, 1, 3, 4, 5, 7, 9, 10, 12])
+@pytest.mark.parametrize("case", [0, 1, 3, 4, 5, 7, 9, 10, 12, 13])
 def test_prefill_dequantize_once_is_bit_identical(T, monkeypatch, case):
     # Keys dequantized once into scratch (mlx::dequantize's bits) and then
     # copied into LDS give the same bf16 operands as dequantizing them in
