@@ -1159,16 +1159,24 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
   }
   // D <= 256: the lane's key row of the next tile loads while this tile's
   // softmax and values run (16 B a load, D / 16 registers of 4 words).
+  // D = 256 (kVRegs): once a tile's keys are scored, their 64 registers take
+  // the tile's 64 value words (one 4-byte load a token, all issued at once,
+  // landing under the softmax), and the next tile's key row loads a quarter
+  // at a time as the value words are used up. A value loop that loaded
+  // words as it went waited for memory every four tokens.
   constexpr bool kAhead = D <= 256;
+  constexpr bool kVRegs = D == 256;
   constexpr int KW = kAhead ? D / 16 : 1;
   uint4 kn[KW];
-  auto load_keys = [&](int64_t at) {
-    if (at < t1) {
-      const uint8_t* row = kc + (slab + at) * D;
+  // Unconditional loads (a lane past the range re-reads the range's last
+  // row, whose scores it masks): a lane that kept its old row instead would
+  // hold both rows' registers live at once.
+  auto load_keys_part = [&](int64_t at, int i0, int i1) {
+    const uint8_t* row = kc + (slab + (at < t1 ? at : t1 - 1)) * D;
 #pragma unroll
-      for (int i = 0; i < KW; ++i) kn[i] = *reinterpret_cast<const uint4*>(row + 16 * i);
-    }
+    for (int i = i0; i < i1; ++i) kn[i] = *reinterpret_cast<const uint4*>(row + 16 * i);
   };
+  auto load_keys = [&](int64_t at) { load_keys_part(at, 0, KW); };
   if constexpr (kAhead) load_keys(t0 + lane);
   for (int64_t base = t0; base < t1; base += kCbTile) {
     const int64_t t = base + lane;
@@ -1218,7 +1226,18 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
         }
       }
     }
-    if constexpr (kAhead) load_keys(t + kCbTile);  // this tile's keys are scored
+    const int cnt = int(t1 - base < kCbTile ? t1 - base : kCbTile);
+    uint32_t vw[kVRegs ? kCbTile : 1];
+    if constexpr (kVRegs) {
+      // Tokens past the range re-read the last row; their weights are 0.
+      __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* vrow = vc + (slab + base) * D + PER * lane;
+#pragma unroll
+      for (int j = 0; j < kCbTile; ++j)
+        vw[j] = *reinterpret_cast<const uint32_t*>(vrow + int64_t(j < cnt ? j : cnt - 1) * D);
+    } else if constexpr (kAhead) {
+      load_keys(t + kCbTile);  // this tile's keys are scored
+    }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float mx = valid ? sc[h] : -INFINITY;
@@ -1240,9 +1259,25 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     __syncthreads();
     // Values: lane takes channels PER * lane .. + PER - 1 (one PER-byte load
     // of each token's row; the wavefront reads the row whole).
-    const int cnt = int(t1 - base < kCbTile ? t1 - base : kCbTile);
+    if constexpr (kVRegs) {
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+#pragma unroll
+        for (int j = 16 * qq; j < 16 * qq + 16; ++j) {
+#pragma unroll
+          for (int k = 0; k < PER; ++k) {
+            const float c = s_cv[(vw[j] >> (8 * k)) & 0xffu];
+#pragma unroll
+            for (int h = 0; h < G; ++h) acc[h][k] = fmaf(s_p[h][j], c, acc[h][k]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_keys_part(t + kCbTile, qq * (KW / 4), (qq + 1) * (KW / 4));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     const uint8_t* vrow = vc + (slab + base) * D + PER * lane;
-    for (int j = 0; j < cnt; ++j) {
+    for (int j = 0; j < (kVRegs ? 0 : cnt); ++j) {
       uint32_t cw[(PER + 3) / 4];
       if constexpr (PER == 1) {
         cw[0] = vrow[int64_t(j) * D];
