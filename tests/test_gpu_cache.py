@@ -340,7 +340,8 @@ def test_codebook_cache_append_and_decode(T, bits, qjl_words):
 
 
 @pytest.mark.parametrize("B,Hkv,G,D,N,bits", [(16, 8, 2, 128, 2100, 3), (32, 4, 4, 64, 1500, 4),
-                                              (2, 4, 2, 256, 1300, 3)])
+                                              (2, 4, 2, 256, 1300, 3), (1, 2, 8, 256, 700, 4),
+                                              (1, 1, 16, 256, 333, 3)])
 def test_codebook_decode_direct(T, B, Hkv, G, D, N, bits):
     """tqkv_decode_attend_codebook on codes and sigmas it is handed, against
     f64 attention over centroid * sigma in the rotated basis, rotated back;
