@@ -1123,22 +1123,25 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     const float* __restrict__ cent_v, int n_k, int n_v, float qscale, int64_t split_len,
     int n_splits, float* __restrict__ part_o, float* __restrict__ part_m,
     float* __restrict__ part_l, const uint32_t* __restrict__ ksg, const float* __restrict__ krn,
-    const float* __restrict__ pq, int qm) {
+    const float* __restrict__ pq, int qm, int hg) {
   constexpr int PER = D / kWave;
   __shared__ float s_ck[256], s_cv[256];
   __shared__ float s_p[G][kCbTile];
   __shared__ float s_pq[QJL ? G : 1][QJL ? kMaxQjl : 1];
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // blockIdx.y: KV head x head group (hg groups of G query heads each).
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int kvh = int(blockIdx.y) / hg;
+  const int h0 = kvh * G * hg + (int(blockIdx.y) % hg) * G;  // first query head
   const int lane = threadIdx.x;
   // The scaled query of the G heads: every lane reads the same values, so
   // the compiler loads them into scalar registers (s_load) as the scores
   // need them, where copies in LDS took a vector LDS read per four values
   // (measured at config 2's shape: 1.026 -> 0.960 ms a call).
-  const float* qg = qs + (int64_t(b) * H + kvh * G) * D;
+  const float* qg = qs + (int64_t(b) * H + h0) * D;
   if constexpr (QJL) {
     for (int i = lane; i < G * qm; i += kWave) {
       const int h = i / qm, r = i % qm;
-      s_pq[h][r] = pq[(int64_t(b) * H + kvh * G + h) * qm + r];
+      s_pq[h][r] = pq[(int64_t(b) * H + h0 + h) * qm + r];
     }
   }
   for (int i = lane; i < 256; i += kWave) {
@@ -1299,7 +1302,7 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
   }
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const int64_t row = (int64_t(b) * H + kvh * G + h) * n_splits + split;
+    const int64_t row = (int64_t(b) * H + h0 + h) * n_splits + split;
 #pragma unroll
     for (int k = 0; k < PER; ++k) part_o[row * D + PER * lane + k] = acc[h][k];
     if (lane == 0) {
@@ -1350,21 +1353,21 @@ int32_t launch_cb(int G, dim3 grid, hipStream_t st, const float* qs, int H, cons
                   const float* ks, const uint8_t* vc, const float* vs, int64_t cap, int64_t n,
                   int H_kv, const float* ck, const float* cv, int nk, int nv, float qscale,
                   int64_t split_len, int n_splits, float* po, float* pm, float* pl,
-                  const uint32_t* ksg, const float* krn, const float* pq, int m) {
+                  const uint32_t* ksg, const float* krn, const float* pq, int m, int hg) {
 #define TQKV_CB(GG)                                                                           \
   case GG:                                                                                   \
     if (ksg)                                                                                 \
       hipLaunchKernelGGL((cb_decode_kernel<D, GG, true>), grid, dim3(kWave), 0, st, qs, H, kc, \
                          ks, vc, vs, cap, n, H_kv, ck, cv, nk, nv, qscale, split_len, n_splits, \
-                         po, pm, pl, ksg, krn, pq, m);                                        \
+                         po, pm, pl, ksg, krn, pq, m, hg);                                    \
     else                                                                                     \
       hipLaunchKernelGGL((cb_decode_kernel<D, GG, false>), grid, dim3(kWave), 0, st, qs, H, kc,\
                          ks, vc, vs, cap, n, H_kv, ck, cv, nk, nv, qscale, split_len, n_splits, \
-                         po, pm, pl, ksg, krn, pq, m);                                        \
+                         po, pm, pl, ksg, krn, pq, m, hg);                                    \
     break;
   switch (G) {
     TQKV_CB(1) TQKV_CB(2) TQKV_CB(4) TQKV_CB(8) TQKV_CB(16)
-    default: return fail(TQKV_EUNSUPPORTED, "codebook decode with %d query heads per KV head", G);
+    default: return fail(TQKV_EUNSUPPORTED, "codebook decode with %d query heads a wavefront", G);
   }
 #undef TQKV_CB
   TQKV_LAUNCHED();
@@ -1449,7 +1452,8 @@ extern "C" int32_t tqkv_codebook_dequantize(const uint8_t* codes, const float* s
 extern "C" size_t tqkv_decode_codebook_workspace_size(int32_t B, int32_t H, int32_t D,
                                                        int64_t total_tokens) {
   if (B <= 0 || H <= 0 || D <= 0 || total_tokens <= 0) return 0;
-  const int64_t splits = (total_tokens + 511) / 512 < 64 ? (total_tokens + 511) / 512 : 64;
+  // The most splits decode_codebook plans for any context up to total_tokens.
+  const int64_t splits = (total_tokens + 255) / 256 < 64 ? (total_tokens + 255) / 256 : 64;
   return size_t(B) * H *
          (2 * size_t(D) + size_t(tq::kMaxQjl) + size_t(splits) * (size_t(D) + 2)) * sizeof(float);
 }
@@ -1482,14 +1486,29 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
   if (reinterpret_cast<uintptr_t>(k_codes) % 16 != 0)
     return fail(TQKV_EINVAL_ARG, "k_codes must be 16-byte aligned");
   const int G = H / H_kv;
-  // Splits of 512 tokens (at most 64); with 128 or more (batch row, KV head)
-  // units the grid fills the chip with splits of 1024 (at most 32), which
-  // pay the first key load and the merge half as often (config 2's shape:
-  // 1.061 against 1.094 ms). Never more splits than the workspace size
-  // assumes.
-  const bool wide = int64_t(B) * H_kv >= 128;
-  const int64_t per = wide ? 1024 : 512, most = wide ? 32 : 64;
-  const int64_t n_splits64 = (n + per - 1) / per < most ? (n + per - 1) / per : most;
+  // A wavefront takes Gw = G / hg of a KV head's query heads, Gw x D <= 1024
+  // (each head group re-reads the keys and values, mostly from L2): at D =
+  // 512 with 16 heads a KV head (Gemma 4's global layers) one wavefront of
+  // all 16 heads held 251 registers and the few (batch row, KV head) units
+  // left most SIMDs idle.
+  int hg = 1;
+  while (G / hg > 1 && (G / hg) * D > 1024) hg *= 2;
+  const int Gw = G / hg;
+  // Splits: with 128 or more (batch row, KV head, head group) units the grid
+  // fills the chip with splits of 1024 tokens (at most 32), which pay the
+  // first key load and the merge half as often (config 2's shape: 1.061
+  // against 1.094 ms); fewer units take enough splits for ~4,096
+  // wavefronts, never under 256 tokens a split, at most 64 (the workspace
+  // size assumes no more).
+  const int64_t units = int64_t(B) * H_kv * hg;
+  int64_t n_splits64;
+  if (units >= 128) {
+    n_splits64 = (n + 1023) / 1024 < 32 ? (n + 1023) / 1024 : 32;
+  } else {
+    n_splits64 = (4096 + units - 1) / units;
+    if (n_splits64 > (n + 255) / 256) n_splits64 = (n + 255) / 256;
+    if (n_splits64 > 64) n_splits64 = 64;
+  }
   const int n_splits = int(n_splits64);
   const int64_t split_len = (n + n_splits - 1) / n_splits;
   const size_t need = tqkv_decode_codebook_workspace_size(B, H, D, n);
@@ -1520,13 +1539,13 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
     TQKV_LAUNCHED();
   }
   const uint32_t* sg = qjl_m > 0 ? k_signs : nullptr;
-  const dim3 grid{unsigned(n_splits), unsigned(H_kv), unsigned(B)};
+  const dim3 grid{unsigned(n_splits), unsigned(H_kv * hg), unsigned(B)};
   int32_t rc = TQKV_OK;
   switch (D) {
-    case 64: rc = tq::launch_cb<64>(G, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
-    case 128: rc = tq::launch_cb<128>(G, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
-    case 256: rc = tq::launch_cb<256>(G, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
-    case 512: rc = tq::launch_cb<512>(G, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m); break;
+    case 64: rc = tq::launch_cb<64>(Gw, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m, hg); break;
+    case 128: rc = tq::launch_cb<128>(Gw, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m, hg); break;
+    case 256: rc = tq::launch_cb<256>(Gw, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m, hg); break;
+    case 512: rc = tq::launch_cb<512>(Gw, grid, st, qsc, H, k_codes, k_sigma, v_codes, v_sigma, cap, n, H_kv, centroids_k, centroids_v, 1 << bits_k, 1 << bits_v, qscale, split_len, n_splits, po, pm, pl, sg, k_rnorm, pq, qjl_m, hg); break;
     default: return fail(TQKV_EUNSUPPORTED, "codebook decode D=%d not in {64,128,256,512}", D);
   }
   if (rc) return rc;
