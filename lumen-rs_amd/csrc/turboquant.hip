@@ -1231,15 +1231,53 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     }
     const int cnt = int(t1 - base < kCbTile ? t1 - base : kCbTile);
     uint32_t vw[kVRegs ? kCbTile : 1];
+    const uint8_t* vrow = vc + (slab + base) * D + PER * lane;
     if constexpr (kVRegs) {
       // Tokens past the range re-read the last row; their weights are 0.
       __builtin_amdgcn_sched_barrier(0);
-      const uint8_t* vrow = vc + (slab + base) * D + PER * lane;
 #pragma unroll
       for (int j = 0; j < kCbTile; ++j)
         vw[j] = *reinterpret_cast<const uint32_t*>(vrow + int64_t(j < cnt ? j : cnt - 1) * D);
     } else if constexpr (kAhead) {
       load_keys(t + kCbTile);  // this tile's keys are scored
+    }
+    // D < 256: the values' codes go through registers 16 tokens at a time,
+    // two groups in flight (the first two load under the softmax), in
+    // place of a loop that loaded each token's codes as it went.
+    constexpr bool kVGroups = D < 256;
+    constexpr int VWD = (PER + 3) / 4;  // words of a lane's codes a token
+    constexpr int NGT = 16;             // tokens a group
+    uint32_t va[kVGroups ? NGT : 1][VWD], vb[kVGroups ? NGT : 1][VWD];
+    auto load_group = [&](uint32_t (&dst)[kVGroups ? NGT : 1][VWD], int g) {
+#pragma unroll
+      for (int u = 0; u < NGT; ++u) {
+        const int j = g * NGT + u;
+        const uint8_t* src = vrow + int64_t(j < cnt ? j : cnt - 1) * D;
+        if constexpr (PER == 1) {
+          dst[u][0] = *src;
+        } else if constexpr (PER == 2) {
+          dst[u][0] = *reinterpret_cast<const uint16_t*>(src);
+        } else {
+#pragma unroll
+          for (int w = 0; w < VWD; ++w) dst[u][w] = *reinterpret_cast<const uint32_t*>(src + 4 * w);
+        }
+      }
+    };
+    auto use_group = [&](const uint32_t (&src)[kVGroups ? NGT : 1][VWD], int g) {
+#pragma unroll
+      for (int u = 0; u < NGT; ++u) {
+        const int j = g * NGT + u;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+          const float c = s_cv[(src[u][k / 4] >> (8 * (k % 4))) & 0xffu];
+#pragma unroll
+          for (int h = 0; h < G; ++h) acc[h][k] = fmaf(s_p[h][j], c, acc[h][k]);
+        }
+      }
+    };
+    if constexpr (kVGroups) {
+      load_group(va, 0);
+      load_group(vb, 1);
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -1279,18 +1317,22 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    const uint8_t* vrow = vc + (slab + base) * D + PER * lane;
-    for (int j = 0; j < (kVRegs ? 0 : cnt); ++j) {
-      uint32_t cw[(PER + 3) / 4];
-      if constexpr (PER == 1) {
-        cw[0] = vrow[int64_t(j) * D];
-      } else if constexpr (PER == 2) {
-        cw[0] = *reinterpret_cast<const uint16_t*>(vrow + int64_t(j) * D);
-      } else {
+    if constexpr (kVGroups) {
+      // Tokens past the range re-read the last row; their weights are 0.
+      use_group(va, 0);
+      load_group(va, 2);
+      use_group(vb, 1);
+      load_group(vb, 3);
+      use_group(va, 2);
+      use_group(vb, 3);
+    }
+    // D = 512: one token's codes at a time (two words a lane; staged
+    // groups measured slower at Gemma 4's global shape).
+    for (int j = 0; j < (D > 256 ? cnt : 0); ++j) {
+      uint32_t cw[VWD];
 #pragma unroll
-        for (int w = 0; w < PER / 4; ++w)
-          cw[w] = *reinterpret_cast<const uint32_t*>(vrow + int64_t(j) * D + 4 * w);
-      }
+      for (int w = 0; w < VWD; ++w)
+        cw[w] = *reinterpret_cast<const uint32_t*>(vrow + int64_t(j) * D + 4 * w);
 #pragma unroll
       for (int k = 0; k < PER; ++k) {
         const float c = s_cv[(cw[k / 4] >> (8 * (k % 4))) & 0xffu];
