@@ -1528,6 +1528,9 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
   if (reinterpret_cast<uintptr_t>(k_codes) % 16 != 0)
     return fail(TQKV_EINVAL_ARG, "k_codes must be 16-byte aligned");
   const int G = H / H_kv;
+  if (G > 16 || (G & (G - 1)) != 0)
+    return fail(TQKV_EUNSUPPORTED, "codebook decode with %d query heads per KV head (1, 2, 4, "
+                "8 or 16)", G);
   // A wavefront takes Gw = G / hg of a KV head's query heads, Gw x D <= 1024
   // (each head group re-reads the keys and values, mostly from L2): at D =
   // 512 with 16 heads a KV head (Gemma 4's global layers) one wavefront of

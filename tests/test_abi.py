@@ -117,3 +117,17 @@ def test_long_segments_take_the_dot2_kernel(monkeypatch):
     assert tqkv.decode_kernel_for_rows(16, 8, 256, 64, 4, 4, 0) == \
         tqkv.decode_kernel_name(16, 8, 256, 64, 4, 4)
     assert tqkv.decode_kernel_for_rows(16, 8, 256, 64, 4, 4, -1) == ""
+
+
+def test_codebook_decode_refuses_other_head_groups_without_a_gpu():
+    """Query heads per KV head must be 1, 2, 4, 8 or 16: the decode splits a
+    KV head's heads into power-of-two groups across wavefronts, so 3 or 12
+    heads a KV head would leave heads out. The refusal comes before any
+    device call (the pointers below are never dereferenced)."""
+    import tqkv
+    lib = tqkv.lib()
+    p = ctypes.c_void_p(4096)
+    for H, H_kv in ((6, 2), (24, 2), (64, 2)):
+        rc = lib.tqkv_decode_attend_codebook(p, 1, H, H_kv, 512, ctypes.c_float(1.0), p, p, 4, p,
+                                             4, p, p, p, p, 64, 64, p, p, 1 << 20, None)
+        assert rc == tqkv.EUNSUPPORTED, (H, H_kv, rc)
