@@ -1054,30 +1054,53 @@ namespace {
 constexpr int kCbTile = 64;  // tokens per step of a wavefront
 
 // q_rot[b, h, :] = R q[b, h, :] in f32, and qs = q_rot * qscale (the
-// scores' query). A wavefront takes four outputs at a time: its lanes read
-// rows i of R (coalesced) against the query, then sum across the lanes.
-// blockDim: a multiple of 64 with D a multiple of 4 x its wavefronts.
-__global__ void cb_rotate_q_kernel(const uint16_t* __restrict__ q, const float* __restrict__ R,
-                                   int D, float qscale, float* __restrict__ qr,
-                                   float* __restrict__ qs) {
-  const int64_t bh = blockIdx.x;
+// scores' query). A workgroup takes kRotRows (batch row, head) rows and 64
+// outputs (blockIdx.y); a wavefront takes four outputs at a time for all
+// its rows: its lanes read rows i of R (coalesced) against the queries,
+// then sum across the lanes. Each load of R serves kRotRows rows (a
+// workgroup a row, reading all of R, made 128 MiB of L2 reads at config
+// 2's shape). Every output's sum runs in the same order either way.
+// blockDim: 256 (4 wavefronts x 4 outputs x 4 steps = 64 outputs).
+constexpr int kRotRows = 4;
+__global__ __launch_bounds__(256) void cb_rotate_q_kernel(const uint16_t* __restrict__ q,
+                                                          const float* __restrict__ R, int D,
+                                                          int64_t rows, float qscale,
+                                                          float* __restrict__ qr,
+                                                          float* __restrict__ qs) {
+  const int64_t r0 = int64_t(blockIdx.x) * kRotRows;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int waves = blockDim.x / kWave;
-  for (int i0 = 4 * wave; i0 < D; i0 += 4 * waves) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = lane; j < D; j += kWave) {
-      const float x = bf16_to_f32(q[bh * D + j]);
+  const uint16_t* qrow[kRotRows];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = fmaf(R[int64_t(i0 + r) * D + j], x, acc[r]);
+  for (int k = 0; k < kRotRows; ++k)
+    qrow[k] = q + (r0 + k < rows ? r0 + k : rows - 1) * D;  // rows past the end repeat one
+  for (int i0 = int(blockIdx.y) * kWave + 4 * wave; i0 < (int(blockIdx.y) + 1) * kWave;
+       i0 += 16) {
+    float acc[kRotRows][4] = {};
+    for (int j = lane; j < D; j += kWave) {
+      float x[kRotRows];
+#pragma unroll
+      for (int k = 0; k < kRotRows; ++k) x[k] = bf16_to_f32(qrow[k][j]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float rv = R[int64_t(i0 + r) * D + j];
+#pragma unroll
+        for (int k = 0; k < kRotRows; ++k) acc[k][r] = fmaf(rv, x[k], acc[k][r]);
+      }
     }
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] += __shfl_xor(acc[r], off, kWave);
-    if (lane < 4) {
-      const float v = lane == 0 ? acc[0] : lane == 1 ? acc[1] : lane == 2 ? acc[2] : acc[3];
-      qr[bh * D + i0 + lane] = v;
-      qs[bh * D + i0 + lane] = v * qscale;
+      for (int k = 0; k < kRotRows; ++k)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[k][r] += __shfl_xor(acc[k][r], off, kWave);
+#pragma unroll
+    for (int k = 0; k < kRotRows; ++k) {
+      if (lane < 4 && r0 + k < rows) {
+        const float v =
+            lane == 0 ? acc[k][0] : lane == 1 ? acc[k][1] : lane == 2 ? acc[k][2] : acc[k][3];
+        qr[(r0 + k) * D + i0 + lane] = v;
+        qs[(r0 + k) * D + i0 + lane] = v * qscale;
+      }
     }
   }
 }
@@ -1571,8 +1594,10 @@ int32_t decode_codebook(const uint16_t* q, int32_t B, int32_t H, int32_t H_kv, i
   float* pl = pm + size_t(B) * H * n_splits;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const float qscale = scale * 1.4426950408889634f;
-  hipLaunchKernelGGL(tq::cb_rotate_q_kernel, dim3(unsigned(B * H)), dim3(D < 256 ? D : 256), 0,
-                     st, q, rotation, D, qscale, qr, qsc);
+  const int64_t qrows = int64_t(B) * H;
+  hipLaunchKernelGGL(tq::cb_rotate_q_kernel,
+                     dim3(unsigned((qrows + tq::kRotRows - 1) / tq::kRotRows), unsigned(D / 64)),
+                     dim3(256), 0, st, q, rotation, D, qrows, qscale, qr, qsc);
   TQKV_LAUNCHED();
   if (qjl_m > 0) {
     if (qjl_rotated)
