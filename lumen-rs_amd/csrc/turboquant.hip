@@ -1394,14 +1394,15 @@ __global__ void cb_merge_kernel(const float* __restrict__ part_o, const float* _
   for (int s = threadIdx.x; s < n_splits; s += blockDim.x)
     s_w[s] = pm[s] != -INFINITY ? exp2f(pm[s] - mx) : 0.0f;
   __syncthreads();
+  // No branch per split (an empty split's weight is 0, and the decode
+  // writes its partial as zeros), so the unrolled loads issue together: a
+  // test per split had them wait one at a time.
   float ls = 0.0f;
-  for (int s = 0; s < n_splits; ++s)
-    if (pm[s] != -INFINITY) ls += pl[s] * s_w[s];
+  for (int s = 0; s < n_splits; ++s) ls += pl[s] * s_w[s];
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float os = 0.0f;
-#pragma unroll 8
-    for (int s = 0; s < n_splits; ++s)
-      if (pm[s] != -INFINITY) os += part_o[(bh * n_splits + s) * D + d] * s_w[s];
+#pragma unroll 16
+    for (int s = 0; s < n_splits; ++s) os += part_o[(bh * n_splits + s) * D + d] * s_w[s];
     s_o[d] = ls > 0.0f ? os / ls : 0.0f;
   }
   __syncthreads();
