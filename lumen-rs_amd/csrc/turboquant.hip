@@ -1193,6 +1193,10 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
   constexpr bool kAhead = D <= 256;
   constexpr bool kVRegs = D == 256;
   constexpr int KW = kAhead ? D / 16 : 1;
+  // The scores' loop over a key row: whole at D <= 256 (the row is in
+  // registers); at D = 512, eight 16-byte loads in flight (unrolled by one,
+  // each load had waited for the last).
+  constexpr int KU = kAhead ? KW : 8;
   uint4 kn[KW];
   // Unconditional loads (a lane past the range re-reads the range's last
   // row, whose scores it masks): a lane that kept its old row instead would
@@ -1212,7 +1216,7 @@ __global__ __launch_bounds__(kWave) void cb_decode_kernel(
     for (int h = 0; h < G; ++h) sc[h] = 0.0f;
     if (valid) {
       const uint8_t* row = kc + (slab + t) * D;
-#pragma unroll KW
+#pragma unroll KU
       for (int d = 0; d < D; d += 16) {
         const uint4 w = kAhead ? kn[d / 16] : *reinterpret_cast<const uint4*>(row + d);
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
