@@ -1410,12 +1410,25 @@ __global__ void cb_merge_kernel(const float* __restrict__ part_o, const float* _
     s_o[d] = ls > 0.0f ? os / ls : 0.0f;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < D; i += blockDim.x) {
-    float acc = 0.0f;
-#pragma unroll 8
-    for (int j = 0; j < D; ++j) acc = fmaf(R[int64_t(j) * D + i], s_o[j], acc);
-    out[bh * D + i] = f32_to_bf16(acc);
+  // o = R^T o_rot: a thread's outputs (one, or two at D = 512) in one loop,
+  // sixteen steps of loads of R in flight (the sums' order per output is
+  // the sequence j = 0 .. D-1 either way).
+  const int i0 = threadIdx.x, i1 = threadIdx.x + blockDim.x;
+  const bool two = i1 < D;
+  float a0 = 0.0f, a1 = 0.0f;
+  if (two) {
+#pragma unroll 16
+    for (int j = 0; j < D; ++j) {
+      const float o = s_o[j];
+      a0 = fmaf(R[int64_t(j) * D + i0], o, a0);
+      a1 = fmaf(R[int64_t(j) * D + i1], o, a1);
+    }
+  } else {
+#pragma unroll 16
+    for (int j = 0; j < D; ++j) a0 = fmaf(R[int64_t(j) * D + i0], s_o[j], a0);
   }
+  if (i0 < D) out[bh * D + i0] = f32_to_bf16(a0);
+  if (two) out[bh * D + i1] = f32_to_bf16(a1);
 }
 
 template <int D>
